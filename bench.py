@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Benchmark PONNI's batched forward pass on one MI355X.
+
+A step is one forward pass of the headline configuration (BASELINE.json
+configs[1], "c2": fp32 16->64->64->64->8 ReLU MLP, batch 4,194,304) over a
+synthetic input already resident in HBM.  Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--config c2] [--no-others] [--no-cpu]
+
+`value` is samples/s of the whole job (one GPU).  `roofline` prices the
+dominant kernel (the only kernel of a step) against MI355X's published peak:
+achieved = algorithmic work per sample x batch / mean kernel time, the kernel
+time measured with HIP events recorded on the launch stream around each
+launch.  `cpu_baseline` times the CPU restatement of the reference (oracle/,
+OpenMP over samples, as Kokkos' OpenMP RangePolicy) on a bounded sample on
+this host.  Other configurations are reported under "configs".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "samples/sec/GPU for fused MLP forward; % of HBM or MFMA roofline"
+ROTATE_BYTES = 512 << 20  # rotate buffers so the working set exceeds the 256 MB MALL
+
+
+def host_cores() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def make_inputs(cfg, torch, P, C):
+    tdt = torch.float16 if cfg.dtype == "f16" else torch.float32
+    es = 2 if cfg.dtype == "f16" else 4
+    per_set = (cfg.n_in + cfg.n_out) * cfg.batch * es
+    sets = max(1, -(-ROTATE_BYTES // per_set))
+    xs, ys = [], []
+    for i in range(sets):
+        x = torch.empty((cfg.n_in, cfg.batch), dtype=tdt, device="cuda:0")
+        kind, a, b = cfg.input_dist
+        P.fill_synthetic(x, cfg.seed + 7919 * i, C.INPUT_TAG, kind, a, b)
+        xs.append(x)
+        ys.append(torch.empty((cfg.n_out, cfg.batch), dtype=tdt, device="cuda:0"))
+    return xs, ys
+
+
+def time_config(cfg, steps, warmup, torch, P, C):
+    layers = cfg.layers(False)
+    model = P.create_inference_model(*layers, dtype=cfg.dtype)
+    xs, ys = make_inputs(cfg, torch, P, C)
+    stream = torch.cuda.current_stream()
+    B = cfg.batch
+
+    def launch(i):
+        x, y = xs[i % len(xs)], ys[i % len(ys)]
+        model.forward_raw(x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), B, stream.cuda_stream)
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    # Whole-job timing: K back-to-back launches.
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        launch(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(stop)
+    # Per-launch kernel time: events bracket each launch on the launch stream.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        launch(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    mean_ms = sum(per) / len(per)
+    work = cfg.flops_per_sample if cfg.bound == "mfma" else cfg.bytes_per_sample
+    achieved = work * B / (mean_ms * 1e-3)
+    unit = "TFLOP/s" if cfg.bound == "mfma" else "GB/s"
+    scale = 1e12 if cfg.bound == "mfma" else 1e9
+    return {
+        "model": model,
+        "layers": layers,
+        "samples_per_s": B * steps / (total_ms * 1e-3),
+        "ms_per_step": total_ms / steps,
+        "kernel_ms_mean": mean_ms,
+        "kernel_ms_min": per[0],
+        "kernel_ms_median": per[len(per) // 2],
+        "roofline": {
+            "bound": cfg.bound,
+            "achieved": round(achieved / scale, 3),
+            "peak": round(cfg.peak / scale, 3),
+            "unit": unit,
+            "frac": round(achieved / cfg.peak, 4),
+            "traffic": None,
+        },
+        "path": model.path,
+    }
+
+
+def cpu_baseline(cfg, budget_s=10.0):
+    """Time the oracle (CPU restatement of the reference) on a bounded sample."""
+    import numpy as np
+
+    import oracle
+    from ponni_amd import configs as C
+
+    oracle.build()
+    layers = cfg.layers(False)
+    cores = host_cores()
+    mode = oracle.MODE_F16_OPERANDS if cfg.dtype == "f16" else oracle.MODE_F32
+
+    def gen(n):
+        kind, a, b = cfg.input_dist
+        f = C.uniform if kind == "uniform" else C.normal
+        return f(cfg.n_in * n, cfg.seed, C.INPUT_TAG, a, b).reshape(cfg.n_in, n)
+
+    n = 8192
+    x = gen(n)
+    t0 = time.perf_counter()
+    oracle.forward(layers, x, mode, cores)
+    dt = time.perf_counter() - t0
+    n = int(min(cfg.batch, max(8192, n * budget_s / max(dt, 1e-6) * 0.8)))
+    x = gen(n)
+    t0 = time.perf_counter()
+    oracle.forward(layers, x, mode, cores)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(n / dt, 1),
+        "unit": "samples/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{n} samples of {cfg.name} ({cfg.description}), {dt:.1f} s, OpenMP over samples",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-others", action="store_true", help="skip the other configurations")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the forward pass shards over the batch with no "
+              "collective, and this build runs and reports a single MI355X.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import ponni_amd as P
+    from ponni_amd import configs as C
+
+    torch.cuda.init()
+    cfg = C.CONFIGS[args.config]
+    head = time_config(cfg, args.steps, args.warmup, torch, P, C)
+    others = {}
+    if not args.no_others:
+        for name, c in C.CONFIGS.items():
+            if name == cfg.name:
+                continue
+            r = time_config(c, max(5, args.steps // 2), args.warmup, torch, P, C)
+            others[name] = {
+                "samples_per_s": round(r["samples_per_s"], 1),
+                "kernel_ms_mean": round(r["kernel_ms_mean"], 4),
+                "path": r["path"],
+                "batch": c.batch,
+                "dtype": c.dtype,
+                "roofline": r["roofline"],
+            }
+            del r
+            torch.cuda.empty_cache()
+    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(head["samples_per_s"], 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if cfg.dtype == "f32" else "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name}: {cfg.description}",
+            "global_batch": cfg.batch,
+            "path": head["path"],
+            "kernel_ms_mean": round(head["kernel_ms_mean"], 4),
+            "kernel_ms_min": round(head["kernel_ms_min"], 4),
+            "kernel_ms_median": round(head["kernel_ms_median"], 4),
+            "parallelism": "single GPU",
+        },
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "configs": others,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,236 @@
+/*
+ * ponni_hip.h -- C ABI of libponni_hip.so, the MI355X (gfx950) implementation
+ * of PONNI's batched forward pass.
+ *
+ * The reference has no FFI: its operator API is the compile-time C++ layer
+ * contract plus the Inference model object.  Every entry point below replaces
+ * one piece of that contract; the reference file:line it stands in for is
+ * cited on each declaration (paths are relative to the reference root).  The
+ * header-only C++ facade in ponni_amd/include/ponni.h rebuilds the reference's
+ * C++ API (create_inference_model, the layer templates, Inference, PonniFile)
+ * on top of these functions.
+ *
+ * Conventions
+ *   - Status: every int-returning call returns PONNI_OK (0) or a nonzero
+ *     ponni_status; ponni_last_error() then holds a thread-local message.
+ *   - Layout: activations are feature-major [features, batch]; element (f, b)
+ *     of a buffer with row stride ld lives at base + f*ld + b (LayoutRight).
+ *   - Ownership: callers own input and output buffers; a plan owns only its
+ *     device weights and retained scratch.
+ *   - Streams: ponni_forward is asynchronous on the caller's stream and never
+ *     synchronizes (a null stream means the default stream).
+ */
+#ifndef PONNI_HIP_H
+#define PONNI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef HIP_INCLUDE_HIP_HIP_RUNTIME_API_H
+typedef struct ihipStream_t* hipStream_t;
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PONNI_ABI_VERSION 1
+
+typedef enum ponni_status {
+  PONNI_OK = 0,
+  PONNI_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad enum, negative size  */
+  PONNI_ERR_INVALID_MODEL = 2,    /* layer chain fails Inference::validate  */
+  PONNI_ERR_SHAPE = 3,            /* batch == 0 or extents do not match      */
+  PONNI_ERR_UNSUPPORTED = 4,      /* forced kernel path cannot run the model */
+  PONNI_ERR_DEVICE = 5,           /* HIP runtime error                      */
+  PONNI_ERR_IO = 6                /* .ponni file rejected                    */
+} ponni_status;
+
+/* Element type of activations (and of the arithmetic that produces them). */
+typedef enum ponni_dtype {
+  PONNI_F32 = 1,
+  PONNI_F64 = 2,
+  PONNI_F16 = 3,  /* fp16 operands, fp32 accumulation */
+  PONNI_BF16 = 4  /* bf16 operands, fp32 accumulation */
+} ponni_dtype;
+
+/* Built-in layer templates, src/ponni.h:27-48 of the reference. */
+typedef enum ponni_layer_kind {
+  PONNI_LAYER_MATVEC = 1,        /* layers/ponni_Matvec.h: W [n_in, n_out]          */
+  PONNI_LAYER_BIAS = 2,          /* layers/ponni_Bias.h: b [n]                       */
+  PONNI_LAYER_RELU = 3,          /* layers/ponni_Relu.h                              */
+  PONNI_LAYER_LEAKY_RELU = 4,    /* layers/ponni_LeakyRelu.h: attr[0] negative_slope */
+  PONNI_LAYER_ELU = 5,           /* layers/ponni_Elu.h: attr[0] alpha                */
+  PONNI_LAYER_SELU = 6,          /* layers/ponni_Selu.h                              */
+  PONNI_LAYER_GELU = 7,          /* layers/ponni_Gelu.h: flags bit0 = approximate    */
+  PONNI_LAYER_SILU = 8,          /* layers/ponni_Silu.h                              */
+  PONNI_LAYER_SIGMOID = 9,       /* layers/ponni_Sigmoid.h                           */
+  PONNI_LAYER_TANH = 10,         /* layers/ponni_Tanh.h                              */
+  PONNI_LAYER_SOFTPLUS = 11,     /* layers/ponni_Softplus.h: attr[0] beta            */
+  PONNI_LAYER_HARD_SIGMOID = 12, /* layers/ponni_HardSigmoid.h: attr[0] alpha, [1] beta */
+  PONNI_LAYER_HARD_SWISH = 13,   /* layers/ponni_HardSwish.h                         */
+  PONNI_LAYER_MISH = 14,         /* layers/ponni_Mish.h                              */
+  PONNI_LAYER_SOFTMAX = 20,      /* layers/ponni_Softmax.h (barrier)                 */
+  PONNI_LAYER_LOG_SOFTMAX = 21,  /* layers/ponni_LogSoftmax.h (barrier)              */
+  PONNI_LAYER_LAYER_NORM = 22,   /* layers/ponni_LayerNorm.h: gamma[n], beta[n]; attr[0] epsilon */
+  PONNI_LAYER_MIN_MAX_NORM = 23, /* layers/ponni_MinMaxNorm.h: attr out_min, out_max, epsilon */
+  PONNI_LAYER_SAVE_STATE = 30,   /* layers/ponni_Save_State.h: slot = ISAVE          */
+  PONNI_LAYER_BINOP_ADD = 31,    /* layers/ponni_Binop_Add.h: slot = ISAVE           */
+  PONNI_LAYER_BINOP_CONCATENATE = 32, /* layers/ponni_Binop_Concatenate.h: slot; n_in = N1,
+                                         n_out = N1 + N2; flags bit0 = after         */
+  PONNI_LAYER_BINOP_PROJECTION_ADD = 33 /* layers/ponni_Binop_Projection_Add.h: slot;
+                                           n_aux = NSAVE; W [NSAVE, n_in], bias [n_in] */
+} ponni_layer_kind;
+
+/* One layer of the tuple handed to create_inference_model
+ * (src/ponni_create_model.h:40-65).  Widths are the runtime extents the
+ * reference reads from each layer's Views (e.g. ponni_Matvec.h:62-65). */
+typedef struct ponni_layer_desc {
+  int32_t kind;    /* ponni_layer_kind                                      */
+  int32_t n_in;    /* get_num_inputs()                                      */
+  int32_t n_out;   /* get_num_outputs()                                     */
+  int32_t slot;    /* ISAVE of Save_State / Binop_*; ignored otherwise      */
+  int32_t n_aux;   /* NSAVE of Binop_Projection_Add; ignored otherwise      */
+  int32_t flags;   /* PONNI_FLAG_*                                          */
+  double attr[4];  /* scalar configuration (slope, alpha, beta, epsilon...) */
+} ponni_layer_desc;
+
+#define PONNI_FLAG_GELU_APPROXIMATE 1 /* Gelu(n, approximate = true)      */
+#define PONNI_FLAG_CONCAT_AFTER 1     /* Binop_Concatenate(.., after=true) */
+
+/* Kernel families a plan can run on. */
+typedef enum ponni_path {
+  PONNI_PATH_AUTO = 0,    /* pick the fastest path that supports the model          */
+  PONNI_PATH_GENERIC = 1, /* one sample per lane, states in HBM scratch (any model) */
+  PONNI_PATH_NARROW = 2,  /* one sample per lane, states in registers (width <= 16) */
+  PONNI_PATH_MFMA = 3     /* 16x16 MFMA tiles, states in registers (width <= 256)   */
+} ponni_path;
+
+typedef struct ponni_plan_s* ponni_plan;
+
+/* Facts about a compiled plan; mirrors the scratch-planning queries of
+ * src/ponni_Inference.h:92-122, :180, :204-223 and :75-85. */
+typedef struct ponni_plan_info {
+  int32_t path;              /* ponni_path actually selected                      */
+  int32_t dtype;             /* ponni_dtype                                       */
+  int32_t num_layers;
+  int32_t num_inputs;        /* first layer get_num_inputs()                      */
+  int32_t num_outputs;       /* last layer get_num_outputs()                      */
+  int32_t num_fused_dense_blocks;  /* get_num_fused_dense_blocks()                */
+  int32_t num_saved_states;  /* get_num_saved_states()                            */
+  int32_t tmp1_features;     /* get_planned_temporary_size<0>()                   */
+  int32_t tmp2_features;     /* get_planned_temporary_size<1>()                   */
+  int32_t saved_features[8]; /* get_saved_state_size<i>() for slots 0..7          */
+  int64_t num_parameters;    /* all layer parameters, trainable or not           */
+  int64_t internal_state_capacity; /* internal_state_capacity()                   */
+  int32_t max_width;         /* widest state anywhere in the chain                */
+  int32_t width_class;       /* register tile width chosen by NARROW / MFMA       */
+} ponni_plan_info;
+
+/* --- library ------------------------------------------------------------ */
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+const char* ponni_last_error(void);
+
+/* PONNI_ABI_VERSION of the loaded library. */
+int ponni_abi_version(void);
+
+/* --- plans (the Inference object) ---------------------------------------- */
+
+/* Validate a layer chain and build a plan; replaces detail::create_model +
+ * Inference(TUPLE) + Inference::validate (ponni_create_model.h:21-34,
+ * ponni_Inference.h:159-162, :719-737).  Host-only: touches no device.  Each
+ * layer's parameters start at zero until ponni_plan_set_layer_params. */
+int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers,
+                      int32_t dtype, int32_t path, ponni_plan* out_plan);
+
+/* Release a plan, its device weights and scratch (Inference::~Inference). */
+void ponni_plan_destroy(ponni_plan plan);
+
+/* Describe the plan (see ponni_plan_info). */
+int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info);
+
+/* Number of parameter values layer `layer` carries, trainable or not:
+ * Matvec n_in*n_out, Bias n, LayerNorm 2n (gamma then beta),
+ * Projection_Add NSAVE*n_in + n_in (W then bias), others 0. */
+int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer);
+
+/* Copy one layer's parameters from host memory, in the layer's own order
+ * (Matvec W [n_in, n_out] row-major; LayerNorm gamma then beta;
+ * Projection_Add W [NSAVE, n_in] then bias).  `values` is float for F32,
+ * F16 and BF16 plans and double for F64 plans.  Replaces the layer Views
+ * held by each template (e.g. ponni_Matvec.h:29-51) and their
+ * set_trainable_parameters (ponni_Matvec.h:103-109).  Re-packs the device
+ * copy; synchronous with respect to the host. */
+int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer,
+                                const void* values, int64_t count);
+
+/* Read one layer's parameters back into host memory (same order and type). */
+int ponni_plan_get_layer_params(ponni_plan plan, int32_t layer,
+                                void* values, int64_t count);
+
+/* Reallocate batch-dependent scratch to exactly `batch` columns;
+ * Inference::reallocate_internal_state (ponni_Inference.h:169-176).
+ * Synchronizes the device first, as the reference fences. */
+int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch);
+
+/* Batched forward pass: y[n_out, batch] = model(x[n_in, batch]).  Replaces
+ * Inference::forward_batch_parallel(input, output) (ponni_Inference.h:352-389)
+ * and the generated infer_batch (kokkos_nn/emitter.py:1537-1550, :1903-1927).
+ * x and y are device pointers of the plan's dtype with row strides ld_in and
+ * ld_out (>= batch).  Grows scratch on demand (ponni_Inference.h:197-199).
+ * Asynchronous on `stream`; returns PONNI_ERR_SHAPE for batch <= 0, where the
+ * reference aborts (ponni_Inference.h:366). */
+int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y,
+                  int64_t ld_out, int64_t batch, hipStream_t stream);
+
+/* --- synthetic data (bench and tests) ------------------------------------- */
+
+/* Fill n elements of a device buffer of `dtype` with the counter-based
+ * synthetic stream: u64 = splitmix64(seed, tag, index); dist 0 = uniform on
+ * [a, b) from the top 24 bits, dist 1 = normal(mean a, std b) by Box-Muller.
+ * Asynchronous on `stream`. */
+int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed,
+                         uint64_t tag, int32_t dist, double a, double b,
+                         hipStream_t stream);
+
+#define PONNI_DIST_UNIFORM 0
+#define PONNI_DIST_NORMAL 1
+
+/* --- .ponni weight files (host only) ------------------------------------- */
+
+/* FNV-1a-64 of a byte string, utils/ponni_safetensors.h:25-32. */
+uint64_t ponni_fnv1a64(const void* data, size_t size);
+
+/* Fingerprint of the template weight schema of a layer chain, formatted
+ * "fnv1a64:%016x"; Inference::weight_schema_fingerprint
+ * (ponni_Inference.h:270-288).  `labels` are get_label() strings and
+ * `trainable` the per-layer parameter counts exposed to training. */
+int ponni_template_fingerprint(int32_t num_layers, const char* const* labels,
+                               const int32_t* num_inputs,
+                               const int32_t* num_outputs,
+                               const int64_t* num_trainable, char* out,
+                               size_t out_len);
+
+/* Write a .ponni file holding one F32 (elem_size 4) or F64 (elem_size 8)
+ * tensor named "parameters" of `count` elements; write_ponni_file
+ * (utils/ponni_safetensors.h:350-407) as used by Inference::save_weights
+ * (ponni_Inference.h:320-333). */
+int ponni_file_write_parameters(const char* path, const char* model_fingerprint,
+                                const void* values, int64_t count,
+                                int32_t elem_size, const char* target);
+
+/* Load and validate a .ponni file that must hold exactly one tensor
+ * "parameters" of `count` elements of elem_size bytes bound to
+ * `model_fingerprint`; PonniFile::load + PonniFile::validate
+ * (utils/ponni_safetensors.h:187-347) as used by Inference::load_weights
+ * (ponni_Inference.h:295-316).  Returns PONNI_ERR_IO with the reference's
+ * rejection message in ponni_last_error() on failure. */
+int ponni_file_read_parameters(const char* path, const char* model_fingerprint,
+                               void* values, int64_t count, int32_t elem_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PONNI_HIP_H */

@@ -1,0 +1,442 @@
+// TEST INFRASTRUCTURE ONLY -- never linked into or called by the product.
+//
+// CPU oracle and CPU baseline: a plain C++ restatement of the reference's
+// batched forward pass, run with OpenMP over samples the way Kokkos'
+// OpenMP RangePolicy runs it.  Only tests/, __graft_entry__.smoke() and
+// bench.py's cpu_baseline leg may load this library, and only as the checker.
+//
+// What it restates (reference paths relative to the reference root):
+//   traversal / buffers   src/ponni_Inference.h:453-555 (per-sample compile-time
+//                         executor: dense blocks with pointwise epilogues,
+//                         barriers materialized in tmp1 / tmp2 / saved slots,
+//                         each a [features, batch] LayoutRight array)
+//   dense                 src/layers/ponni_Matvec.h:70-79 (v = 0; ascending k)
+//   fused epilogue        src/ponni_Inference.h:412-444, src/ponni_LayerTraits.h:51-61
+//   layers                src/layers/*.h compute_all_outputs / apply (cited below)
+//   fp16 chain            template half model: every operation rounds to half
+//                         (ponni_create_model.h:86-92, Kokkos half_t)
+//
+// Modes: 0 fp32, 1 fp64, 2 fp16 operands with fp32 arithmetic (state rounded
+// to fp16 at every materialization), 3 the same for bf16, 4 fp16 chain.
+//
+// Pinning: tests/test_oracle.py checks every function here against the
+// reference's known-answer tests (unit/core/*.cpp, unit/performance_benchmark)
+// and against brute-force float64 numpy evaluations of random chains.
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "../include/ponni_hip.h"
+
+namespace {
+
+// ---- binary16 / bfloat16 rounding (IEEE round-to-nearest-even) -------------
+float round_half(float v) {
+  if (std::isnan(v) || std::isinf(v)) return v;
+  float const a = std::fabs(v);
+  if (a >= 65520.0f) return std::copysign(INFINITY, v);  // rounds past max half (65504)
+  if (a < std::ldexp(1.0f, -14)) {
+    // Subnormal range: quantum 2^-24.
+    float const q = std::ldexp(1.0f, -24);
+    return std::copysign(std::nearbyint(a / q) * q, v);
+  }
+  int e = 0;
+  std::frexp(a, &e);  // a = m * 2^e, m in [0.5, 1)
+  float const q = std::ldexp(1.0f, e - 11);  // 10 explicit mantissa bits
+  return std::copysign(std::nearbyint(a / q) * q, v);
+}
+
+float round_bf16(float v) {
+  if (std::isnan(v) || std::isinf(v)) return v;
+  uint32_t x;
+  std::memcpy(&x, &v, 4);
+  uint32_t const lsb = (x >> 16) & 1u;
+  x += 0x7fffu + lsb;
+  x &= 0xffff0000u;
+  float out;
+  std::memcpy(&out, &x, 4);
+  return out;
+}
+
+// ---- arithmetic types -------------------------------------------------------
+// H16: every operation on it rounds to binary16, as Kokkos half_t on the host.
+struct H16 {
+  float v = 0.0f;
+  H16() = default;
+  H16(double x) : v(round_half(static_cast<float>(x))) {}
+  explicit operator double() const { return v; }
+  explicit operator float() const { return v; }
+};
+inline H16 operator+(H16 a, H16 b) { return H16(a.v + b.v); }
+inline H16 operator-(H16 a, H16 b) { return H16(a.v - b.v); }
+inline H16 operator-(H16 a) { return H16(-a.v); }
+inline H16 operator*(H16 a, H16 b) { return H16(a.v * b.v); }
+inline H16 operator/(H16 a, H16 b) { return H16(a.v / b.v); }
+inline H16& operator+=(H16& a, H16 b) { return a = a + b; }
+inline H16& operator/=(H16& a, H16 b) { return a = a / b; }
+inline bool operator>(H16 a, H16 b) { return a.v > b.v; }
+inline bool operator<(H16 a, H16 b) { return a.v < b.v; }
+inline bool operator>=(H16 a, H16 b) { return a.v >= b.v; }
+inline H16 o_exp(H16 x) { return H16(std::exp(x.v)); }
+inline H16 o_log(H16 x) { return H16(std::log(x.v)); }
+inline H16 o_tanh(H16 x) { return H16(std::tanh(x.v)); }
+inline H16 o_erf(H16 x) { return H16(std::erf(x.v)); }
+inline H16 o_sqrt(H16 x) { return H16(std::sqrt(x.v)); }
+inline float o_exp(float x) { return std::exp(x); }
+inline float o_log(float x) { return std::log(x); }
+inline float o_tanh(float x) { return std::tanh(x); }
+inline float o_erf(float x) { return std::erf(x); }
+inline float o_sqrt(float x) { return std::sqrt(x); }
+inline double o_exp(double x) { return std::exp(x); }
+inline double o_log(double x) { return std::log(x); }
+inline double o_tanh(double x) { return std::tanh(x); }
+inline double o_erf(double x) { return std::erf(x); }
+inline double o_sqrt(double x) { return std::sqrt(x); }
+
+// ---- pointwise layers (apply) ----------------------------------------------
+template <class T>
+T pointwise(ponni_layer_desc const& d, double const* p, T x, int f) {
+  switch (d.kind) {
+    case PONNI_LAYER_BIAS:  // ponni_Bias.h:66-68
+      return x + T(p[f]);
+    case PONNI_LAYER_RELU:  // ponni_Relu.h:49-51
+      return x > T(0) ? x : T(0);
+    case PONNI_LAYER_LEAKY_RELU:  // ponni_LeakyRelu.h:53-55
+      return x > T(0) ? x : T(d.attr[0]) * x;
+    case PONNI_LAYER_ELU:  // ponni_Elu.h:48-50
+      return x > T(0) ? x : T(d.attr[0]) * (o_exp(x) - T(1));
+    case PONNI_LAYER_SELU: {  // ponni_Selu.h:45-49
+      T const alpha = T(1.6732632423543772848);
+      T const scale = T(1.0507009873554804934);
+      return x > T(0) ? scale * x : scale * alpha * (o_exp(x) - T(1));
+    }
+    case PONNI_LAYER_GELU:
+      if (d.flags & PONNI_FLAG_GELU_APPROXIMATE) {  // ponni_Gelu.h:48-53
+        T const x3 = x * x * x;
+        return T(0.5) * x * (T(1) + o_tanh(T(0.79788456080286535588) * (x + T(0.044715) * x3)));
+      }
+      return T(0.5) * x * (T(1) + o_erf(x / T(1.4142135623730950488)));  // ponni_Gelu.h:55-56
+    case PONNI_LAYER_SILU:  // ponni_Silu.h:45-49
+      if (x >= T(0)) return x / (T(1) + o_exp(-x));
+      return x * o_exp(x) / (T(1) + o_exp(x));
+    case PONNI_LAYER_SIGMOID:  // ponni_Sigmoid.h:45-49
+      if (x >= T(0)) return T(1) / (T(1) + o_exp(-x));
+      return o_exp(x) / (T(1) + o_exp(x));
+    case PONNI_LAYER_TANH:  // ponni_Tanh.h:44
+      return o_tanh(x);
+    case PONNI_LAYER_SOFTPLUS: {  // ponni_Softplus.h:44-50
+      T const beta = T(d.attr[0]);
+      T const s = beta * x;
+      if (s > T(0)) return (s + o_log(T(1) + o_exp(-s))) / beta;
+      return o_log(T(1) + o_exp(s)) / beta;
+    }
+    case PONNI_LAYER_HARD_SIGMOID: {  // ponni_HardSigmoid.h:52-56
+      T v = T(d.attr[0]) * x + T(d.attr[1]);
+      v = v < T(0) ? T(0) : v;
+      return v > T(1) ? T(1) : v;
+    }
+    case PONNI_LAYER_HARD_SWISH: {  // ponni_HardSwish.h:42-47
+      T r = x + T(3);
+      r = r < T(0) ? T(0) : r;
+      r = r > T(6) ? T(6) : r;
+      return x * r / T(6);
+    }
+    case PONNI_LAYER_MISH: {  // ponni_Mish.h:44-52
+      T sp = x > T(0) ? x + o_log(T(1) + o_exp(-x)) : o_log(T(1) + o_exp(x));
+      return x * o_tanh(sp);
+    }
+    default:
+      return x;
+  }
+}
+
+bool is_pointwise(int k) { return k == PONNI_LAYER_BIAS || (k >= PONNI_LAYER_RELU && k <= PONNI_LAYER_MISH); }
+
+// ---- buffers ------------------------------------------------------------------
+// A [features, batch] LayoutRight array of T with row stride ld.  `store`
+// applies the storage rounding of the mode (fp16 / bf16 operands).
+template <class T>
+struct Buf {
+  T* p = nullptr;
+  int64_t ld = 0;
+  T& operator()(int f, int64_t b) const { return p[int64_t(f) * ld + b]; }
+};
+
+template <class T>
+struct Ctx {
+  std::vector<ponni_layer_desc> layers;
+  std::vector<double const*> params;
+  int mode = 0;
+  T store(T v) const {
+    if constexpr (std::is_same_v<T, float>) {
+      if (mode == 2) return round_half(v);
+      if (mode == 3) return round_bf16(v);
+    }
+    return v;
+  }
+};
+
+// Barrier layer compute_all_outputs(in[, saved], out) for one sample.
+template <class T>
+void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_t b) {
+  ponni_layer_desc const& d = c.layers[i];
+  double const* p = c.params[i];
+  int const n = d.n_in;
+  switch (d.kind) {
+    case PONNI_LAYER_LAYER_NORM: {  // ponni_LayerNorm.h:76-99
+      T mean = T(0);
+      for (int f = 0; f < n; f++) mean += in(f, b);
+      mean /= T(n);
+      T var = T(0);
+      for (int f = 0; f < n; f++) {
+        T const dlt = in(f, b) - mean;
+        var += dlt * dlt;
+      }
+      var /= T(n);
+      T const inv_std = T(1) / o_sqrt(var + T(d.attr[0]));
+      for (int f = 0; f < n; f++) {
+        T const xhat = (in(f, b) - mean) * inv_std;
+        out(f, b) = c.store(T(p[f]) * xhat + T(p[n + f]));
+      }
+      return;
+    }
+    case PONNI_LAYER_SOFTMAX: {  // ponni_Softmax.h:45-56
+      T mx = in(0, b);
+      for (int f = 1; f < n; f++) mx = in(f, b) > mx ? in(f, b) : mx;
+      T sum = T(0);
+      for (int f = 0; f < n; f++) sum += o_exp(in(f, b) - mx);
+      for (int f = 0; f < n; f++) out(f, b) = c.store(o_exp(in(f, b) - mx) / sum);
+      return;
+    }
+    case PONNI_LAYER_LOG_SOFTMAX: {  // ponni_LogSoftmax.h:45-57
+      T mx = in(0, b);
+      for (int f = 1; f < n; f++) mx = in(f, b) > mx ? in(f, b) : mx;
+      T sum = T(0);
+      for (int f = 0; f < n; f++) sum += o_exp(in(f, b) - mx);
+      T const lse = o_log(sum) + mx;
+      for (int f = 0; f < n; f++) out(f, b) = c.store(in(f, b) - lse);
+      return;
+    }
+    case PONNI_LAYER_MIN_MAX_NORM: {  // ponni_MinMaxNorm.h:67-84
+      T lo = in(0, b), hi = in(0, b);
+      for (int f = 1; f < n; f++) {
+        if (in(f, b) < lo) lo = in(f, b);
+        if (in(f, b) > hi) hi = in(f, b);
+      }
+      T const scale = (T(d.attr[1]) - T(d.attr[0])) / ((hi - lo) + T(d.attr[2]));
+      for (int f = 0; f < n; f++) out(f, b) = c.store(T(d.attr[0]) + (in(f, b) - lo) * scale);
+      return;
+    }
+    case PONNI_LAYER_SAVE_STATE:  // ponni_Save_State.h:57-67
+      for (int f = 0; f < d.n_out; f++) out(f, b) = in(f, b);
+      return;
+    case PONNI_LAYER_BINOP_ADD:  // ponni_Binop_Add.h:57-68
+      for (int f = 0; f < d.n_out; f++) out(f, b) = c.store(in(f, b) + saved(f, b));
+      return;
+    case PONNI_LAYER_BINOP_CONCATENATE: {  // ponni_Binop_Concatenate.h:63-86
+      // Read the current rows before writing: the reference writes in place
+      // and, for after == false, would overwrite rows it still has to read.
+      std::vector<T> cur(n);
+      for (int f = 0; f < n; f++) cur[f] = in(f, b);
+      int const n_out = d.n_out;
+      if (d.flags & PONNI_FLAG_CONCAT_AFTER) {
+        for (int f = 0; f < n_out; f++) out(f, b) = f < n ? cur[f] : saved(f - n, b);
+      } else {
+        int const n2 = n_out - n;
+        for (int f = 0; f < n_out; f++) out(f, b) = f < n2 ? saved(f, b) : cur[f - n2];
+      }
+      return;
+    }
+    case PONNI_LAYER_BINOP_PROJECTION_ADD: {  // ponni_Binop_Projection_Add.h:81-95
+      int const nsave = d.n_aux;
+      for (int i2 = 0; i2 < n; i2++) {
+        T proj = T(p[int64_t(nsave) * n + i2]);
+        for (int k = 0; k < nsave; k++) proj += T(p[int64_t(k) * n + i2]) * saved(k, b);
+        out(i2, b) = c.store(in(i2, b) + proj);
+      }
+      return;
+    }
+    default:  // a lone pointwise layer
+      for (int f = 0; f < n; f++) out(f, b) = c.store(pointwise<T>(d, p, in(f, b), f));
+      return;
+  }
+}
+
+// traverse_mixed_batch_parallel (ponni_Inference.h:453-555) for one sample.
+template <class T>
+void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, Buf<T> const* saved, int64_t b) {
+  int const L = static_cast<int>(c.layers.size());
+  bool in_tmp1 = false;
+  int i = 0;
+  while (i < L) {
+    ponni_layer_desc const& d = c.layers[i];
+    if (d.kind == PONNI_LAYER_MATVEC) {
+      int end = i + 1;
+      while (end < L && is_pointwise(c.layers[end].kind)) end++;
+      Buf<T> in = i == 0 ? x : (in_tmp1 ? tmp1 : tmp2);
+      Buf<T> out;
+      if (end == L) {
+        out = y;
+      } else {
+        bool const out_tmp1 = i == 0 ? true : !in_tmp1;
+        out = out_tmp1 ? tmp1 : tmp2;
+        in_tmp1 = out_tmp1;
+      }
+      double const* w = c.params[i];
+      for (int f = 0; f < d.n_out; f++) {  // compute_fused_dense_block, ponni_Inference.h:431-444
+        T v = T(0);
+        for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(k) * d.n_out + f]) * in(k, b);
+        for (int e = i + 1; e < end; e++) v = pointwise<T>(c.layers[e], c.params[e], v, f);
+        out(f, b) = c.store(v);
+      }
+      i = end;
+      continue;
+    }
+    Buf<T> const sv = (d.kind >= PONNI_LAYER_SAVE_STATE) ? saved[d.slot] : Buf<T>{};
+    if (i == 0 && L == 1) {
+      barrier(c, i, x, sv, y, b);
+    } else if (i == 0) {
+      if (d.kind == PONNI_LAYER_SAVE_STATE) barrier(c, i, x, sv, saved[d.slot], b);
+      barrier(c, i, x, sv, tmp1, b);
+      in_tmp1 = true;
+    } else if (i < L - 1) {
+      Buf<T> const in = in_tmp1 ? tmp1 : tmp2;
+      Buf<T> const out = d.kind == PONNI_LAYER_SAVE_STATE ? saved[d.slot] : in;
+      barrier(c, i, in, sv, out, b);
+    } else {
+      barrier(c, i, in_tmp1 ? tmp1 : tmp2, sv, y, b);
+    }
+    i++;
+  }
+}
+
+// Scratch widths, get_planned_temporary_size<0/1>() and get_saved_state_size<s>().
+void plan_widths(std::vector<ponni_layer_desc> const& layers, int* tmp, int* saved) {
+  int const L = static_cast<int>(layers.size());
+  tmp[0] = tmp[1] = 0;
+  for (int s = 0; s < 8; s++) saved[s] = 0;
+  bool in_tmp1 = false;
+  int i = 0;
+  while (i < L) {
+    ponni_layer_desc const& d = layers[i];
+    if (d.kind == PONNI_LAYER_SAVE_STATE && d.slot >= 0 && d.slot < 8) saved[d.slot] = std::max(saved[d.slot], d.n_out);
+    if (d.kind == PONNI_LAYER_MATVEC) {
+      int end = i + 1;
+      while (end < L && is_pointwise(layers[end].kind)) end++;
+      if (end != L) {
+        bool const out_tmp1 = i == 0 ? true : !in_tmp1;
+        tmp[out_tmp1 ? 0 : 1] = std::max(tmp[out_tmp1 ? 0 : 1], d.n_out);
+        in_tmp1 = out_tmp1;
+      }
+      i = end;
+      continue;
+    }
+    if (i != L - 1) {
+      bool const out_tmp1 = i == 0 ? true : in_tmp1;
+      tmp[out_tmp1 ? 0 : 1] = std::max(tmp[out_tmp1 ? 0 : 1], d.n_out);
+      in_tmp1 = out_tmp1;
+    }
+    i++;
+  }
+}
+
+template <class T, class IO>
+int forward(std::vector<ponni_layer_desc> const& layers, std::vector<double const*> const& params, int mode,
+            IO const* x_io, int64_t ld_x, IO* y_io, int64_t ld_y, int64_t batch, int threads) {
+  Ctx<T> c;
+  c.layers = layers;
+  c.params = params;
+  c.mode = mode;
+  int tmpw[2], savedw[8];
+  plan_widths(layers, tmpw, savedw);
+  int const n_in = layers.front().n_in;
+  int const n_out = layers.back().n_out;
+  // Inputs and outputs are converted to T at the boundary; scratch is T.
+  std::vector<T> xs(size_t(n_in) * size_t(batch)), ys(size_t(n_out) * size_t(batch));
+  std::vector<T> t1(size_t(tmpw[0]) * size_t(batch)), t2(size_t(tmpw[1]) * size_t(batch));
+  std::vector<std::vector<T>> sv(8);
+  Buf<T> saved[8];
+  for (int s = 0; s < 8; s++) {
+    sv[s].resize(size_t(savedw[s]) * size_t(batch));
+    saved[s] = Buf<T>{sv[s].data(), batch};
+  }
+  Buf<T> const x{xs.data(), batch}, y{ys.data(), batch}, tmp1{t1.data(), batch}, tmp2{t2.data(), batch};
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < batch; b++)
+    for (int f = 0; f < n_in; f++) x(f, b) = c.store(T(x_io[int64_t(f) * ld_x + b]));
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < batch; b++) run_sample<T>(c, x, y, tmp1, tmp2, saved, b);
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < batch; b++)
+    for (int f = 0; f < n_out; f++) y_io[int64_t(f) * ld_y + b] = static_cast<IO>(static_cast<double>(y(f, b)));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Per-layer parameters are concatenated in layer order, each in the layer's
+// own layout (Matvec W [n_in, n_out]; LayerNorm gamma, beta; Projection_Add
+// W [NSAVE, n_in], bias).  x / y are float for modes 0, 2, 3, 4 and double for
+// mode 1.  Returns 0 on success.
+int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double const* params, int32_t mode,
+                   void const* x, int64_t ld_x, void* y, int64_t ld_y, int64_t batch, int32_t threads) {
+  if (!layers || num_layers <= 0 || batch <= 0) return 1;
+  std::vector<ponni_layer_desc> ls(layers, layers + num_layers);
+  std::vector<double const*> ps(num_layers);
+  int64_t off = 0;
+  for (int i = 0; i < num_layers; i++) {
+    ps[i] = params + off;
+    auto const& d = ls[i];
+    switch (d.kind) {
+      case PONNI_LAYER_MATVEC: off += int64_t(d.n_in) * d.n_out; break;
+      case PONNI_LAYER_BIAS: off += d.n_in; break;
+      case PONNI_LAYER_LAYER_NORM: off += 2 * int64_t(d.n_in); break;
+      case PONNI_LAYER_BINOP_PROJECTION_ADD: off += int64_t(d.n_aux) * d.n_in + d.n_in; break;
+      default: break;
+    }
+  }
+  // fp16 / bf16 operand modes see every parameter at the operand precision.
+  std::vector<double> rounded;
+  if (mode == 2 || mode == 3) {
+    rounded.assign(params, params + off);
+    for (double& v : rounded) v = mode == 2 ? round_half(float(v)) : round_bf16(float(v));
+    for (int i = 0; i < num_layers; i++) ps[i] = rounded.data() + (ps[i] - params);
+  }
+  switch (mode) {
+    case 0:
+    case 2:
+    case 3:
+      return forward<float, float>(ls, ps, mode, static_cast<float const*>(x), ld_x, static_cast<float*>(y), ld_y,
+                                   batch, threads);
+    case 1:
+      return forward<double, double>(ls, ps, mode, static_cast<double const*>(x), ld_x, static_cast<double*>(y),
+                                     ld_y, batch, threads);
+    case 4:
+      return forward<H16, float>(ls, ps, mode, static_cast<float const*>(x), ld_x, static_cast<float*>(y), ld_y,
+                                 batch, threads);
+    default:
+      return 2;
+  }
+}
+
+// Scratch planning of the reference: tmp1, tmp2, saved slot widths.
+void oracle_plan_widths(ponni_layer_desc const* layers, int32_t num_layers, int32_t* tmp, int32_t* saved) {
+  std::vector<ponni_layer_desc> ls(layers, layers + num_layers);
+  int t[2], s[8];
+  plan_widths(ls, t, s);
+  tmp[0] = t[0];
+  tmp[1] = t[1];
+  for (int i = 0; i < 8; i++) saved[i] = s[i];
+}
+
+float oracle_round_half(float v) { return round_half(v); }
+float oracle_round_bf16(float v) { return round_bf16(v); }
+
+}  // extern "C"

@@ -1,0 +1,707 @@
+// Host side of libponni_hip: layer-chain validation, lowering to the lane
+// program, scratch planning, parameter packing and the C ABI entry points.
+//
+// Reference behaviour restated here:
+//   - validation         src/ponni_Inference.h:719-737 plus each layer's validate()
+//   - block planning     src/ponni_Inference.h:56-85 (dense + following pointwise)
+//   - buffer selection   src/ponni_Inference.h:453-555 (tmp1/tmp2/saved ping-pong)
+//   - scratch sizing     src/ponni_Inference.h:92-122, :204-223
+//   - forward contract   src/ponni_Inference.h:352-389
+#include "plan.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "host_half.h"
+
+using namespace ponni_hip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, std::string const& message) {
+  g_last_error = message;
+  return status;
+}
+
+bool is_pointwise(int kind) {
+  return kind == PONNI_LAYER_BIAS || (kind >= PONNI_LAYER_RELU && kind <= PONNI_LAYER_MISH);
+}
+
+bool is_save(int kind) { return kind == PONNI_LAYER_SAVE_STATE; }
+
+bool is_binop(int kind) {
+  return kind == PONNI_LAYER_BINOP_ADD || kind == PONNI_LAYER_BINOP_CONCATENATE ||
+         kind == PONNI_LAYER_BINOP_PROJECTION_ADD;
+}
+
+bool known_kind(int kind) {
+  return kind == PONNI_LAYER_MATVEC || is_pointwise(kind) ||
+         (kind >= PONNI_LAYER_SOFTMAX && kind <= PONNI_LAYER_MIN_MAX_NORM) || is_save(kind) ||
+         is_binop(kind);
+}
+
+char const* label_of(int kind) {
+  switch (kind) {
+    case PONNI_LAYER_MATVEC: return "Matvec";
+    case PONNI_LAYER_BIAS: return "Bias";
+    case PONNI_LAYER_RELU: return "ReLU";
+    case PONNI_LAYER_LEAKY_RELU: return "LeakyReLU";
+    case PONNI_LAYER_ELU: return "ELU";
+    case PONNI_LAYER_SELU: return "SELU";
+    case PONNI_LAYER_GELU: return "GELU";
+    case PONNI_LAYER_SILU: return "SiLU";
+    case PONNI_LAYER_SIGMOID: return "Sigmoid";
+    case PONNI_LAYER_TANH: return "Tanh";
+    case PONNI_LAYER_SOFTPLUS: return "Softplus";
+    case PONNI_LAYER_HARD_SIGMOID: return "HardSigmoid";
+    case PONNI_LAYER_HARD_SWISH: return "HardSwish";
+    case PONNI_LAYER_MISH: return "Mish";
+    case PONNI_LAYER_SOFTMAX: return "Softmax";
+    case PONNI_LAYER_LOG_SOFTMAX: return "LogSoftmax";
+    case PONNI_LAYER_LAYER_NORM: return "LayerNorm";
+    case PONNI_LAYER_MIN_MAX_NORM: return "MinMaxNorm";
+    case PONNI_LAYER_SAVE_STATE: return "Save_State";
+    case PONNI_LAYER_BINOP_ADD: return "Binop_Add";
+    case PONNI_LAYER_BINOP_CONCATENATE: return "Binop_Concatenate";
+    case PONNI_LAYER_BINOP_PROJECTION_ADD: return "Binop_Projection_Add";
+    default: return "?";
+  }
+}
+
+int64_t param_count(ponni_layer_desc const& d) {
+  switch (d.kind) {
+    case PONNI_LAYER_MATVEC: return int64_t(d.n_in) * d.n_out;
+    case PONNI_LAYER_BIAS: return d.n_in;
+    case PONNI_LAYER_LAYER_NORM: return 2 * int64_t(d.n_in);
+    case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(d.n_aux) * d.n_in + d.n_in;
+    default: return 0;
+  }
+}
+
+// Each layer's own validate() plus the chain check of Inference::validate.
+int validate_chain(ponni_layer_desc const* layers, int n) {
+  std::string where;
+  int saved_size[kMaxSlots];
+  bool saved_seen[kMaxSlots] = {};
+  for (int i = 0; i < n; i++) {
+    ponni_layer_desc const& d = layers[i];
+    where = "layer " + std::to_string(i) + " (" + label_of(d.kind) + "): ";
+    if (!known_kind(d.kind)) return fail(PONNI_ERR_INVALID_ARGUMENT, where + "unknown layer kind " + std::to_string(d.kind));
+    if (d.n_in <= 0 || d.n_out <= 0) return fail(PONNI_ERR_INVALID_MODEL, where + "num_inputs and num_outputs must be > 0");
+    bool const same_width = d.kind != PONNI_LAYER_MATVEC && d.kind != PONNI_LAYER_BINOP_CONCATENATE;
+    if (same_width && d.n_in != d.n_out) return fail(PONNI_ERR_INVALID_MODEL, where + "input/output size mismatch");
+    if (is_save(d.kind) || is_binop(d.kind)) {
+      if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
+    }
+    switch (d.kind) {
+      case PONNI_LAYER_ELU:
+        if (!(d.attr[0] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "ELU alpha must be > 0");
+        break;
+      case PONNI_LAYER_SOFTPLUS:
+        if (!(d.attr[0] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "Softplus beta must be > 0");
+        break;
+      case PONNI_LAYER_HARD_SIGMOID:
+        if (!(d.attr[0] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "HardSigmoid alpha must be > 0");
+        break;
+      case PONNI_LAYER_LAYER_NORM:
+        if (!(d.attr[0] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "LayerNorm epsilon must be > 0");
+        break;
+      case PONNI_LAYER_MIN_MAX_NORM:
+        if (!(d.attr[1] > d.attr[0])) return fail(PONNI_ERR_INVALID_MODEL, where + "MinMaxNorm requires out_max > out_min");
+        if (!(d.attr[2] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "MinMaxNorm epsilon must be > 0");
+        break;
+      case PONNI_LAYER_SAVE_STATE:
+        saved_size[d.slot] = d.n_in;
+        saved_seen[d.slot] = true;
+        break;
+      case PONNI_LAYER_BINOP_ADD:
+      case PONNI_LAYER_BINOP_CONCATENATE:
+      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
+        if (i == 0) return fail(PONNI_ERR_INVALID_MODEL, where + "a binary layer cannot be first: no state has been saved");
+        if (!saved_seen[d.slot]) return fail(PONNI_ERR_INVALID_MODEL, where + "reads saved state " + std::to_string(d.slot) + " before any Save_State wrote it");
+        int const saved = saved_size[d.slot];
+        if (d.kind == PONNI_LAYER_BINOP_ADD && saved != d.n_in)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "Saved layer num inputs != this layer's num inputs");
+        if (d.kind == PONNI_LAYER_BINOP_CONCATENATE && d.n_out != saved + d.n_in)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "this layer's num outputs != this layer's num inputs + saved layer's num inputs");
+        if (d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD && (d.n_aux <= 0 || d.n_aux != saved))
+          return fail(PONNI_ERR_INVALID_MODEL, where + "saved layer size incompatible with projection weights");
+        break;
+      }
+      default:
+        break;
+    }
+    if (i + 1 < n && d.n_out != layers[i + 1].n_in)
+      return fail(PONNI_ERR_INVALID_MODEL, where + "This layer's num outputs != next layer's num inputs");
+  }
+  return PONNI_OK;
+}
+
+Step make_step(ponni_layer_desc const& d) {
+  Step s{};
+  switch (d.kind) {
+    case PONNI_LAYER_BIAS: s.act = ACT_BIAS; break;
+    case PONNI_LAYER_RELU: s.act = ACT_RELU; break;
+    case PONNI_LAYER_LEAKY_RELU: s.act = ACT_LEAKY_RELU; s.a = float(d.attr[0]); break;
+    case PONNI_LAYER_ELU: s.act = ACT_ELU; s.a = float(d.attr[0]); break;
+    case PONNI_LAYER_SELU: s.act = ACT_SELU; break;
+    case PONNI_LAYER_GELU: s.act = (d.flags & PONNI_FLAG_GELU_APPROXIMATE) ? ACT_GELU_TANH : ACT_GELU_ERF; break;
+    case PONNI_LAYER_SILU: s.act = ACT_SILU; break;
+    case PONNI_LAYER_SIGMOID: s.act = ACT_SIGMOID; break;
+    case PONNI_LAYER_TANH: s.act = ACT_TANH; break;
+    case PONNI_LAYER_SOFTPLUS: s.act = ACT_SOFTPLUS; s.a = float(d.attr[0]); break;
+    case PONNI_LAYER_HARD_SIGMOID: s.act = ACT_HARD_SIGMOID; s.a = float(d.attr[0]); s.b = float(d.attr[1]); break;
+    case PONNI_LAYER_HARD_SWISH: s.act = ACT_HARD_SWISH; break;
+    case PONNI_LAYER_MISH: s.act = ACT_MISH; break;
+    default: break;
+  }
+  return s;
+}
+
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// Per-path packed size and layout of one layer's parameters.
+// GENERIC: reference layout.  NARROW: padded to the width class W.
+// MFMA: dense weights in A-fragment order, vectors padded to 16.
+int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
+  int const W = p.width_class;
+  switch (p.path) {
+    case PONNI_PATH_NARROW:
+      switch (d.kind) {
+        case PONNI_LAYER_MATVEC: return int64_t(W) * W;
+        case PONNI_LAYER_BIAS: return W;
+        case PONNI_LAYER_LAYER_NORM: return 2 * W;
+        case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(W) * W + W;
+        default: return 0;
+      }
+    case PONNI_PATH_MFMA: {
+      auto tiles = [](int n) { return (n + 15) / 16; };
+      switch (d.kind) {
+        case PONNI_LAYER_MATVEC: return int64_t(tiles(d.n_in)) * tiles(d.n_out) * 256;
+        case PONNI_LAYER_BIAS: return round_up(d.n_in, 16);
+        case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
+        case PONNI_LAYER_BINOP_PROJECTION_ADD:
+          return int64_t(tiles(d.n_aux)) * tiles(d.n_in) * 256 + round_up(d.n_in, 16);
+        default: return 0;
+      }
+    }
+    default:
+      return param_count(d);
+  }
+}
+
+// Lower the chain into ops; mirrors the traversal of ponni_Inference.h:453-555.
+void lower(ponni_plan_s& p) {
+  int const L = static_cast<int>(p.layers.size());
+  p.ops.clear();
+  p.steps.clear();
+  p.layer_param_offset.assign(L, 0);
+  int64_t off = 0;
+  for (int i = 0; i < L; i++) {
+    p.layer_param_offset[i] = off;
+    off += packed_size(p, p.layers[i]);
+  }
+  p.packed_elements = off;
+
+  int vec_stride_ln = 0;  // offset of beta after gamma
+  bool in_tmp1 = false;
+  int tmp_max[2] = {0, 0};
+  p.num_fused_blocks = 0;
+  for (int i = 0; i < L;) {
+    ponni_layer_desc const& d = p.layers[i];
+    Op op{};
+    op.n_in = d.n_in;
+    op.n_out = d.n_out;
+    op.slot = d.slot;
+    op.woff = static_cast<int32_t>(p.layer_param_offset[i]);
+    if (d.kind == PONNI_LAYER_MATVEC) {
+      int end = i + 1;
+      while (end < L && is_pointwise(p.layers[end].kind)) end++;
+      op.code = OP_DENSE;
+      op.epi_begin = static_cast<int32_t>(p.steps.size());
+      for (int j = i + 1; j < end; j++) {
+        Step s = make_step(p.layers[j]);
+        s.off = static_cast<int32_t>(p.layer_param_offset[j]);
+        p.steps.push_back(s);
+      }
+      op.epi_count = end - (i + 1);
+      op.n_out = p.layers[end - 1].n_out;
+      p.num_fused_blocks++;
+      if (i == 0) {
+        op.src = BUF_INPUT;
+        if (end == L) {
+          op.dst = BUF_OUTPUT;
+        } else {
+          op.dst = BUF_TMP1;
+          tmp_max[0] = std::max(tmp_max[0], d.n_out);
+          in_tmp1 = true;
+        }
+      } else {
+        op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
+        if (end == L) {
+          op.dst = BUF_OUTPUT;
+        } else {
+          bool const out_tmp1 = !in_tmp1;
+          op.dst = out_tmp1 ? BUF_TMP1 : BUF_TMP2;
+          tmp_max[out_tmp1 ? 0 : 1] = std::max(tmp_max[out_tmp1 ? 0 : 1], d.n_out);
+          in_tmp1 = out_tmp1;
+        }
+      }
+      p.ops.push_back(op);
+      i = end;
+      continue;
+    }
+    // Barrier (or lone pointwise) layer.
+    switch (d.kind) {
+      case PONNI_LAYER_LAYER_NORM:
+        op.code = OP_LAYER_NORM;
+        vec_stride_ln = static_cast<int>(packed_size(p, d) / 2);
+        op.boff = op.woff + vec_stride_ln;
+        op.f0 = static_cast<float>(d.attr[0]);
+        break;
+      case PONNI_LAYER_SOFTMAX: op.code = OP_SOFTMAX; break;
+      case PONNI_LAYER_LOG_SOFTMAX: op.code = OP_LOG_SOFTMAX; break;
+      case PONNI_LAYER_MIN_MAX_NORM:
+        op.code = OP_MIN_MAX;
+        op.f0 = static_cast<float>(d.attr[0]);
+        op.f1 = static_cast<float>(d.attr[1]);
+        op.f2 = static_cast<float>(d.attr[2]);
+        break;
+      case PONNI_LAYER_SAVE_STATE: op.code = OP_SAVE; break;
+      case PONNI_LAYER_BINOP_ADD: op.code = OP_ADD; break;
+      case PONNI_LAYER_BINOP_CONCATENATE:
+        op.code = OP_CONCAT;
+        op.aux = (d.flags & PONNI_FLAG_CONCAT_AFTER) ? 1 : 0;
+        break;
+      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
+        op.code = OP_PROJ_ADD;
+        op.aux = d.n_aux;
+        int64_t const wsize = packed_size(p, d) - (p.path == PONNI_PATH_GENERIC ? d.n_in
+                                                   : p.path == PONNI_PATH_NARROW ? p.width_class
+                                                                                 : round_up(d.n_in, 16));
+        op.boff = static_cast<int32_t>(op.woff + wsize);
+        break;
+      }
+      default: {  // lone pointwise layer
+        op.code = OP_POINTWISE;
+        op.epi_begin = static_cast<int32_t>(p.steps.size());
+        Step s = make_step(d);
+        s.off = op.woff;
+        p.steps.push_back(s);
+        op.epi_count = 1;
+        break;
+      }
+    }
+    if (i == 0 && L == 1) {
+      op.src = BUF_INPUT;
+      op.dst = BUF_OUTPUT;
+    } else if (i == 0) {
+      // A leading barrier materializes into tmp1; a leading save also fills
+      // its slot (ponni_Inference.h:499-514).
+      op.src = BUF_INPUT;
+      if (is_save(d.kind)) {
+        op.dst = BUF_SAVED + d.slot;
+        op.aux = 1;  // also copy to tmp1
+      } else {
+        op.dst = BUF_TMP1;
+      }
+      tmp_max[0] = std::max(tmp_max[0], d.n_out);
+      in_tmp1 = true;
+    } else if (i < L - 1) {
+      // Every built-in barrier declares overwrite_input = true, so the main
+      // state keeps its buffer; a save writes its slot instead.
+      op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
+      op.dst = is_save(d.kind) ? BUF_SAVED + d.slot : op.src;
+      tmp_max[in_tmp1 ? 0 : 1] = std::max(tmp_max[in_tmp1 ? 0 : 1], d.n_out);
+    } else {
+      op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
+      op.dst = BUF_OUTPUT;
+    }
+    p.ops.push_back(op);
+    i++;
+  }
+  p.tmp_features[0] = tmp_max[0];
+  p.tmp_features[1] = tmp_max[1];
+}
+
+bool mfma_supports(ponni_plan_s const& p) {
+  for (auto const& d : p.layers) {
+    if (d.kind == PONNI_LAYER_BINOP_CONCATENATE) {
+      int const first = (d.flags & PONNI_FLAG_CONCAT_AFTER) ? d.n_in : d.n_out - d.n_in;
+      if (first % 16 != 0) return false;  // tile-granular moves only
+    }
+  }
+  return true;
+}
+
+void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
+  out.assign(static_cast<size_t>(p.packed_elements), 0.0);
+  int const L = static_cast<int>(p.layers.size());
+  int const W = p.width_class;
+  for (int i = 0; i < L; i++) {
+    ponni_layer_desc const& d = p.layers[i];
+    std::vector<double> const& src = p.params[i];
+    double* dst = out.data() + p.layer_param_offset[i];
+    auto rnd = [&](double v) { return round_to_dtype(v, p.dtype); };
+    // Dense weights W [K, N] (row k, column o) in the path's layout.
+    auto pack_dense = [&](double const* w, int K, int N, double* o) {
+      if (p.path == PONNI_PATH_GENERIC) {
+        for (int64_t e = 0; e < int64_t(K) * N; e++) o[e] = rnd(w[e]);
+      } else if (p.path == PONNI_PATH_NARROW) {
+        for (int k = 0; k < K; k++)
+          for (int n = 0; n < N; n++) o[k * W + n] = rnd(w[int64_t(k) * N + n]);
+      } else {
+        // A fragment of v_mfma_f32_16x16x4f32 for output tile mo and input
+        // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16].
+        int const TK = (K + 15) / 16, TN = (N + 15) / 16;
+        for (int mo = 0; mo < TN; mo++)
+          for (int m = 0; m < TK; m++)
+            for (int l = 0; l < 64; l++)
+              for (int v = 0; v < 4; v++) {
+                int const k = 16 * m + 4 * (l >> 4) + v;
+                int const n = 16 * mo + (l & 15);
+                double val = (k < K && n < N) ? rnd(w[int64_t(k) * N + n]) : 0.0;
+                o[((int64_t(mo) * TK + m) * 64 + l) * 4 + v] = val;
+              }
+      }
+    };
+    switch (d.kind) {
+      case PONNI_LAYER_MATVEC:
+        pack_dense(src.data(), d.n_in, d.n_out, dst);
+        break;
+      case PONNI_LAYER_BIAS:
+        for (int f = 0; f < d.n_in; f++) dst[f] = rnd(src[f]);
+        break;
+      case PONNI_LAYER_LAYER_NORM: {
+        int64_t const stride = packed_size(p, d) / 2;
+        for (int f = 0; f < d.n_in; f++) {
+          dst[f] = rnd(src[f]);
+          dst[stride + f] = rnd(src[d.n_in + f]);
+        }
+        break;
+      }
+      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
+        int64_t const bsize = p.path == PONNI_PATH_GENERIC ? d.n_in
+                              : p.path == PONNI_PATH_NARROW ? W
+                                                            : round_up(d.n_in, 16);
+        int64_t const wsize = packed_size(p, d) - bsize;
+        pack_dense(src.data(), d.n_aux, d.n_in, dst);
+        for (int f = 0; f < d.n_in; f++) dst[wsize + f] = rnd(src[int64_t(d.n_aux) * d.n_in + f]);
+        break;
+      }
+      default:
+        break;
+    }
+  }
+}
+
+int element_size(int dtype) {
+  switch (dtype) {
+    case PONNI_F64: return 8;
+    case PONNI_F16:
+    case PONNI_BF16: return 2;
+    default: return 4;
+  }
+}
+
+// Parameters live in the compute type: double for F64, float otherwise.
+int param_element_size(ponni_plan_s const& p) { return p.dtype == PONNI_F64 ? 8 : 4; }
+
+#define HIP_TRY(expr)                                                                         \
+  do {                                                                                        \
+    hipError_t const e_ = (expr);                                                             \
+    if (e_ != hipSuccess)                                                                     \
+      return fail(PONNI_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));       \
+  } while (0)
+
+int upload(ponni_plan_s& p) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (p.device >= 0 && p.device != dev)
+    return fail(PONNI_ERR_DEVICE, "plan was first used on another device");
+  p.device = dev;
+  // Parameters may be read by a launch still in flight; the reference's
+  // deep_copy fences as well.
+  HIP_TRY(hipDeviceSynchronize());
+  if (p.d_ops == nullptr) {
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_ops), sizeof(Op) * kMaxOps));
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_steps), sizeof(Step) * kMaxSteps));
+  }
+  HIP_TRY(hipMemcpy(p.d_ops, p.ops.data(), sizeof(Op) * p.ops.size(), hipMemcpyHostToDevice));
+  if (!p.steps.empty())
+    HIP_TRY(hipMemcpy(p.d_steps, p.steps.data(), sizeof(Step) * p.steps.size(), hipMemcpyHostToDevice));
+  std::vector<double> packed;
+  pack_params(p, packed);
+  size_t const bytes = std::max<size_t>(packed.size() * param_element_size(p), 16);
+  if (bytes > p.d_params_bytes) {
+    if (p.d_params) HIP_TRY(hipFree(p.d_params));
+    p.d_params = nullptr;
+    HIP_TRY(hipMalloc(&p.d_params, bytes));
+    p.d_params_bytes = bytes;
+  }
+  if (!packed.empty()) {
+    if (p.dtype == PONNI_F64) {
+      HIP_TRY(hipMemcpy(p.d_params, packed.data(), packed.size() * 8, hipMemcpyHostToDevice));
+    } else {
+      std::vector<float> f(packed.begin(), packed.end());
+      HIP_TRY(hipMemcpy(p.d_params, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+    }
+  }
+  p.device_dirty = false;
+  return PONNI_OK;
+}
+
+void release_scratch(ponni_plan_s& p) {
+  for (auto& s : p.d_scratch) {
+    if (s) (void)hipFree(s);
+    s = nullptr;
+  }
+}
+
+int reallocate_scratch(ponni_plan_s& p, int64_t batch) {
+  HIP_TRY(hipDeviceSynchronize());
+  release_scratch(p);
+  p.capacity = batch;
+  if (p.path != PONNI_PATH_GENERIC || batch == 0) return PONNI_OK;
+  size_t const es = element_size(p.dtype);
+  for (int b = 0; b < 2; b++) {
+    if (p.tmp_features[b] > 0)
+      HIP_TRY(hipMalloc(&p.d_scratch[b], es * size_t(p.tmp_features[b]) * size_t(batch)));
+  }
+  for (int s = 0; s < p.num_slots; s++) {
+    if (p.saved_features[s] > 0)
+      HIP_TRY(hipMalloc(&p.d_scratch[2 + s], es * size_t(p.saved_features[s]) * size_t(batch)));
+  }
+  return PONNI_OK;
+}
+
+}  // namespace
+
+namespace ponni_hip {
+int set_error(int status, std::string const& message) { return fail(status, message); }
+}  // namespace ponni_hip
+
+extern "C" {
+
+const char* ponni_last_error(void) { return g_last_error.c_str(); }
+
+int ponni_abi_version(void) { return PONNI_ABI_VERSION; }
+
+int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_t dtype,
+                      int32_t path, ponni_plan* out_plan) {
+  g_last_error.clear();
+  if (out_plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out_plan is null");
+  *out_plan = nullptr;
+  if (layers == nullptr || num_layers <= 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "a model needs at least one layer");
+  if (num_layers > kMaxOps) return fail(PONNI_ERR_INVALID_ARGUMENT, "too many layers (limit 256)");
+  if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (path < PONNI_PATH_AUTO || path > PONNI_PATH_MFMA) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
+  int const st = validate_chain(layers, num_layers);
+  if (st != PONNI_OK) return st;
+
+  auto* p = new (std::nothrow) ponni_plan_s();
+  if (p == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+  p->layers.assign(layers, layers + num_layers);
+  p->dtype = dtype;
+  p->params.resize(num_layers);
+  int max_width = 0;
+  for (int i = 0; i < num_layers; i++) {
+    auto const& d = layers[i];
+    p->params[i].assign(static_cast<size_t>(param_count(d)), 0.0);
+    max_width = std::max({max_width, d.n_in, d.n_out, d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD ? d.n_aux : 0});
+    if (is_save(d.kind)) {
+      p->num_slots = std::max(p->num_slots, d.slot + 1);
+      p->saved_features[d.slot] = std::max(p->saved_features[d.slot], d.n_out);
+    }
+  }
+  p->max_width = max_width;
+  // LayerNorm defaults are gamma = 1, beta = 0 (ponni_LayerNorm.h:39-45).
+  for (int i = 0; i < num_layers; i++)
+    if (layers[i].kind == PONNI_LAYER_LAYER_NORM)
+      for (int f = 0; f < layers[i].n_in; f++) p->params[i][f] = 1.0;
+
+  int const narrow = narrow_width_class(max_width);
+  int const mfma = mfma_width_class(dtype, max_width);
+  int chosen = path;
+  if (chosen == PONNI_PATH_AUTO) {
+    if (dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
+    else chosen = PONNI_PATH_GENERIC;
+  } else if (chosen == PONNI_PATH_NARROW) {
+    if (dtype == PONNI_F64 || narrow == 0 || p->num_slots > kNarrowMaxSlots) {
+      delete p;
+      return fail(PONNI_ERR_UNSUPPORTED, "NARROW path needs F32/F16/BF16, width <= 16 and at most 2 saved states");
+    }
+  } else if (chosen == PONNI_PATH_MFMA) {
+    if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {
+      delete p;
+      return fail(PONNI_ERR_UNSUPPORTED,
+                  "MFMA path needs F32/F16/BF16, width <= 256, at most 2 saved states and 16-aligned concatenation");
+    }
+  }
+  p->path = chosen;
+  p->width_class = chosen == PONNI_PATH_NARROW ? narrow : chosen == PONNI_PATH_MFMA ? mfma : 0;
+  lower(*p);
+  *out_plan = p;
+  return PONNI_OK;
+}
+
+void ponni_plan_destroy(ponni_plan plan) {
+  if (plan == nullptr) return;
+  if (plan->device >= 0) {
+    int cur = 0;
+    if (hipGetDevice(&cur) == hipSuccess && cur != plan->device) (void)hipSetDevice(plan->device);
+    (void)hipDeviceSynchronize();
+    release_scratch(*plan);
+    if (plan->d_ops) (void)hipFree(plan->d_ops);
+    if (plan->d_steps) (void)hipFree(plan->d_steps);
+    if (plan->d_params) (void)hipFree(plan->d_params);
+    if (cur != plan->device) (void)hipSetDevice(cur);
+  }
+  delete plan;
+}
+
+int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info) {
+  if (plan == nullptr || info == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or info");
+  std::memset(info, 0, sizeof(*info));
+  info->path = plan->path;
+  info->dtype = plan->dtype;
+  info->num_layers = static_cast<int32_t>(plan->layers.size());
+  info->num_inputs = plan->layers.front().n_in;
+  info->num_outputs = plan->layers.back().n_out;
+  info->num_fused_dense_blocks = plan->num_fused_blocks;
+  info->num_saved_states = plan->num_slots;
+  info->tmp1_features = plan->tmp_features[0];
+  info->tmp2_features = plan->tmp_features[1];
+  for (int s = 0; s < kMaxSlots; s++) info->saved_features[s] = plan->saved_features[s];
+  int64_t total = 0;
+  for (auto const& v : plan->params) total += static_cast<int64_t>(v.size());
+  info->num_parameters = total;
+  info->internal_state_capacity = plan->capacity;
+  info->max_width = plan->max_width;
+  info->width_class = plan->width_class;
+  return PONNI_OK;
+}
+
+int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer) {
+  if (plan == nullptr || layer < 0 || layer >= static_cast<int32_t>(plan->layers.size())) {
+    fail(PONNI_ERR_INVALID_ARGUMENT, "layer index out of range");
+    return -1;
+  }
+  return static_cast<int64_t>(plan->params[layer].size());
+}
+
+int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer, const void* values, int64_t count) {
+  if (plan == nullptr || layer < 0 || layer >= static_cast<int32_t>(plan->layers.size()))
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "layer index out of range");
+  auto& dst = plan->params[layer];
+  if (count != static_cast<int64_t>(dst.size()))
+    return fail(PONNI_ERR_SHAPE, "layer " + std::to_string(layer) + " expects " + std::to_string(dst.size()) +
+                                     " parameters, got " + std::to_string(count));
+  if (count > 0 && values == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "values is null");
+  if (plan->dtype == PONNI_F64) {
+    auto const* v = static_cast<double const*>(values);
+    for (int64_t i = 0; i < count; i++) dst[i] = v[i];
+  } else {
+    auto const* v = static_cast<float const*>(values);
+    for (int64_t i = 0; i < count; i++) dst[i] = v[i];
+  }
+  plan->device_dirty = true;
+  return PONNI_OK;
+}
+
+int ponni_plan_get_layer_params(ponni_plan plan, int32_t layer, void* values, int64_t count) {
+  if (plan == nullptr || layer < 0 || layer >= static_cast<int32_t>(plan->layers.size()))
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "layer index out of range");
+  auto const& src = plan->params[layer];
+  if (count != static_cast<int64_t>(src.size()))
+    return fail(PONNI_ERR_SHAPE, "layer " + std::to_string(layer) + " holds " + std::to_string(src.size()) +
+                                     " parameters, asked for " + std::to_string(count));
+  if (count > 0 && values == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "values is null");
+  if (plan->dtype == PONNI_F64) {
+    auto* v = static_cast<double*>(values);
+    for (int64_t i = 0; i < count; i++) v[i] = src[i];
+  } else {
+    auto* v = static_cast<float*>(values);
+    for (int64_t i = 0; i < count; i++) v[i] = static_cast<float>(src[i]);
+  }
+  return PONNI_OK;
+}
+
+int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch) {
+  if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+  if (batch < 0) return fail(PONNI_ERR_SHAPE, "Inference internal-state batch size must be nonnegative");
+  return reallocate_scratch(*plan, batch);
+}
+
+int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                  hipStream_t stream) {
+  if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+  if (batch <= 0) return fail(PONNI_ERR_SHAPE, "Inference requires a nonzero batch size");
+  if (batch > INT32_MAX) return fail(PONNI_ERR_SHAPE, "batch exceeds INT_MAX");
+  if (x == nullptr || y == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "input or output pointer is null");
+  if (ld_in < batch || ld_out < batch)
+    return fail(PONNI_ERR_SHAPE, "Error: Provided output dimensions do not match the model and input batch");
+  if (plan->device_dirty) {
+    int const st = upload(*plan);
+    if (st != PONNI_OK) return st;
+  } else {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != plan->device) return fail(PONNI_ERR_DEVICE, "plan was first used on another device");
+  }
+  if (plan->path == PONNI_PATH_GENERIC && batch > plan->capacity) {
+    int const st = reallocate_scratch(*plan, batch);
+    if (st != PONNI_OK) return st;
+  } else if (batch > plan->capacity) {
+    plan->capacity = batch;  // register paths keep no batch scratch
+  }
+  LaunchArgs a{};
+  a.ops = plan->d_ops;
+  a.num_ops = static_cast<int32_t>(plan->ops.size());
+  a.steps = plan->d_steps;
+  a.params = plan->d_params;
+  a.x = x;
+  a.ld_x = ld_in;
+  a.y = y;
+  a.ld_y = ld_out;
+  a.batch = batch;
+  a.num_inputs = plan->layers.front().n_in;
+  a.num_outputs = plan->layers.back().n_out;
+  a.buffers[BUF_INPUT] = const_cast<void*>(x);
+  a.buffer_ld[BUF_INPUT] = ld_in;
+  a.buffers[BUF_OUTPUT] = y;
+  a.buffer_ld[BUF_OUTPUT] = ld_out;
+  for (int b = 0; b < 2 + kMaxSlots; b++) {
+    a.buffers[BUF_TMP1 + b] = plan->d_scratch[b];
+    a.buffer_ld[BUF_TMP1 + b] = plan->capacity;
+  }
+  hipError_t err = hipSuccess;
+  switch (plan->path) {
+    case PONNI_PATH_NARROW: err = launch_narrow(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
+    case PONNI_PATH_MFMA: err = launch_mfma(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
+    default: err = launch_generic(plan->dtype, a, stream); break;
+  }
+  if (err != hipSuccess) return fail(PONNI_ERR_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(err));
+  return PONNI_OK;
+}
+
+int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed, uint64_t tag, int32_t dist, double a,
+                         double b, hipStream_t stream) {
+  if (x == nullptr && n > 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "buffer is null");
+  if (n < 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "negative element count");
+  if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (dist != PONNI_DIST_UNIFORM && dist != PONNI_DIST_NORMAL) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown distribution");
+  if (n == 0) return PONNI_OK;
+  hipError_t const err = launch_fill(x, dtype, n, seed, tag, dist, a, b, stream);
+  if (err != hipSuccess) return fail(PONNI_ERR_DEVICE, std::string("fill launch failed: ") + hipGetErrorString(err));
+  return PONNI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// Internal plan object behind the ponni_plan handle of include/ponni_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/ponni_hip.h"
+#include "program.h"
+
+namespace ponni_hip {
+
+// Device launch entry points, one per kernel family (kernels_*.hip).
+struct LaunchArgs {
+  const Op* ops;
+  int32_t num_ops;
+  const Step* steps;
+  const void* params;
+  const void* x;
+  int64_t ld_x;
+  void* y;
+  int64_t ld_y;
+  int64_t batch;
+  int32_t num_inputs;
+  int32_t num_outputs;
+  // generic path scratch (unused elsewhere)
+  void* buffers[BUF_SAVED + kMaxSlots];
+  int64_t buffer_ld[BUF_SAVED + kMaxSlots];
+};
+
+hipError_t launch_generic(int dtype, LaunchArgs const& args, hipStream_t stream);
+hipError_t launch_narrow(int dtype, int width_class, int num_slots, LaunchArgs const& args,
+                         hipStream_t stream);
+hipError_t launch_mfma(int dtype, int width_class, int num_slots, LaunchArgs const& args,
+                       hipStream_t stream);
+hipError_t launch_fill(void* x, int dtype, int64_t n, uint64_t seed, uint64_t tag, int dist,
+                       double a, double b, hipStream_t stream);
+
+// Width classes each register path is instantiated for.
+int narrow_width_class(int max_width);      // 0 if too wide
+int mfma_width_class(int dtype, int max_width);  // tiles of 16 features; 0 if too wide
+constexpr int kNarrowMaxSlots = 2;
+constexpr int kMfmaMaxSlots = 2;
+
+}  // namespace ponni_hip
+
+struct ponni_plan_s {
+  std::vector<ponni_layer_desc> layers;
+  int32_t dtype = PONNI_F32;
+  int32_t path = PONNI_PATH_GENERIC;
+  int32_t width_class = 0;
+  int32_t max_width = 0;
+  int32_t num_slots = 0;           // get_num_saved_states()
+  int32_t num_fused_blocks = 0;
+  int32_t tmp_features[2] = {0, 0};
+  int32_t saved_features[ponni_hip::kMaxSlots] = {};
+
+  // Host master copy of every layer's parameters (exact in double).
+  std::vector<std::vector<double>> params;
+
+  // Lowered program; offsets into the packed parameter buffer of `path`.
+  std::vector<ponni_hip::Op> ops;
+  std::vector<ponni_hip::Step> steps;
+  std::vector<int64_t> layer_param_offset;  // per layer, in packed elements
+  int64_t packed_elements = 0;
+
+  // Device state.
+  bool device_dirty = true;
+  int device = -1;
+  ponni_hip::Op* d_ops = nullptr;
+  ponni_hip::Step* d_steps = nullptr;
+  void* d_params = nullptr;
+  size_t d_params_bytes = 0;
+  void* d_scratch[2 + ponni_hip::kMaxSlots] = {};  // tmp1, tmp2, saved slots
+  int64_t capacity = 0;
+};

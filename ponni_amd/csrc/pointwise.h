@@ -1,0 +1,131 @@
+// Pointwise layer math shared by every kernel family.  Each formula follows the
+// reference layer's apply() (file:line on each function) term for term,
+// including its branch structure, so results agree with the reference to
+// rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "program.h"
+
+namespace ponni_hip {
+
+__device__ inline float d_exp(float x) { return expf(x); }
+__device__ inline double d_exp(double x) { return exp(x); }
+__device__ inline float d_log(float x) { return logf(x); }
+__device__ inline double d_log(double x) { return log(x); }
+__device__ inline float d_tanh(float x) { return tanhf(x); }
+__device__ inline double d_tanh(double x) { return tanh(x); }
+__device__ inline float d_erf(float x) { return erff(x); }
+__device__ inline double d_erf(double x) { return erf(x); }
+__device__ inline float d_sqrt(float x) { return sqrtf(x); }
+__device__ inline double d_sqrt(double x) { return sqrt(x); }
+
+// ponni_Relu.h:49-51
+template <class T> __device__ inline T act_relu(T x) { return x > T(0) ? x : T(0); }
+// ponni_LeakyRelu.h:53-55
+template <class T> __device__ inline T act_leaky_relu(T x, T slope) { return x > T(0) ? x : slope * x; }
+// ponni_Elu.h:48-50
+template <class T> __device__ inline T act_elu(T x, T alpha) { return x > T(0) ? x : alpha * (d_exp(x) - T(1)); }
+// ponni_Selu.h:45-49
+template <class T> __device__ inline T act_selu(T x) {
+  T const alpha = T(1.6732632423543772848);
+  T const scale = T(1.0507009873554804934);
+  return x > T(0) ? scale * x : scale * alpha * (d_exp(x) - T(1));
+}
+// ponni_Gelu.h:55-56
+template <class T> __device__ inline T act_gelu_erf(T x) {
+  return T(0.5) * x * (T(1) + d_erf(x / T(1.4142135623730950488)));
+}
+// ponni_Gelu.h:48-53
+template <class T> __device__ inline T act_gelu_tanh(T x) {
+  T const x3 = x * x * x;
+  return T(0.5) * x * (T(1) + d_tanh(T(0.79788456080286535588) * (x + T(0.044715) * x3)));
+}
+// ponni_Silu.h:45-49
+template <class T> __device__ inline T act_silu(T x) {
+  if (x >= T(0)) return x / (T(1) + d_exp(-x));
+  T const e = d_exp(x);
+  return x * e / (T(1) + e);
+}
+// ponni_Sigmoid.h:45-49
+template <class T> __device__ inline T act_sigmoid(T x) {
+  if (x >= T(0)) return T(1) / (T(1) + d_exp(-x));
+  T const e = d_exp(x);
+  return e / (T(1) + e);
+}
+// ponni_Tanh.h:44
+template <class T> __device__ inline T act_tanh(T x) { return d_tanh(x); }
+// ponni_Softplus.h:44-50
+template <class T> __device__ inline T act_softplus(T x, T beta) {
+  T const s = beta * x;
+  if (s > T(0)) return (s + d_log(T(1) + d_exp(-s))) / beta;
+  return d_log(T(1) + d_exp(s)) / beta;
+}
+// ponni_HardSigmoid.h:52-56
+template <class T> __device__ inline T act_hard_sigmoid(T x, T alpha, T beta) {
+  T v = alpha * x + beta;
+  v = v < T(0) ? T(0) : v;
+  return v > T(1) ? T(1) : v;
+}
+// ponni_HardSwish.h:42-47
+template <class T> __device__ inline T act_hard_swish(T x) {
+  T r = x + T(3);
+  r = r < T(0) ? T(0) : r;
+  r = r > T(6) ? T(6) : r;
+  return x * r / T(6);
+}
+// ponni_Mish.h:44-52
+template <class T> __device__ inline T act_mish(T x) {
+  T sp;
+  if (x > T(0)) sp = x + d_log(T(1) + d_exp(-x));
+  else sp = d_log(T(1) + d_exp(x));
+  return x * d_tanh(sp);
+}
+
+// Apply one parameter-free (or scalar-parameter) activation to every element
+// visited by `each`.  The switch sits outside the element loop so each case is
+// one straight-line loop.  `each(f)` must call f(float&) on every element.
+template <class T, class Each>
+__device__ inline void map_activation(int act, T a, T b, Each&& each) {
+  switch (act) {
+    case ACT_RELU: each([](T& v) { v = act_relu(v); }); break;
+    case ACT_LEAKY_RELU: each([a](T& v) { v = act_leaky_relu(v, a); }); break;
+    case ACT_ELU: each([a](T& v) { v = act_elu(v, a); }); break;
+    case ACT_SELU: each([](T& v) { v = act_selu(v); }); break;
+    case ACT_GELU_ERF: each([](T& v) { v = act_gelu_erf(v); }); break;
+    case ACT_GELU_TANH: each([](T& v) { v = act_gelu_tanh(v); }); break;
+    case ACT_SILU: each([](T& v) { v = act_silu(v); }); break;
+    case ACT_SIGMOID: each([](T& v) { v = act_sigmoid(v); }); break;
+    case ACT_TANH: each([](T& v) { v = act_tanh(v); }); break;
+    case ACT_SOFTPLUS: each([a](T& v) { v = act_softplus(v, a); }); break;
+    case ACT_HARD_SIGMOID: each([a, b](T& v) { v = act_hard_sigmoid(v, a, b); }); break;
+    case ACT_HARD_SWISH: each([](T& v) { v = act_hard_swish(v); }); break;
+    case ACT_MISH: each([](T& v) { v = act_mish(v); }); break;
+    default: break;
+  }
+}
+
+// Scalar form for the per-sample generic kernel.
+template <class T>
+__device__ inline T apply_step(int act, T x, T bias, T a, T b) {
+  switch (act) {
+    case ACT_BIAS: return x + bias;  // ponni_Bias.h:66-68
+    case ACT_RELU: return act_relu(x);
+    case ACT_LEAKY_RELU: return act_leaky_relu(x, a);
+    case ACT_ELU: return act_elu(x, a);
+    case ACT_SELU: return act_selu(x);
+    case ACT_GELU_ERF: return act_gelu_erf(x);
+    case ACT_GELU_TANH: return act_gelu_tanh(x);
+    case ACT_SILU: return act_silu(x);
+    case ACT_SIGMOID: return act_sigmoid(x);
+    case ACT_TANH: return act_tanh(x);
+    case ACT_SOFTPLUS: return act_softplus(x, a);
+    case ACT_HARD_SIGMOID: return act_hard_sigmoid(x, a, b);
+    case ACT_HARD_SWISH: return act_hard_swish(x);
+    case ACT_MISH: return act_mish(x);
+    default: return x;
+  }
+}
+
+}  // namespace ponni_hip

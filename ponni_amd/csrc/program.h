@@ -1,0 +1,78 @@
+// Internal "lane program": the plan compiler lowers a PONNI layer chain into a
+// flat list of Op records that every kernel family interprets with uniform
+// (scalar) control flow.  The record is shared by host and device code.
+#pragma once
+
+#include <cstdint>
+
+namespace ponni_hip {
+
+// Pointwise step kinds.  A dense op carries the pointwise layers that follow
+// it as an epilogue, exactly the fused block of ponni_Inference.h:412-444.
+enum Act : int32_t {
+  ACT_BIAS = 1,          // v + b[f]                         ponni_Bias.h:66-68
+  ACT_RELU = 2,          // v > 0 ? v : 0                    ponni_Relu.h:49-51
+  ACT_LEAKY_RELU = 3,    // v > 0 ? v : a*v                  ponni_LeakyRelu.h:53-55
+  ACT_ELU = 4,           // v > 0 ? v : a*(exp(v)-1)         ponni_Elu.h:48-50
+  ACT_SELU = 5,          //                                  ponni_Selu.h:45-49
+  ACT_GELU_ERF = 6,      // 0.5 v (1 + erf(v/sqrt2))         ponni_Gelu.h:55-56
+  ACT_GELU_TANH = 7,     // tanh form                        ponni_Gelu.h:48-53
+  ACT_SILU = 8,          //                                  ponni_Silu.h:45-49
+  ACT_SIGMOID = 9,       //                                  ponni_Sigmoid.h:45-49
+  ACT_TANH = 10,         //                                  ponni_Tanh.h:44
+  ACT_SOFTPLUS = 11,     // a = beta                         ponni_Softplus.h:44-50
+  ACT_HARD_SIGMOID = 12, // a = alpha, b = beta              ponni_HardSigmoid.h:52-56
+  ACT_HARD_SWISH = 13,   //                                  ponni_HardSwish.h:42-47
+  ACT_MISH = 14          //                                  ponni_Mish.h:44-52
+};
+
+struct Step {
+  int32_t act;   // Act
+  int32_t off;   // parameter offset of the bias vector (ACT_BIAS only)
+  float a;       // scalar attribute (slope, alpha, beta)
+  float b;       // second scalar attribute
+};
+
+enum OpCode : int32_t {
+  OP_DENSE = 1,       // out = epilogue(W^T in)                     Matvec + pointwise
+  OP_POINTWISE = 2,   // state = epilogue(state), in place          lone pointwise layer
+  OP_LAYER_NORM = 3,  // two-pass mean/var, gamma/beta              ponni_LayerNorm.h:76-99
+  OP_SOFTMAX = 4,     //                                            ponni_Softmax.h:45-56
+  OP_LOG_SOFTMAX = 5, //                                            ponni_LogSoftmax.h:45-57
+  OP_MIN_MAX = 6,     //                                            ponni_MinMaxNorm.h:67-84
+  OP_SAVE = 7,        // saved[slot] = state                        ponni_Save_State.h:57-67
+  OP_ADD = 8,         // state = state + saved[slot]                ponni_Binop_Add.h:57-68
+  OP_CONCAT = 9,      // state = [state; saved] or [saved; state]   ponni_Binop_Concatenate.h:63-86
+  OP_PROJ_ADD = 10    // state = state + (b + W^T saved[slot])      ponni_Binop_Projection_Add.h:81-95
+};
+
+// Buffers of the generic (HBM scratch) path, chosen at plan time exactly as
+// traverse_mixed_batch_parallel picks them (ponni_Inference.h:453-555).
+enum Buffer : int32_t {
+  BUF_INPUT = 0,
+  BUF_OUTPUT = 1,
+  BUF_TMP1 = 2,
+  BUF_TMP2 = 3,
+  BUF_SAVED = 4  // BUF_SAVED + slot
+};
+
+struct Op {
+  int32_t code;       // OpCode
+  int32_t n_in;       // features read from the main state
+  int32_t n_out;      // features written to the main state
+  int32_t slot;       // saved-state slot (SAVE/ADD/CONCAT/PROJ_ADD)
+  int32_t aux;        // CONCAT: 1 = after; PROJ_ADD: NSAVE
+  int32_t woff;       // offset of W / gamma in the path's parameter buffer
+  int32_t boff;       // offset of bias / beta
+  int32_t epi_begin;  // first Step of the epilogue
+  int32_t epi_count;  // number of Steps
+  int32_t src;        // generic path: input buffer
+  int32_t dst;        // generic path: output buffer
+  float f0, f1, f2;   // scalar attributes (epsilon, out_min, out_max)
+};
+
+constexpr int kMaxSlots = 8;  // saved-state slots a plan may use
+constexpr int kMaxOps = 256;
+constexpr int kMaxSteps = 512;
+
+}  // namespace ponni_hip

@@ -1,0 +1,228 @@
+"""GPU parity: every kernel path of libponni_hip.so against the CPU oracle.
+
+fp32 bar: relative L2 <= 1e-5 and max-abs <= 1e-4
+(max-abs scaled by max(1, max|reference|) for random chains whose outputs are
+not O(1)).  fp16 / bf16 bar: relative L2 <= 2e-3 against the oracle's
+fp16-operand / fp32-accumulate mode on the same inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import ponni_amd as P
+from ponni_amd import configs as C
+from tests import test_oracle as K
+
+pytestmark = pytest.mark.gpu
+
+PATHS = ["generic", "narrow", "mfma"]
+TORCH_DT = {"f32": "float32", "f16": "float16", "bf16": "bfloat16", "f64": "float64"}
+ORACLE_MODE = {"f32": oracle.MODE_F32, "f64": oracle.MODE_F64, "f16": oracle.MODE_F16_OPERANDS,
+               "bf16": oracle.MODE_BF16_OPERANDS}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_built():
+    oracle.build()
+
+
+def gpu_run(layers, x_np, dtype="f32", path="auto", pad=0, dev="cuda:0"):
+    import torch
+
+    tdt = getattr(torch, TORCH_DT[dtype])
+    try:
+        m = P.create_inference_model(*layers, dtype=dtype, path=path)
+    except P.PonniError as e:
+        if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+            pytest.skip(f"{path} does not support this chain: {e.message}")
+        raise
+    n_in, B = x_np.shape
+    xs = torch.zeros((n_in, B + pad), dtype=tdt, device=dev)
+    xs[:, :B] = torch.from_numpy(np.asarray(x_np, dtype=np.float64)).to(tdt)
+    x = xs[:, :B]
+    ys = torch.full((m.get_num_outputs(), B + pad), float("nan"), dtype=tdt, device=dev)
+    y = ys[:, :B]
+    m.forward_batch_parallel(x, y)
+    torch.cuda.synchronize()
+    if pad:
+        assert torch.isnan(ys[:, B:].float()).all(), "kernel wrote past the batch"
+    return y.double().cpu().numpy(), xs[:, :B].double().cpu().numpy(), m
+
+
+def check_f32(got, want, scale_tol=True):
+    err = np.abs(got - want)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    lim = 1e-4 * (max(1.0, np.abs(want).max()) if scale_tol else 1.0)
+    assert np.isfinite(got).all()
+    assert rel <= 1e-5 and err.max() <= lim, f"relL2={rel:.3e} maxabs={err.max():.3e}"
+
+
+def check_half(got, want, tol=2e-3):
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    assert np.isfinite(got).all() and rel <= tol, f"relL2={rel:.3e}"
+
+
+KNOWN = {
+    "first_model": ([P.Matvec(np.ones((2, 2))), P.Bias(np.ones(2)), P.LeakyRelu(2, 0.1)], [[1.0], [2.0]],
+                    [[4.0], [4.0]]),
+    "layout_36_42": ([P.Matvec(np.arange(10.0, 16.0).reshape(2, 3))], [[1.0], [2.0]], [[36.0], [39.0], [42.0]]),
+    "leading_save": ([P.Save_State(0, 2), P.Relu(2), P.Binop_Add(0, 2)], [[-2.0], [3.0]], [[-2.0], [6.0]]),
+    "multi_save": ([P.Save_State(0, 2), P.Relu(2), P.Binop_Concatenate(0, 2, 4, True), P.Save_State(1, 4),
+                    P.Relu(4), P.Binop_Add(1, 4), P.Binop_Concatenate(0, 4, 6, True)], [[-2.0], [3.0]],
+                   [[0.0], [6.0], [-2.0], [6.0], [-2.0], [3.0]]),
+    "projection": ([P.Save_State(0, 2), P.Matvec(np.array([[0.25, 0.0, 0.0], [0.0, 0.4, 0.6]])),
+                    P.Binop_Projection_Add(0, np.array([[1.0, 0.0, 0.5], [0.0, 1.0, 0.5]]), [0.1, 0.2, 0.3])],
+                   [[4.0], [5.0]], [[5.1], [7.2], [7.8]]),
+    "softmax_barrier": ([P.Matvec(np.ones((2, 3))), P.Bias([0.0, 1.0, 2.0]), P.Relu(3), P.Softmax(3),
+                         P.Matvec(np.ones((3, 2))), P.Bias([0.0, -1.0]), P.Tanh(2)], [[0.5], [0.5]],
+                        [[math.tanh(1.0)], [0.0]]),
+}
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("name", sorted(KNOWN))
+def test_known_answers(cuda, name, path):
+    layers, x, want = KNOWN[name]
+    x = np.tile(np.asarray(x), (1, 70))  # several waves, ragged last wave
+    got, _, _ = gpu_run(layers, x, path=path)
+    assert np.allclose(got, np.tile(np.asarray(want), (1, 70)), atol=1e-5), got[:, :3]
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_four_block_closed_form(cuda, path):
+    layers = [P.Matvec(np.ones((2, 5))), P.Bias(np.full(5, 0.5)), P.Relu(5), P.Tanh(5),
+              P.Matvec(np.ones((5, 3))), P.Bias(np.full(3, -0.25)), P.Sigmoid(3),
+              P.Matvec(np.ones((3, 7))), P.Bias(np.full(7, 0.1)), P.LeakyRelu(7, 0.2),
+              P.Matvec(np.ones((7, 2))), P.Bias(np.full(2, -0.2)), P.HardSwish(2)]
+    x = np.random.default_rng(0).uniform(-2, 2, (2, 1000))
+    got, xg, _ = gpu_run(layers, x, path=path)
+    check_f32(got, oracle.forward(layers, xg))
+
+
+def test_performance_benchmark_closed_form(cuda):
+    # unit/performance_benchmark: 8-wide, ones, LeakyRelu(0.1), x = 0.1 -> mean 15.4
+    layers = [P.Matvec(np.ones((8, 8))), P.Bias(np.ones(8)), P.LeakyRelu(8, 0.1),
+              P.Matvec(np.ones((8, 8))), P.Bias(np.ones(8)), P.LeakyRelu(8, 0.1)]
+    for path in PATHS:
+        got, _, _ = gpu_run(layers, np.full((8, 1 << 16), 0.1), path=path)
+        assert abs(got.mean() - 15.4) <= 1e-3 and np.allclose(got, 15.4, atol=1e-4)
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("seed", range(10))
+def test_random_chains(cuda, seed, path):
+    rng = np.random.default_rng(500 + seed)
+    width = [3, 8, 13, 16, 24, 40, 64, 100, 128, 7][seed]
+    layers = K.random_chain(rng, width, 2 + seed % 4)
+    B = [1, 31, 33, 255, 257, 1000, 4097, 64, 129, 2049][seed]
+    x = rng.standard_normal((width, B))
+    got, xg, _ = gpu_run(layers, x, path=path, pad=3)
+    check_f32(got, oracle.forward(layers, xg))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("path", PATHS)
+def test_reduced_precision_paths(cuda, dtype, path):
+    rng = np.random.default_rng(11)
+    layers = [P.Matvec(rng.standard_normal((12, 16)) * 0.3), P.Bias(rng.uniform(-0.1, 0.1, 16)), P.Tanh(16),
+              P.Save_State(0, 16), P.LayerNorm(16), P.Matvec(rng.standard_normal((16, 16)) * 0.25),
+              P.Gelu(16, True), P.Binop_Add(0, 16), P.Matvec(rng.standard_normal((16, 6)) * 0.3), P.Softmax(6)]
+    x = rng.standard_normal((12, 3000))
+    got, xg, _ = gpu_run(layers, x, dtype=dtype, path=path)
+    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
+
+
+def test_f64_generic(cuda):
+    rng = np.random.default_rng(12)
+    layers = K.random_chain(rng, 20, 3)
+    x = rng.standard_normal((20, 500))
+    got, xg, _ = gpu_run(layers, x, dtype="f64", path="generic")
+    want = oracle.forward(layers, xg, oracle.MODE_F64)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def config_input(cfg, B, dev="cuda:0"):
+    import torch
+
+    tdt = torch.float16 if cfg.dtype == "f16" else torch.float32
+    x = torch.empty((cfg.n_in, B), dtype=tdt, device=dev)
+    kind, a, b = cfg.input_dist
+    P.fill_synthetic(x, cfg.seed, C.INPUT_TAG, kind, a, b)
+    return x
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+def test_configs_small_batch(cuda, name):
+    """Each BASELINE config (with nonzero biases) on its auto path vs the oracle."""
+    import torch
+
+    cfg = C.CONFIGS[name]
+    layers = cfg.layers(True)
+    B = 20_000 + 13
+    x = config_input(cfg, B)
+    m = P.create_inference_model(*layers, dtype=cfg.dtype)
+    y = m.forward_batch_parallel(x)
+    torch.cuda.synchronize()
+    xg = x.double().cpu().numpy()
+    got = y.double().cpu().numpy()
+    if cfg.dtype == "f32":
+        check_f32(got, oracle.forward(layers, xg), scale_tol=False)
+    else:
+        check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+def test_configs_full_size_columns(cuda, name):
+    """Full BASELINE batch: samples are independent, so a strided subset of
+    columns of the full-size output must equal the oracle on those columns."""
+    import torch
+
+    cfg = C.CONFIGS[name]
+    layers = cfg.layers(False)
+    x = config_input(cfg, cfg.batch)
+    m = P.create_inference_model(*layers, dtype=cfg.dtype)
+    y = m.forward_batch_parallel(x)
+    torch.cuda.synchronize()
+    cols = torch.arange(0, cfg.batch, 4099, device=x.device)
+    cols = torch.cat([cols, torch.tensor([cfg.batch - 1], device=x.device)])
+    xg = x[:, cols].double().cpu().numpy()
+    got = y[:, cols].double().cpu().numpy()
+    assert torch.isfinite(y.float()).all()
+    if cfg.dtype == "f32":
+        check_f32(got, oracle.forward(layers, xg), scale_tol=False)
+    else:
+        check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
+
+
+def test_strided_views_and_stream(cuda):
+    """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    layers = C.c2_layers(True)
+    x = rng.standard_normal((16, 777))
+    got, xg, _ = gpu_run(layers, x, pad=50)
+    check_f32(got, oracle.forward(layers, xg), scale_tol=False)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        got2, _, _ = gpu_run(layers, x, pad=0)
+    s.synchronize()
+    assert np.array_equal(got, got2)
+
+
+def test_parameter_update_is_seen(cuda):
+    rng = np.random.default_rng(9)
+    layers = C.c2_layers(True)
+    x = rng.standard_normal((16, 300))
+    got, xg, m = gpu_run(layers, x)
+    import torch
+
+    w = rng.standard_normal((16, 64)) * 0.1
+    m.set_layer_params(0, w)
+    layers[0].params = w.reshape(-1)
+    xt = torch.from_numpy(xg).float().cuda()
+    y = m.forward_batch_parallel(xt)
+    torch.cuda.synchronize()
+    check_f32(y.double().cpu().numpy(), oracle.forward(layers, xg), scale_tol=False)
