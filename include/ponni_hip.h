@@ -103,7 +103,9 @@ typedef enum ponni_path {
   PONNI_PATH_AUTO = 0,    /* pick the fastest path that supports the model          */
   PONNI_PATH_GENERIC = 1, /* one sample per lane, states in HBM scratch (any model) */
   PONNI_PATH_NARROW = 2,  /* one sample per lane, states in registers (width <= 16) */
-  PONNI_PATH_MFMA = 3     /* 16x16 MFMA tiles, states in registers (width <= 256)   */
+  PONNI_PATH_MFMA = 3,    /* 16x16 MFMA tiles, states in registers (width <= 128)   */
+  PONNI_PATH_FUSED = 4    /* MFMA tiles in a kernel generated for this plan and
+                             compiled with hipRTC on first use (width <= 256)      */
 } ponni_path;
 
 typedef struct ponni_plan_s* ponni_plan;
@@ -183,6 +185,21 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch);
  * reference aborts (ponni_Inference.h:366). */
 int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y,
                   int64_t ld_out, int64_t batch, hipStream_t stream);
+
+/* Source text of the kernel generated for a FUSED plan -- the counterpart of
+ * the per-model executor the reference instantiates at compile time
+ * (ponni_Inference.h:453-555) and of the emitted infer_batch body
+ * (kokkos_nn/emitter.py:1537-1550).  Returns the length including the
+ * terminating NUL (copying it when buf holds at least that many bytes), or
+ * -1 for a non-FUSED plan. */
+int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len);
+
+/* Compile a FUSED plan's kernel with hipRTC now (no device needed; the result
+ * is cached in-process and under $PONNI_JIT_CACHE or ~/.cache/ponni_hip) so the
+ * first ponni_forward does not pay for it.  A no-op for the other paths.
+ * Stands in for the compile step of building a reference model, which
+ * happens when the application is compiled. */
+int ponni_plan_compile(ponni_plan plan);
 
 /* --- synthetic data (bench and tests) ------------------------------------- */
 

@@ -17,8 +17,9 @@ PONNI_ERR_DEVICE = 5
 PONNI_ERR_IO = 6
 
 F32, F64, F16, BF16 = 1, 2, 3, 4
-PATH_AUTO, PATH_GENERIC, PATH_NARROW, PATH_MFMA = 0, 1, 2, 3
-PATH_NAMES = {PATH_AUTO: "auto", PATH_GENERIC: "generic", PATH_NARROW: "narrow", PATH_MFMA: "mfma"}
+PATH_AUTO, PATH_GENERIC, PATH_NARROW, PATH_MFMA, PATH_FUSED = 0, 1, 2, 3, 4
+PATH_NAMES = {PATH_AUTO: "auto", PATH_GENERIC: "generic", PATH_NARROW: "narrow", PATH_MFMA: "mfma",
+              PATH_FUSED: "fused"}
 
 LAYER_MATVEC = 1
 LAYER_BIAS = 2
@@ -118,6 +119,10 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_reallocate_internal_state.argtypes = [vp, i64]
     L.ponni_forward.restype = ctypes.c_int
     L.ponni_forward.argtypes = [vp, vp, i64, vp, i64, i64, vp]
+    L.ponni_plan_kernel_source.restype = i64
+    L.ponni_plan_kernel_source.argtypes = [vp, ctypes.c_char_p, i64]
+    L.ponni_plan_compile.restype = ctypes.c_int
+    L.ponni_plan_compile.argtypes = [vp]
     L.ponni_fill_synthetic.restype = ctypes.c_int
     L.ponni_fill_synthetic.argtypes = [vp, i32, i64, u64, u64, i32, ctypes.c_double, ctypes.c_double, vp]
     L.ponni_fnv1a64.restype = u64

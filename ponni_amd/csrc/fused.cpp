@@ -1,0 +1,391 @@
+// FUSED path: per-plan kernel specialization.
+//
+// The reference instantiates one executor per model at C++ compile time
+// (traverse_mixed_batch_parallel, src/ponni_Inference.h:453-555, and the
+// generated infer_batch of kokkos_nn/emitter.py:1537-1550).  Here the plan's
+// lowered op list is turned into HIP source that calls the tile library of
+// fused_f32.h with every width a compile-time constant; hipRTC compiles it for
+// gfx950 once per distinct source (in-process and on-disk cache), and the
+// module is launched like any other kernel.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <algorithm>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "fused.h"
+
+namespace ponni_hip {
+
+// Embedded header texts (generated at build time from csrc/*.h).
+extern char const* const kJitHeaderNames[];
+extern char const* const kJitHeaderTexts[];
+extern int const kJitHeaderCount;
+
+namespace {
+
+int tiles(int n) { return (n + 15) / 16; }
+
+std::string flit(float v) {
+  char buf[64];
+  std::snprintf(buf, sizeof(buf), "%a", static_cast<double>(v));
+  return std::string(buf) + "f";
+}
+
+bool zero_at_zero(int act) {
+  return !(act == ACT_SIGMOID || act == ACT_SOFTPLUS || act == ACT_HARD_SIGMOID);
+}
+
+std::string act_expr(Step const& s) {
+  switch (s.act) {
+    case ACT_RELU: return "act_relu(v)";
+    case ACT_LEAKY_RELU: return "act_leaky_relu(v, " + flit(s.a) + ")";
+    case ACT_ELU: return "act_elu(v, " + flit(s.a) + ")";
+    case ACT_SELU: return "act_selu(v)";
+    case ACT_GELU_ERF: return "act_gelu_erf(v)";
+    case ACT_GELU_TANH: return "act_gelu_tanh(v)";
+    case ACT_SILU: return "act_silu(v)";
+    case ACT_SIGMOID: return "act_sigmoid(v)";
+    case ACT_TANH: return "act_tanh(v)";
+    case ACT_SOFTPLUS: return "act_softplus(v, " + flit(s.a) + ")";
+    case ACT_HARD_SIGMOID: return "act_hard_sigmoid(v, " + flit(s.a) + ", " + flit(s.b) + ")";
+    case ACT_HARD_SWISH: return "act_hard_swish(v)";
+    case ACT_MISH: return "act_mish(v)";
+    default: return "v";
+  }
+}
+
+uint64_t fnv(std::string const& s) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (unsigned char ch : s) {
+    h ^= ch;
+    h *= 0x100000001b3ull;
+  }
+  return h;
+}
+
+struct Module {
+  hipModule_t module = nullptr;
+  hipFunction_t fn = nullptr;
+  int blocks_per_cu = 0;
+};
+
+std::mutex g_mutex;
+std::map<std::pair<int, std::string>, std::shared_ptr<Module>> g_modules;  // (device, key)
+
+std::string cache_dir() {
+  if (char const* d = std::getenv("PONNI_JIT_CACHE")) return d;
+  if (char const* d = std::getenv("XDG_CACHE_HOME")) return std::string(d) + "/ponni_hip";
+  if (char const* d = std::getenv("HOME")) return std::string(d) + "/.cache/ponni_hip";
+  return "";
+}
+
+char const* const kOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+                                "-Xclang", "-packed-fp32-ops"};
+
+bool compile(std::string const& source, std::vector<char>& code, std::string& log) {
+  hiprtcProgram prog = nullptr;
+  if (hiprtcCreateProgram(&prog, source.c_str(), "ponni_fused.hip", kJitHeaderCount, kJitHeaderTexts,
+                          kJitHeaderNames) != HIPRTC_SUCCESS) {
+    log = "hiprtcCreateProgram failed";
+    return false;
+  }
+  hiprtcResult const r = hiprtcCompileProgram(prog, int(sizeof(kOptions) / sizeof(kOptions[0])), kOptions);
+  size_t n = 0;
+  hiprtcGetProgramLogSize(prog, &n);
+  log.assign(n, '\0');
+  if (n) hiprtcGetProgramLog(prog, &log[0]);
+  if (r != HIPRTC_SUCCESS) {
+    hiprtcDestroyProgram(&prog);
+    return false;
+  }
+  hiprtcGetCodeSize(prog, &n);
+  code.resize(n);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  return true;
+}
+
+}  // namespace
+
+// Can the FUSED generator express this chain?
+bool fused_supports(ponni_plan_s const& p) {
+  if (p.dtype != PONNI_F32) return false;
+  if (p.max_width > 256) return false;
+  for (auto const& d : p.layers) {
+    if (d.kind == PONNI_LAYER_BINOP_CONCATENATE) {
+      int const lead = (d.flags & PONNI_FLAG_CONCAT_AFTER) ? d.n_in : d.n_out - d.n_in;
+      if (lead % 16 != 0) return false;
+    }
+  }
+  return true;
+}
+
+// Generate the HIP source of the plan's kernel.  Offsets are those of the
+// MFMA packing (plan.cpp, pack_params).
+std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
+  int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
+  cfg.lds_bytes = param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
+  cfg.waves = 4;
+  cfg.columns_per_block = 4 * 32;
+  // Register budget.  Every live tile holds 4 * kNT floats per lane; a dense
+  // op holds its input, its output and one output tile's A fragments (4 floats
+  // per input tile).  Parameters small enough to live in registers next to
+  // that state are loaded once per wave and reused for every column tile.
+  int worst = 0;
+  {
+    int cur = tiles(p.layers.front().n_in);
+    std::map<int, int> slots;
+    for (Op const& op : p.ops) {
+      int saved_regs = 0;
+      for (auto const& kv : slots) saved_regs += kv.second * 8;
+      int need = cur * 8;
+      switch (op.code) {
+        case OP_DENSE: need = (tiles(op.n_in) + tiles(op.n_out)) * 8 + tiles(op.n_in) * 4; cur = tiles(op.n_out); break;
+        case OP_PROJ_ADD: need = (cur + 2 * tiles(op.n_out)) * 8 + tiles(op.aux) * 4; break;
+        case OP_CONCAT: need = 2 * tiles(op.n_out) * 8; cur = tiles(op.n_out); break;
+        case OP_SAVE: slots[op.slot] = cur; break;
+        default: break;
+      }
+      worst = std::max(worst, need + saved_regs);
+    }
+  }
+  int const overhead = 32;
+  int64_t const param_regs = (p.packed_elements + 63) / 64;
+  cfg.params_in_registers = worst + overhead + param_regs <= 256;
+  int const regs = worst + overhead + (cfg.params_in_registers ? static_cast<int>(param_regs) : 0);
+  cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
+  if (cfg.params_in_registers) cfg.lds_bytes = 0;
+  if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
+    int const v = std::atoi(w);
+    if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
+  }
+  std::ostringstream o;
+  o << "// generated by libponni_hip for one plan\n";
+  o << "#include \"fused_f32.h\"\n";
+  o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
+  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void ponni_fused(float const* __restrict__ gparams, "
+       "float const* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy, int64_t batch) {\n";
+  if (cfg.lds_bytes > 0) {
+    o << "  __shared__ floatx4 lds_p[" << cfg.lds_bytes / 16 << "];\n";
+    o << "  stage(lds_p, gparams, " << cfg.lds_bytes / 4 << ");\n";
+    o << "  float const* __restrict__ P0 = reinterpret_cast<float const*>(lds_p);\n";
+  } else {
+    o << "  float const* __restrict__ P0 = gparams;\n";
+  }
+  o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
+  o << "  int64_t const tiles = (batch + 127) / 128;\n";
+  o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
+  o << "    L.col0 = (tile * 4 + (threadIdx.x >> 6)) * 32;\n";
+  // Register-resident parameters may be hoisted out of the tile loop; otherwise
+  // pin() hides the pointer's loop invariance so they are re-read per tile.
+  o << (cfg.params_in_registers ? "    float const* __restrict__ P = P0;\n" : "    float const* __restrict__ P = pin(P0);\n");
+  int var = 0;
+  auto fresh = [&]() { return "s" + std::to_string(var++); };
+  std::string cur = fresh();
+  int cur_n = p.layers.front().n_in;
+  o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
+  std::map<int, std::pair<std::string, int>> saved;  // slot -> (variable, width)
+  auto epilogue = [&](std::string const& v, int n, int begin, int count) {
+    bool pad = false;
+    for (int s = 0; s < count; s++) {
+      Step const& st = p.steps[begin + s];
+      if (st.act == ACT_BIAS) {
+        o << "    add_rows<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L);\n";
+      } else {
+        o << "    map<" << tiles(n) << ">(" << v << ", [](float v) { return " << act_expr(st) << "; });\n";
+        if (!zero_at_zero(st.act)) pad = true;
+      }
+    }
+    if (pad && n % 16) o << "    zero_pad<" << n << ", " << tiles(n) << ">(" << v << ", L);\n";
+  };
+  for (Op const& op : p.ops) {
+    o << "    // op code " << op.code << "\n";
+    switch (op.code) {
+      case OP_DENSE: {
+        std::string const nv = fresh();
+        o << "    auto " << nv << " = dense<" << tiles(op.n_in) << ", " << tiles(op.n_out) << ">(" << cur << ", P + "
+          << op.woff << ", zeros<" << tiles(op.n_out) << ">(), L);\n";
+        epilogue(nv, op.n_out, op.epi_begin, op.epi_count);
+        cur = nv;
+        cur_n = op.n_out;
+        break;
+      }
+      case OP_POINTWISE:
+        epilogue(cur, cur_n, op.epi_begin, op.epi_count);
+        break;
+      case OP_LAYER_NORM:
+        o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", P + " << op.woff << ", P + "
+          << op.boff << ", " << flit(op.f0) << ", L);\n";
+        break;
+      case OP_SOFTMAX:
+      case OP_LOG_SOFTMAX:
+        o << "    softmax<" << cur_n << ", " << tiles(cur_n) << ", " << (op.code == OP_LOG_SOFTMAX ? "true" : "false")
+          << ">(" << cur << ", L);\n";
+        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", L);\n";
+        break;
+      case OP_MIN_MAX:
+        o << "    min_max<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", " << flit(op.f0) << ", "
+          << flit(op.f1) << ", " << flit(op.f2) << ", L);\n";
+        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", L);\n";
+        break;
+      case OP_SAVE: {
+        std::string const sv = "sv" + std::to_string(op.slot) + "_" + std::to_string(var++);
+        o << "    auto " << sv << " = " << cur << ";\n";
+        saved[op.slot] = {sv, cur_n};
+        break;
+      }
+      case OP_ADD:
+        o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << saved[op.slot].first << ");\n";
+        break;
+      case OP_CONCAT: {
+        auto const& sv = saved[op.slot];
+        std::string const nv = fresh();
+        if (op.aux)
+          o << "    auto " << nv << " = concat<" << tiles(cur_n) << ", " << tiles(sv.second) << ">(" << cur << ", "
+            << sv.first << ");\n";
+        else
+          o << "    auto " << nv << " = concat<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
+            << ", " << cur << ");\n";
+        cur = nv;
+        cur_n = op.n_out;
+        break;
+      }
+      case OP_PROJ_ADD: {
+        // proj = b + W^T saved (bias first, ponni_Binop_Projection_Add.h:91-92); out = in + proj.
+        auto const& sv = saved[op.slot];
+        std::string const b = fresh(), nv = fresh();
+        o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
+        o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", P + " << op.boff << ", L);\n";
+        o << "    auto " << nv << " = dense<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
+          << ", P + " << op.woff << ", " << b << ", L);\n";
+        o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << nv << ");\n";
+        break;
+      }
+      default:
+        break;
+    }
+  }
+  o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  o << "  }\n}\n";
+  return o.str();
+}
+
+namespace {
+
+std::string cache_key(std::string const& src) {
+  std::string opts;
+  for (auto const* o : kOptions) opts += std::string(o) + " ";
+  std::string hdrs;
+  for (int i = 0; i < kJitHeaderCount; i++) hdrs += kJitHeaderTexts[i];
+  char buf[32];
+  std::snprintf(buf, sizeof(buf), "%016llx", static_cast<unsigned long long>(fnv(src + opts + hdrs)));
+  return buf;
+}
+
+std::mutex g_code_mutex;
+std::map<std::string, std::vector<char>> g_code;  // key -> code object
+
+}  // namespace
+
+int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error) {
+  FusedConfig cfg;
+  std::string const src = fused_source(p, cfg);
+  key = cache_key(src);
+  std::lock_guard<std::mutex> lock(g_code_mutex);
+  auto it = g_code.find(key);
+  if (it != g_code.end()) {
+    code = it->second;
+    return PONNI_OK;
+  }
+  std::string const dir = cache_dir();
+  std::string const path = dir.empty() ? "" : dir + "/" + key + ".co";
+  code.clear();
+  if (!path.empty()) {
+    std::ifstream in(path, std::ios::binary);
+    if (in) code.assign(std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>());
+  }
+  if (code.empty()) {
+    std::string log;
+    if (!compile(src, code, log)) {
+      error = "hipRTC failed to compile the fused kernel:\n" + log;
+      return PONNI_ERR_DEVICE;
+    }
+    if (!path.empty()) {
+      ::mkdir(dir.c_str(), 0755);
+      std::string const tmp = path + ".tmp" + std::to_string(::getpid());
+      std::ofstream out(tmp, std::ios::binary);
+      out.write(code.data(), static_cast<std::streamsize>(code.size()));
+      out.close();
+      if (out) std::rename(tmp.c_str(), path.c_str());
+      else std::remove(tmp.c_str());
+    }
+  }
+  g_code[key] = code;
+  return PONNI_OK;
+}
+
+int fused_prepare(ponni_plan_s& p, std::string& error) {
+  FusedConfig cfg;
+  (void)fused_source(p, cfg);
+  std::string key;
+  std::vector<char> code;
+  int const st = fused_compile(p, key, code, error);
+  if (st != PONNI_OK) return st;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    error = "no HIP device";
+    return PONNI_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_mutex);
+  auto it = g_modules.find({dev, key});
+  if (it == g_modules.end()) {
+    auto m = std::make_shared<Module>();
+    hipError_t e = hipModuleLoadData(&m->module, code.data());
+    if (e == hipSuccess) e = hipModuleGetFunction(&m->fn, m->module, "ponni_fused");
+    if (e == hipSuccess)
+      e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&m->blocks_per_cu, m->fn, cfg.waves * 64, 0);
+    if (e != hipSuccess) {
+      error = std::string("loading the fused kernel failed: ") + hipGetErrorString(e);
+      return PONNI_ERR_DEVICE;
+    }
+    it = g_modules.emplace(std::make_pair(dev, key), m).first;
+  }
+  p.fused_fn = it->second->fn;
+  p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
+  p.fused_persistent = cfg.lds_bytes > 0 || cfg.params_in_registers;
+  p.fused_columns_per_block = cfg.columns_per_block;
+  return PONNI_OK;
+}
+
+hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t stream) {
+  int64_t const blocks = (a.batch + p.fused_columns_per_block - 1) / p.fused_columns_per_block;
+  int64_t grid = blocks;
+  if (p.fused_persistent) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    int64_t const resident = int64_t(cus) * p.fused_blocks_per_cu;
+    grid = blocks < resident ? blocks : resident;
+  }
+  void const* params = a.params;
+  void const* x = a.x;
+  void* y = a.y;
+  int64_t ldx = a.ld_x, ldy = a.ld_y, batch = a.batch;
+  void* args[] = {&params, &x, &ldx, &y, &ldy, &batch};
+  return hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, 0, stream, args, nullptr);
+}
+
+}  // namespace ponni_hip

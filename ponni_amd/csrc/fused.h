@@ -1,0 +1,30 @@
+// FUSED path: per-plan generated kernels compiled with hipRTC (fused.cpp).
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "plan.h"
+
+namespace ponni_hip {
+
+// Packed parameter blocks up to this size are staged in LDS by the kernel.
+constexpr int64_t kFusedLdsParamBytes = 64 * 1024;
+
+struct FusedConfig {
+  int lds_bytes = 0;          // 0: parameters stream from L2
+  int waves = 4;              // waves per workgroup
+  int waves_per_simd = 2;     // occupancy the kernel is compiled for
+  bool params_in_registers = false;  // parameters loaded once per wave, kept in VGPRs
+  int columns_per_block = 128;
+};
+
+bool fused_supports(ponni_plan_s const& p);
+std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg);
+// Compile (or fetch from cache) the plan's kernel; needs no device.
+int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error);
+// Compile if needed and load the module on the current device.
+int fused_prepare(ponni_plan_s& p, std::string& error);
+hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t stream);
+
+}  // namespace ponni_hip

@@ -45,22 +45,27 @@ __device__ inline float xor_min(float v) {
   return v;
 }
 
-// acc[mo][n] = sum over input tiles of W^T * src, for output tiles mo < mto.
+// acc[mo][n] += sum over input tiles of W^T * src, for output tiles mo < mto.
+// All A fragments of one output tile are fetched before its MFMAs, so the
+// load latency is paid once per output tile rather than once per fragment.
 template <int MT>
 __device__ inline void dense_tiles(floatx4 (&acc)[MT][kNT], floatx4 const (&src)[MT][kNT],
                                    float const* __restrict__ wp, int mti, int mto, int lane) {
 #pragma unroll
   for (int mo = 0; mo < MT; mo++) {
     if (mo < mto) {
+      floatx4 w[MT];
+#pragma unroll
+      for (int m = 0; m < MT; m++)
+        if (m < mti) w[m] = *reinterpret_cast<floatx4 const*>(wp + ((mo * mti + m) * 64 + lane) * 4);
 #pragma unroll
       for (int m = 0; m < MT; m++) {
         if (m < mti) {
-          floatx4 const w = *reinterpret_cast<floatx4 const*>(wp + ((mo * mti + m) * 64 + lane) * 4);
 #pragma unroll
           for (int v = 0; v < 4; v++)
 #pragma unroll
             for (int n = 0; n < kNT; n++)
-              acc[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[v], src[m][n][v], acc[mo][n], 0, 0, 0);
+              acc[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[m][v], src[m][n][v], acc[mo][n], 0, 0, 0);
         }
       }
     }
@@ -97,16 +102,31 @@ __device__ inline void apply_step_tiles(Step const& sp, float const* __restrict_
   });
 }
 
-template <int MT, int NS>
+// LDS: when the packed parameters fit, each workgroup stages them in LDS once
+// and then loops over column tiles (persistent), so every A fragment, bias and
+// gamma is an LDS read; otherwise they stream from L2.
+template <int MT, int NS, bool LDS>
 __global__ __launch_bounds__(256) void mfma_forward_f32(LaunchArgs a) {
+  extern __shared__ floatx4 lds_params[];
   int const lane = threadIdx.x & 63;
   int const wave = threadIdx.x >> 6;
   int const g = lane >> 4;
   int const c = lane & 15;
-  int64_t const col0 = (int64_t(blockIdx.x) * kWaves + wave) * (16 * kNT);
-  float const* __restrict__ prm = static_cast<float const*>(a.params);
+  float const* __restrict__ prm;
+  if constexpr (LDS) {
+    floatx4 const* src = static_cast<floatx4 const*>(a.params);
+    int const n4 = static_cast<int>((a.param_count + 3) >> 2);
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) lds_params[i] = src[i];
+    __syncthreads();
+    prm = reinterpret_cast<float const*>(lds_params);
+  } else {
+    prm = static_cast<float const*>(a.params);
+  }
   float const* __restrict__ x = static_cast<float const*>(a.x);
   float* __restrict__ y = static_cast<float*>(a.y);
+  int64_t const tiles = (a.batch + kWaves * 16 * kNT - 1) / (kWaves * 16 * kNT);
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+  int64_t const col0 = (tile * kWaves + wave) * (16 * kNT);
 
   floatx4 st[MT][kNT];
   floatx4 sv[NS > 0 ? NS : 1][MT][kNT];
@@ -337,17 +357,40 @@ __global__ __launch_bounds__(256) void mfma_forward_f32(LaunchArgs a) {
       }
     }
   }
+  }  // column tiles
+}
+
+// Largest packed parameter block staged in LDS (two workgroups per CU fit).
+constexpr int64_t kLdsParamBytes = 64 * 1024;
+
+template <int MT, int NS>
+hipError_t launch_ns(LaunchArgs const& a, hipStream_t stream) {
+  int64_t const per_block = int64_t(kWaves) * 16 * kNT;
+  int64_t const tiles = (a.batch + per_block - 1) / per_block;
+  dim3 const block(kWaves * 64);
+  size_t const bytes = static_cast<size_t>((a.param_count + 3) / 4 * 16);
+  if (int64_t(bytes) <= kLdsParamBytes) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mfma_forward_f32<MT, NS, true>, kWaves * 64, bytes);
+    if (e != hipSuccess) return e;
+    int64_t const resident = int64_t(cus) * (per_cu > 0 ? per_cu : 1);
+    dim3 const grid(static_cast<unsigned>(tiles < resident ? tiles : resident));
+    hipLaunchKernelGGL((mfma_forward_f32<MT, NS, true>), grid, block, bytes, stream, a);
+  } else {
+    dim3 const grid(static_cast<unsigned>(tiles));
+    hipLaunchKernelGGL((mfma_forward_f32<MT, NS, false>), grid, block, 0, stream, a);
+  }
+  return hipGetLastError();
 }
 
 template <int MT>
 hipError_t launch(int num_slots, LaunchArgs const& a, hipStream_t stream) {
-  int64_t const per_block = int64_t(kWaves) * 16 * kNT;
-  dim3 const grid(static_cast<unsigned>((a.batch + per_block - 1) / per_block));
-  dim3 const block(kWaves * 64);
-  if (num_slots == 0) hipLaunchKernelGGL((mfma_forward_f32<MT, 0>), grid, block, 0, stream, a);
-  else if (num_slots == 1) hipLaunchKernelGGL((mfma_forward_f32<MT, 1>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((mfma_forward_f32<MT, 2>), grid, block, 0, stream, a);
-  return hipGetLastError();
+  if (num_slots == 0) return launch_ns<MT, 0>(a, stream);
+  if (num_slots == 1) return launch_ns<MT, 1>(a, stream);
+  return launch_ns<MT, 2>(a, stream);
 }
 
 }  // namespace mfma_f32

@@ -12,10 +12,12 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
 
+#include "fused.h"
 #include "host_half.h"
 
 using namespace ponni_hip;
@@ -180,7 +182,8 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
         case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(W) * W + W;
         default: return 0;
       }
-    case PONNI_PATH_MFMA: {
+    case PONNI_PATH_MFMA:
+    case PONNI_PATH_FUSED: {
       auto tiles = [](int n) { return (n + 15) / 16; };
       switch (d.kind) {
         case PONNI_LAYER_MATVEC: return int64_t(tiles(d.n_in)) * tiles(d.n_out) * 256;
@@ -438,7 +441,8 @@ int upload(ponni_plan_s& p) {
     HIP_TRY(hipMemcpy(p.d_steps, p.steps.data(), sizeof(Step) * p.steps.size(), hipMemcpyHostToDevice));
   std::vector<double> packed;
   pack_params(p, packed);
-  size_t const bytes = std::max<size_t>(packed.size() * param_element_size(p), 16);
+  // Rounded up so vector reads of the last packed block stay inside the allocation.
+  size_t const bytes = std::max<size_t>((packed.size() * param_element_size(p) + 255) / 256 * 256, 256);
   if (bytes > p.d_params_bytes) {
     if (p.d_params) HIP_TRY(hipFree(p.d_params));
     p.d_params = nullptr;
@@ -452,6 +456,11 @@ int upload(ponni_plan_s& p) {
       std::vector<float> f(packed.begin(), packed.end());
       HIP_TRY(hipMemcpy(p.d_params, f.data(), f.size() * 4, hipMemcpyHostToDevice));
     }
+  }
+  if (p.path == PONNI_PATH_FUSED && p.fused_fn == nullptr) {
+    std::string error;
+    int const st = fused_prepare(p, error);
+    if (st != PONNI_OK) return fail(st, error);
   }
   p.device_dirty = false;
   return PONNI_OK;
@@ -501,7 +510,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   if (layers == nullptr || num_layers <= 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "a model needs at least one layer");
   if (num_layers > kMaxOps) return fail(PONNI_ERR_INVALID_ARGUMENT, "too many layers (limit 256)");
   if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
-  if (path < PONNI_PATH_AUTO || path > PONNI_PATH_MFMA) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
+  if (path < PONNI_PATH_AUTO || path > PONNI_PATH_FUSED) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
   int const st = validate_chain(layers, num_layers);
   if (st != PONNI_OK) return st;
 
@@ -528,15 +537,24 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
 
   int const narrow = narrow_width_class(max_width);
   int const mfma = mfma_width_class(dtype, max_width);
+  char const* jit_env = std::getenv("PONNI_JIT");
+  bool const jit_enabled = jit_env == nullptr || std::strcmp(jit_env, "0") != 0;
   int chosen = path;
   if (chosen == PONNI_PATH_AUTO) {
-    if (dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    if (dtype != PONNI_F64 && max_width <= 8 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    else if (jit_enabled && fused_supports(*p)) chosen = PONNI_PATH_FUSED;
+    else if (dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
     else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
     else chosen = PONNI_PATH_GENERIC;
   } else if (chosen == PONNI_PATH_NARROW) {
     if (dtype == PONNI_F64 || narrow == 0 || p->num_slots > kNarrowMaxSlots) {
       delete p;
       return fail(PONNI_ERR_UNSUPPORTED, "NARROW path needs F32/F16/BF16, width <= 16 and at most 2 saved states");
+    }
+  } else if (chosen == PONNI_PATH_FUSED) {
+    if (!fused_supports(*p)) {
+      delete p;
+      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs F32, width <= 256 and 16-aligned concatenation");
     }
   } else if (chosen == PONNI_PATH_MFMA) {
     if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {
@@ -667,6 +685,7 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_
   a.num_ops = static_cast<int32_t>(plan->ops.size());
   a.steps = plan->d_steps;
   a.params = plan->d_params;
+  a.param_count = plan->packed_elements;
   a.x = x;
   a.ld_x = ld_in;
   a.y = y;
@@ -686,10 +705,42 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_
   switch (plan->path) {
     case PONNI_PATH_NARROW: err = launch_narrow(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
     case PONNI_PATH_MFMA: err = launch_mfma(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
+    case PONNI_PATH_FUSED: err = fused_launch(*plan, a, stream); break;
     default: err = launch_generic(plan->dtype, a, stream); break;
   }
   if (err != hipSuccess) return fail(PONNI_ERR_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return PONNI_OK;
+}
+
+int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {
+  if (plan == nullptr) {
+    fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+    return -1;
+  }
+  if (plan->path != PONNI_PATH_FUSED) {
+    fail(PONNI_ERR_UNSUPPORTED, "only FUSED plans generate a kernel");
+    return -1;
+  }
+  FusedConfig cfg;
+  std::string const src = fused_source(*plan, cfg);
+  int64_t const need = static_cast<int64_t>(src.size()) + 1;
+  if (buf != nullptr) {
+    if (len < need) {
+      fail(PONNI_ERR_INVALID_ARGUMENT, "buffer too small for the kernel source");
+      return -1;
+    }
+    std::memcpy(buf, src.c_str(), static_cast<size_t>(need));
+  }
+  return need;
+}
+
+int ponni_plan_compile(ponni_plan plan) {
+  if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+  if (plan->path != PONNI_PATH_FUSED) return PONNI_OK;
+  std::string key, error;
+  std::vector<char> code;
+  int const st = fused_compile(*plan, key, code, error);
+  return st == PONNI_OK ? PONNI_OK : fail(st, error);
 }
 
 int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed, uint64_t tag, int32_t dist, double a,

@@ -18,6 +18,7 @@ struct LaunchArgs {
   int32_t num_ops;
   const Step* steps;
   const void* params;
+  int64_t param_count;  // packed parameter elements
   const void* x;
   int64_t ld_x;
   void* y;
@@ -75,4 +76,10 @@ struct ponni_plan_s {
   size_t d_params_bytes = 0;
   void* d_scratch[2 + ponni_hip::kMaxSlots] = {};  // tmp1, tmp2, saved slots
   int64_t capacity = 0;
+
+  // FUSED path: the plan's generated kernel (compiled on first forward).
+  hipFunction_t fused_fn = nullptr;
+  int fused_blocks_per_cu = 1;
+  bool fused_persistent = false;  // grid sized to the resident workgroups
+  int fused_columns_per_block = 128;
 };

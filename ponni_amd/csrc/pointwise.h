@@ -4,7 +4,9 @@
 // rounding.
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
+#endif
 
 #include "program.h"
 

@@ -3,7 +3,13 @@
 // (scalar) control flow.  The record is shared by host and device code.
 #pragma once
 
+#ifdef __HIPCC_RTC__
+using __hip_internal::int32_t;
+using __hip_internal::int64_t;
+using __hip_internal::uint64_t;
+#else
 #include <cstdint>
+#endif
 
 namespace ponni_hip {
 

@@ -19,7 +19,8 @@ import numpy as np
 from . import _abi as A
 
 _DTYPES = {"f32": A.F32, "f64": A.F64, "f16": A.F16, "bf16": A.BF16}
-_PATHS = {"auto": A.PATH_AUTO, "generic": A.PATH_GENERIC, "narrow": A.PATH_NARROW, "mfma": A.PATH_MFMA}
+_PATHS = {"auto": A.PATH_AUTO, "generic": A.PATH_GENERIC, "narrow": A.PATH_NARROW, "mfma": A.PATH_MFMA,
+          "fused": A.PATH_FUSED}
 
 
 @dataclass
@@ -195,6 +196,18 @@ class Inference:
                     raise ValueError(f"{l.label} trainable input too small")
                 self.set_layer_params(i, v[off:off + n])
                 off += n
+
+    # -- generated kernel ---------------------------------------------------------
+    def kernel_source(self) -> str:
+        n = A.lib().ponni_plan_kernel_source(self._plan, None, 0)
+        if n < 0:
+            A.check(A.PONNI_ERR_UNSUPPORTED)
+        buf = ctypes.create_string_buffer(n)
+        A.lib().ponni_plan_kernel_source(self._plan, buf, n)
+        return buf.value.decode()
+
+    def compile(self) -> None:
+        A.check(A.lib().ponni_plan_compile(self._plan))
 
     # -- info -------------------------------------------------------------------
     def info(self) -> A.PlanInfo:

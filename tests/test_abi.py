@@ -68,8 +68,8 @@ def test_plan_info_and_path_selection():
     inf = m.info()
     assert m.path == "narrow" and inf.width_class == 4 and inf.num_fused_dense_blocks == 2
     assert (inf.num_inputs, inf.num_outputs, inf.num_parameters) == (2, 1, 12)
-    assert create(P.configs.CONFIGS["c2"].layers(False)).path == "mfma"
-    assert create(P.configs.CONFIGS["c3"].layers(False)).path == "mfma"
+    assert create(P.configs.CONFIGS["c2"].layers(False)).path == "fused"
+    assert create(P.configs.CONFIGS["c3"].layers(False)).path == "fused"
     assert create([P.Matvec(np.ones((2, 2)))], dtype="f64").path == "generic"
 
 
@@ -246,3 +246,27 @@ def test_ponni_file_layout(tmp_path):
     schema = "ponni-tensor-schema-v1\nparameters\tF32\t3\n"
     assert md["ponni.schema_fingerprint"] == "fnv1a64:%016x" % fnv(schema.encode())
     assert np.array_equal(np.frombuffer(data[8 + n:], dtype="<f4"), vals)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_fused_kernels_compile_on_the_host(seed, tmp_path, monkeypatch):
+    """The generated FUSED kernel of a plan compiles with hipRTC without a GPU."""
+    monkeypatch.setenv("PONNI_JIT_CACHE", str(tmp_path))
+    rng = np.random.default_rng(40 + seed)
+    layers = random_chain(rng, [5, 16, 33, 64][seed], 2)
+    try:
+        m = create(layers, path="fused")
+    except P.PonniError as e:
+        pytest.skip(e.message)
+    src = m.kernel_source()
+    assert "ponni_fused" in src and "dense<" in src
+    m.compile()
+    assert any(f.suffix == ".co" for f in tmp_path.iterdir())
+
+
+def test_fused_config_sources():
+    for name in ["c2", "c3"]:
+        m = create(P.configs.CONFIGS[name].layers(False))
+        assert m.path == "fused"
+        src = m.kernel_source()
+        assert src.count("dense<") == (4 if name == "c2" else 10)

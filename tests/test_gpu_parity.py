@@ -17,7 +17,7 @@ from tests import test_oracle as K
 
 pytestmark = pytest.mark.gpu
 
-PATHS = ["generic", "narrow", "mfma"]
+PATHS = ["generic", "narrow", "mfma", "fused"]
 TORCH_DT = {"f32": "float32", "f16": "float16", "bf16": "bfloat16", "f64": "float64"}
 ORACLE_MODE = {"f32": oracle.MODE_F32, "f64": oracle.MODE_F64, "f16": oracle.MODE_F16_OPERANDS,
                "bf16": oracle.MODE_BF16_OPERANDS}
@@ -123,7 +123,7 @@ def test_random_chains(cuda, seed, path):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("path", ["generic", "narrow", "mfma"])
 def test_reduced_precision_paths(cuda, dtype, path):
     rng = np.random.default_rng(11)
     layers = [P.Matvec(rng.standard_normal((12, 16)) * 0.3), P.Bias(rng.uniform(-0.1, 0.1, 16)), P.Tanh(16),
@@ -154,15 +154,19 @@ def config_input(cfg, B, dev="cuda:0"):
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
-def test_configs_small_batch(cuda, name):
-    """Each BASELINE config (with nonzero biases) on its auto path vs the oracle."""
+@pytest.mark.parametrize("path", ["auto", "mfma"])
+def test_configs_small_batch(cuda, name, path):
+    """Each BASELINE config (with nonzero biases) vs the oracle."""
     import torch
 
     cfg = C.CONFIGS[name]
     layers = cfg.layers(True)
     B = 20_000 + 13
     x = config_input(cfg, B)
-    m = P.create_inference_model(*layers, dtype=cfg.dtype)
+    try:
+        m = P.create_inference_model(*layers, dtype=cfg.dtype, path=path)
+    except P.PonniError as e:
+        pytest.skip(e.message)
     y = m.forward_batch_parallel(x)
     torch.cuda.synchronize()
     xg = x.double().cpu().numpy()
