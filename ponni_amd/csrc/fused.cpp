@@ -134,6 +134,18 @@ bool fused_supports(ponni_plan_s const& p) {
 
 // Generate the HIP source of the plan's kernel.  Offsets are those of the
 // MFMA packing (plan.cpp, pack_params).
+// Kernel symbol: ponni_fused_<in>x..x<out>_<hash of the op list>, so traces name the model.
+std::string fused_kernel_name(ponni_plan_s const& p) {
+  std::string sig((char const*)p.ops.data(), p.ops.size() * sizeof(Op));
+  sig.append((char const*)p.steps.data(), p.steps.size() * sizeof(Step));
+  std::string widths = std::to_string(p.layers.front().n_in);
+  for (Op const& op : p.ops)
+    if (op.code == OP_DENSE) widths += "x" + std::to_string(op.n_out);
+  char buf[16];
+  std::snprintf(buf, sizeof(buf), "%08x", static_cast<unsigned>(fnv(sig) & 0xffffffffu));
+  return "ponni_fused_" + widths + "_" + buf;
+}
+
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
   cfg.lds_bytes = param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
@@ -143,13 +155,14 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   // op holds its input, its output and one output tile's A fragments (4 floats
   // per input tile).  Parameters small enough to live in registers next to
   // that state are loaded once per wave and reused for every column tile.
-  int worst = 0;
+  int worst = 0, worst_saved_regs = 0;
   {
     int cur = tiles(p.layers.front().n_in);
     std::map<int, int> slots;
     for (Op const& op : p.ops) {
       int saved_regs = 0;
       for (auto const& kv : slots) saved_regs += kv.second * 8;
+      worst_saved_regs = std::max(worst_saved_regs, saved_regs);
       int need = cur * 8;
       switch (op.code) {
         case OP_DENSE: need = (tiles(op.n_in) + tiles(op.n_out)) * 8 + tiles(op.n_in) * 4; cur = tiles(op.n_out); break;
@@ -164,9 +177,21 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   int const overhead = 32;
   int64_t const param_regs = (p.packed_elements + 63) / 64;
   cfg.params_in_registers = worst + overhead + param_regs <= 256;
-  int const regs = worst + overhead + (cfg.params_in_registers ? static_cast<int>(param_regs) : 0);
-  cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
+  int regs = worst + overhead + (cfg.params_in_registers ? static_cast<int>(param_regs) : 0);
   if (cfg.params_in_registers) cfg.lds_bytes = 0;
+  // Saved residuals move to LDS when that is what it takes to run two waves
+  // per SIMD (so one wave's VALU epilogue overlaps another's MFMAs).
+  {
+    int saved_tiles = 0;
+    for (int s = 0; s < kMaxSlots; s++) saved_tiles += tiles(p.saved_features[s]);
+    int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 16 * 4;  // per workgroup (4 waves)
+    if (regs + 32 > 256 && worst_saved_regs > 0 && regs - worst_saved_regs <= 224 &&
+        cfg.lds_bytes + saved_bytes <= 80 * 1024) {
+      cfg.saved_in_lds = true;
+      regs -= worst_saved_regs;
+    }
+  }
+  cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
   if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
     int const v = std::atoi(w);
     if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
@@ -175,7 +200,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o << "// generated by libponni_hip for one plan\n";
   o << "#include \"fused_f32.h\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
-  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void ponni_fused(float const* __restrict__ gparams, "
+  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void " << fused_kernel_name(p) << "(float const* __restrict__ gparams, "
        "float const* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy, int64_t batch) {\n";
   if (cfg.lds_bytes > 0) {
     o << "  __shared__ floatx4 lds_p[" << cfg.lds_bytes / 16 << "];\n";
@@ -183,6 +208,17 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "  float const* __restrict__ P0 = reinterpret_cast<float const*>(lds_p);\n";
   } else {
     o << "  float const* __restrict__ P0 = gparams;\n";
+  }
+  std::map<int, int> slot_off;  // slot -> floatx4 offset in the wave's LDS region
+  if (cfg.saved_in_lds) {
+    int off = 0;
+    for (int sl = 0; sl < kMaxSlots; sl++)
+      if (p.saved_features[sl] > 0) {
+        slot_off[sl] = off;
+        off += tiles(p.saved_features[sl]) * 2 * 64;
+      }
+    o << "  __shared__ floatx4 lds_saved[4][" << off << "];\n";
+    o << "  floatx4* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
   }
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
   o << "  int64_t const tiles = (batch + 127) / 128;\n";
@@ -214,12 +250,25 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "    // op code " << op.code << "\n";
     switch (op.code) {
       case OP_DENSE: {
+        // Bias and activations run per output tile inside the contraction.
         std::string const nv = fresh();
-        o << "    auto " << nv << " = dense<" << tiles(op.n_in) << ", " << tiles(op.n_out) << ">(" << cur << ", P + "
-          << op.woff << ", zeros<" << tiles(op.n_out) << ">(), L);\n";
-        epilogue(nv, op.n_out, op.epi_begin, op.epi_count);
+        int const n = op.n_out;
+        bool pad = false;
+        o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
+          << op.woff << ", zeros<" << tiles(n) << ">(), L, [&](int mo, floatx4 (&t)[kNT]) {\n";
+        for (int s = 0; s < op.epi_count; s++) {
+          Step const& st = p.steps[op.epi_begin + s];
+          if (st.act == ACT_BIAS) {
+            o << "      tile_add_rows(t, P + " << st.off << ", mo, L);\n";
+          } else {
+            o << "      tile_map(t, [](float v) { return " << act_expr(st) << "; });\n";
+            if (!zero_at_zero(st.act)) pad = true;
+          }
+        }
+        if (pad && n % 16) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
+        o << "    });\n";
         cur = nv;
-        cur_n = op.n_out;
+        cur_n = n;
         break;
       }
       case OP_POINTWISE:
@@ -241,13 +290,23 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", L);\n";
         break;
       case OP_SAVE: {
-        std::string const sv = "sv" + std::to_string(op.slot) + "_" + std::to_string(var++);
-        o << "    auto " << sv << " = " << cur << ";\n";
-        saved[op.slot] = {sv, cur_n};
+        if (cfg.saved_in_lds) {
+          o << "    save_lds<" << tiles(cur_n) << ">(" << cur << ", SV + " << slot_off[op.slot] << ", L);\n";
+          saved[op.slot] = {"load_lds<" + std::to_string(tiles(cur_n)) + ">(SV + " + std::to_string(slot_off[op.slot]) +
+                                ", L)",
+                            cur_n};
+        } else {
+          std::string const sv = "sv" + std::to_string(op.slot) + "_" + std::to_string(var++);
+          o << "    auto " << sv << " = " << cur << ";\n";
+          saved[op.slot] = {sv, cur_n};
+        }
         break;
       }
       case OP_ADD:
-        o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << saved[op.slot].first << ");\n";
+        if (cfg.saved_in_lds)
+          o << "    add_lds<" << tiles(cur_n) << ">(" << cur << ", SV + " << slot_off[op.slot] << ", L);\n";
+        else
+          o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << saved[op.slot].first << ");\n";
         break;
       case OP_CONCAT: {
         auto const& sv = saved[op.slot];
@@ -353,7 +412,7 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   if (it == g_modules.end()) {
     auto m = std::make_shared<Module>();
     hipError_t e = hipModuleLoadData(&m->module, code.data());
-    if (e == hipSuccess) e = hipModuleGetFunction(&m->fn, m->module, "ponni_fused");
+    if (e == hipSuccess) e = hipModuleGetFunction(&m->fn, m->module, fused_kernel_name(p).c_str());
     if (e == hipSuccess)
       e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&m->blocks_per_cu, m->fn, cfg.waves * 64, 0);
     if (e != hipSuccess) {

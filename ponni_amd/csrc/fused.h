@@ -10,16 +10,19 @@ namespace ponni_hip {
 
 // Packed parameter blocks up to this size are staged in LDS by the kernel.
 constexpr int64_t kFusedLdsParamBytes = 64 * 1024;
+constexpr int kNTColumns = 32;  // batch columns per wave (fused_f32.h kNT * 16)
 
 struct FusedConfig {
   int lds_bytes = 0;          // 0: parameters stream from L2
   int waves = 4;              // waves per workgroup
   int waves_per_simd = 2;     // occupancy the kernel is compiled for
   bool params_in_registers = false;  // parameters loaded once per wave, kept in VGPRs
+  bool saved_in_lds = false;         // Save_State slots kept in LDS, not registers
   int columns_per_block = 128;
 };
 
 bool fused_supports(ponni_plan_s const& p);
+std::string fused_kernel_name(ponni_plan_s const& p);
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg);
 // Compile (or fetch from cache) the plan's kernel; needs no device.
 int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error);

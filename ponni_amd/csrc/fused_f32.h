@@ -49,11 +49,12 @@ __device__ inline float xmin(float v) {
 
 __device__ inline floatx4 ld4(float const* p) { return *reinterpret_cast<floatx4 const*>(p); }
 
-// An opaque copy of a pointer: loads through it cannot be hoisted out of the
-// loop it is taken in.
+// p plus an opaque zero: loads through the result cannot be hoisted out of
+// the loop it is taken in, while p's address space (LDS or global) is kept.
 __device__ inline float const* pin(float const* p) {
-  asm volatile("" : "+s"(p));
-  return p;
+  int z = 0;
+  asm volatile("" : "+s"(z));
+  return p + z;
 }
 
 // x [N, batch] (row stride ld) -> tile; rows >= N and columns >= batch read 0.
@@ -61,15 +62,17 @@ template <int N>
 __device__ inline S<(N + 15) / 16> load_rows(float const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   S<T> s;
+  // Row 16m + e of the lane's row group 4g: a uniform offset from one per-lane pointer.
+  float const* __restrict__ xl = x + int64_t(4 * L.g) * ld + L.col0 + L.c;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
     for (int n = 0; n < kNT; n++) {
-      int64_t const b = L.col0 + 16 * n + L.c;
+      bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         int const f = 16 * m + 4 * L.g + e;
-        s.v[m][n][e] = (f < N && b < L.batch) ? x[int64_t(f) * ld + b] : 0.0f;
+        s.v[m][n][e] = (f < N && col_ok) ? xl[int64_t(16 * m + e) * ld + 16 * n] : 0.0f;
       }
     }
   return s;
@@ -77,15 +80,16 @@ __device__ inline S<(N + 15) / 16> load_rows(float const* __restrict__ x, int64_
 
 template <int N, int T>
 __device__ inline void store_rows(S<T> const& s, float* __restrict__ y, int64_t ld, Lane const& L) {
+  float* __restrict__ yl = y + int64_t(4 * L.g) * ld + L.col0 + L.c;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
     for (int n = 0; n < kNT; n++) {
-      int64_t const b = L.col0 + 16 * n + L.c;
+      bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         int const f = 16 * m + 4 * L.g + e;
-        if (f < N && b < L.batch) y[int64_t(f) * ld + b] = s.v[m][n][e];
+        if (f < N && col_ok) yl[int64_t(16 * m + e) * ld + 16 * n] = s.v[m][n][e];
       }
     }
 }
@@ -97,7 +101,7 @@ __device__ inline S<TO> dense(S<TI> const& in, float const* __restrict__ w, S<TO
   for (int mo = 0; mo < TO; mo++) {
     floatx4 a[TI];
 #pragma unroll
-    for (int m = 0; m < TI; m++) a[m] = ld4(w + ((mo * TI + m) * 64 + L.lane) * 4);
+    for (int m = 0; m < TI; m++) a[m] = ld4(w + (mo * TI + m) * 256 + L.lane * 4);
 #pragma unroll
     for (int m = 0; m < TI; m++)
 #pragma unroll
@@ -107,6 +111,61 @@ __device__ inline S<TO> dense(S<TI> const& in, float const* __restrict__ w, S<TO
           acc.v[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m][e], in.v[m][n][e], acc.v[mo][n], 0, 0, 0);
   }
   return acc;
+}
+
+// The same contraction with the epilogue of output tile mo-1 issued after the
+// MFMAs of tile mo (so its VALU work overlaps the matrix pipe), and the A
+// fragments streamed through a D-deep register ring: fragment i + D is
+// requested while fragment i is consumed.  epi(mo, tile) finishes one output
+// tile in place.
+template <int TI, int TO, int D = 4, class Epi>
+__device__ inline S<TO> dense_ep(S<TI> const& in, float const* __restrict__ w, S<TO> acc, Lane const& L, Epi epi) {
+  constexpr int NF = TI * TO;
+  constexpr int R = D < NF ? D : NF;
+  floatx4 ring[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) ring[i] = ld4(w + i * 256 + L.lane * 4);
+#pragma unroll
+  for (int mo = 0; mo < TO; mo++) {
+#pragma unroll
+    for (int m = 0; m < TI; m++) {
+      int const i = mo * TI + m;
+      floatx4 const a = ring[i % R];
+      if (i + R < NF) ring[i % R] = ld4(w + (i + R) * 256 + L.lane * 4);
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int n = 0; n < kNT; n++)
+          acc.v[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], in.v[m][n][e], acc.v[mo][n], 0, 0, 0);
+    }
+    if (mo > 0) epi(mo - 1, acc.v[mo - 1]);
+  }
+  epi(TO - 1, acc.v[TO - 1]);
+  return acc;
+}
+
+// Per-tile epilogue helpers (tile = one 16-feature row block, kNT columns).
+__device__ inline void tile_add_rows(floatx4 (&t)[kNT], float const* __restrict__ b, int mo, Lane const& L) {
+  floatx4 const bb = ld4(b + 16 * mo + 4 * L.g);
+#pragma unroll
+  for (int n = 0; n < kNT; n++) t[n] += bb;
+}
+
+template <class F>
+__device__ inline void tile_map(floatx4 (&t)[kNT], F f) {
+#pragma unroll
+  for (int n = 0; n < kNT; n++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) t[n][e] = f(t[n][e]);
+}
+
+template <int N>
+__device__ inline void tile_zero_pad(floatx4 (&t)[kNT], int mo, Lane const& L) {
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    if (16 * mo + 4 * L.g + e >= N)
+#pragma unroll
+      for (int n = 0; n < kNT; n++) t[n][e] = 0.0f;
 }
 
 template <int T>
@@ -280,6 +339,34 @@ __device__ inline S<T2> widen(S<T> const& s) {
 #pragma unroll
     for (int n = 0; n < kNT; n++) o.v[m][n] = s.v[m][n];
   return o;
+}
+
+// Saved residual states may live in LDS instead of registers (one region per
+// wave, lane-contiguous 16-byte chunks, so accesses are bank-conflict free).
+template <int T>
+__device__ inline void save_lds(S<T> const& s, floatx4* __restrict__ slot, Lane const& L) {
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < kNT; n++) slot[(m * kNT + n) * 64 + L.lane] = s.v[m][n];
+}
+
+template <int T>
+__device__ inline S<T> load_lds(floatx4 const* __restrict__ slot, Lane const& L) {
+  S<T> s;
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < kNT; n++) s.v[m][n] = slot[(m * kNT + n) * 64 + L.lane];
+  return s;
+}
+
+template <int T>
+__device__ inline void add_lds(S<T>& s, floatx4 const* __restrict__ slot, Lane const& L) {
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < kNT; n++) s.v[m][n] += slot[(m * kNT + n) * 64 + L.lane];
 }
 
 // Stage `count` floats (a multiple of 4) of packed parameters into LDS.

@@ -259,7 +259,7 @@ def test_fused_kernels_compile_on_the_host(seed, tmp_path, monkeypatch):
     except P.PonniError as e:
         pytest.skip(e.message)
     src = m.kernel_source()
-    assert "ponni_fused" in src and "dense<" in src
+    assert "ponni_fused_" in src and "dense" in src
     m.compile()
     assert any(f.suffix == ".co" for f in tmp_path.iterdir())
 
@@ -269,4 +269,4 @@ def test_fused_config_sources():
         m = create(P.configs.CONFIGS[name].layers(False))
         assert m.path == "fused"
         src = m.kernel_source()
-        assert src.count("dense<") == (4 if name == "c2" else 10)
+        assert src.count("dense_ep<") == (4 if name == "c2" else 10)
