@@ -121,7 +121,7 @@ bool compile(std::string const& source, std::vector<char>& code, std::string& lo
 
 // Can the FUSED generator express this chain?
 bool fused_supports(ponni_plan_s const& p) {
-  if (p.dtype != PONNI_F32) return false;
+  if (p.dtype == PONNI_F64) return false;
   if (p.max_width > 256) return false;
   for (auto const& d : p.layers) {
     if (d.kind == PONNI_LAYER_BINOP_CONCATENATE) {
@@ -147,14 +147,17 @@ std::string fused_kernel_name(ponni_plan_s const& p) {
 }
 
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
+  bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
+  std::string const E = p.dtype == PONNI_BF16 ? "__bf16" : "_Float16";
+  int const NT = half ? 4 : 2;  // 16-column tiles per wave
   int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
-  cfg.lds_bytes = param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
+  cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   cfg.waves = 4;
-  cfg.columns_per_block = 4 * 32;
-  // Register budget.  Every live tile holds 4 * kNT floats per lane; a dense
-  // op holds its input, its output and one output tile's A fragments (4 floats
-  // per input tile).  Parameters small enough to live in registers next to
-  // that state are loaded once per wave and reused for every column tile.
+  cfg.columns_per_block = 4 * 16 * NT;
+  // Register budget.  A live tile holds 8 registers per lane (fp32 with 2
+  // column tiles, or 16-bit with 4); a dense op holds its input, its output
+  // and its A-fragment ring.  Parameters small enough to live in registers
+  // next to that state are loaded once per wave and reused for every tile.
   int worst = 0, worst_saved_regs = 0;
   {
     int cur = tiles(p.layers.front().n_in);
@@ -165,23 +168,26 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       worst_saved_regs = std::max(worst_saved_regs, saved_regs);
       int need = cur * 8;
       switch (op.code) {
-        case OP_DENSE: need = (tiles(op.n_in) + tiles(op.n_out)) * 8 + tiles(op.n_in) * 4; cur = tiles(op.n_out); break;
+        case OP_DENSE:
+          need = (tiles(op.n_in) + tiles(op.n_out)) * 8 + (half ? 16 + 2 * NT * 4 : tiles(op.n_in) * 4);
+          cur = tiles(op.n_out);
+          break;
         case OP_PROJ_ADD: need = (cur + 2 * tiles(op.n_out)) * 8 + tiles(op.aux) * 4; break;
         case OP_CONCAT: need = 2 * tiles(op.n_out) * 8; cur = tiles(op.n_out); break;
         case OP_SAVE: slots[op.slot] = cur; break;
-        default: break;
+        default: need = half ? cur * 16 : cur * 8; break;  // 16-bit states widen to fp32 for barriers
       }
       worst = std::max(worst, need + saved_regs);
     }
   }
   int const overhead = 32;
   int64_t const param_regs = (p.packed_elements + 63) / 64;
-  cfg.params_in_registers = worst + overhead + param_regs <= 256;
+  cfg.params_in_registers = !half && worst + overhead + param_regs <= 256;
   int regs = worst + overhead + (cfg.params_in_registers ? static_cast<int>(param_regs) : 0);
   if (cfg.params_in_registers) cfg.lds_bytes = 0;
   // Saved residuals move to LDS when that is what it takes to run two waves
   // per SIMD (so one wave's VALU epilogue overlaps another's MFMAs).
-  {
+  if (!half) {
     int saved_tiles = 0;
     for (int s = 0; s < kMaxSlots; s++) saved_tiles += tiles(p.saved_features[s]);
     int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 16 * 4;  // per workgroup (4 waves)
@@ -196,12 +202,16 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(w);
     if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
   }
+
   std::ostringstream o;
+  std::string const IO = half ? E : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
-  o << "#include \"fused_f32.h\"\n";
+  o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
-  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void " << fused_kernel_name(p) << "(float const* __restrict__ gparams, "
-       "float const* __restrict__ x, int64_t ldx, float* __restrict__ y, int64_t ldy, int64_t batch) {\n";
+  if (half) o << "typedef " << E << " E;\n";
+  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void " << fused_kernel_name(p)
+    << "(float const* __restrict__ gparams, " << IO << " const* __restrict__ x, int64_t ldx, " << IO
+    << "* __restrict__ y, int64_t ldy, int64_t batch) {\n";
   if (cfg.lds_bytes > 0) {
     o << "  __shared__ floatx4 lds_p[" << cfg.lds_bytes / 16 << "];\n";
     o << "  stage(lds_p, gparams, " << cfg.lds_bytes / 4 << ");\n";
@@ -215,15 +225,15 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     for (int sl = 0; sl < kMaxSlots; sl++)
       if (p.saved_features[sl] > 0) {
         slot_off[sl] = off;
-        off += tiles(p.saved_features[sl]) * 2 * 64;
+        off += tiles(p.saved_features[sl]) * NT * 64;
       }
     o << "  __shared__ floatx4 lds_saved[4][" << off << "];\n";
     o << "  floatx4* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
   }
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
-  o << "  int64_t const tiles = (batch + 127) / 128;\n";
+  o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
-  o << "    L.col0 = (tile * 4 + (threadIdx.x >> 6)) * 32;\n";
+  o << "    L.col0 = (tile * 4 + (threadIdx.x >> 6)) * " << 16 * NT << ";\n";
   // Register-resident parameters may be hoisted out of the tile loop; otherwise
   // pin() hides the pointer's loop invariance so they are re-read per tile.
   o << (cfg.params_in_registers ? "    float const* __restrict__ P = P0;\n" : "    float const* __restrict__ P = pin(P0);\n");
@@ -231,8 +241,22 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   auto fresh = [&]() { return "s" + std::to_string(var++); };
   std::string cur = fresh();
   int cur_n = p.layers.front().n_in;
-  o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
-  std::map<int, std::pair<std::string, int>> saved;  // slot -> (variable, width)
+  if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
+  else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
+  std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
+  auto act = [&](Step const& st) {
+    return half && st.act == ACT_TANH ? std::string("act_tanh_fast(v)") : act_expr(st);
+  };
+  // fp32 view of the state for barrier ops: the state itself (fp32 path) or a
+  // widened copy that is rounded back afterwards (16-bit path).
+  auto open32 = [&]() -> std::string {
+    if (!half) return cur;
+    o << "    {\n    auto f = to_f32(" << cur << ");\n";
+    return "f";
+  };
+  auto close32 = [&]() {
+    if (half) o << "    " << cur << " = to_h<E>(f);\n    }\n";
+  };
   auto epilogue = [&](std::string const& v, int n, int begin, int count) {
     bool pad = false;
     for (int s = 0; s < count; s++) {
@@ -240,7 +264,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       if (st.act == ACT_BIAS) {
         o << "    add_rows<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L);\n";
       } else {
-        o << "    map<" << tiles(n) << ">(" << v << ", [](float v) { return " << act_expr(st) << "; });\n";
+        o << "    map<" << tiles(n) << ">(" << v << ", [](float v) { return " << act(st) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
       }
     }
@@ -254,14 +278,18 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         std::string const nv = fresh();
         int const n = op.n_out;
         bool pad = false;
-        o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
-          << op.woff << ", zeros<" << tiles(n) << ">(), L, [&](int mo, floatx4 (&t)[kNT]) {\n";
+        if (half)
+          o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
+            << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
+        else
+          o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
+            << op.woff << ", zeros<" << tiles(n) << ">(), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
         for (int s = 0; s < op.epi_count; s++) {
           Step const& st = p.steps[op.epi_begin + s];
           if (st.act == ACT_BIAS) {
             o << "      tile_add_rows(t, P + " << st.off << ", mo, L);\n";
           } else {
-            o << "      tile_map(t, [](float v) { return " << act_expr(st) << "; });\n";
+            o << "      tile_map(t, [](float v) { return " << act(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
@@ -271,24 +299,35 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         cur_n = n;
         break;
       }
-      case OP_POINTWISE:
-        epilogue(cur, cur_n, op.epi_begin, op.epi_count);
+      case OP_POINTWISE: {
+        std::string const f = open32();
+        epilogue(f, cur_n, op.epi_begin, op.epi_count);
+        close32();
         break;
-      case OP_LAYER_NORM:
-        o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", P + " << op.woff << ", P + "
+      }
+      case OP_LAYER_NORM: {
+        std::string const f = open32();
+        o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", P + " << op.woff << ", P + "
           << op.boff << ", " << flit(op.f0) << ", L);\n";
+        close32();
         break;
+      }
       case OP_SOFTMAX:
-      case OP_LOG_SOFTMAX:
-        o << "    softmax<" << cur_n << ", " << tiles(cur_n) << ", " << (op.code == OP_LOG_SOFTMAX ? "true" : "false")
-          << ">(" << cur << ", L);\n";
-        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", L);\n";
+      case OP_LOG_SOFTMAX: {
+        std::string const f = open32();
+        o << "    softmax<" << cur_n << ", " << (op.code == OP_LOG_SOFTMAX ? "true" : "false") << ">(" << f << ", L);\n";
+        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", L);\n";
+        close32();
         break;
-      case OP_MIN_MAX:
-        o << "    min_max<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", " << flit(op.f0) << ", "
+      }
+      case OP_MIN_MAX: {
+        std::string const f = open32();
+        o << "    min_max<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", " << flit(op.f0) << ", "
           << flit(op.f1) << ", " << flit(op.f2) << ", L);\n";
-        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << cur << ", L);\n";
+        if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", L);\n";
+        close32();
         break;
+      }
       case OP_SAVE: {
         if (cfg.saved_in_lds) {
           o << "    save_lds<" << tiles(cur_n) << ">(" << cur << ", SV + " << slot_off[op.slot] << ", L);\n";
@@ -303,20 +342,26 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         break;
       }
       case OP_ADD:
-        if (cfg.saved_in_lds)
+        if (cfg.saved_in_lds) {
           o << "    add_lds<" << tiles(cur_n) << ">(" << cur << ", SV + " << slot_off[op.slot] << ", L);\n";
-        else
-          o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << saved[op.slot].first << ");\n";
+        } else if (half) {
+          std::string const f = open32();
+          o << "    add(" << f << ", to_f32(" << saved[op.slot].first << "));\n";
+          close32();
+        } else {
+          o << "    add(" << cur << ", " << saved[op.slot].first << ");\n";
+        }
         break;
       case OP_CONCAT: {
         auto const& sv = saved[op.slot];
         std::string const nv = fresh();
+        std::string const fn = half ? "concat_h" : "concat";
         if (op.aux)
-          o << "    auto " << nv << " = concat<" << tiles(cur_n) << ", " << tiles(sv.second) << ">(" << cur << ", "
-            << sv.first << ");\n";
+          o << "    auto " << nv << " = " << fn << "<" << tiles(cur_n) << ", " << tiles(sv.second) << ">(" << cur
+            << ", " << sv.first << ");\n";
         else
-          o << "    auto " << nv << " = concat<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
-            << ", " << cur << ");\n";
+          o << "    auto " << nv << " = " << fn << "<" << tiles(sv.second) << ", " << tiles(cur_n) << ">("
+            << sv.first << ", " << cur << ");\n";
         cur = nv;
         cur_n = op.n_out;
         break;
@@ -324,19 +369,25 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       case OP_PROJ_ADD: {
         // proj = b + W^T saved (bias first, ponni_Binop_Projection_Add.h:91-92); out = in + proj.
         auto const& sv = saved[op.slot];
-        std::string const b = fresh(), nv = fresh();
-        o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
-        o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", P + " << op.boff << ", L);\n";
-        o << "    auto " << nv << " = dense<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
-          << ", P + " << op.woff << ", " << b << ", L);\n";
-        o << "    add<" << tiles(cur_n) << ">(" << cur << ", " << nv << ");\n";
+        if (half) {
+          o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << cur << ", " << sv.first
+            << ", reinterpret_cast<E const*>(P + " << op.woff << "), P + " << op.boff << ", L);\n";
+        } else {
+          std::string const b = fresh(), nv = fresh();
+          o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
+          o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", P + " << op.boff << ", L);\n";
+          o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
+            << ", P + " << op.woff << ", " << b << ", L, [](int, floatx4 (&)[" << NT << "]) {});\n";
+          o << "    add(" << cur << ", " << nv << ");\n";
+        }
         break;
       }
       default:
         break;
     }
   }
-  o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";
   return o.str();
 }

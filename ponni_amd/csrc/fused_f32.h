@@ -1,12 +1,12 @@
-// Device template library of the FUSED path (fp32): the building blocks that
+// Device template library of the FUSED path: the building blocks that
 // per-plan generated kernels call with every width a compile-time constant.
 // It is compiled at run time by hipRTC together with the generated kernel
-// (see codegen.cpp), so the compiler sees a straight-line op sequence with
+// (see fused.cpp), so the compiler sees a straight-line op sequence with
 // exact tile counts and no runtime guards.
 //
-// Register tile layout (one wave, kNT*16 batch columns):
-//   S<T>::v[m][n][e] (lane l, g = l/16, c = l%16) <-> feature 16m + 4g + e,
-//                                                   column  col0 + 16n + c,
+// fp32 register tile layout (one wave, NT*16 batch columns):
+//   S<T,NT>::v[m][n][e] (lane l, g = l/16, c = l%16) <-> feature 16m + 4g + e,
+//                                                      column  col0 + 16n + c,
 // which is the D layout of v_mfma_f32_16x16x4f32, and -- contracting the
 // feature set {16m + 4k + e : k = 0..3} -- also its B layout, so a dense
 // layer feeds the next one straight from registers.  Dense weights arrive
@@ -21,11 +21,11 @@ namespace fused {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kNT = 2;  // 16-column tiles per wave
+constexpr int kNT = 2;  // default 16-column tiles per wave (fp32 path)
 
-template <int T>
+template <int T, int NT = kNT>
 struct S {
-  floatx4 v[T > 0 ? T : 1][kNT];
+  floatx4 v[T > 0 ? T : 1][NT];
 };
 
 struct Lane {
@@ -51,23 +51,24 @@ __device__ inline floatx4 ld4(float const* p) { return *reinterpret_cast<floatx4
 
 // p plus an opaque zero: loads through the result cannot be hoisted out of
 // the loop it is taken in, while p's address space (LDS or global) is kept.
-__device__ inline float const* pin(float const* p) {
+template <class P>
+__device__ inline P const* pin(P const* p) {
   int z = 0;
   asm volatile("" : "+s"(z));
   return p + z;
 }
 
 // x [N, batch] (row stride ld) -> tile; rows >= N and columns >= batch read 0.
-template <int N>
-__device__ inline S<(N + 15) / 16> load_rows(float const* __restrict__ x, int64_t ld, Lane const& L) {
+template <int N, int NT = kNT>
+__device__ inline S<(N + 15) / 16, NT> load_rows(float const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
-  S<T> s;
+  S<T, NT> s;
   // Row 16m + e of the lane's row group 4g: a uniform offset from one per-lane pointer.
   float const* __restrict__ xl = x + int64_t(4 * L.g) * ld + L.col0 + L.c;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) {
+    for (int n = 0; n < NT; n++) {
       bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -78,13 +79,13 @@ __device__ inline S<(N + 15) / 16> load_rows(float const* __restrict__ x, int64_
   return s;
 }
 
-template <int N, int T>
-__device__ inline void store_rows(S<T> const& s, float* __restrict__ y, int64_t ld, Lane const& L) {
+template <int N, int T, int NT>
+__device__ inline void store_rows(S<T, NT> const& s, float* __restrict__ y, int64_t ld, Lane const& L) {
   float* __restrict__ yl = y + int64_t(4 * L.g) * ld + L.col0 + L.c;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) {
+    for (int n = 0; n < NT; n++) {
       bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -94,32 +95,24 @@ __device__ inline void store_rows(S<T> const& s, float* __restrict__ y, int64_t 
     }
 }
 
-// out = C + W^T in over TI input tiles and TO output tiles.
-template <int TI, int TO>
-__device__ inline S<TO> dense(S<TI> const& in, float const* __restrict__ w, S<TO> acc, Lane const& L) {
+template <int T, int NT = kNT>
+__device__ inline S<T, NT> zeros() {
+  S<T, NT> s;
 #pragma unroll
-  for (int mo = 0; mo < TO; mo++) {
-    floatx4 a[TI];
+  for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int m = 0; m < TI; m++) a[m] = ld4(w + (mo * TI + m) * 256 + L.lane * 4);
-#pragma unroll
-    for (int m = 0; m < TI; m++)
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-#pragma unroll
-        for (int n = 0; n < kNT; n++)
-          acc.v[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m][e], in.v[m][n][e], acc.v[mo][n], 0, 0, 0);
-  }
-  return acc;
+    for (int n = 0; n < NT; n++) s.v[m][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  return s;
 }
 
-// The same contraction with the epilogue of output tile mo-1 issued after the
-// MFMAs of tile mo (so its VALU work overlaps the matrix pipe), and the A
-// fragments streamed through a D-deep register ring: fragment i + D is
-// requested while fragment i is consumed.  epi(mo, tile) finishes one output
-// tile in place.
-template <int TI, int TO, int D = 4, class Epi>
-__device__ inline S<TO> dense_ep(S<TI> const& in, float const* __restrict__ w, S<TO> acc, Lane const& L, Epi epi) {
+// out = C + W^T in over TI input tiles and TO output tiles, with the
+// epilogue of output tile mo-1 issued after the MFMAs of tile mo (so its VALU
+// work overlaps the matrix pipe) and the A fragments streamed through an
+// R-deep register ring: fragment i + R is requested while fragment i is
+// consumed.  epi(mo, tile) finishes one output tile in place.
+template <int TI, int TO, int NT, class Epi, int D = 4>
+__device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, float const* __restrict__ w, S<TO, NT> acc,
+                                     Lane const& L, Epi epi) {
   constexpr int NF = TI * TO;
   constexpr int R = D < NF ? D : NF;
   floatx4 ring[R];
@@ -135,7 +128,7 @@ __device__ inline S<TO> dense_ep(S<TI> const& in, float const* __restrict__ w, S
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
-        for (int n = 0; n < kNT; n++)
+        for (int n = 0; n < NT; n++)
           acc.v[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], in.v[m][n][e], acc.v[mo][n], 0, 0, 0);
     }
     if (mo > 0) epi(mo - 1, acc.v[mo - 1]);
@@ -144,64 +137,55 @@ __device__ inline S<TO> dense_ep(S<TI> const& in, float const* __restrict__ w, S
   return acc;
 }
 
-// Per-tile epilogue helpers (tile = one 16-feature row block, kNT columns).
-__device__ inline void tile_add_rows(floatx4 (&t)[kNT], float const* __restrict__ b, int mo, Lane const& L) {
+// Per-tile epilogue helpers (tile = one 16-feature row block, NT columns).
+template <int NT>
+__device__ inline void tile_add_rows(floatx4 (&t)[NT], float const* __restrict__ b, int mo, Lane const& L) {
   floatx4 const bb = ld4(b + 16 * mo + 4 * L.g);
 #pragma unroll
-  for (int n = 0; n < kNT; n++) t[n] += bb;
+  for (int n = 0; n < NT; n++) t[n] += bb;
 }
 
-template <class F>
-__device__ inline void tile_map(floatx4 (&t)[kNT], F f) {
+template <int NT, class F>
+__device__ inline void tile_map(floatx4 (&t)[NT], F f) {
 #pragma unroll
-  for (int n = 0; n < kNT; n++)
+  for (int n = 0; n < NT; n++)
 #pragma unroll
     for (int e = 0; e < 4; e++) t[n][e] = f(t[n][e]);
 }
 
-template <int N>
-__device__ inline void tile_zero_pad(floatx4 (&t)[kNT], int mo, Lane const& L) {
+template <int N, int NT>
+__device__ inline void tile_zero_pad(floatx4 (&t)[NT], int mo, Lane const& L) {
 #pragma unroll
   for (int e = 0; e < 4; e++)
     if (16 * mo + 4 * L.g + e >= N)
 #pragma unroll
-      for (int n = 0; n < kNT; n++) t[n][e] = 0.0f;
+      for (int n = 0; n < NT; n++) t[n][e] = 0.0f;
 }
 
-template <int T>
-__device__ inline S<T> zeros() {
-  S<T> s;
-#pragma unroll
-  for (int m = 0; m < T; m++)
-#pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  return s;
-}
-
-// Per-feature vector (bias, gamma, beta) padded to 16*T, as a tile-shaped constant.
-template <int T>
-__device__ inline void add_rows(S<T>& s, float const* __restrict__ b, Lane const& L) {
+// Per-feature vector (bias, gamma, beta) padded to 16*T.
+template <int T, int NT>
+__device__ inline void add_rows(S<T, NT>& s, float const* __restrict__ b, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++) {
     floatx4 const bb = ld4(b + 16 * m + 4 * L.g);
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] += bb;
+    for (int n = 0; n < NT; n++) s.v[m][n] += bb;
   }
 }
 
-template <int T, class F>
-__device__ inline void map(S<T>& s, F f) {
+template <int T, int NT, class F>
+__device__ inline void map(S<T, NT>& s, F f) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++)
+    for (int n = 0; n < NT; n++)
 #pragma unroll
       for (int e = 0; e < 4; e++) s.v[m][n][e] = f(s.v[m][n][e]);
 }
 
 // Rows >= N return to exactly zero (they are K padding of the next layer).
-template <int N, int T>
-__device__ inline void zero_pad(S<T>& s, Lane const& L) {
+template <int N, int T, int NT>
+__device__ inline void zero_pad(S<T, NT>& s, Lane const& L) {
   if constexpr (N < 16 * T) {
 #pragma unroll
     for (int m = N / 16; m < T; m++)
@@ -209,24 +193,24 @@ __device__ inline void zero_pad(S<T>& s, Lane const& L) {
       for (int e = 0; e < 4; e++)
         if (16 * m + 4 * L.g + e >= N)
 #pragma unroll
-          for (int n = 0; n < kNT; n++) s.v[m][n][e] = 0.0f;
+          for (int n = 0; n < NT; n++) s.v[m][n][e] = 0.0f;
   }
 }
 
-template <int T>
-__device__ inline void add(S<T>& s, S<T> const& o) {
+template <int T, int NT>
+__device__ inline void add(S<T, NT>& s, S<T, NT> const& o) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] += o.v[m][n];
+    for (int n = 0; n < NT; n++) s.v[m][n] += o.v[m][n];
 }
 
 // Two-pass LayerNorm over N features, ponni_LayerNorm.h:82-98.
-template <int N, int T>
-__device__ inline void layer_norm(S<T>& s, float const* __restrict__ gamma, float const* __restrict__ beta, float eps,
-                                  Lane const& L) {
+template <int N, int T, int NT>
+__device__ inline void layer_norm(S<T, NT>& s, float const* __restrict__ gamma, float const* __restrict__ beta,
+                                  float eps, Lane const& L) {
 #pragma unroll
-  for (int n = 0; n < kNT; n++) {
+  for (int n = 0; n < NT; n++) {
     float sum = 0.0f;
 #pragma unroll
     for (int m = 0; m < T; m++)
@@ -255,10 +239,10 @@ __device__ inline void layer_norm(S<T>& s, float const* __restrict__ gamma, floa
 }
 
 // Softmax / LogSoftmax over N features, ponni_Softmax.h:45-56, ponni_LogSoftmax.h:45-57.
-template <int N, int T, bool LOG>
-__device__ inline void softmax(S<T>& s, Lane const& L) {
+template <int N, bool LOG, int T, int NT>
+__device__ inline void softmax(S<T, NT>& s, Lane const& L) {
 #pragma unroll
-  for (int n = 0; n < kNT; n++) {
+  for (int n = 0; n < NT; n++) {
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int m = 0; m < T; m++)
@@ -292,10 +276,10 @@ __device__ inline void softmax(S<T>& s, Lane const& L) {
 }
 
 // MinMaxNorm over N features, ponni_MinMaxNorm.h:67-84.
-template <int N, int T>
-__device__ inline void min_max(S<T>& s, float out_min, float out_max, float eps, Lane const& L) {
+template <int N, int T, int NT>
+__device__ inline void min_max(S<T, NT>& s, float out_min, float out_max, float eps, Lane const& L) {
 #pragma unroll
-  for (int n = 0; n < kNT; n++) {
+  for (int n = 0; n < NT; n++) {
     float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
 #pragma unroll
     for (int m = 0; m < T; m++)
@@ -316,57 +300,46 @@ __device__ inline void min_max(S<T>& s, float out_min, float out_max, float eps,
 }
 
 // [a; b] for tile-aligned operands.
-template <int TA, int TB>
-__device__ inline S<TA + TB> concat(S<TA> const& a, S<TB> const& b) {
-  S<TA + TB> s;
+template <int TA, int TB, int NT>
+__device__ inline S<TA + TB, NT> concat(S<TA, NT> const& a, S<TB, NT> const& b) {
+  S<TA + TB, NT> s;
 #pragma unroll
   for (int m = 0; m < TA; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] = a.v[m][n];
+    for (int n = 0; n < NT; n++) s.v[m][n] = a.v[m][n];
 #pragma unroll
   for (int m = 0; m < TB; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[TA + m][n] = b.v[m][n];
+    for (int n = 0; n < NT; n++) s.v[TA + m][n] = b.v[m][n];
   return s;
-}
-
-// Resize a tile to T2 tiles (extra tiles are zero).
-template <int T2, int T>
-__device__ inline S<T2> widen(S<T> const& s) {
-  S<T2> o = zeros<T2>();
-#pragma unroll
-  for (int m = 0; m < (T < T2 ? T : T2); m++)
-#pragma unroll
-    for (int n = 0; n < kNT; n++) o.v[m][n] = s.v[m][n];
-  return o;
 }
 
 // Saved residual states may live in LDS instead of registers (one region per
 // wave, lane-contiguous 16-byte chunks, so accesses are bank-conflict free).
-template <int T>
-__device__ inline void save_lds(S<T> const& s, floatx4* __restrict__ slot, Lane const& L) {
+template <int T, int NT>
+__device__ inline void save_lds(S<T, NT> const& s, floatx4* __restrict__ slot, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) slot[(m * kNT + n) * 64 + L.lane] = s.v[m][n];
+    for (int n = 0; n < NT; n++) slot[(m * NT + n) * 64 + L.lane] = s.v[m][n];
 }
 
-template <int T>
-__device__ inline S<T> load_lds(floatx4 const* __restrict__ slot, Lane const& L) {
-  S<T> s;
+template <int T, int NT = kNT>
+__device__ inline S<T, NT> load_lds(floatx4 const* __restrict__ slot, Lane const& L) {
+  S<T, NT> s;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] = slot[(m * kNT + n) * 64 + L.lane];
+    for (int n = 0; n < NT; n++) s.v[m][n] = slot[(m * NT + n) * 64 + L.lane];
   return s;
 }
 
-template <int T>
-__device__ inline void add_lds(S<T>& s, floatx4 const* __restrict__ slot, Lane const& L) {
+template <int T, int NT>
+__device__ inline void add_lds(S<T, NT>& s, floatx4 const* __restrict__ slot, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < kNT; n++) s.v[m][n] += slot[(m * kNT + n) * 64 + L.lane];
+    for (int n = 0; n < NT; n++) s.v[m][n] += slot[(m * NT + n) * 64 + L.lane];
 }
 
 // Stage `count` floats (a multiple of 4) of packed parameters into LDS.

@@ -185,6 +185,19 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
     case PONNI_PATH_MFMA:
     case PONNI_PATH_FUSED: {
       auto tiles = [](int n) { return (n + 15) / 16; };
+      if (p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16)) {
+        // Dense blocks: one 1 KB fragment (256 four-byte units) per output tile
+        // and 32-feature step; vectors stay fp32.
+        auto steps = [&](int n) { return (tiles(n) + 1) / 2; };
+        switch (d.kind) {
+          case PONNI_LAYER_MATVEC: return int64_t(steps(d.n_in)) * tiles(d.n_out) * 256;
+          case PONNI_LAYER_BIAS: return round_up(d.n_in, 16);
+          case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
+          case PONNI_LAYER_BINOP_PROJECTION_ADD:
+            return int64_t(steps(d.n_aux)) * tiles(d.n_in) * 256 + round_up(d.n_in, 16);
+          default: return 0;
+        }
+      }
       switch (d.kind) {
         case PONNI_LAYER_MATVEC: return int64_t(tiles(d.n_in)) * tiles(d.n_out) * 256;
         case PONNI_LAYER_BIAS: return round_up(d.n_in, 16);
@@ -404,6 +417,63 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
   }
 }
 
+// Parameters of FUSED fp16 / bf16 plans as 32-bit words: dense blocks hold
+// pairs of 16-bit operands in the v_mfma_f32_16x16x32 A-fragment order (see
+// fused_f16.h), vectors hold fp32 values already rounded to the operand type.
+void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
+  out.assign(static_cast<size_t>(p.packed_elements), 0u);
+  auto bits16 = [&](double v) -> uint16_t {
+    float const f = static_cast<float>(v);
+    return p.dtype == PONNI_F16 ? float_to_half_bits(f) : float_to_bf16_bits(f);
+  };
+  auto fbits = [&](double v) {
+    float const f = static_cast<float>(round_to_dtype(v, p.dtype));
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+  };
+  auto pack_dense = [&](double const* w, int K, int N, uint32_t* o) {
+    int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
+    auto* h = reinterpret_cast<uint16_t*>(o);
+    for (int mo = 0; mo < TN; mo++)
+      for (int t = 0; t < TS; t++)
+        for (int l = 0; l < 64; l++)
+          for (int j = 0; j < 8; j++) {
+            int const k = 16 * (2 * t + j / 4) + 4 * (l >> 4) + (j & 3);
+            int const n = 16 * mo + (l & 15);
+            h[((int64_t(mo) * TS + t) * 64 + l) * 8 + j] = (k < K && n < N) ? bits16(w[int64_t(k) * N + n]) : 0;
+          }
+  };
+  int const L = static_cast<int>(p.layers.size());
+  for (int i = 0; i < L; i++) {
+    ponni_layer_desc const& d = p.layers[i];
+    std::vector<double> const& src = p.params[i];
+    uint32_t* dst = out.data() + p.layer_param_offset[i];
+    switch (d.kind) {
+      case PONNI_LAYER_MATVEC: pack_dense(src.data(), d.n_in, d.n_out, dst); break;
+      case PONNI_LAYER_BIAS:
+        for (int f = 0; f < d.n_in; f++) dst[f] = fbits(src[f]);
+        break;
+      case PONNI_LAYER_LAYER_NORM: {
+        int64_t const stride = packed_size(p, d) / 2;
+        for (int f = 0; f < d.n_in; f++) {
+          dst[f] = fbits(src[f]);
+          dst[stride + f] = fbits(src[d.n_in + f]);
+        }
+        break;
+      }
+      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
+        int64_t const wsize = packed_size(p, d) - round_up(d.n_in, 16);
+        pack_dense(src.data(), d.n_aux, d.n_in, dst);
+        for (int f = 0; f < d.n_in; f++) dst[wsize + f] = fbits(src[int64_t(d.n_aux) * d.n_in + f]);
+        break;
+      }
+      default:
+        break;
+    }
+  }
+}
+
 int element_size(int dtype) {
   switch (dtype) {
     case PONNI_F64: return 8;
@@ -440,16 +510,22 @@ int upload(ponni_plan_s& p) {
   if (!p.steps.empty())
     HIP_TRY(hipMemcpy(p.d_steps, p.steps.data(), sizeof(Step) * p.steps.size(), hipMemcpyHostToDevice));
   std::vector<double> packed;
-  pack_params(p, packed);
+  std::vector<uint32_t> words;
+  bool const half_fused = p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16);
+  if (half_fused) pack_words_half(p, words);
+  else pack_params(p, packed);
+  size_t const count = half_fused ? words.size() : packed.size();
   // Rounded up so vector reads of the last packed block stay inside the allocation.
-  size_t const bytes = std::max<size_t>((packed.size() * param_element_size(p) + 255) / 256 * 256, 256);
+  size_t const bytes = std::max<size_t>((count * param_element_size(p) + 255) / 256 * 256, 256);
   if (bytes > p.d_params_bytes) {
     if (p.d_params) HIP_TRY(hipFree(p.d_params));
     p.d_params = nullptr;
     HIP_TRY(hipMalloc(&p.d_params, bytes));
     p.d_params_bytes = bytes;
   }
-  if (!packed.empty()) {
+  if (half_fused) {
+    if (!words.empty()) HIP_TRY(hipMemcpy(p.d_params, words.data(), words.size() * 4, hipMemcpyHostToDevice));
+  } else if (!packed.empty()) {
     if (p.dtype == PONNI_F64) {
       HIP_TRY(hipMemcpy(p.d_params, packed.data(), packed.size() * 8, hipMemcpyHostToDevice));
     } else {
@@ -554,7 +630,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {
       delete p;
-      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs F32, width <= 256 and 16-aligned concatenation");
+      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs F32/F16/BF16, width <= 256 and 16-aligned concatenation");
     }
   } else if (chosen == PONNI_PATH_MFMA) {
     if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {

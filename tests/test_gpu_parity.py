@@ -123,7 +123,7 @@ def test_random_chains(cuda, seed, path):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("path", ["generic", "narrow", "mfma"])
+@pytest.mark.parametrize("path", PATHS)
 def test_reduced_precision_paths(cuda, dtype, path):
     rng = np.random.default_rng(11)
     layers = [P.Matvec(rng.standard_normal((12, 16)) * 0.3), P.Bias(rng.uniform(-0.1, 0.1, 16)), P.Tanh(16),
@@ -154,7 +154,7 @@ def config_input(cfg, B, dev="cuda:0"):
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
-@pytest.mark.parametrize("path", ["auto", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "mfma", "generic"])
 def test_configs_small_batch(cuda, name, path):
     """Each BASELINE config (with nonzero biases) vs the oracle."""
     import torch
@@ -230,3 +230,14 @@ def test_parameter_update_is_seen(cuda):
     y = m.forward_batch_parallel(xt)
     torch.cuda.synchronize()
     check_f32(y.double().cpu().numpy(), oracle.forward(layers, xg), scale_tol=False)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("seed", range(4))
+def test_random_chains_reduced_precision_fused(cuda, dtype, seed):
+    rng = np.random.default_rng(900 + seed)
+    width = [24, 40, 64, 96][seed]
+    layers = K.random_chain(rng, width, 2 + seed % 3)
+    x = rng.standard_normal((width, 777))
+    got, xg, _ = gpu_run(layers, x, dtype=dtype, path="fused", pad=2)
+    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
