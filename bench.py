@@ -30,6 +30,17 @@ METRIC = "samples/sec/GPU for fused MLP forward; % of HBM or MFMA roofline"
 ROTATE_BYTES = 512 << 20  # rotate buffers so the working set exceeds the 256 MB MALL
 
 
+def pmc_traffic(config_name: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs (profiles/traffic.json)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get(config_name)
+    except (OSError, ValueError):
+        return None
+    return entry.get("bytes_per_launch") if entry else None
+
+
 def host_cores() -> int:
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
@@ -104,7 +115,7 @@ def time_config(cfg, steps, warmup, torch, P, C):
             "peak": round(cfg.peak / scale, 3),
             "unit": unit,
             "frac": round(achieved / cfg.peak, 4),
-            "traffic": None,
+            "traffic": pmc_traffic(cfg.name),
         },
         "path": model.path,
     }
@@ -155,6 +166,8 @@ def main() -> int:
     ap.add_argument("--no-others", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a device copy of 256 MiB (reference for PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the forward pass shards over the batch with no "
@@ -167,6 +180,13 @@ def main() -> int:
     from ponni_amd import configs as C
 
     torch.cuda.init()
+    if args.calibrate_copy:
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0")
+        P.fill_synthetic(src, 1, 2, "uniform", 0.0, 1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cfg = C.CONFIGS[args.config]
     head = time_config(cfg, args.steps, args.warmup, torch, P, C)
     others = {}

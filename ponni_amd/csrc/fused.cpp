@@ -206,6 +206,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::ostringstream o;
   std::string const IO = half ? E : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
+  // 16-bit plans keep a workgroup's waves on one output tile at a time, so the
+  // three waves that follow the first read its A fragments from L1.
+  if (half) o << "#define PONNI_TILE_BARRIER 1\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
@@ -286,7 +289,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             << op.woff << ", zeros<" << tiles(n) << ">(), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
         for (int s = 0; s < op.epi_count; s++) {
           Step const& st = p.steps[op.epi_begin + s];
-          if (st.act == ACT_BIAS) {
+          bool const bias_tanh = half && st.act == ACT_BIAS && s + 1 < op.epi_count &&
+                                 p.steps[op.epi_begin + s + 1].act == ACT_TANH;
+          if (bias_tanh) {
+            o << "      tile_bias_tanh(t, P + " << st.off << ", mo, L);\n";
+            s++;
+          } else if (st.act == ACT_BIAS) {
             o << "      tile_add_rows(t, P + " << st.off << ", mo, L);\n";
           } else {
             o << "      tile_map(t, [](float v) { return " << act(st) << "; });\n";

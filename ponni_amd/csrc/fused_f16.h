@@ -49,6 +49,26 @@ __device__ inline float act_tanh_fast(float x) {
   return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Bias and tanh of one output tile in a single pass:
+// tanh(v + b) = 1 - 2 / (1 + 2^(k v + k b)), k = 2 log2(e); five VALU ops per
+// element, two of them transcendental.
+template <int NT>
+__device__ inline void tile_bias_tanh(floatx4 (&t)[NT], float const* __restrict__ b, int mo, Lane const& L) {
+  constexpr float k = 2.8853900817779268f;
+  floatx4 const kb = ld4(b + 16 * mo + 4 * L.g) * k;
+#pragma unroll
+  for (int n = 0; n < NT; n++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float const ex = __builtin_amdgcn_exp2f(fmaf(t[n][e], k, kb[e]));
+      t[n][e] = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + ex), 1.0f);
+    }
+}
+
+#ifndef PONNI_RING_DEPTH
+#define PONNI_RING_DEPTH 4
+#endif
+
 template <int N, int NT, class E>
 __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
@@ -118,7 +138,7 @@ __device__ inline H<T, NT, E> to_h(S<T, NT> const& s) {
 // epilogue of output tile mo-1 runs after the MFMAs of tile mo; A fragments
 // stream through an R-deep ring (1 KB per fragment: 16 B per lane).
 // If `acc0` is given (projection add) it seeds every output tile's accumulator.
-template <int TI, int TO, int NT, class E, class Epi, int D = 4>
+template <int TI, int TO, int NT, class E, class Epi, int D = PONNI_RING_DEPTH>
 __device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restrict__ w, Lane const& L, Epi epi) {
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
@@ -132,6 +152,11 @@ __device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restri
   floatx4 prev[NT];
 #pragma unroll
   for (int mo = 0; mo < TO; mo++) {
+#ifdef PONNI_TILE_BARRIER
+    // Keep the workgroup's waves on the same output tile so their identical
+    // A-fragment reads hit in L1 after the first wave's miss.
+    __syncthreads();
+#endif
     floatx4 acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) acc[n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
