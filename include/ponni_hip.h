@@ -78,9 +78,72 @@ typedef enum ponni_layer_kind {
   PONNI_LAYER_BINOP_ADD = 31,    /* layers/ponni_Binop_Add.h: slot = ISAVE           */
   PONNI_LAYER_BINOP_CONCATENATE = 32, /* layers/ponni_Binop_Concatenate.h: slot; n_in = N1,
                                          n_out = N1 + N2; flags bit0 = after         */
-  PONNI_LAYER_BINOP_PROJECTION_ADD = 33 /* layers/ponni_Binop_Projection_Add.h: slot;
+  PONNI_LAYER_BINOP_PROJECTION_ADD = 33, /* layers/ponni_Binop_Projection_Add.h: slot;
                                            n_aux = NSAVE; W [NSAVE, n_in], bias [n_in] */
+
+  /* Operations of generated graphs (the canonical IR of kokkos_nn/ir.py as the
+   * emitter lowers it, kokkos_nn/emitter.py:693-941).  They have no layer
+   * template; ponni_amd/graph.py linearizes a graph into a chain that uses
+   * them together with the kinds above. */
+  PONNI_LAYER_DENSE = 40,        /* emitter.py:693-734: W [n_out, n_in] row-major, then
+                                    bias [n_out] when flags bit0; sum = bias, += W x   */
+  PONNI_LAYER_LOAD_STATE = 41,   /* state = saved[slot]; n_out = that slot's width      */
+  PONNI_LAYER_BINARY = 42,       /* emitter.py:735-741: state = op(a, b) of the state and
+                                    saved[slot]; attr[0] = ponni_binary_op; flags bit0 =
+                                    saved operand on the left; n_aux = saved width; each
+                                    operand has 1 or n_out features (scalar broadcast) */
+  PONNI_LAYER_REDUCE = 43,       /* emitter.py:475-547: n_in features -> 1;
+                                    attr[0] = ponni_reduce_op                           */
+  PONNI_LAYER_UNARY = 44,        /* emitter.py:218-258: pointwise; attr[0] = ponni_unary_op,
+                                    attr[1] alpha, attr[2] gamma                       */
+  PONNI_LAYER_CONST_BINARY = 45  /* pointwise op(state, c) with a constant c [n_in];
+                                    attr[0] = ponni_binary_op; flags bit0 = c on the left */
 } ponni_layer_kind;
+
+/* Element-wise binary operations of PONNI_LAYER_BINARY / _CONST_BINARY. */
+typedef enum ponni_binary_op {
+  PONNI_BINARY_ADD = 0,
+  PONNI_BINARY_SUB = 1,
+  PONNI_BINARY_MUL = 2,
+  PONNI_BINARY_DIV = 3,
+  PONNI_BINARY_MIN = 4, /* a < b ? a : b */
+  PONNI_BINARY_MAX = 5, /* a > b ? a : b */
+  PONNI_BINARY_POW = 6
+} ponni_binary_op;
+
+/* Feature reductions of PONNI_LAYER_REDUCE (emitter.py:475-512). */
+typedef enum ponni_reduce_op {
+  PONNI_REDUCE_SUM = 0,
+  PONNI_REDUCE_MEAN = 1,
+  PONNI_REDUCE_MAX = 2,
+  PONNI_REDUCE_MIN = 3,
+  PONNI_REDUCE_L1 = 4,
+  PONNI_REDUCE_L2 = 5,
+  PONNI_REDUCE_SUM_SQUARE = 6,
+  PONNI_REDUCE_LOG_SUM = 7,
+  PONNI_REDUCE_LOG_SUM_EXP = 8,
+  PONNI_REDUCE_PROD = 9
+} ponni_reduce_op;
+
+/* Unary operations of PONNI_LAYER_UNARY without a layer template
+ * (emitter.py:218-258). */
+typedef enum ponni_unary_op {
+  PONNI_UNARY_ABS = 0,
+  PONNI_UNARY_NEG = 1,
+  PONNI_UNARY_EXP = 2,
+  PONNI_UNARY_LOG = 3,
+  PONNI_UNARY_SQRT = 4,
+  PONNI_UNARY_RECIPROCAL = 5,
+  PONNI_UNARY_SOFTSIGN = 6,
+  PONNI_UNARY_CELU = 7,             /* attr[1] alpha */
+  PONNI_UNARY_THRESHOLDED_RELU = 8, /* attr[1] alpha */
+  PONNI_UNARY_ERF = 9,
+  PONNI_UNARY_SELU = 10             /* attr[1] alpha, attr[2] gamma: gamma * (x > 0 ? x : alpha*(e^x - 1)) */
+} ponni_unary_op;
+
+#define PONNI_FLAG_DENSE_BIAS 1 /* PONNI_LAYER_DENSE carries a bias     */
+#define PONNI_FLAG_SAVED_LEFT 1 /* PONNI_LAYER_BINARY: saved[slot] op state */
+#define PONNI_FLAG_CONST_LEFT 1 /* PONNI_LAYER_CONST_BINARY: c op state  */
 
 /* One layer of the tuple handed to create_inference_model
  * (src/ponni_create_model.h:40-65).  Widths are the runtime extents the
@@ -154,7 +217,8 @@ int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info);
 
 /* Number of parameter values layer `layer` carries, trainable or not:
  * Matvec n_in*n_out, Bias n, LayerNorm 2n (gamma then beta),
- * Projection_Add NSAVE*n_in + n_in (W then bias), others 0. */
+ * Projection_Add NSAVE*n_in + n_in (W then bias), Dense n_out*n_in (+ n_out
+ * with a bias), Const_Binary n_in, others 0. */
 int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer);
 
 /* Copy one layer's parameters from host memory, in the layer's own order
@@ -245,6 +309,33 @@ int ponni_file_write_parameters(const char* path, const char* model_fingerprint,
  * rejection message in ponni_last_error() on failure. */
 int ponni_file_read_parameters(const char* path, const char* model_fingerprint,
                                void* values, int64_t count, int32_t elem_size);
+
+/* One named tensor of a multi-tensor .ponni file, as a generated model's
+ * weight_specs() lists it (kokkos_nn/emitter.py:1438-1447): `offset` is the
+ * tensor's first element in the model's flat parameter storage. */
+typedef struct ponni_tensor_spec {
+  const char* name;
+  int32_t rank;
+  int64_t shape[8];
+  int64_t offset;
+} ponni_tensor_spec;
+
+/* Write tensors gathered from `storage` (double; stored as F32 when
+ * stored_elem_size is 4, F64 when 8) into a .ponni file in name order with
+ * the profile metadata; kokkos_nn/weights.py:95-153 and the generated
+ * save_parameters (emitter.py:1754-1766). */
+int ponni_file_write_tensors(const char* path, const char* model_fingerprint,
+                             const ponni_tensor_spec* specs, int32_t num_specs,
+                             const double* storage, int32_t stored_elem_size,
+                             const char* source_framework, const char* target);
+
+/* Load, validate against exactly these tensors and fingerprint, and scatter
+ * every tensor into `storage` (double) at its offset; the generated
+ * load_weights (emitter.py:1724-1752) over PonniFile::load / validate
+ * (utils/ponni_safetensors.h:187-347). */
+int ponni_file_read_tensors(const char* path, const char* model_fingerprint,
+                            const ponni_tensor_spec* specs, int32_t num_specs,
+                            double* storage, int32_t stored_elem_size);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,11 @@
 //   layers                src/layers/*.h compute_all_outputs / apply (cited below)
 //   fp16 chain            template half model: every operation rounds to half
 //                         (ponni_create_model.h:86-92, Kokkos half_t)
+//   generated-graph ops   the emitted per-sample code of kokkos_nn/emitter.py:
+//                         Dense :693-734 (sum = bias first), unary :218-258,
+//                         binary :261-275 with scalar broadcast :735-741,
+//                         reductions :475-547; a graph reaches the oracle as
+//                         the same linearized chain the product receives
 //
 // Modes: 0 fp32, 1 fp64, 2 fp16 operands with fp32 arithmetic (state rounded
 // to fp16 at every materialization), 3 the same for bf16, 4 fp16 chain.
@@ -96,6 +101,29 @@ inline double o_log(double x) { return std::log(x); }
 inline double o_tanh(double x) { return std::tanh(x); }
 inline double o_erf(double x) { return std::erf(x); }
 inline double o_sqrt(double x) { return std::sqrt(x); }
+inline H16 o_abs(H16 x) { return H16(std::fabs(x.v)); }
+inline H16 o_pow(H16 x, H16 y) { return H16(std::pow(x.v, y.v)); }
+inline bool o_isinf(H16 x) { return std::isinf(x.v); }
+inline float o_abs(float x) { return std::fabs(x); }
+inline float o_pow(float x, float y) { return std::pow(x, y); }
+inline bool o_isinf(float x) { return std::isinf(x); }
+inline double o_abs(double x) { return std::fabs(x); }
+inline double o_pow(double x, double y) { return std::pow(x, y); }
+inline bool o_isinf(double x) { return std::isinf(x); }
+
+// emitter.py:261-275
+template <class T>
+T binary_op(int op, T l, T r) {
+  switch (op) {
+    case PONNI_BINARY_ADD: return l + r;
+    case PONNI_BINARY_SUB: return l - r;
+    case PONNI_BINARY_MUL: return l * r;
+    case PONNI_BINARY_DIV: return l / r;
+    case PONNI_BINARY_MIN: return l < r ? l : r;
+    case PONNI_BINARY_MAX: return l > r ? l : r;
+    default: return o_pow(l, r);
+  }
+}
 
 // ---- pointwise layers (apply) ----------------------------------------------
 template <class T>
@@ -149,12 +177,42 @@ T pointwise(ponni_layer_desc const& d, double const* p, T x, int f) {
       T sp = x > T(0) ? x + o_log(T(1) + o_exp(-x)) : o_log(T(1) + o_exp(x));
       return x * o_tanh(sp);
     }
+    case PONNI_LAYER_UNARY: {  // emitter.py:218-258
+      T const alpha = T(d.attr[1]);
+      switch (static_cast<int>(d.attr[0])) {
+        case PONNI_UNARY_ABS: return o_abs(x);
+        case PONNI_UNARY_NEG: return -x;
+        case PONNI_UNARY_EXP: return o_exp(x);
+        case PONNI_UNARY_LOG: return o_log(x);
+        case PONNI_UNARY_SQRT: return o_sqrt(x);
+        case PONNI_UNARY_RECIPROCAL: return T(1) / x;
+        case PONNI_UNARY_SOFTSIGN: return x / (T(1) + o_abs(x));
+        case PONNI_UNARY_CELU: return x > T(0) ? x : alpha * (o_exp(x / alpha) - T(1));
+        case PONNI_UNARY_THRESHOLDED_RELU: return x > alpha ? x : T(0);
+        case PONNI_UNARY_SELU: return T(d.attr[2]) * (x > T(0) ? x : alpha * (o_exp(x) - T(1)));
+        default: return o_erf(x);
+      }
+    }
+    case PONNI_LAYER_CONST_BINARY: {  // binary op with a constant operand
+      int const op = static_cast<int>(d.attr[0]);
+      return (d.flags & PONNI_FLAG_CONST_LEFT) ? binary_op<T>(op, T(p[f]), x) : binary_op<T>(op, x, T(p[f]));
+    }
     default:
       return x;
   }
 }
 
-bool is_pointwise(int k) { return k == PONNI_LAYER_BIAS || (k >= PONNI_LAYER_RELU && k <= PONNI_LAYER_MISH); }
+bool is_pointwise(int k) {
+  return k == PONNI_LAYER_BIAS || (k >= PONNI_LAYER_RELU && k <= PONNI_LAYER_MISH) || k == PONNI_LAYER_UNARY ||
+         k == PONNI_LAYER_CONST_BINARY;
+}
+
+bool is_dense(int k) { return k == PONNI_LAYER_MATVEC || k == PONNI_LAYER_DENSE; }
+
+bool reads_slot(int k) {
+  return k == PONNI_LAYER_BINOP_ADD || k == PONNI_LAYER_BINOP_CONCATENATE || k == PONNI_LAYER_BINOP_PROJECTION_ADD ||
+         k == PONNI_LAYER_LOAD_STATE || k == PONNI_LAYER_BINARY;
+}
 
 // ---- buffers ------------------------------------------------------------------
 // A [features, batch] LayoutRight array of T with row stride ld.  `store`
@@ -260,6 +318,52 @@ void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_
       }
       return;
     }
+    case PONNI_LAYER_LOAD_STATE:  // the state becomes saved[slot]
+      for (int f = 0; f < d.n_out; f++) out(f, b) = saved(f, b);
+      return;
+    case PONNI_LAYER_BINARY: {  // emitter.py:735-741, operands of 1 or n_out features
+      int const op = static_cast<int>(d.attr[0]);
+      bool const saved_left = d.flags & PONNI_FLAG_SAVED_LEFT;
+      std::vector<T> cur(n), sv(d.n_aux);
+      for (int f = 0; f < n; f++) cur[f] = in(f, b);
+      for (int f = 0; f < d.n_aux; f++) sv[f] = saved(f, b);
+      for (int f = 0; f < d.n_out; f++) {
+        T const a = cur[n == 1 ? 0 : f];
+        T const s2 = sv[d.n_aux == 1 ? 0 : f];
+        out(f, b) = c.store(saved_left ? binary_op<T>(op, s2, a) : binary_op<T>(op, a, s2));
+      }
+      return;
+    }
+    case PONNI_LAYER_REDUCE: {  // emitter.py:475-547
+      int const op = static_cast<int>(d.attr[0]);
+      T r;
+      if (op == PONNI_REDUCE_MAX || op == PONNI_REDUCE_MIN || op == PONNI_REDUCE_LOG_SUM_EXP) {
+        r = in(0, b);
+        for (int f = 1; f < n; f++) {
+          T const v = in(f, b);
+          r = op == PONNI_REDUCE_MIN ? (v < r ? v : r) : (v > r ? v : r);
+        }
+        if (op == PONNI_REDUCE_LOG_SUM_EXP) {
+          T sum = T(0);
+          for (int f = 0; f < n; f++) sum += o_exp(in(f, b) - r);
+          r = o_isinf(r) ? r : r + o_log(sum);
+        }
+      } else {
+        r = op == PONNI_REDUCE_PROD ? T(1) : T(0);
+        for (int f = 0; f < n; f++) {
+          T const v = in(f, b);
+          if (op == PONNI_REDUCE_L1) r += o_abs(v);
+          else if (op == PONNI_REDUCE_L2 || op == PONNI_REDUCE_SUM_SQUARE) r += v * v;
+          else if (op == PONNI_REDUCE_PROD) r = r * v;
+          else r += v;
+        }
+        if (op == PONNI_REDUCE_MEAN) r /= T(n);
+        else if (op == PONNI_REDUCE_L2) r = o_sqrt(r);
+        else if (op == PONNI_REDUCE_LOG_SUM) r = o_log(r);
+      }
+      out(0, b) = c.store(r);
+      return;
+    }
     default:  // a lone pointwise layer
       for (int f = 0; f < n; f++) out(f, b) = c.store(pointwise<T>(d, p, in(f, b), f));
       return;
@@ -274,7 +378,7 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
   int i = 0;
   while (i < L) {
     ponni_layer_desc const& d = c.layers[i];
-    if (d.kind == PONNI_LAYER_MATVEC) {
+    if (is_dense(d.kind)) {
       int end = i + 1;
       while (end < L && is_pointwise(c.layers[end].kind)) end++;
       Buf<T> in = i == 0 ? x : (in_tmp1 ? tmp1 : tmp2);
@@ -287,16 +391,23 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
         in_tmp1 = out_tmp1;
       }
       double const* w = c.params[i];
+      bool const generated = d.kind == PONNI_LAYER_DENSE;
+      bool const bias = generated && (d.flags & PONNI_FLAG_DENSE_BIAS);
       for (int f = 0; f < d.n_out; f++) {  // compute_fused_dense_block, ponni_Inference.h:431-444
         T v = T(0);
-        for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(k) * d.n_out + f]) * in(k, b);
+        if (generated) {  // emitter.py:701-710: sum = bias; sum += W[f][k] x[k]
+          if (bias) v = T(w[int64_t(d.n_out) * d.n_in + f]);
+          for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(f) * d.n_in + k]) * in(k, b);
+        } else {
+          for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(k) * d.n_out + f]) * in(k, b);
+        }
         for (int e = i + 1; e < end; e++) v = pointwise<T>(c.layers[e], c.params[e], v, f);
         out(f, b) = c.store(v);
       }
       i = end;
       continue;
     }
-    Buf<T> const sv = (d.kind >= PONNI_LAYER_SAVE_STATE) ? saved[d.slot] : Buf<T>{};
+    Buf<T> const sv = reads_slot(d.kind) ? saved[d.slot] : Buf<T>{};
     if (i == 0 && L == 1) {
       barrier(c, i, x, sv, y, b);
     } else if (i == 0) {
@@ -324,7 +435,7 @@ void plan_widths(std::vector<ponni_layer_desc> const& layers, int* tmp, int* sav
   while (i < L) {
     ponni_layer_desc const& d = layers[i];
     if (d.kind == PONNI_LAYER_SAVE_STATE && d.slot >= 0 && d.slot < 8) saved[d.slot] = std::max(saved[d.slot], d.n_out);
-    if (d.kind == PONNI_LAYER_MATVEC) {
+    if (is_dense(d.kind)) {
       int end = i + 1;
       while (end < L && is_pointwise(layers[end].kind)) end++;
       if (end != L) {
@@ -383,7 +494,7 @@ extern "C" {
 
 // Per-layer parameters are concatenated in layer order, each in the layer's
 // own layout (Matvec W [n_in, n_out]; LayerNorm gamma, beta; Projection_Add
-// W [NSAVE, n_in], bias).  x / y are float for modes 0, 2, 3, 4 and double for
+// W [NSAVE, n_in], bias; Dense W [n_out, n_in], bias; Const_Binary c [n_in]).  x / y are float for modes 0, 2, 3, 4 and double for
 // mode 1.  Returns 0 on success.
 int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double const* params, int32_t mode,
                    void const* x, int64_t ld_x, void* y, int64_t ld_y, int64_t batch, int32_t threads) {
@@ -399,6 +510,10 @@ int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double co
       case PONNI_LAYER_BIAS: off += d.n_in; break;
       case PONNI_LAYER_LAYER_NORM: off += 2 * int64_t(d.n_in); break;
       case PONNI_LAYER_BINOP_PROJECTION_ADD: off += int64_t(d.n_aux) * d.n_in + d.n_in; break;
+      case PONNI_LAYER_DENSE:
+        off += int64_t(d.n_out) * d.n_in + ((d.flags & PONNI_FLAG_DENSE_BIAS) ? d.n_out : 0);
+        break;
+      case PONNI_LAYER_CONST_BINARY: off += d.n_in; break;
       default: break;
     }
   }

@@ -44,8 +44,24 @@ LAYER_BINOP_ADD = 31
 LAYER_BINOP_CONCATENATE = 32
 LAYER_BINOP_PROJECTION_ADD = 33
 
+LAYER_DENSE = 40
+LAYER_LOAD_STATE = 41
+LAYER_BINARY = 42
+LAYER_REDUCE = 43
+LAYER_UNARY = 44
+LAYER_CONST_BINARY = 45
+
+BINARY_OPS = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Min": 4, "Max": 5, "Pow": 6}
+REDUCE_OPS = {"ReduceSum": 0, "ReduceMean": 1, "ReduceMax": 2, "ReduceMin": 3, "ReduceL1": 4, "ReduceL2": 5,
+              "ReduceSumSquare": 6, "ReduceLogSum": 7, "ReduceLogSumExp": 8, "ReduceProd": 9}
+UNARY_OPS = {"Abs": 0, "Neg": 1, "Exp": 2, "Log": 3, "Sqrt": 4, "Reciprocal": 5, "Softsign": 6, "Celu": 7,
+             "ThresholdedRelu": 8, "Erf": 9, "Selu": 10}
+
 FLAG_GELU_APPROXIMATE = 1
 FLAG_CONCAT_AFTER = 1
+FLAG_DENSE_BIAS = 1
+FLAG_SAVED_LEFT = 1
+FLAG_CONST_LEFT = 1
 
 
 class LayerDesc(ctypes.Structure):
@@ -57,6 +73,15 @@ class LayerDesc(ctypes.Structure):
         ("n_aux", ctypes.c_int32),
         ("flags", ctypes.c_int32),
         ("attr", ctypes.c_double * 4),
+    ]
+
+
+class TensorSpec(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("rank", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 8),
+        ("offset", ctypes.c_int64),
     ]
 
 
@@ -136,6 +161,11 @@ def lib() -> ctypes.CDLL:
     L.ponni_file_write_parameters.argtypes = [ctypes.c_char_p, ctypes.c_char_p, vp, i64, i32, ctypes.c_char_p]
     L.ponni_file_read_parameters.restype = ctypes.c_int
     L.ponni_file_read_parameters.argtypes = [ctypes.c_char_p, ctypes.c_char_p, vp, i64, i32]
+    L.ponni_file_write_tensors.restype = ctypes.c_int
+    L.ponni_file_write_tensors.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(TensorSpec), i32, vp, i32,
+                                           ctypes.c_char_p, ctypes.c_char_p]
+    L.ponni_file_read_tensors.restype = ctypes.c_int
+    L.ponni_file_read_tensors.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(TensorSpec), i32, vp, i32]
     _lib = L
     return L
 

@@ -134,6 +134,42 @@ def c4_layers(nonzero_bias: bool = False) -> List[M.Layer]:
     return out
 
 
+def c5_graph(nonzero_bias: bool = False):
+    """The generator-style branched graph of configs[4] in the canonical IR:
+    Dense weights are [out, in] (Glorot over fan_in = in, fan_out = out),
+    biases zero unless nonzero_bias, Concat order [branch A, branch B]."""
+    from .graph import GraphBuilder
+
+    s = 4
+
+    def w(n_in, n_out, tag):
+        return glorot_uniform(n_in, n_out, s, tag).T.copy()
+
+    g = GraphBuilder(24)
+    x = g.input
+    a = g.unary("Relu", g.dense(x, w(24, 96, 1), _bias(96, s, 2, nonzero_bias), name="branch_a.fc1"))
+    a = g.dense(a, w(96, 48, 3), _bias(48, s, 4, nonzero_bias), name="branch_a.fc2")
+    b = g.unary("Sigmoid", g.dense(x, w(24, 48, 5), _bias(48, s, 6, nonzero_bias), name="branch_b.fc"))
+    c = g.concat(a, b)
+    p = g.dense(x, w(24, 96, 7), _bias(96, s, 8, nonzero_bias), name="skip.proj")
+    t = g.binary("Add", c, p)
+    t = g.binary("Sub", t, g.reduce("ReduceMean", t))
+    out = g.softmax(g.dense(t, w(96, 10, 9), _bias(10, s, 10, nonzero_bias), name="head.fc"))
+    return g.finish(out)
+
+
+def c5_layers(nonzero_bias: bool = False) -> List[M.Layer]:
+    """c5 linearized into the layer chain libponni_hip runs, parameters set."""
+    from .graph import GeneratedModel
+
+    gm = GeneratedModel(c5_graph(nonzero_bias))
+    layers = gm.lowered.layers
+    for l, v in zip(layers, gm.lowered.layer_params(gm._constants("f64"))):
+        if v.size:
+            l.params = v
+    return layers
+
+
 CONFIGS = {
     "c1": Config("c1", "Template-mode MLP 2->3->1 fp32", 1_000_000, 2, 1, "f32", c1_layers, ("uniform", -1.0, 1.0),
                  0, "hbm", 12, 18, HBM_PEAK),
@@ -143,4 +179,6 @@ CONFIGS = {
                  "f32", c3_layers, ("normal", 0.0, 1.0), 2, "mfma", 192, 274_432, FP32_PEAK),
     "c4": Config("c4", "fp16 MLP 64->256->256->256->64, tanh, fp32 accumulate", 8_388_608, 64, 64, "f16", c4_layers,
                  ("normal", 0.0, 1.0), 3, "mfma", 256, 327_680, FP16_PEAK),
+    "c5": Config("c5", "Generated branched fp32 graph 24->[96->48 | 48]->concat 96 + proj skip, centre, ->10 softmax",
+                 4_194_304, 24, 10, "f32", c5_layers, ("normal", 0.0, 1.0), 4, "mfma", 136, 22_656, FP32_PEAK),
 }

@@ -43,8 +43,65 @@ std::string flit(float v) {
   return std::string(buf) + "f";
 }
 
+// Steps that keep a zero padding row at zero (padded parameter entries are 0).
 bool zero_at_zero(int act) {
-  return !(act == ACT_SIGMOID || act == ACT_SOFTPLUS || act == ACT_HARD_SIGMOID);
+  switch (act) {
+    case ACT_BIAS:
+    case ACT_RELU:
+    case ACT_LEAKY_RELU:
+    case ACT_ELU:
+    case ACT_SELU:
+    case ACT_GELU_ERF:
+    case ACT_GELU_TANH:
+    case ACT_SILU:
+    case ACT_TANH:
+    case ACT_HARD_SWISH:
+    case ACT_MISH:
+    case ACT_ABS:
+    case ACT_NEG:
+    case ACT_SQRT:
+    case ACT_SOFTSIGN:
+    case ACT_CELU:
+    case ACT_ERF:
+    case ACT_SELU_AG:
+    case ACT_MUL_C:
+      return true;
+    case ACT_THRESHOLDED_RELU:
+      return true;  // 0 > a ? 0 : 0
+    default:
+      return false;
+  }
+}
+
+// f(v, c) of a step with a constant vector operand.
+std::string const_expr(int act) {
+  switch (act) {
+    case ACT_BIAS: return "v + c";
+    case ACT_SUB_C: return "v - c";
+    case ACT_RSUB_C: return "c - v";
+    case ACT_MUL_C: return "v * c";
+    case ACT_DIV_C: return "v / c";
+    case ACT_RDIV_C: return "c / v";
+    case ACT_MIN_C: return "v < c ? v : c";
+    case ACT_RMIN_C: return "c < v ? c : v";
+    case ACT_MAX_C: return "v > c ? v : c";
+    case ACT_RMAX_C: return "c > v ? c : v";
+    case ACT_POW_C: return "powf(v, c)";
+    default: return "powf(c, v)";
+  }
+}
+
+// Binary operation of OP_BINARY on operands x (left) and y (right).
+std::string binary_expr(int op) {
+  switch (op) {
+    case PONNI_BINARY_ADD: return "x + y";
+    case PONNI_BINARY_SUB: return "x - y";
+    case PONNI_BINARY_MUL: return "x * y";
+    case PONNI_BINARY_DIV: return "x / y";
+    case PONNI_BINARY_MIN: return "x < y ? x : y";
+    case PONNI_BINARY_MAX: return "x > y ? x : y";
+    default: return "powf(x, y)";
+  }
 }
 
 std::string act_expr(Step const& s) {
@@ -62,6 +119,17 @@ std::string act_expr(Step const& s) {
     case ACT_HARD_SIGMOID: return "act_hard_sigmoid(v, " + flit(s.a) + ", " + flit(s.b) + ")";
     case ACT_HARD_SWISH: return "act_hard_swish(v)";
     case ACT_MISH: return "act_mish(v)";
+    case ACT_ABS: return "fabsf(v)";
+    case ACT_NEG: return "-v";
+    case ACT_EXP: return "expf(v)";
+    case ACT_LOG: return "logf(v)";
+    case ACT_SQRT: return "sqrtf(v)";
+    case ACT_RECIPROCAL: return "1.0f / v";
+    case ACT_SOFTSIGN: return "act_softsign(v)";
+    case ACT_CELU: return "act_celu(v, " + flit(s.a) + ")";
+    case ACT_THRESHOLDED_RELU: return "act_thresholded_relu(v, " + flit(s.a) + ")";
+    case ACT_ERF: return "erff(v)";
+    case ACT_SELU_AG: return "act_selu_ag(v, " + flit(s.a) + ", " + flit(s.b) + ")";
     default: return "v";
   }
 }
@@ -175,6 +243,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         case OP_PROJ_ADD: need = (cur + 2 * tiles(op.n_out)) * 8 + tiles(op.aux) * 4; break;
         case OP_CONCAT: need = 2 * tiles(op.n_out) * 8; cur = tiles(op.n_out); break;
         case OP_SAVE: slots[op.slot] = cur; break;
+        case OP_LOAD: cur = tiles(op.n_out); need = cur * 8; break;
+        case OP_BINARY: need = (cur + 2 * tiles(op.n_out)) * (half ? 16 : 8); cur = tiles(op.n_out); break;
+        case OP_REDUCE: need = cur * (half ? 16 : 8); cur = 1; break;
         default: need = half ? cur * 16 : cur * 8; break;  // 16-bit states widen to fp32 for barriers
       }
       worst = std::max(worst, need + saved_regs);
@@ -266,6 +337,10 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       Step const& st = p.steps[begin + s];
       if (st.act == ACT_BIAS) {
         o << "    add_rows<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L);\n";
+      } else if (act_has_param(st.act)) {
+        o << "    map_const<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L, [](float v, float c) { return "
+          << const_expr(st.act) << "; });\n";
+        if (!zero_at_zero(st.act)) pad = true;
       } else {
         o << "    map<" << tiles(n) << ">(" << v << ", [](float v) { return " << act(st) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
@@ -281,13 +356,18 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         std::string const nv = fresh();
         int const n = op.n_out;
         bool pad = false;
+        // A generated Dense's bias seeds the fp32 accumulator (sum = bias first).
+        bool const seed = !half && (op.aux & DENSE_BIAS_FIRST);
+        std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(P + " +
+                                            std::to_string(p.steps[op.epi_begin].off) + ", L)"
+                                      : "zeros<" + std::to_string(tiles(n)) + ">()";
         if (half)
           o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
         else
           o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
-            << op.woff << ", zeros<" << tiles(n) << ">(), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
-        for (int s = 0; s < op.epi_count; s++) {
+            << op.woff << ", " << init << ", L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
+        for (int s = seed ? 1 : 0; s < op.epi_count; s++) {
           Step const& st = p.steps[op.epi_begin + s];
           bool const bias_tanh = half && st.act == ACT_BIAS && s + 1 < op.epi_count &&
                                  p.steps[op.epi_begin + s + 1].act == ACT_TANH;
@@ -296,6 +376,10 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             s++;
           } else if (st.act == ACT_BIAS) {
             o << "      tile_add_rows(t, P + " << st.off << ", mo, L);\n";
+          } else if (act_has_param(st.act)) {
+            o << "      tile_const(t, P + " << st.off << ", mo, L, [](float v, float c) { return " << const_expr(st.act)
+              << "; });\n";
+            if (!zero_at_zero(st.act)) pad = true;
           } else {
             o << "      tile_map(t, [](float v) { return " << act(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
@@ -388,6 +472,44 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             << ", P + " << op.woff << ", " << b << ", L, [](int, floatx4 (&)[" << NT << "]) {});\n";
           o << "    add(" << cur << ", " << nv << ");\n";
         }
+        break;
+      }
+      case OP_LOAD: {
+        auto const& sv = saved[op.slot];
+        std::string const nv = fresh();
+        o << "    auto " << nv << " = " << sv.first << ";\n";
+        cur = nv;
+        cur_n = sv.second;
+        break;
+      }
+      case OP_BINARY: {
+        // out = f(x, y), x the left operand; a one-feature operand broadcasts.
+        auto const& sv = saved[op.slot];
+        bool const saved_left = op.aux & BIN_SAVED_LEFT;
+        bool const state_scalar = op.aux & BIN_STATE_SCALAR, saved_scalar = op.aux & BIN_SAVED_SCALAR;
+        std::string const nv = fresh();
+        std::string const a = half ? "to_f32(" + cur + ")" : cur;
+        std::string const b = half ? "to_f32(" + sv.first + ")" : sv.first;
+        std::string const lhs = saved_left ? b : a, rhs = saved_left ? a : b;
+        bool const lhs_scalar = saved_left ? saved_scalar : state_scalar;
+        bool const rhs_scalar = saved_left ? state_scalar : saved_scalar;
+        std::string call = "binary<" + std::to_string(op.n_out) + ", " + (lhs_scalar ? "true" : "false") + ", " +
+                           (rhs_scalar ? "true" : "false") + ">(" + lhs + ", " + rhs +
+                           ", L, [](float x, float y) { return " + binary_expr(op.aux & 0xff) + "; })";
+        if (half) call = "to_h<E>(" + call + ")";
+        o << "    auto " << nv << " = " << call << ";\n";
+        cur = nv;
+        cur_n = op.n_out;
+        break;
+      }
+      case OP_REDUCE: {
+        std::string const nv = fresh();
+        std::string call = "reduce<" + std::to_string(op.aux) + ", " + std::to_string(cur_n) + ">(" +
+                           (half ? "to_f32(" + cur + ")" : cur) + ", L)";
+        if (half) call = "to_h<E>(" + call + ")";
+        o << "    auto " << nv << " = " << call << ";\n";
+        cur = nv;
+        cur_n = 1;
         break;
       }
       default:

@@ -342,6 +342,124 @@ __device__ inline void add_lds(S<T, NT>& s, floatx4 const* __restrict__ slot, La
     for (int n = 0; n < NT; n++) s.v[m][n] += slot[(m * NT + n) * 64 + L.lane];
 }
 
+// ---- generated-graph operations (kokkos_nn/emitter.py) -------------------
+
+// Per-feature vector b broadcast over the tile's columns (a Dense bias that
+// seeds the accumulator: sum = bias; sum += W x, emitter.py:701-710).
+template <int T, int NT = kNT>
+__device__ inline S<T, NT> bias_rows(float const* __restrict__ b, Lane const& L) {
+  S<T, NT> s;
+#pragma unroll
+  for (int m = 0; m < T; m++) {
+    floatx4 const bb = ld4(b + 16 * m + 4 * L.g);
+#pragma unroll
+    for (int n = 0; n < NT; n++) s.v[m][n] = bb;
+  }
+  return s;
+}
+
+// Element-wise op with a constant vector c (padded to 16 T): f(v, c).
+template <int NT, class F>
+__device__ inline void tile_const(floatx4 (&t)[NT], float const* __restrict__ c, int mo, Lane const& L, F f) {
+  floatx4 const cc = ld4(c + 16 * mo + 4 * L.g);
+#pragma unroll
+  for (int n = 0; n < NT; n++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) t[n][e] = f(t[n][e], cc[e]);
+}
+
+template <int T, int NT, class F>
+__device__ inline void map_const(S<T, NT>& s, float const* __restrict__ c, Lane const& L, F f) {
+#pragma unroll
+  for (int m = 0; m < T; m++) tile_const(s.v[m], c, m, L, f);
+}
+
+// Feature 0 of every column of the wave's tile, in each lane's own column:
+// feature 0 sits in lane c (group 0), element 0.
+template <int T, int NT>
+__device__ inline float feature0(S<T, NT> const& s, int n, Lane const& L) {
+  return __shfl(s.v[0][n][0], L.c);
+}
+
+// out = f(a, b) over N output features; an operand with one feature (TA or
+// TB == 1 with SA / SB set) is broadcast (emitter.py:735-741).
+template <int N, bool SA, bool SB, int TA, int TB, int NT, class F>
+__device__ inline S<(N + 15) / 16, NT> binary(S<TA, NT> const& a, S<TB, NT> const& b, Lane const& L, F f) {
+  constexpr int T = (N + 15) / 16;
+  S<T, NT> out;
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    float const a0 = SA ? feature0(a, n, L) : 0.0f;
+    float const b0 = SB ? feature0(b, n, L) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < T; m++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float const x = SA ? a0 : a.v[SA ? 0 : m][n][e];
+        float const y = SB ? b0 : b.v[SB ? 0 : m][n][e];
+        out.v[m][n][e] = f(x, y);
+      }
+  }
+  zero_pad<N, T, NT>(out, L);
+  return out;
+}
+
+__device__ inline float xprod(float v) {
+  v *= __shfl_xor(v, 16);
+  return v * __shfl_xor(v, 32);
+}
+
+// Feature reduction to one feature, emitter.py:475-547; OP is a
+// ponni_reduce_op value.  The result is feature 0; padding rows are 0.
+template <int OP, int N, int T, int NT>
+__device__ inline S<1, NT> reduce(S<T, NT> const& s, Lane const& L) {
+  S<1, NT> out;
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    float r;
+    if constexpr (OP == 2 || OP == 3 || OP == 8) {  // MAX, MIN, LOG_SUM_EXP
+      float mx = OP == 3 ? __builtin_huge_valf() : -__builtin_huge_valf();
+#pragma unroll
+      for (int m = 0; m < T; m++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = OP == 3 ? fminf(mx, s.v[m][n][e]) : fmaxf(mx, s.v[m][n][e]);
+      mx = OP == 3 ? xmin(mx) : xmax(mx);
+      r = mx;
+      if constexpr (OP == 8) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int m = 0; m < T; m++)
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += expf(s.v[m][n][e] - mx);
+        sum = xsum(sum);
+        r = __builtin_isinf(mx) ? mx : mx + logf(sum);
+      }
+    } else {
+      float acc = OP == 9 ? 1.0f : 0.0f;
+#pragma unroll
+      for (int m = 0; m < T; m++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) {
+            float const v = s.v[m][n][e];
+            if constexpr (OP == 4) acc += fabsf(v);
+            else if constexpr (OP == 5 || OP == 6) acc += v * v;
+            else if constexpr (OP == 9) acc *= v;
+            else acc += v;
+          }
+      acc = OP == 9 ? xprod(acc) : xsum(acc);
+      if constexpr (OP == 1) acc = acc / float(N);
+      else if constexpr (OP == 5) acc = sqrtf(acc);
+      else if constexpr (OP == 7) acc = logf(acc);
+      r = acc;
+    }
+    out.v[0][n] = floatx4{L.g == 0 ? r : 0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  return out;
+}
+
 // Stage `count` floats (a multiple of 4) of packed parameters into LDS.
 __device__ inline void stage(floatx4* __restrict__ lds, float const* __restrict__ src, int count) {
   floatx4 const* s4 = reinterpret_cast<floatx4 const*>(src);

@@ -57,13 +57,15 @@ __global__ __launch_bounds__(256) void generic_forward(LaunchArgs args) {
     switch (op.code) {
       case OP_DENSE: {
         // ponni_Inference.h:431-444 with Matvec::compute_output (ponni_Matvec.h:70-79).
+        // A generated Dense seeds the sum with its bias (emitter.py:701-710).
         C const* w = params + op.woff;
+        int const first = (op.aux & DENSE_BIAS_FIRST) ? 1 : 0;
         for (int f = 0; f < op.n_out; f++) {
-          C v = C(0);
+          C v = first ? params[args.steps[op.epi_begin].off + f] : C(0);
           for (int k = 0; k < op.n_in; k++) v += w[int64_t(k) * op.n_out + f] * load_as<S>(at<S>(in, k, b));
-          for (int s = 0; s < op.epi_count; s++) {
+          for (int s = first; s < op.epi_count; s++) {
             Step const st = args.steps[op.epi_begin + s];
-            C const bias = st.act == ACT_BIAS ? params[st.off + f] : C(0);
+            C const bias = act_has_param(st.act) ? params[st.off + f] : C(0);
             v = apply_step<C>(st.act, v, bias, C(st.a), C(st.b));
           }
           store_as<S, C>(at<S>(out, f, b), v);
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(256) void generic_forward(LaunchArgs args) {
       case OP_POINTWISE: {
         Step const st = args.steps[op.epi_begin];
         for (int f = 0; f < op.n_out; f++) {
-          C const bias = st.act == ACT_BIAS ? params[st.off + f] : C(0);
+          C const bias = act_has_param(st.act) ? params[st.off + f] : C(0);
           store_as<S, C>(at<S>(out, f, b), apply_step<C>(st.act, load_as<S>(at<S>(in, f, b)), bias, C(st.a), C(st.b)));
         }
         break;
@@ -170,6 +172,57 @@ __global__ __launch_bounds__(256) void generic_forward(LaunchArgs args) {
           for (int k = 0; k < nsave; k++) proj += w[int64_t(k) * n + i] * load_as<S>(at<S>(sv, k, b));
           store_as<S, C>(at<S>(out, i, b), load_as<S>(at<S>(in, i, b)) + proj);
         }
+        break;
+      }
+      case OP_LOAD: {  // the state becomes a saved one
+        for (int f = 0; f < op.n_out; f++) *at<S>(out, f, b) = *at<S>(in, f, b);
+        break;
+      }
+      case OP_BINARY: {  // emitter.py:735-741 with scalar-or-exact broadcasting
+        View2 const sv = buf[BUF_SAVED + op.slot];
+        int const bop = op.aux & 0xff;
+        bool const saved_left = op.aux & BIN_SAVED_LEFT;
+        C const s0 = load_as<S>(at<S>(in, 0, b));
+        C const v0 = load_as<S>(at<S>(sv, 0, b));
+        for (int f = 0; f < op.n_out; f++) {
+          C const a = (op.aux & BIN_STATE_SCALAR) ? s0 : load_as<S>(at<S>(in, f, b));
+          C const c = (op.aux & BIN_SAVED_SCALAR) ? v0 : load_as<S>(at<S>(sv, f, b));
+          store_as<S, C>(at<S>(out, f, b), saved_left ? apply_binary<C>(bop, c, a) : apply_binary<C>(bop, a, c));
+        }
+        break;
+      }
+      case OP_REDUCE: {  // emitter.py:475-547
+        int const n = op.n_in;
+        C r;
+        if (op.aux == PONNI_REDUCE_MAX || op.aux == PONNI_REDUCE_MIN || op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
+          bool const mn = op.aux == PONNI_REDUCE_MIN;
+          r = load_as<S>(at<S>(in, 0, b));
+          for (int f = 1; f < n; f++) {
+            C const v = load_as<S>(at<S>(in, f, b));
+            r = mn ? (v < r ? v : r) : (v > r ? v : r);
+          }
+          if (op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
+            C sum = C(0);
+            for (int f = 0; f < n; f++) sum += d_exp(load_as<S>(at<S>(in, f, b)) - r);
+            r = isinf(r) ? r : r + d_log(sum);
+          }
+        } else {
+          r = op.aux == PONNI_REDUCE_PROD ? C(1) : C(0);
+          for (int f = 0; f < n; f++) {
+            C const v = load_as<S>(at<S>(in, f, b));
+            switch (op.aux) {
+              case PONNI_REDUCE_L1: r += d_abs(v); break;
+              case PONNI_REDUCE_L2:
+              case PONNI_REDUCE_SUM_SQUARE: r += v * v; break;
+              case PONNI_REDUCE_PROD: r *= v; break;
+              default: r += v; break;
+            }
+          }
+          if (op.aux == PONNI_REDUCE_MEAN) r /= C(n);
+          else if (op.aux == PONNI_REDUCE_L2) r = d_sqrt(r);
+          else if (op.aux == PONNI_REDUCE_LOG_SUM) r = d_log(r);
+        }
+        store_as<S, C>(at<S>(out, 0, b), r);
         break;
       }
       default:

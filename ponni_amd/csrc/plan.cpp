@@ -32,8 +32,19 @@ int fail(int status, std::string const& message) {
 }
 
 bool is_pointwise(int kind) {
-  return kind == PONNI_LAYER_BIAS || (kind >= PONNI_LAYER_RELU && kind <= PONNI_LAYER_MISH);
+  return kind == PONNI_LAYER_BIAS || (kind >= PONNI_LAYER_RELU && kind <= PONNI_LAYER_MISH) ||
+         kind == PONNI_LAYER_UNARY || kind == PONNI_LAYER_CONST_BINARY;
 }
+
+bool is_dense(int kind) { return kind == PONNI_LAYER_MATVEC || kind == PONNI_LAYER_DENSE; }
+
+// Kinds that read a saved slot.
+bool reads_slot(int kind) {
+  return kind == PONNI_LAYER_BINOP_ADD || kind == PONNI_LAYER_BINOP_CONCATENATE ||
+         kind == PONNI_LAYER_BINOP_PROJECTION_ADD || kind == PONNI_LAYER_LOAD_STATE || kind == PONNI_LAYER_BINARY;
+}
+
+bool is_graph_kind(int kind) { return kind >= PONNI_LAYER_DENSE && kind <= PONNI_LAYER_CONST_BINARY; }
 
 bool is_save(int kind) { return kind == PONNI_LAYER_SAVE_STATE; }
 
@@ -45,7 +56,7 @@ bool is_binop(int kind) {
 bool known_kind(int kind) {
   return kind == PONNI_LAYER_MATVEC || is_pointwise(kind) ||
          (kind >= PONNI_LAYER_SOFTMAX && kind <= PONNI_LAYER_MIN_MAX_NORM) || is_save(kind) ||
-         is_binop(kind);
+         is_binop(kind) || is_graph_kind(kind);
 }
 
 char const* label_of(int kind) {
@@ -72,6 +83,12 @@ char const* label_of(int kind) {
     case PONNI_LAYER_BINOP_ADD: return "Binop_Add";
     case PONNI_LAYER_BINOP_CONCATENATE: return "Binop_Concatenate";
     case PONNI_LAYER_BINOP_PROJECTION_ADD: return "Binop_Projection_Add";
+    case PONNI_LAYER_DENSE: return "Dense";
+    case PONNI_LAYER_LOAD_STATE: return "Load_State";
+    case PONNI_LAYER_BINARY: return "Binary";
+    case PONNI_LAYER_REDUCE: return "Reduce";
+    case PONNI_LAYER_UNARY: return "Unary";
+    case PONNI_LAYER_CONST_BINARY: return "Const_Binary";
     default: return "?";
   }
 }
@@ -82,6 +99,8 @@ int64_t param_count(ponni_layer_desc const& d) {
     case PONNI_LAYER_BIAS: return d.n_in;
     case PONNI_LAYER_LAYER_NORM: return 2 * int64_t(d.n_in);
     case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(d.n_aux) * d.n_in + d.n_in;
+    case PONNI_LAYER_DENSE: return int64_t(d.n_out) * d.n_in + ((d.flags & PONNI_FLAG_DENSE_BIAS) ? d.n_out : 0);
+    case PONNI_LAYER_CONST_BINARY: return d.n_in;
     default: return 0;
   }
 }
@@ -96,9 +115,11 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
     where = "layer " + std::to_string(i) + " (" + label_of(d.kind) + "): ";
     if (!known_kind(d.kind)) return fail(PONNI_ERR_INVALID_ARGUMENT, where + "unknown layer kind " + std::to_string(d.kind));
     if (d.n_in <= 0 || d.n_out <= 0) return fail(PONNI_ERR_INVALID_MODEL, where + "num_inputs and num_outputs must be > 0");
-    bool const same_width = d.kind != PONNI_LAYER_MATVEC && d.kind != PONNI_LAYER_BINOP_CONCATENATE;
+    bool const same_width = !is_dense(d.kind) && d.kind != PONNI_LAYER_BINOP_CONCATENATE &&
+                            d.kind != PONNI_LAYER_LOAD_STATE && d.kind != PONNI_LAYER_BINARY &&
+                            d.kind != PONNI_LAYER_REDUCE;
     if (same_width && d.n_in != d.n_out) return fail(PONNI_ERR_INVALID_MODEL, where + "input/output size mismatch");
-    if (is_save(d.kind) || is_binop(d.kind)) {
+    if (is_save(d.kind) || reads_slot(d.kind)) {
       if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
     }
     switch (d.kind) {
@@ -122,6 +143,46 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
         saved_size[d.slot] = d.n_in;
         saved_seen[d.slot] = true;
         break;
+      case PONNI_LAYER_LOAD_STATE:
+      case PONNI_LAYER_BINARY: {
+        if (!saved_seen[d.slot])
+          return fail(PONNI_ERR_INVALID_MODEL, where + "reads saved state " + std::to_string(d.slot) + " before any Save_State wrote it");
+        int const saved = saved_size[d.slot];
+        if (d.kind == PONNI_LAYER_LOAD_STATE && d.n_out != saved)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "num outputs != the saved state's width");
+        if (d.kind == PONNI_LAYER_BINARY) {
+          int const op = static_cast<int>(d.attr[0]);
+          if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_POW)
+            return fail(PONNI_ERR_INVALID_MODEL, where + "unknown binary operation");
+          if (d.n_aux != saved) return fail(PONNI_ERR_INVALID_MODEL, where + "n_aux != the saved state's width");
+          if ((saved != 1 && saved != d.n_out) || (d.n_in != 1 && d.n_in != d.n_out) ||
+              (d.n_out != std::max(d.n_in, saved)))
+            return fail(PONNI_ERR_INVALID_MODEL, where + "unsupported broadcasting: operand sizes " + std::to_string(d.n_in) +
+                                                     " and " + std::to_string(saved) + ", output size " +
+                                                     std::to_string(d.n_out));
+        }
+        break;
+      }
+      case PONNI_LAYER_REDUCE: {
+        int const op = static_cast<int>(d.attr[0]);
+        if (d.attr[0] != op || op < PONNI_REDUCE_SUM || op > PONNI_REDUCE_PROD)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "unknown reduction");
+        if (d.n_out != 1) return fail(PONNI_ERR_INVALID_MODEL, where + "a reduction has one output");
+        break;
+      }
+      case PONNI_LAYER_UNARY: {
+        int const op = static_cast<int>(d.attr[0]);
+        if (d.attr[0] != op || op < PONNI_UNARY_ABS || op > PONNI_UNARY_SELU)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "unknown unary operation");
+        if (op == PONNI_UNARY_CELU && !(d.attr[1] != 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "Celu alpha must be nonzero");
+        break;
+      }
+      case PONNI_LAYER_CONST_BINARY: {
+        int const op = static_cast<int>(d.attr[0]);
+        if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_POW)
+          return fail(PONNI_ERR_INVALID_MODEL, where + "unknown binary operation");
+        break;
+      }
       case PONNI_LAYER_BINOP_ADD:
       case PONNI_LAYER_BINOP_CONCATENATE:
       case PONNI_LAYER_BINOP_PROJECTION_ADD: {
@@ -161,6 +222,24 @@ Step make_step(ponni_layer_desc const& d) {
     case PONNI_LAYER_HARD_SIGMOID: s.act = ACT_HARD_SIGMOID; s.a = float(d.attr[0]); s.b = float(d.attr[1]); break;
     case PONNI_LAYER_HARD_SWISH: s.act = ACT_HARD_SWISH; break;
     case PONNI_LAYER_MISH: s.act = ACT_MISH; break;
+    case PONNI_LAYER_UNARY:
+      s.act = ACT_ABS + static_cast<int>(d.attr[0]);  // ponni_unary_op order
+      s.a = float(d.attr[1]);
+      s.b = float(d.attr[2]);
+      break;
+    case PONNI_LAYER_CONST_BINARY: {
+      bool const left = d.flags & PONNI_FLAG_CONST_LEFT;
+      switch (static_cast<int>(d.attr[0])) {
+        case PONNI_BINARY_ADD: s.act = ACT_BIAS; break;
+        case PONNI_BINARY_SUB: s.act = left ? ACT_RSUB_C : ACT_SUB_C; break;
+        case PONNI_BINARY_MUL: s.act = ACT_MUL_C; break;
+        case PONNI_BINARY_DIV: s.act = left ? ACT_RDIV_C : ACT_DIV_C; break;
+        case PONNI_BINARY_MIN: s.act = left ? ACT_RMIN_C : ACT_MIN_C; break;
+        case PONNI_BINARY_MAX: s.act = left ? ACT_RMAX_C : ACT_MAX_C; break;
+        default: s.act = left ? ACT_RPOW_C : ACT_POW_C; break;
+      }
+      break;
+    }
     default: break;
   }
   return s;
@@ -177,6 +256,8 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
     case PONNI_PATH_NARROW:
       switch (d.kind) {
         case PONNI_LAYER_MATVEC: return int64_t(W) * W;
+        case PONNI_LAYER_DENSE: return int64_t(W) * W + ((d.flags & PONNI_FLAG_DENSE_BIAS) ? W : 0);
+        case PONNI_LAYER_CONST_BINARY: return W;
         case PONNI_LAYER_BIAS: return W;
         case PONNI_LAYER_LAYER_NORM: return 2 * W;
         case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(W) * W + W;
@@ -191,6 +272,10 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
         auto steps = [&](int n) { return (tiles(n) + 1) / 2; };
         switch (d.kind) {
           case PONNI_LAYER_MATVEC: return int64_t(steps(d.n_in)) * tiles(d.n_out) * 256;
+          case PONNI_LAYER_DENSE:
+            return int64_t(steps(d.n_in)) * tiles(d.n_out) * 256 +
+                   ((d.flags & PONNI_FLAG_DENSE_BIAS) ? round_up(d.n_out, 16) : 0);
+          case PONNI_LAYER_CONST_BINARY:
           case PONNI_LAYER_BIAS: return round_up(d.n_in, 16);
           case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
           case PONNI_LAYER_BINOP_PROJECTION_ADD:
@@ -200,6 +285,10 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
       }
       switch (d.kind) {
         case PONNI_LAYER_MATVEC: return int64_t(tiles(d.n_in)) * tiles(d.n_out) * 256;
+        case PONNI_LAYER_DENSE:
+          return int64_t(tiles(d.n_in)) * tiles(d.n_out) * 256 +
+                 ((d.flags & PONNI_FLAG_DENSE_BIAS) ? round_up(d.n_out, 16) : 0);
+        case PONNI_LAYER_CONST_BINARY:
         case PONNI_LAYER_BIAS: return round_up(d.n_in, 16);
         case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
         case PONNI_LAYER_BINOP_PROJECTION_ADD:
@@ -209,6 +298,15 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
     }
     default:
       return param_count(d);
+  }
+}
+
+// Packed length of a per-feature vector of n features in the path's layout.
+int64_t vec_size(ponni_plan_s const& p, int n) {
+  switch (p.path) {
+    case PONNI_PATH_GENERIC: return n;
+    case PONNI_PATH_NARROW: return p.width_class;
+    default: return round_up(n, 16);
   }
 }
 
@@ -236,17 +334,26 @@ void lower(ponni_plan_s& p) {
     op.n_out = d.n_out;
     op.slot = d.slot;
     op.woff = static_cast<int32_t>(p.layer_param_offset[i]);
-    if (d.kind == PONNI_LAYER_MATVEC) {
+    if (is_dense(d.kind)) {
       int end = i + 1;
       while (end < L && is_pointwise(p.layers[end].kind)) end++;
       op.code = OP_DENSE;
       op.epi_begin = static_cast<int32_t>(p.steps.size());
+      op.epi_count = end - (i + 1);
+      if (d.kind == PONNI_LAYER_DENSE && (d.flags & PONNI_FLAG_DENSE_BIAS)) {
+        // Generated Dense: its bias (stored after W) seeds the sum.
+        Step s{};
+        s.act = ACT_BIAS;
+        s.off = static_cast<int32_t>(p.layer_param_offset[i] + packed_size(p, d) - vec_size(p, d.n_out));
+        p.steps.push_back(s);
+        op.epi_count++;
+        op.aux = DENSE_BIAS_FIRST;
+      }
       for (int j = i + 1; j < end; j++) {
         Step s = make_step(p.layers[j]);
         s.off = static_cast<int32_t>(p.layer_param_offset[j]);
         p.steps.push_back(s);
       }
-      op.epi_count = end - (i + 1);
       op.n_out = p.layers[end - 1].n_out;
       p.num_fused_blocks++;
       if (i == 0) {
@@ -298,12 +405,20 @@ void lower(ponni_plan_s& p) {
       case PONNI_LAYER_BINOP_PROJECTION_ADD: {
         op.code = OP_PROJ_ADD;
         op.aux = d.n_aux;
-        int64_t const wsize = packed_size(p, d) - (p.path == PONNI_PATH_GENERIC ? d.n_in
-                                                   : p.path == PONNI_PATH_NARROW ? p.width_class
-                                                                                 : round_up(d.n_in, 16));
-        op.boff = static_cast<int32_t>(op.woff + wsize);
+        op.boff = static_cast<int32_t>(op.woff + packed_size(p, d) - vec_size(p, d.n_in));
         break;
       }
+      case PONNI_LAYER_LOAD_STATE: op.code = OP_LOAD; break;
+      case PONNI_LAYER_BINARY:
+        op.code = OP_BINARY;
+        op.aux = static_cast<int>(d.attr[0]) | ((d.flags & PONNI_FLAG_SAVED_LEFT) ? BIN_SAVED_LEFT : 0) |
+                 (d.n_aux == 1 && d.n_out > 1 ? BIN_SAVED_SCALAR : 0) |
+                 (d.n_in == 1 && d.n_out > 1 ? BIN_STATE_SCALAR : 0);
+        break;
+      case PONNI_LAYER_REDUCE:
+        op.code = OP_REDUCE;
+        op.aux = static_cast<int>(d.attr[0]);
+        break;
       default: {  // lone pointwise layer
         op.code = OP_POINTWISE;
         op.epi_begin = static_cast<int32_t>(p.steps.size());
@@ -339,6 +454,9 @@ void lower(ponni_plan_s& p) {
       op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
       op.dst = BUF_OUTPUT;
     }
+    // A load replaces the state with a saved one: it reads the slot and
+    // writes where the state lives (or the output).
+    if (d.kind == PONNI_LAYER_LOAD_STATE) op.src = BUF_SAVED + d.slot;
     p.ops.push_back(op);
     i++;
   }
@@ -365,13 +483,18 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
     std::vector<double> const& src = p.params[i];
     double* dst = out.data() + p.layer_param_offset[i];
     auto rnd = [&](double v) { return round_to_dtype(v, p.dtype); };
-    // Dense weights W [K, N] (row k, column o) in the path's layout.
-    auto pack_dense = [&](double const* w, int K, int N, double* o) {
+    // Dense weights W [K, N] (row k, column o) in the path's layout; a
+    // transposed source holds W^T [N, K] (generated Dense, "output_input").
+    auto pack_dense = [&](double const* wsrc, int K, int N, double* o, bool transposed = false) {
+      auto w = [&](int64_t idx) {
+        int64_t const k = idx / N, n = idx % N;
+        return transposed ? wsrc[n * K + k] : wsrc[idx];
+      };
       if (p.path == PONNI_PATH_GENERIC) {
-        for (int64_t e = 0; e < int64_t(K) * N; e++) o[e] = rnd(w[e]);
+        for (int64_t e = 0; e < int64_t(K) * N; e++) o[e] = rnd(w(e));
       } else if (p.path == PONNI_PATH_NARROW) {
         for (int k = 0; k < K; k++)
-          for (int n = 0; n < N; n++) o[k * W + n] = rnd(w[int64_t(k) * N + n]);
+          for (int n = 0; n < N; n++) o[k * W + n] = rnd(w(int64_t(k) * N + n));
       } else {
         // A fragment of v_mfma_f32_16x16x4f32 for output tile mo and input
         // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16].
@@ -382,7 +505,7 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
               for (int v = 0; v < 4; v++) {
                 int const k = 16 * m + 4 * (l >> 4) + v;
                 int const n = 16 * mo + (l & 15);
-                double val = (k < K && n < N) ? rnd(w[int64_t(k) * N + n]) : 0.0;
+                double val = (k < K && n < N) ? rnd(w(int64_t(k) * N + n)) : 0.0;
                 o[((int64_t(mo) * TK + m) * 64 + l) * 4 + v] = val;
               }
       }
@@ -391,6 +514,14 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
       case PONNI_LAYER_MATVEC:
         pack_dense(src.data(), d.n_in, d.n_out, dst);
         break;
+      case PONNI_LAYER_DENSE:
+        pack_dense(src.data(), d.n_in, d.n_out, dst, true);
+        if (d.flags & PONNI_FLAG_DENSE_BIAS) {
+          double* b = dst + packed_size(p, d) - vec_size(p, d.n_out);
+          for (int f = 0; f < d.n_out; f++) b[f] = rnd(src[int64_t(d.n_out) * d.n_in + f]);
+        }
+        break;
+      case PONNI_LAYER_CONST_BINARY:
       case PONNI_LAYER_BIAS:
         for (int f = 0; f < d.n_in; f++) dst[f] = rnd(src[f]);
         break;
@@ -403,10 +534,7 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
         break;
       }
       case PONNI_LAYER_BINOP_PROJECTION_ADD: {
-        int64_t const bsize = p.path == PONNI_PATH_GENERIC ? d.n_in
-                              : p.path == PONNI_PATH_NARROW ? W
-                                                            : round_up(d.n_in, 16);
-        int64_t const wsize = packed_size(p, d) - bsize;
+        int64_t const wsize = packed_size(p, d) - vec_size(p, d.n_in);
         pack_dense(src.data(), d.n_aux, d.n_in, dst);
         for (int f = 0; f < d.n_in; f++) dst[wsize + f] = rnd(src[int64_t(d.n_aux) * d.n_in + f]);
         break;
@@ -432,7 +560,7 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
     std::memcpy(&u, &f, 4);
     return u;
   };
-  auto pack_dense = [&](double const* w, int K, int N, uint32_t* o) {
+  auto pack_dense = [&](double const* w, int K, int N, uint32_t* o, bool transposed = false) {
     int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
     auto* h = reinterpret_cast<uint16_t*>(o);
     for (int mo = 0; mo < TN; mo++)
@@ -441,7 +569,8 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
           for (int j = 0; j < 8; j++) {
             int const k = 16 * (2 * t + j / 4) + 4 * (l >> 4) + (j & 3);
             int const n = 16 * mo + (l & 15);
-            h[((int64_t(mo) * TS + t) * 64 + l) * 8 + j] = (k < K && n < N) ? bits16(w[int64_t(k) * N + n]) : 0;
+            double const v = (k < K && n < N) ? (transposed ? w[int64_t(n) * K + k] : w[int64_t(k) * N + n]) : 0.0;
+            h[((int64_t(mo) * TS + t) * 64 + l) * 8 + j] = (k < K && n < N) ? bits16(v) : 0;
           }
   };
   int const L = static_cast<int>(p.layers.size());
@@ -451,6 +580,14 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
     uint32_t* dst = out.data() + p.layer_param_offset[i];
     switch (d.kind) {
       case PONNI_LAYER_MATVEC: pack_dense(src.data(), d.n_in, d.n_out, dst); break;
+      case PONNI_LAYER_DENSE:
+        pack_dense(src.data(), d.n_in, d.n_out, dst, true);
+        if (d.flags & PONNI_FLAG_DENSE_BIAS) {
+          uint32_t* b = dst + packed_size(p, d) - round_up(d.n_out, 16);
+          for (int f = 0; f < d.n_out; f++) b[f] = fbits(src[int64_t(d.n_out) * d.n_in + f]);
+        }
+        break;
+      case PONNI_LAYER_CONST_BINARY:
       case PONNI_LAYER_BIAS:
         for (int f = 0; f < d.n_in; f++) dst[f] = fbits(src[f]);
         break;
@@ -599,7 +736,8 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   for (int i = 0; i < num_layers; i++) {
     auto const& d = layers[i];
     p->params[i].assign(static_cast<size_t>(param_count(d)), 0.0);
-    max_width = std::max({max_width, d.n_in, d.n_out, d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD ? d.n_aux : 0});
+    max_width = std::max({max_width, d.n_in, d.n_out,
+                          d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD || d.kind == PONNI_LAYER_BINARY ? d.n_aux : 0});
     if (is_save(d.kind)) {
       p->num_slots = std::max(p->num_slots, d.slot + 1);
       p->saved_features[d.slot] = std::max(p->saved_features[d.slot], d.n_out);
@@ -611,13 +749,16 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     if (layers[i].kind == PONNI_LAYER_LAYER_NORM)
       for (int f = 0; f < layers[i].n_in; f++) p->params[i][f] = 1.0;
 
-  int const narrow = narrow_width_class(max_width);
-  int const mfma = mfma_width_class(dtype, max_width);
+  bool graph_ops = false;
+  for (int i = 0; i < num_layers; i++) graph_ops = graph_ops || is_graph_kind(layers[i].kind);
+  // NARROW and MFMA interpret layer-template chains only.
+  int const narrow = graph_ops ? 0 : narrow_width_class(max_width);
+  int const mfma = graph_ops ? 0 : mfma_width_class(dtype, max_width);
   char const* jit_env = std::getenv("PONNI_JIT");
   bool const jit_enabled = jit_env == nullptr || std::strcmp(jit_env, "0") != 0;
   int chosen = path;
   if (chosen == PONNI_PATH_AUTO) {
-    if (dtype != PONNI_F64 && max_width <= 8 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    if (dtype != PONNI_F64 && narrow > 0 && max_width <= 8 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
     else if (jit_enabled && fused_supports(*p)) chosen = PONNI_PATH_FUSED;
     else if (dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
     else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
@@ -625,7 +766,8 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   } else if (chosen == PONNI_PATH_NARROW) {
     if (dtype == PONNI_F64 || narrow == 0 || p->num_slots > kNarrowMaxSlots) {
       delete p;
-      return fail(PONNI_ERR_UNSUPPORTED, "NARROW path needs F32/F16/BF16, width <= 16 and at most 2 saved states");
+      return fail(PONNI_ERR_UNSUPPORTED,
+                  "NARROW path needs a layer-template chain in F32/F16/BF16, width <= 16 and at most 2 saved states");
     }
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {
@@ -636,7 +778,8 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {
       delete p;
       return fail(PONNI_ERR_UNSUPPORTED,
-                  "MFMA path needs F32/F16/BF16, width <= 256, at most 2 saved states and 16-aligned concatenation");
+                  "MFMA path needs a layer-template chain in F32/F16/BF16, width <= 256, at most 2 saved states and "
+                  "16-aligned concatenation");
     }
   }
   p->path = chosen;

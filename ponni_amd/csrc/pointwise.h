@@ -22,6 +22,10 @@ __device__ inline float d_erf(float x) { return erff(x); }
 __device__ inline double d_erf(double x) { return erf(x); }
 __device__ inline float d_sqrt(float x) { return sqrtf(x); }
 __device__ inline double d_sqrt(double x) { return sqrt(x); }
+__device__ inline float d_pow(float x, float y) { return powf(x, y); }
+__device__ inline double d_pow(double x, double y) { return pow(x, y); }
+__device__ inline float d_abs(float x) { return fabsf(x); }
+__device__ inline double d_abs(double x) { return fabs(x); }
 
 // ponni_Relu.h:49-51
 template <class T> __device__ inline T act_relu(T x) { return x > T(0) ? x : T(0); }
@@ -85,8 +89,51 @@ template <class T> __device__ inline T act_mish(T x) {
   return x * d_tanh(sp);
 }
 
-// Apply one parameter-free (or scalar-parameter) activation to every element
-// visited by `each`.  The switch sits outside the element loop so each case is
+// Unary operations of generated graphs, kokkos_nn/emitter.py:218-258.
+template <class T> __device__ inline T act_softsign(T x) { return x / (T(1) + d_abs(x)); }
+template <class T> __device__ inline T act_celu(T x, T alpha) {
+  return x > T(0) ? x : alpha * (d_exp(x / alpha) - T(1));
+}
+template <class T> __device__ inline T act_thresholded_relu(T x, T alpha) { return x > alpha ? x : T(0); }
+template <class T> __device__ inline T act_selu_ag(T x, T alpha, T gamma) {
+  return gamma * (x > T(0) ? x : alpha * (d_exp(x) - T(1)));
+}
+
+// Element-wise op of the state v with a constant c, emitter.py:261-275.
+template <class T> __device__ inline T act_const(int act, T v, T c) {
+  switch (act) {
+    case ACT_BIAS: return v + c;
+    case ACT_SUB_C: return v - c;
+    case ACT_RSUB_C: return c - v;
+    case ACT_MUL_C: return v * c;
+    case ACT_DIV_C: return v / c;
+    case ACT_RDIV_C: return c / v;
+    case ACT_MIN_C: return v < c ? v : c;
+    case ACT_RMIN_C: return c < v ? c : v;
+    case ACT_MAX_C: return v > c ? v : c;
+    case ACT_RMAX_C: return c > v ? c : v;
+    case ACT_POW_C: return d_pow(v, c);
+    case ACT_RPOW_C: return d_pow(c, v);
+    default: return v;
+  }
+}
+
+// Tensor-tensor binary operation of generated graphs, emitter.py:261-275.
+template <class T> __device__ inline T apply_binary(int op, T l, T r) {
+  switch (op) {
+    case 0: return l + r;
+    case 1: return l - r;
+    case 2: return l * r;
+    case 3: return l / r;
+    case 4: return l < r ? l : r;
+    case 5: return l > r ? l : r;
+    default: return d_pow(l, r);
+  }
+}
+
+// Apply one parameter-free (or scalar-parameter) layer-template activation
+// to every element visited by `each` (the NARROW and MFMA families, which run
+// template chains only).  The switch sits outside the element loop so each case is
 // one straight-line loop.  `each(f)` must call f(float&) on every element.
 template <class T, class Each>
 __device__ inline void map_activation(int act, T a, T b, Each&& each) {
@@ -108,11 +155,23 @@ __device__ inline void map_activation(int act, T a, T b, Each&& each) {
   }
 }
 
-// Scalar form for the per-sample generic kernel.
+// Scalar form for the per-sample generic kernel; `bias` is the step's
+// parameter element (bias or constant operand) for the feature.
 template <class T>
 __device__ inline T apply_step(int act, T x, T bias, T a, T b) {
   switch (act) {
     case ACT_BIAS: return x + bias;  // ponni_Bias.h:66-68
+    case ACT_ABS: return d_abs(x);
+    case ACT_NEG: return -x;
+    case ACT_EXP: return d_exp(x);
+    case ACT_LOG: return d_log(x);
+    case ACT_SQRT: return d_sqrt(x);
+    case ACT_RECIPROCAL: return T(1) / x;
+    case ACT_SOFTSIGN: return act_softsign(x);
+    case ACT_CELU: return act_celu(x, a);
+    case ACT_THRESHOLDED_RELU: return act_thresholded_relu(x, a);
+    case ACT_ERF: return d_erf(x);
+    case ACT_SELU_AG: return act_selu_ag(x, a, b);
     case ACT_RELU: return act_relu(x);
     case ACT_LEAKY_RELU: return act_leaky_relu(x, a);
     case ACT_ELU: return act_elu(x, a);
@@ -126,7 +185,7 @@ __device__ inline T apply_step(int act, T x, T bias, T a, T b) {
     case ACT_HARD_SIGMOID: return act_hard_sigmoid(x, a, b);
     case ACT_HARD_SWISH: return act_hard_swish(x);
     case ACT_MISH: return act_mish(x);
-    default: return x;
+    default: return act_has_param(act) ? act_const(act, x, bias) : x;
   }
 }
 

@@ -29,8 +29,37 @@ enum Act : int32_t {
   ACT_SOFTPLUS = 11,     // a = beta                         ponni_Softplus.h:44-50
   ACT_HARD_SIGMOID = 12, // a = alpha, b = beta              ponni_HardSigmoid.h:52-56
   ACT_HARD_SWISH = 13,   //                                  ponni_HardSwish.h:42-47
-  ACT_MISH = 14          //                                  ponni_Mish.h:44-52
+  ACT_MISH = 14,         //                                  ponni_Mish.h:44-52
+  // Unary operations of generated graphs (kokkos_nn/emitter.py:218-258).
+  ACT_ABS = 20,
+  ACT_NEG = 21,
+  ACT_EXP = 22,
+  ACT_LOG = 23,
+  ACT_SQRT = 24,
+  ACT_RECIPROCAL = 25,
+  ACT_SOFTSIGN = 26,          // v / (1 + |v|)
+  ACT_CELU = 27,              // v > 0 ? v : a*(exp(v/a)-1)
+  ACT_THRESHOLDED_RELU = 28,  // v > a ? v : 0
+  ACT_ERF = 29,
+  ACT_SELU_AG = 30,           // b * (v > 0 ? v : a*(exp(v)-1)), generated Selu(alpha, gamma)
+  // Element-wise op with a constant vector c = params[off + f] (generated
+  // Add/Sub/Mul/Div/Min/Max/Pow with one constant operand, emitter.py:261-275).
+  // ACT_BIAS doubles as v + c.
+  ACT_SUB_C = 40,   // v - c
+  ACT_RSUB_C = 41,  // c - v
+  ACT_MUL_C = 42,   // v * c
+  ACT_DIV_C = 43,   // v / c
+  ACT_RDIV_C = 44,  // c / v
+  ACT_MIN_C = 45,   // v < c ? v : c
+  ACT_RMIN_C = 46,  // c < v ? c : v
+  ACT_MAX_C = 47,   // v > c ? v : c
+  ACT_RMAX_C = 48,  // c > v ? c : v
+  ACT_POW_C = 49,   // pow(v, c)
+  ACT_RPOW_C = 50   // pow(c, v)
 };
+
+// Steps that read a per-feature parameter vector at Step::off.
+constexpr bool act_has_param(int act) { return act == ACT_BIAS || (act >= ACT_SUB_C && act <= ACT_RPOW_C); }
 
 struct Step {
   int32_t act;   // Act
@@ -49,8 +78,23 @@ enum OpCode : int32_t {
   OP_SAVE = 7,        // saved[slot] = state                        ponni_Save_State.h:57-67
   OP_ADD = 8,         // state = state + saved[slot]                ponni_Binop_Add.h:57-68
   OP_CONCAT = 9,      // state = [state; saved] or [saved; state]   ponni_Binop_Concatenate.h:63-86
-  OP_PROJ_ADD = 10    // state = state + (b + W^T saved[slot])      ponni_Binop_Projection_Add.h:81-95
+  OP_PROJ_ADD = 10,   // state = state + (b + W^T saved[slot])      ponni_Binop_Projection_Add.h:81-95
+  // Generated-graph operations (kokkos_nn/emitter.py).
+  OP_LOAD = 11,       // state = saved[slot]
+  OP_BINARY = 12,     // state = op(state, saved) / op(saved, state); aux = BinaryAux bits
+  OP_REDUCE = 13      // state[0] = reduce(state[0..n_in)); aux = ponni_reduce_op   emitter.py:475-547
 };
+
+// OP_BINARY's aux: bits 0-7 ponni_binary_op, then these flags.
+enum BinaryAux : int32_t {
+  BIN_SAVED_LEFT = 1 << 8,    // saved operand is the left one
+  BIN_SAVED_SCALAR = 1 << 9,  // saved operand has one feature (broadcast)
+  BIN_STATE_SCALAR = 1 << 10  // state operand has one feature (broadcast)
+};
+
+// OP_DENSE's aux: the first epilogue step is a bias that seeds the sum
+// (generated Dense: sum = bias; sum += W x, emitter.py:701-710).
+constexpr int32_t DENSE_BIAS_FIRST = 1;
 
 // Buffers of the generic (HBM scratch) path, chosen at plan time exactly as
 // traverse_mixed_batch_parallel picks them (ponni_Inference.h:453-555).
@@ -67,7 +111,8 @@ struct Op {
   int32_t n_in;       // features read from the main state
   int32_t n_out;      // features written to the main state
   int32_t slot;       // saved-state slot (SAVE/ADD/CONCAT/PROJ_ADD)
-  int32_t aux;        // CONCAT: 1 = after; PROJ_ADD: NSAVE
+  int32_t aux;        // CONCAT: 1 = after; PROJ_ADD: NSAVE; BINARY: BinaryAux; REDUCE: op;
+                      // DENSE: DENSE_BIAS_FIRST
   int32_t woff;       // offset of W / gamma in the path's parameter buffer
   int32_t boff;       // offset of bias / beta
   int32_t epi_begin;  // first Step of the epilogue

@@ -540,7 +540,7 @@ class PonniFile {
 template <class Scalar>
 inline bool write_ponni_file(std::string const& path, std::vector<PonniTensorSpec> specs,
                              std::string const& model_fingerprint, Scalar const* source, std::string* error = nullptr,
-                             std::string const& target = "ponni") {
+                             std::string const& target = "ponni", std::string const& source_framework = "ponni-cpp") {
   static_assert(std::is_same_v<Scalar, float> || std::is_same_v<Scalar, double>, "F32 or F64 payloads");
   auto fail = [&](std::string const& m) {
     if (error) *error = m;
@@ -564,7 +564,7 @@ inline bool write_ponni_file(std::string const& path, std::vector<PonniTensorSpe
   header += "\"ponni.schema_fingerprint\":" + detail::json_quote(detail::schema_fingerprint(tensors)) + ",";
   header += "\"ponni.payload_checksum_fnv1a64\":" +
             detail::json_quote(ponni_fnv1a64_string(ponni_fnv1a64(payload.data(), payload.size()))) + ",";
-  header += "\"ponni.source_framework\":\"ponni-cpp\",";
+  header += "\"ponni.source_framework\":" + detail::json_quote(source_framework) + ",";
   header += "\"ponni.target\":" + detail::json_quote(target) + "}";
   for (auto const& t : tensors) {
     header += "," + detail::json_quote(t.name) + ":{\"dtype\":" + detail::json_quote(t.dtype) + ",\"shape\":[";

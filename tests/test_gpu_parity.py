@@ -153,7 +153,7 @@ def config_input(cfg, B, dev="cuda:0"):
     return x
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
 @pytest.mark.parametrize("path", ["auto", "mfma", "generic"])
 def test_configs_small_batch(cuda, name, path):
     """Each BASELINE config (with nonzero biases) vs the oracle."""
@@ -177,7 +177,7 @@ def test_configs_small_batch(cuda, name, path):
         check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
 def test_configs_full_size_columns(cuda, name):
     """Full BASELINE batch: samples are independent, so a strided subset of
     columns of the full-size output must equal the oracle on those columns."""
