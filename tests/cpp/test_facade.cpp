@@ -1,0 +1,288 @@
+// C++ facade tests (ponni_amd/include/ponni.h): the reference's own C++ unit
+// tests restated against the facade.  `--cpu` runs only the checks that touch
+// no device (model construction, scratch planning, parameters, fingerprints,
+// .ponni files, 16-bit conversions); without it the forward passes run on
+// the GPU as well.
+//
+// Known answers (reference files relative to its root):
+//   unit/core/test_core_unit.cpp:200-221   first model -> (4, 4), no scratch
+//   unit/core/test_core_unit.cpp:262-326   four fused blocks, closed form, tmp 7 / 3
+//   unit/core/test_core_unit.cpp:331-378   Softmax barrier -> (tanh 1, 0), tmp 3 / 0
+//   unit/core/test_core_unit.cpp:516-546   Matvec [in, out] layout -> 36, 39, 42
+//   unit/core/test_core_unit.cpp:814-872   projection skip -> (5.1, 7.2, 7.8)
+//   unit/core/test_template_coverage.cpp:414-500  multi-slot save -> {0,6,-2,6,-2,3}
+//   unit/core/test_template_coverage.cpp:503-525  half / bhalf factories -> 5
+//   unit/performance_benchmark/performance_benchmark.cpp:21-53  mean 15.4
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ponni.h"
+
+namespace {
+
+int g_failures = 0;
+int g_checks = 0;
+
+#define CHECK(cond)                                                              \
+  do {                                                                           \
+    g_checks++;                                                                  \
+    if (!(cond)) {                                                               \
+      g_failures++;                                                              \
+      std::fprintf(stderr, "FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);     \
+    }                                                                            \
+  } while (0)
+
+bool near(double a, double b, double tol) { return std::fabs(a - b) <= tol; }
+
+template <class real>
+ponni::View<real> device_matrix(int rows, int cols, std::vector<float> const& v) {
+  ponni::View<real> d("x", rows, cols);
+  std::vector<real> h(v.begin(), v.end());
+  d.copy_from_host(h);
+  return d;
+}
+
+template <class V>
+std::vector<double> host(V const& v) {
+  auto h = v.copy_to_host();
+  return std::vector<double>(h.begin(), h.end());
+}
+
+ponni::Matrix<float> ones(int r, int c) { return ponni::Matrix<float>(r, c, 1.0f); }
+
+auto four_block_model() {
+  using namespace ponni;
+  return create_inference_model(
+      Matvec<float>(ones(2, 5)), Bias<float>(std::vector<float>(5, 0.5f)), Relu<float>(5), Tanh<float>(5),
+      Matvec<float>(ones(5, 3)), Bias<float>(std::vector<float>(3, -0.25f)), Sigmoid<float>(3),
+      Matvec<float>(ones(3, 7)), Bias<float>(std::vector<float>(7, 0.1f)), LeakyRelu<float>(7, 0.2f),
+      Matvec<float>(ones(7, 2)), Bias<float>(std::vector<float>(2, -0.2f)), HardSwish<float>(2));
+}
+
+double four_block_closed_form(double x0, double x1) {
+  double const s = x0 + x1;
+  double const h1 = std::tanh(std::max(0.0, s + 0.5));
+  double const h2 = 1.0 / (1.0 + std::exp(-(5 * h1 - 0.25)));
+  double const d3 = 3 * h2 + 0.1;
+  double const h3 = d3 > 0 ? d3 : 0.2 * d3;
+  double const d4 = 7 * h3 - 0.2;
+  return d4 <= -3 ? 0.0 : d4 >= 3 ? d4 : d4 * (d4 + 3) / 6;
+}
+
+// ---- host-only checks ----------------------------------------------------------------
+
+void test_structure_and_planning() {
+  using namespace ponni;
+  auto first = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{1, 1}),
+                                      LeakyRelu<float>(2, 0.1f));
+  CHECK(first.get_num_inputs() == 2 && first.get_num_outputs() == 2);
+  CHECK(first.get_planned_temporary_size<0>() == 0 && first.get_planned_temporary_size<1>() == 0);
+  CHECK(first.get_num_fused_dense_blocks() == 1);
+  auto four = four_block_model();
+  CHECK(four.get_planned_temporary_size<0>() == 7 && four.get_planned_temporary_size<1>() == 3);
+  CHECK(four.get_num_fused_dense_blocks() == 4);
+  four.validate();
+  auto soft = create_inference_model(Matvec<float>(ones(2, 3)), Bias<float>(std::vector<float>{0, 1, 2}),
+                                     Relu<float>(3), Softmax<float>(3), Matvec<float>(ones(3, 2)),
+                                     Bias<float>(std::vector<float>{0, -1}), Tanh<float>(2));
+  CHECK(soft.get_planned_temporary_size<0>() == 3 && soft.get_planned_temporary_size<1>() == 0);
+  auto res = create_inference_model(Save_State<0>(2), Relu<float>(2), Binop_Concatenate<0>(2, 4, true),
+                                    Save_State<1>(4), Relu<float>(4), Binop_Add<1>(4),
+                                    Binop_Concatenate<0>(4, 6, true));
+  CHECK(res.get_num_saved_states() == 2);
+  res.validate();
+}
+
+void test_parameters_and_fingerprint() {
+  using namespace ponni;
+  ponni::Matrix<float> w(2, 3, std::vector<float>{1, 2, 3, 4, 5, 6});
+  auto m = create_inference_model(Matvec<float>(w), Bias<float>(std::vector<float>{7, 8, 9}), Relu<float>(3),
+                                  LayerNorm<float>(3), Matvec<float>(ones(3, 1), false));
+  CHECK(m.get_num_trainable_parameters() == 6 + 3 + 6);  // the last Matvec is frozen
+  auto p = m.get_trainable_parameters();
+  std::vector<float> want{1, 2, 3, 4, 5, 6, 7, 8, 9, 1, 1, 1, 0, 0, 0};
+  CHECK(p.size() == want.size() && std::equal(p.begin(), p.end(), want.begin()));
+  std::vector<float> q(15);
+  for (int i = 0; i < 15; i++) q[i] = 0.5f * i;
+  m.set_trainable_parameters(q);
+  p = m.get_trainable_parameters();
+  CHECK(std::equal(p.begin(), p.end(), q.begin()));
+  CHECK(m.get_layer<1>().params[0] == 3.0);
+  // "ponni-template-model-v1\n" + "I\tlabel\tnin\tnout\tntrainable\n" (ponni_Inference.h:270-288)
+  std::string text = "ponni-template-model-v1\n0\tMatvec\t2\t3\t6\n1\tBias\t3\t3\t3\n2\tReLU\t3\t3\t0\n"
+                     "3\tLayerNorm\t3\t3\t6\n4\tMatvec\t3\t1\t0\n";
+  std::string fp = ponni::ponni_fnv1a64_string(
+      ponni::ponni_fnv1a64(reinterpret_cast<unsigned char const*>(text.data()), text.size()));
+  CHECK(m.weight_schema_fingerprint() == fp);
+}
+
+void test_weights_files() {
+  using namespace ponni;
+  char const* path = "/tmp/ponni_facade_test.ponni";
+  auto a = create_inference_model(Matvec<float>(ponni::Matrix<float>(2, 2, std::vector<float>{1, 2, 3, 4})),
+                                  Bias<float>(std::vector<float>{5, 6}));
+  std::string err;
+  CHECK(a.save_weights(path, &err));
+  auto b = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{0, 0}));
+  CHECK(b.load_weights(path, &err));
+  auto p = b.get_trainable_parameters();
+  CHECK(p.size() == 6 && p[0] == 1 && p[3] == 4 && p[5] == 6);
+  auto c = create_inference_model(Matvec<float>(ones(2, 2)), Relu<float>(2), Bias<float>(std::vector<float>{0, 0}));
+  CHECK(!c.load_weights(path, &err));
+  CHECK(err.find("fingerprint") != std::string::npos);
+  auto d = create_inference_model(Relu<float>(2));
+  CHECK(!d.load_weights(path, &err));
+  CHECK(err == "cannot load weights into a model with no trainable parameters");
+  CHECK(!d.save_weights(path, &err));
+  CHECK(err == "cannot save weights from a model with no trainable parameters");
+  auto e = create_inference_model_double_precision(Matvec<double>(ones(2, 2)), Bias<double>(std::vector<double>{0, 0}));
+  CHECK(!e.load_weights(path, &err));  // F32 file, F64 model: dtype mismatch
+  std::remove(path);
+}
+
+void test_sixteen_bit_types() {
+  using ponni::bhalf_t;
+  using ponni::half_t;
+  CHECK(half_t(1.0f).bits == 0x3c00 && half_t(-2.0f).bits == 0xc000);
+  CHECK(half_t(65504.0f).bits == 0x7bff && half_t(65520.0f).bits == 0x7c00);
+  CHECK(half_t(std::ldexp(1.0f, -24)).bits == 0x0001 && half_t(std::ldexp(1.0f, -25)).bits == 0x0000);
+  CHECK(float(half_t(0.1f)) == 0.0999755859375f);
+  CHECK(half_t(1.0f + std::ldexp(1.0f, -11)).bits == 0x3c00);       // tie to even
+  CHECK(half_t(1.0f + 3 * std::ldexp(1.0f, -11)).bits == 0x3c02);   // tie to even (up)
+  CHECK(bhalf_t(1.0f).bits == 0x3f80 && float(bhalf_t(3.0f)) == 3.0f);
+  CHECK(float(bhalf_t(1.00390625f)) == 1.0f);  // tie to even
+}
+
+// ---- device checks -----------------------------------------------------------------------
+
+void test_known_answers_gpu() {
+  using namespace ponni;
+  {  // first model
+    auto m = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{1, 1}),
+                                    LeakyRelu<float>(2, 0.1f));
+    auto x = device_matrix<float>(2, 1, {1, 2});
+    auto y = host(m.forward_batch_parallel(x));
+    CHECK(near(y[0], 4, 1e-6) && near(y[1], 4, 1e-6));
+  }
+  {  // Matvec layout
+    auto m = create_inference_model(Matvec<float>(ponni::Matrix<float>(2, 3, std::vector<float>{10, 11, 12, 13, 14, 15})));
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {1, 2})));
+    CHECK(y[0] == 36 && y[1] == 39 && y[2] == 42);
+  }
+  {  // four blocks
+    auto m = four_block_model();
+    std::vector<float> xv{1, -2, 0, 0.3f, 2, 0.5f, 0, -1};
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 4, xv)));
+    for (int b = 0; b < 4; b++) {
+      double const e = four_block_closed_form(xv[b], xv[4 + b]);
+      CHECK(near(y[b], e, 1e-4) && near(y[4 + b], e, 1e-4));
+    }
+  }
+  {  // Softmax barrier
+    auto m = create_inference_model(Matvec<float>(ones(2, 3)), Bias<float>(std::vector<float>{0, 1, 2}),
+                                    Relu<float>(3), Softmax<float>(3), Matvec<float>(ones(3, 2)),
+                                    Bias<float>(std::vector<float>{0, -1}), Tanh<float>(2));
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 2, {0.5f, 0.5f, 0.5f, 0.5f})));
+    CHECK(near(y[0], std::tanh(1.0), 1e-5) && near(y[1], std::tanh(1.0), 1e-5));
+    CHECK(near(y[2], 0.0, 1e-5) && near(y[3], 0.0, 1e-5));
+  }
+  {  // multi-slot save
+    auto m = create_inference_model(Save_State<0>(2), Relu<float>(2), Binop_Concatenate<0>(2, 4, true),
+                                    Save_State<1>(4), Relu<float>(4), Binop_Add<1>(4),
+                                    Binop_Concatenate<0>(4, 6, true));
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {-2, 3})));
+    std::vector<double> want{0, 6, -2, 6, -2, 3};
+    CHECK(y == want);
+  }
+  {  // projection skip
+    auto m = create_inference_model(
+        Save_State<0>(2), Matvec<float>(ponni::Matrix<float>(2, 3, std::vector<float>{0.25f, 0, 0, 0, 0.4f, 0.6f})),
+        Binop_Projection_Add<0>(ponni::Matrix<float>(2, 3, std::vector<float>{1, 0, 0.5f, 0, 1, 0.5f}),
+                                std::vector<float>{0.1f, 0.2f, 0.3f}));
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {4, 5})));
+    CHECK(near(y[0], 5.1, 1e-5) && near(y[1], 7.2, 1e-5) && near(y[2], 7.8, 1e-5));
+  }
+  {  // performance benchmark: mean 15.4
+    auto m = create_inference_model(Matvec<float>(ones(8, 8)), Bias<float>(std::vector<float>(8, 1.0f)),
+                                    LeakyRelu<float>(8, 0.1f), Matvec<float>(ones(8, 8)),
+                                    Bias<float>(std::vector<float>(8, 1.0f)), LeakyRelu<float>(8, 0.1f));
+    int const B = 1 << 16;
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(8, B, std::vector<float>(8 * B, 0.1f))));
+    double mean = 0;
+    for (double v : y) mean += v;
+    mean /= y.size();
+    CHECK(near(mean, 15.4, 1e-3));
+  }
+  {  // half / bhalf factories: W = (2, -1), x = (3, 1) -> 5
+    auto mh = create_inference_model_half_precision(Matvec<half_t>(ponni::Matrix<float>(2, 1, std::vector<float>{2, -1})));
+    auto yh = host(mh.forward_batch_parallel(device_matrix<half_t>(2, 1, {3, 1})));
+    CHECK(near(yh[0], 5.0, 2e-2));
+    auto mb = create_inference_model_bhalf_precision(Matvec<bhalf_t>(ponni::Matrix<float>(2, 1, std::vector<float>{2, -1})));
+    auto yb = host(mb.forward_batch_parallel(device_matrix<bhalf_t>(2, 1, {3, 1})));
+    CHECK(near(yb[0], 5.0, 5e-2));
+    auto md = create_inference_model_double_precision(Matvec<double>(ponni::Matrix<double>(2, 1, std::vector<double>{2, -1})));
+    ponni::View<double> xd("x", 2, 1);
+    xd.copy_from_host({3.0, 1.0});
+    auto yd = host(md.forward_batch_parallel(xd));
+    CHECK(yd[0] == 5.0);
+  }
+}
+
+void test_views_streams_capacity_gpu() {
+  using namespace ponni;
+  auto m = four_block_model();
+  int const B = 1000, LD = 1300;
+  std::vector<float> xv(2 * LD);
+  for (int i = 0; i < 2 * LD; i++) xv[i] = std::sin(0.01 * i);
+  auto xw = device_matrix<float>(2, LD, xv);
+  ponni::View<float> yw("y", 2, LD);
+  auto x = xw.columns(100, 100 + B);  // stride(0) = 1300 > extent(1)
+  auto y = yw.columns(100, 100 + B);
+  hipStream_t s;
+  CHECK(hipStreamCreate(&s) == hipSuccess);
+  auto ms = create_inference_model(s, Matvec<float>(ones(2, 5)), Bias<float>(std::vector<float>(5, 0.5f)),
+                                   Relu<float>(5), Tanh<float>(5), Matvec<float>(ones(5, 3)),
+                                   Bias<float>(std::vector<float>(3, -0.25f)), Sigmoid<float>(3),
+                                   Matvec<float>(ones(3, 7)), Bias<float>(std::vector<float>(7, 0.1f)),
+                                   LeakyRelu<float>(7, 0.2f), Matvec<float>(ones(7, 2)),
+                                   Bias<float>(std::vector<float>(2, -0.2f)), HardSwish<float>(2));
+  ms.forward_batch_parallel(x, y);
+  CHECK(hipStreamSynchronize(s) == hipSuccess);
+  auto yh = host(yw);
+  bool ok = true;
+  for (int b = 0; b < LD; b++) {
+    double const e = (b >= 100 && b < 100 + B) ? four_block_closed_form(xv[b], xv[LD + b]) : 0.0;
+    ok = ok && near(yh[b], e, 1e-4) && near(yh[LD + b], e, 1e-4);
+  }
+  CHECK(ok);
+  CHECK(ms.internal_state_capacity() == B);
+  ms.reallocate_internal_state(0);
+  CHECK(ms.internal_state_capacity() == 0);
+  CHECK(hipStreamDestroy(s) == hipSuccess);
+  // Parameter edits through get_layer + mark_modified reach the device.
+  auto one = create_inference_model(Matvec<float>(ones(2, 1)));
+  one.get_layer<0>().params = {3.0, 4.0};
+  one.get_layer<0>().mark_modified();
+  auto r = host(one.forward_batch_parallel(device_matrix<float>(2, 1, {1, 1})));
+  CHECK(r[0] == 7.0);
+  (void)m;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  bool const cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+  test_structure_and_planning();
+  test_parameters_and_fingerprint();
+  test_weights_files();
+  test_sixteen_bit_types();
+  if (!cpu_only) {
+    test_known_answers_gpu();
+    test_views_streams_capacity_gpu();
+  }
+  std::printf("%s: %d checks, %d failures\n", cpu_only ? "cpu" : "cpu+gpu", g_checks, g_failures);
+  return g_failures == 0 ? 0 : 1;
+}
