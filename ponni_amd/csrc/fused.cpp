@@ -221,7 +221,6 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   cfg.waves = 4;
-  cfg.columns_per_block = 4 * 16 * NT;
   // Register budget.  A live tile holds 8 registers per lane (fp32 with 2
   // column tiles, or 16-bit with 4); a dense op holds its input, its output
   // and its A-fragment ring.  Parameters small enough to live in registers
@@ -273,6 +272,31 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(w);
     if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
   }
+  // Waves per workgroup: LDS-staged parameters are copied once per
+  // workgroup, so when copies would cap the resident workgroups below the
+  // register-limited occupancy, fewer and larger workgroups share one copy.
+  {
+    int saved_per_wave = 0;  // bytes of LDS-resident saved states per wave
+    if (cfg.saved_in_lds)
+      for (int s = 0; s < kMaxSlots; s++) saved_per_wave += tiles(p.saved_features[s]) * NT * 64 * 16;
+    int const target = 4 * cfg.waves_per_simd;  // waves per CU the registers allow
+    int best = 0;
+    for (int w = 4; w <= 16; w += 4) {
+      int const per_block_lds = cfg.lds_bytes + w * saved_per_wave;
+      if (per_block_lds > 160 * 1024) break;
+      int const by_lds = per_block_lds > 0 ? (160 * 1024) / per_block_lds : 1 << 20;
+      int const blocks = std::min(by_lds, target / w);
+      if (blocks * w > best) {
+        best = blocks * w;
+        cfg.waves = w;
+      }
+    }
+  }
+  if (char const* w = std::getenv("PONNI_FUSED_WAVES")) {  // tuning override
+    int const v = std::atoi(w);
+    if (v == 4 || v == 8 || v == 12 || v == 16) cfg.waves = v;
+  }
+  cfg.columns_per_block = cfg.waves * 16 * NT;
 
   std::ostringstream o;
   std::string const IO = half ? E : std::string("float");
@@ -283,7 +307,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
-  o << "extern \"C\" __global__ __launch_bounds__(256, " << cfg.waves_per_simd << ") void " << fused_kernel_name(p)
+  o << "extern \"C\" __global__ __launch_bounds__(" << 64 * cfg.waves << ", " << cfg.waves_per_simd << ") void "
+    << fused_kernel_name(p)
     << "(float const* __restrict__ gparams, " << IO << " const* __restrict__ x, int64_t ldx, " << IO
     << "* __restrict__ y, int64_t ldy, int64_t batch) {\n";
   if (cfg.lds_bytes > 0) {
@@ -301,13 +326,13 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         slot_off[sl] = off;
         off += tiles(p.saved_features[sl]) * NT * 64;
       }
-    o << "  __shared__ floatx4 lds_saved[4][" << off << "];\n";
+    o << "  __shared__ floatx4 lds_saved[" << cfg.waves << "][" << off << "];\n";
     o << "  floatx4* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
   }
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
   o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
-  o << "    L.col0 = (tile * 4 + (threadIdx.x >> 6)) * " << 16 * NT << ";\n";
+  o << "    L.col0 = (tile * " << cfg.waves << " + (threadIdx.x >> 6)) * " << 16 * NT << ";\n";
   // Register-resident parameters may be hoisted out of the tile loop; otherwise
   // pin() hides the pointer's loop invariance so they are re-read per tile.
   o << (cfg.params_in_registers ? "    float const* __restrict__ P = P0;\n" : "    float const* __restrict__ P = pin(P0);\n");
@@ -318,8 +343,15 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
+  // The logistic family runs on the hardware transcendentals (fused_f32.h).
   auto act = [&](Step const& st) {
-    return half && st.act == ACT_TANH ? std::string("act_tanh_fast(v)") : act_expr(st);
+    switch (st.act) {
+      case ACT_TANH: return std::string("act_tanh_fast(v)");
+      case ACT_SIGMOID: return std::string("act_sigmoid_fast(v)");
+      case ACT_SILU: return std::string("act_silu_fast(v)");
+      case ACT_GELU_TANH: return std::string("act_gelu_tanh_fast(v)");
+      default: return act_expr(st);
+    }
   };
   // fp32 view of the state for barrier ops: the state itself (fp32 path) or a
   // widened copy that is rounded back afterwards (16-bit path).
@@ -606,6 +638,7 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
   p.fused_persistent = cfg.lds_bytes > 0 || cfg.params_in_registers;
   p.fused_columns_per_block = cfg.columns_per_block;
+  p.fused_waves = cfg.waves;
   return PONNI_OK;
 }
 
@@ -625,7 +658,8 @@ hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t 
   void* y = a.y;
   int64_t ldx = a.ld_x, ldy = a.ld_y, batch = a.batch;
   void* args[] = {&params, &x, &ldx, &y, &ldy, &batch};
-  return hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, 256, 1, 1, 0, stream, args, nullptr);
+  return hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, 64 * p.fused_waves, 1, 1, 0, stream, args,
+                               nullptr);
 }
 
 }  // namespace ponni_hip

@@ -40,15 +40,6 @@ struct H {
   typename Vec<E>::x4 v[T > 0 ? T : 1][NT];
 };
 
-// tanh(x) = 1 - 2 / (1 + 2^(2 x log2 e)): two hardware transcendentals
-// (v_exp_f32, v_rcp_f32); saturates to +-1 through exp2 -> inf / 0.  Its
-// error (a few fp32 ulp, absolute ~1e-7 near 0) is far below the binary16 /
-// bfloat16 rounding the result goes through.
-__device__ inline float act_tanh_fast(float x) {
-  float const e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 // Bias and tanh of one output tile in a single pass:
 // tanh(v + b) = 1 - 2 / (1 + 2^(k v + k b)), k = 2 log2(e); five VALU ops per
 // element, two of them transcendental.
@@ -73,7 +64,7 @@ template <int N, int NT, class E>
 __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   H<T, NT, E> s;
-  E const* __restrict__ xl = x + int64_t(4 * L.g) * ld + L.col0 + L.c;
+  E const* __restrict__ xl = x + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -90,7 +81,7 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
 
 template <int N, int T, int NT, class E>
 __device__ inline void store_rows_h(H<T, NT, E> const& s, E* __restrict__ y, int64_t ld, Lane const& L) {
-  E* __restrict__ yl = y + int64_t(4 * L.g) * ld + L.col0 + L.c;
+  E* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll

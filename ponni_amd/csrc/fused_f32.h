@@ -58,13 +58,55 @@ __device__ inline P const* pin(P const* p) {
   return p + z;
 }
 
+// ---- activations on the hardware transcendentals -------------------------
+// The FUSED kernels evaluate the logistic family through v_exp_f32 and
+// v_rcp_f32 (2^x and 1/x, about 1 ulp each), branch-free.  Each is the same
+// function as the reference formula it replaces, rewritten with
+// sigmoid(t) = 1 / (1 + 2^(-t log2 e)); the results differ from the
+// reference's libm-based evaluation by a few fp32 ulp relative to the
+// quantities that are summed later (tanh near 0 carries ~1e-7 absolute,
+// not relative, error, which is what 1 + tanh, the GELU and the next dense
+// layer see).  Saturation comes out of 2^x -> inf / 0 and 1/inf = 0.
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ inline float fast_sigmoid(float t) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * t));
+}
+// ponni_Sigmoid.h:45-49
+__device__ inline float act_sigmoid_fast(float x) { return fast_sigmoid(x); }
+// ponni_Silu.h:45-49: x * sigmoid(x)
+__device__ inline float act_silu_fast(float x) { return x * fast_sigmoid(x); }
+// ponni_Tanh.h:44: tanh(x) = 1 - 2 / (1 + 2^(2 x log2 e))
+__device__ inline float act_tanh_fast(float x) {
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.0f * kLog2e * x)), 1.0f);
+}
+// ponni_Gelu.h:48-53: 0.5 x (1 + tanh(u)) = x sigmoid(2u),
+// u = sqrt(2/pi) (x + 0.044715 x^3)
+__device__ inline float act_gelu_tanh_fast(float x) {
+  float const u = 0.79788456080286535588f * (x + 0.044715f * (x * x * x));
+  return x * fast_sigmoid(2.0f * u);
+}
+
+// A lane value made opaque at this point: what is derived from it is
+// computed here, inside the caller's loop, instead of being hoisted out of
+// the tile loop and held in registers (or spilled) for the whole kernel.
+__device__ inline int fresh(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Offset of lane (g, c) in a [rows, ld] array: row 4g, column c.
+__device__ inline int64_t lane_offset(Lane const& L, int64_t ld) {
+  return int64_t(fresh(4 * L.g)) * ld + fresh(L.c);
+}
+
 // x [N, batch] (row stride ld) -> tile; rows >= N and columns >= batch read 0.
 template <int N, int NT = kNT>
 __device__ inline S<(N + 15) / 16, NT> load_rows(float const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   S<T, NT> s;
   // Row 16m + e of the lane's row group 4g: a uniform offset from one per-lane pointer.
-  float const* __restrict__ xl = x + int64_t(4 * L.g) * ld + L.col0 + L.c;
+  float const* __restrict__ xl = x + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -81,7 +123,7 @@ __device__ inline S<(N + 15) / 16, NT> load_rows(float const* __restrict__ x, in
 
 template <int N, int T, int NT>
 __device__ inline void store_rows(S<T, NT> const& s, float* __restrict__ y, int64_t ld, Lane const& L) {
-  float* __restrict__ yl = y + int64_t(4 * L.g) * ld + L.col0 + L.c;
+  float* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll

@@ -82,4 +82,5 @@ struct ponni_plan_s {
   int fused_blocks_per_cu = 1;
   bool fused_persistent = false;  // grid sized to the resident workgroups
   int fused_columns_per_block = 128;
+  int fused_waves = 4;  // waves per workgroup
 };
