@@ -268,10 +268,14 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
+  if (p.fused_wps > 0) cfg.waves_per_simd = p.fused_wps;  // measured by fused_compile
   if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
     int const v = std::atoi(w);
     if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
   }
+  // At one wave per SIMD the wave has the whole register file: saved states
+  // stay in registers.
+  if (cfg.waves_per_simd == 1) cfg.saved_in_lds = false;
   // Waves per workgroup: LDS-staged parameters are copied once per
   // workgroup, so when copies would cap the resident workgroups below the
   // register-limited occupancy, fewer and larger workgroups share one copy.
@@ -571,7 +575,71 @@ std::map<std::string, std::vector<char>> g_code;  // key -> code object
 
 }  // namespace
 
-int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error) {
+namespace {
+
+// Register use of the kernel in a gfx950 code object, read from its AMDGPU
+// metadata note (msgpack map entries ".vgpr_count", ".agpr_count",
+// ".vgpr_spill_count"); -1 when absent.
+int metadata_int(std::vector<char> const& code, char const* key) {
+  std::string const k = key;
+  std::string pattern(1, static_cast<char>(0xa0 | k.size()));
+  pattern += k;
+  std::string const blob(code.begin(), code.end());
+  size_t const at = blob.find(pattern);
+  if (at == std::string::npos || at + pattern.size() >= blob.size()) return -1;
+  auto const* b = reinterpret_cast<unsigned char const*>(blob.data()) + at + pattern.size();
+  size_t const left = blob.size() - at - pattern.size();
+  if (b[0] < 0x80) return b[0];
+  if (b[0] == 0xcc && left >= 2) return b[1];
+  if (b[0] == 0xcd && left >= 3) return (b[1] << 8) | b[2];
+  return -1;
+}
+
+int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error);
+
+}  // namespace
+
+// Occupancy is settled by measurement: the kernel is compiled at the
+// estimated waves per SIMD; with register spills it is recompiled for one
+// wave fewer, and when it fits the next occupancy's register budget (512 /
+// waves, a multiple of 8) without spills it moves up one.
+int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, std::string& error) {
+  if (p.fused_wps == 0 && std::getenv("PONNI_FUSED_WAVES_PER_SIMD") == nullptr) {
+    FusedConfig est;
+    (void)fused_source(p, est);
+    int wps = est.waves_per_simd;
+    auto spills_regs = [&](int w, int& spills, int& regs) -> int {
+      p.fused_wps = w;
+      int const st = compile_cached(p, key, code, error);
+      if (st != PONNI_OK) return st;
+      spills = metadata_int(code, ".vgpr_spill_count");
+      int const v = metadata_int(code, ".vgpr_count"), a = metadata_int(code, ".agpr_count");
+      regs = (v < 0 ? 512 : v) + (a < 0 ? 0 : a);
+      return static_cast<int>(PONNI_OK);
+    };
+    int spills = 0, regs = 0;
+    int st = spills_regs(wps, spills, regs);
+    if (st != PONNI_OK) return st;
+    while (spills > 0 && wps > 1) {
+      wps--;
+      st = spills_regs(wps, spills, regs);
+      if (st != PONNI_OK) return st;
+    }
+    auto budget = [](int w) { return (512 / w) / 8 * 8; };
+    if (spills == 0 && wps < 4 && regs <= budget(wps + 1)) {
+      int up_spills = 0, up_regs = 0;
+      st = spills_regs(wps + 1, up_spills, up_regs);
+      if (st != PONNI_OK) return st;
+      if (up_spills == 0) wps = wps + 1;
+    }
+    p.fused_wps = wps;
+  }
+  return compile_cached(p, key, code, error);
+}
+
+namespace {
+
+int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error) {
   FusedConfig cfg;
   std::string const src = fused_source(p, cfg);
   key = cache_key(src);
@@ -608,13 +676,15 @@ int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& co
   return PONNI_OK;
 }
 
+}  // namespace
+
 int fused_prepare(ponni_plan_s& p, std::string& error) {
-  FusedConfig cfg;
-  (void)fused_source(p, cfg);
   std::string key;
   std::vector<char> code;
   int const st = fused_compile(p, key, code, error);
   if (st != PONNI_OK) return st;
+  FusedConfig cfg;
+  (void)fused_source(p, cfg);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     error = "no HIP device";

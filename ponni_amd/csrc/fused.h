@@ -24,8 +24,9 @@ struct FusedConfig {
 bool fused_supports(ponni_plan_s const& p);
 std::string fused_kernel_name(ponni_plan_s const& p);
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg);
-// Compile (or fetch from cache) the plan's kernel; needs no device.
-int fused_compile(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error);
+// Compile (or fetch from cache) the plan's kernel; needs no device.  The
+// first call settles the plan's occupancy (ponni_plan_s::fused_wps).
+int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, std::string& error);
 // Compile if needed and load the module on the current device.
 int fused_prepare(ponni_plan_s& p, std::string& error);
 hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t stream);

@@ -83,4 +83,5 @@ struct ponni_plan_s {
   bool fused_persistent = false;  // grid sized to the resident workgroups
   int fused_columns_per_block = 128;
   int fused_waves = 4;  // waves per workgroup
+  int fused_wps = 0;    // waves per SIMD the kernel is compiled for (0: not settled yet)
 };

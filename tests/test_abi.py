@@ -270,3 +270,19 @@ def test_fused_config_sources():
         assert m.path == "fused"
         src = m.kernel_source()
         assert src.count("dense_ep<") == (4 if name == "c2" else 10)
+
+
+def test_fused_occupancy_settled_by_compilation(tmp_path, monkeypatch):
+    # The first compile measures register use: c3 spills at two waves per SIMD
+    # and settles at one (saved states back in registers); c5 fits three.
+    monkeypatch.setenv("PONNI_JIT_CACHE", str(tmp_path))
+    monkeypatch.delenv("PONNI_FUSED_WAVES_PER_SIMD", raising=False)
+    monkeypatch.delenv("PONNI_FUSED_WAVES", raising=False)
+    want = {"c3": "__launch_bounds__(256, 1)", "c5": "__launch_bounds__(768, 3)"}
+    for name, bounds in want.items():
+        m = create(P.configs.CONFIGS[name].layers(False))
+        m.compile()
+        src = m.kernel_source()
+        assert bounds in src, [l for l in src.splitlines() if "launch_bounds" in l]
+        if name == "c3":
+            assert "lds_saved" not in src
