@@ -273,9 +273,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(w);
     if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
   }
-  // At one wave per SIMD the wave has the whole register file: saved states
-  // stay in registers.
-  if (cfg.waves_per_simd == 1) cfg.saved_in_lds = false;
+
   // Waves per workgroup: LDS-staged parameters are copied once per
   // workgroup, so when copies would cap the resident workgroups below the
   // register-limited occupancy, fewer and larger workgroups share one copy.
