@@ -217,9 +217,17 @@ std::string fused_kernel_name(ponni_plan_s const& p) {
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
   std::string const E = p.dtype == PONNI_BF16 ? "__bf16" : "_Float16";
-  int const NT = half ? 4 : 2;  // 16-column tiles per wave
+  // 16-column tiles per wave.  16-bit plans run two waves per SIMD (32
+  // columns each) with A fragments staged through LDS (fused_f16.h dense_hs).
+  int const NT = 2;
   int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
+  // The LDS tanh table is opt-in: its random 2-byte LDS reads contend with
+  // the A-fragment reads of the workgroup's waves (measured slower than the
+  // hardware transcendentals on c4).
+  cfg.lut_bytes = 0;
+  if (char const* v = std::getenv("PONNI_TANH_LUT"))  // tuning override: 1 = table lookup
+    if (std::strcmp(v, "1") == 0 && half && p.lut_tanh_off >= 0) cfg.lut_bytes = kLutWords * 4;
   cfg.waves = 4;
   // Register budget.  A live tile holds 8 registers per lane (fp32 with 2
   // column tiles, or 16-bit with 4); a dense op holds its input, its output
@@ -268,6 +276,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
+  if (half) cfg.waves_per_simd = 2;
   if (p.fused_wps > 0) cfg.waves_per_simd = p.fused_wps;  // measured by fused_compile
   if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
     int const v = std::atoi(w);
@@ -284,7 +293,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const target = 4 * cfg.waves_per_simd;  // waves per CU the registers allow
     int best = 0;
     for (int w = 4; w <= 16; w += 4) {
-      int const per_block_lds = cfg.lds_bytes + w * saved_per_wave;
+      int const per_block_lds = cfg.lds_bytes + cfg.lut_bytes + w * saved_per_wave;
       if (per_block_lds > 160 * 1024) break;
       int const by_lds = per_block_lds > 0 ? (160 * 1024) / per_block_lds : 1 << 20;
       int const blocks = std::min(by_lds, target / w);
@@ -298,14 +307,30 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(w);
     if (v == 4 || v == 8 || v == 12 || v == 16) cfg.waves = v;
   }
+  // A workgroup of 16-bit plans is one wave per SIMD per occupancy level: its
+  // waves share the staged A fragments and the activation table.
+  if (half) cfg.waves = 4 * std::min(cfg.waves_per_simd, 2);
   cfg.columns_per_block = cfg.waves * 16 * NT;
 
   std::ostringstream o;
   std::string const IO = half ? E : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
-  // 16-bit plans keep a workgroup's waves on one output tile at a time, so the
-  // three waves that follow the first read its A fragments from L1.
-  if (half) o << "#define PONNI_TILE_BARRIER 1\n";
+  if (char const* d = std::getenv("PONNI_KSPLIT")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 1 && v <= 4) o << "#define PONNI_KSPLIT " << v << "\n";
+  }
+  if (char const* d = std::getenv("PONNI_LDS_RING")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 1 && v <= 8) o << "#define PONNI_LDS_RING " << v << "\n";
+  }
+  if (char const* d = std::getenv("PONNI_CHUNK_TILES")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 1 && v <= 8) o << "#define PONNI_CHUNK_TILES " << v << "\n";
+  }
+  if (char const* d = std::getenv("PONNI_RING_DEPTH")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
+  }
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
@@ -320,6 +345,27 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   } else {
     o << "  float const* __restrict__ P0 = gparams;\n";
   }
+  if (cfg.lut_bytes > 0) {
+    o << "  __shared__ unsigned short lut_tanh[" << cfg.lut_bytes / 2 << "];\n";
+    o << "  stage_bytes(lut_tanh, gparams + " << p.lut_tanh_off << ", " << cfg.lut_bytes << ");\n";
+    o << "  __syncthreads();\n";
+  }
+  // 16-bit plans: dense layers in program order (weights, 32-feature steps);
+  // the last one's successor is the first (the next tile of the loop).
+  struct DenseRef {
+    int woff, ts, to;
+  };
+  std::vector<DenseRef> dense_seq;
+  for (Op const& op : p.ops)
+    if (op.code == OP_DENSE) dense_seq.push_back({op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
+  if (half && !dense_seq.empty()) {
+    o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
+    o << "  Stage<E> st{a_slots, 0};\n";
+    o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", " << cfg.waves
+      << ">(st, reinterpret_cast<E const*>(gparams + " << dense_seq[0].woff << "));\n";
+    o << "  __syncthreads();\n";
+  }
+  size_t dense_index = 0;
   std::map<int, int> slot_off;  // slot -> floatx4 offset in the wave's LDS region
   if (cfg.saved_in_lds) {
     int off = 0;
@@ -331,10 +377,36 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "  __shared__ floatx4 lds_saved[" << cfg.waves << "][" << off << "];\n";
     o << "  floatx4* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
   }
+  // Per-feature vectors (biases, LayerNorm gamma / beta, constant operands)
+  // of plans whose parameters stream from L2 are staged into LDS once per
+  // workgroup, so the tile loop issues no global load besides its A
+  // fragments (a late global load would wait behind them: vmcnt is in order).
+  // (Measured: c4 unchanged, c3 slower as a persistent fp32 kernel, so only
+  // 16-bit plans, which are persistent anyway, stage them by default.)
+  bool stage_vecs = half && cfg.lds_bytes == 0 && !cfg.params_in_registers;
+  if (char const* v = std::getenv("PONNI_STAGE_VECS"))  // tuning override
+    stage_vecs = std::strcmp(v, "1") == 0 && cfg.lds_bytes == 0 && !cfg.params_in_registers;
+  std::map<int, std::pair<int, int>> vec_lds;  // packed offset -> (LDS offset, length)
+  int vec_total = 0;
+  auto vec = [&](int off, int n) -> std::string {
+    if (!stage_vecs) return "P + " + std::to_string(off);
+    int const len = (n + 15) / 16 * 16;
+    auto it = vec_lds.find(off);
+    if (it == vec_lds.end()) {
+      it = vec_lds.emplace(off, std::make_pair(vec_total, len)).first;
+      vec_total += len;
+    } else if (it->second.second < len) {
+      it->second.second = len;  // never happens for a consistent plan; keep the longest
+    }
+    return "VP + " + std::to_string(it->second.first);
+  };
+  std::ostringstream head;
+  head << o.str();
+  o.str("");
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
   o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
-  o << "    L.col0 = (tile * " << cfg.waves << " + (threadIdx.x >> 6)) * " << 16 * NT << ";\n";
+  o << "    L.col0 = (tile * " << cfg.waves << " + wave_id()) * " << 16 * NT << ";\n";
   // Register-resident parameters may be hoisted out of the tile loop; otherwise
   // pin() hides the pointer's loop invariance so they are re-read per tile.
   o << (cfg.params_in_registers ? "    float const* __restrict__ P = P0;\n" : "    float const* __restrict__ P = pin(P0);\n");
@@ -370,9 +442,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     for (int s = 0; s < count; s++) {
       Step const& st = p.steps[begin + s];
       if (st.act == ACT_BIAS) {
-        o << "    add_rows<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L);\n";
+        o << "    add_rows<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L);\n";
       } else if (act_has_param(st.act)) {
-        o << "    map_const<" << tiles(n) << ">(" << v << ", P + " << st.off << ", L, [](float v, float c) { return "
+        o << "    map_const<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L, [](float v, float c) { return "
           << const_expr(st.act) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
       } else {
@@ -390,28 +462,35 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         std::string const nv = fresh();
         int const n = op.n_out;
         bool pad = false;
-        // A generated Dense's bias seeds the fp32 accumulator (sum = bias first).
-        bool const seed = !half && (op.aux & DENSE_BIAS_FIRST);
-        std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(P + " +
-                                            std::to_string(p.steps[op.epi_begin].off) + ", L)"
-                                      : "zeros<" + std::to_string(tiles(n)) + ">()";
-        if (half)
-          o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
-            << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
-        else
+        // A generated Dense's bias seeds the fp32 accumulator (sum = bias first);
+        // 16-bit plans seed any leading bias (their tolerance is that of the
+        // 16-bit rounding, and the add then costs no VALU op).
+        bool const lead_bias = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
+        bool const seed = lead_bias && (half || (op.aux & DENSE_BIAS_FIRST));
+        // A 16-bit block ending in Tanh looks the activation up in the LDS table.
+        bool const lut_tanh = half && cfg.lut_bytes > 0 && op.epi_count > (seed ? 1 : 0) &&
+                              p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH;
+        if (half) {
+          std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
+          auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
+          dense_index++;
+          o << "    auto " << nv << " = dense_hs<" << tiles(op.n_in) << ", " << tiles(n) << ", " << NT << ", "
+            << cfg.waves << ", " << next.ts << ", " << next.to << ">(" << cur << ", reinterpret_cast<E const*>(P + "
+            << op.woff << "), reinterpret_cast<E const*>(P + " << next.woff << "), st, L, " << init
+            << ", [&](int mo, floatx4 (&t)[" << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
+        } else {
+          std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(" + vec(p.steps[op.epi_begin].off, n) + ", L)"
+                                        : "zeros<" + std::to_string(tiles(n)) + ">()";
           o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
             << op.woff << ", " << init << ", L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
-        for (int s = seed ? 1 : 0; s < op.epi_count; s++) {
+        }
+        int const last = op.epi_count - (lut_tanh ? 1 : 0);
+        for (int s = seed ? 1 : 0; s < last; s++) {
           Step const& st = p.steps[op.epi_begin + s];
-          bool const bias_tanh = half && st.act == ACT_BIAS && s + 1 < op.epi_count &&
-                                 p.steps[op.epi_begin + s + 1].act == ACT_TANH;
-          if (bias_tanh) {
-            o << "      tile_bias_tanh(t, P + " << st.off << ", mo, L);\n";
-            s++;
-          } else if (st.act == ACT_BIAS) {
-            o << "      tile_add_rows(t, P + " << st.off << ", mo, L);\n";
+          if (st.act == ACT_BIAS) {
+            o << "      tile_add_rows(t, " << vec(st.off, n) << ", mo, L);\n";
           } else if (act_has_param(st.act)) {
-            o << "      tile_const(t, P + " << st.off << ", mo, L, [](float v, float c) { return " << const_expr(st.act)
+            o << "      tile_const(t, " << vec(st.off, n) << ", mo, L, [](float v, float c) { return " << const_expr(st.act)
               << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           } else {
@@ -420,6 +499,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
           }
         }
         if (pad && n % 16) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
+        if (half) o << (lut_tanh ? "      tile_lut_odd<E>(t, o, lut_tanh);\n" : "      tile_round<E>(t, o);\n");
         o << "    });\n";
         cur = nv;
         cur_n = n;
@@ -433,8 +513,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       }
       case OP_LAYER_NORM: {
         std::string const f = open32();
-        o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", P + " << op.woff << ", P + "
-          << op.boff << ", " << flit(op.f0) << ", L);\n";
+        o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", " << vec(op.woff, cur_n) << ", "
+          << vec(op.boff, cur_n) << ", " << flit(op.f0) << ", L);\n";
         close32();
         break;
       }
@@ -497,11 +577,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         auto const& sv = saved[op.slot];
         if (half) {
           o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << cur << ", " << sv.first
-            << ", reinterpret_cast<E const*>(P + " << op.woff << "), P + " << op.boff << ", L);\n";
+            << ", reinterpret_cast<E const*>(P + " << op.woff << "), " << vec(op.boff, cur_n) << ", L);\n";
         } else {
           std::string const b = fresh(), nv = fresh();
           o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
-          o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", P + " << op.boff << ", L);\n";
+          o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", " << vec(op.boff, cur_n) << ", L);\n";
           o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
             << ", P + " << op.woff << ", " << b << ", L, [](int, floatx4 (&)[" << NT << "]) {});\n";
           o << "    add(" << cur << ", " << nv << ");\n";
@@ -553,7 +633,16 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";
-  return o.str();
+  if (!vec_lds.empty()) {
+    head << "  __shared__ floatx4 lds_vec[" << vec_total / 4 << "];\n";
+    for (auto const& kv : vec_lds)
+      head << "  stage_vec(lds_vec + " << kv.second.first / 4 << ", gparams + " << kv.first << ", "
+           << kv.second.second / 4 << ");\n";
+    head << "  __syncthreads();\n";
+    head << "  float const* __restrict__ VP = reinterpret_cast<float const*>(lds_vec);\n";
+  }
+  cfg.vec_bytes = vec_total * 4;
+  return head.str() + o.str();
 }
 
 namespace {
@@ -704,7 +793,7 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   }
   p.fused_fn = it->second->fn;
   p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
-  p.fused_persistent = cfg.lds_bytes > 0 || cfg.params_in_registers;
+  p.fused_persistent = cfg.lds_bytes > 0 || cfg.lut_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers;
   p.fused_columns_per_block = cfg.columns_per_block;
   p.fused_waves = cfg.waves;
   return PONNI_OK;

@@ -40,31 +40,84 @@ struct H {
   typename Vec<E>::x4 v[T > 0 ? T : 1][NT];
 };
 
-// Bias and tanh of one output tile in a single pass:
-// tanh(v + b) = 1 - 2 / (1 + 2^(k v + k b)), k = 2 log2(e); five VALU ops per
-// element, two of them transcendental.
-template <int NT>
-__device__ inline void tile_bias_tanh(floatx4 (&t)[NT], float const* __restrict__ b, int mo, Lane const& L) {
-  constexpr float k = 2.8853900817779268f;
-  floatx4 const kb = ld4(b + 16 * mo + 4 * L.g) * k;
+template <class E>
+__device__ inline typename Vec<E>::x4 round4(floatx4 v) {
+  return __builtin_convertvector(v, typename Vec<E>::x4);
+}
+
+template <class E>
+__device__ inline floatx4 widen4(typename Vec<E>::x4 v) {
+  return __builtin_convertvector(v, floatx4);
+}
+
+// Odd activation of a 16-bit value by table lookup.  `lut` holds f(|h|)
+// rounded to E for all 32768 non-negative bit patterns h (index = bits of
+// |h|); the sign is copied back, which is exact for an odd f (tanh).  Each
+// pair of elements costs one packed shift, two bit extractions, two LDS
+// reads and one and-or: no transcendental.  The value looked up is the
+// 16-bit rounding of the fp32 result, so f runs on a 16-bit operand, as the
+// reference's half arithmetic evaluates activations on a half value
+// (ponni_TwoHalf.h:138-153: fp32 per lane of a half input, rounded back).
+template <class E, int NT>
+__device__ inline void tile_lut_odd(floatx4 const (&t)[NT], typename Vec<E>::x4 (&o)[NT],
+                                    unsigned short const* __restrict__ lut) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  char const* __restrict__ base = reinterpret_cast<char const*>(lut);
 #pragma unroll
-  for (int n = 0; n < NT; n++)
+  for (int n = 0; n < NT; n++) {
+    u32x2 const bits = __builtin_bit_cast(u32x2, round4<E>(t[n]));
+    u32x2 r;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      float const ex = __builtin_amdgcn_exp2f(fmaf(t[n][e], k, kb[e]));
-      t[n][e] = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + ex), 1.0f);
+    for (int k = 0; k < 2; k++) {
+      // Byte offsets 2|h| of both halves at once; the sign bits shift out.
+      // (The element is copied to a scalar first: a bit cast of a vector
+      // element lvalue reads element 0 with this compiler.)
+      unsigned const pk = bits[k];
+      unsigned const q = __builtin_bit_cast(unsigned, __builtin_bit_cast(u16x2, pk) << (unsigned short)1);
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      h2 v;
+      v[0] = *reinterpret_cast<_Float16 const*>(base + (q & 0xffffu));
+      v[1] = *reinterpret_cast<_Float16 const*>(base + (q >> 16));
+      r[k] = __builtin_bit_cast(unsigned, v) | (pk & 0x80008000u);
     }
+    o[n] = __builtin_bit_cast(typename Vec<E>::x4, r);
+  }
 }
 
 #ifndef PONNI_RING_DEPTH
 #define PONNI_RING_DEPTH 4
 #endif
 
+// The lane's element pointer for row 4g, column col0 + c, opaque to the
+// compiler so that every row is one 64-bit add of a uniform (SGPR) offset.
+template <class E>
+__device__ inline E* lane_ptr(E* p, int64_t ld, Lane const& L) {
+  int64_t off = int64_t(4 * L.g) * ld + L.col0 + L.c;
+  asm volatile("" : "+v"(off));
+  return p + off;
+}
+
+// x [N, batch] (row stride ld) -> tile; rows >= N and columns >= batch read 0.
+// Waves whose columns are all inside the batch (all but the last) load
+// without per-element predication.
 template <int N, int NT, class E>
 __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   H<T, NT, E> s;
-  E const* __restrict__ xl = x + lane_offset(L, ld) + L.col0;
+  E const* __restrict__ xl = lane_ptr(x, ld, L);
+  if (L.col0 + 16 * NT <= L.batch) {
+#pragma unroll
+    for (int m = 0; m < T; m++)
+#pragma unroll
+      for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          int const f = 16 * m + 4 * L.g + e;
+          s.v[m][n][e] = (N % 16 == 0 || f < N) ? xl[int64_t(16 * m + e) * ld + 16 * n] : E(0.0f);
+        }
+    return s;
+  }
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -81,28 +134,19 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
 
 template <int N, int T, int NT, class E>
 __device__ inline void store_rows_h(H<T, NT, E> const& s, E* __restrict__ y, int64_t ld, Lane const& L) {
-  E* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
+  E* __restrict__ yl = lane_ptr(y, ld, L);
+  bool const full = L.col0 + 16 * NT <= L.batch;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-      bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
+      bool const col_ok = full || L.col0 + 16 * n + L.c < L.batch;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         int const f = 16 * m + 4 * L.g + e;
-        if (f < N && col_ok) yl[int64_t(16 * m + e) * ld + 16 * n] = s.v[m][n][e];
+        if ((N % 16 == 0 || f < N) && col_ok) yl[int64_t(16 * m + e) * ld + 16 * n] = s.v[m][n][e];
       }
     }
-}
-
-template <class E>
-__device__ inline typename Vec<E>::x4 round4(floatx4 v) {
-  return __builtin_convertvector(v, typename Vec<E>::x4);
-}
-
-template <class E>
-__device__ inline floatx4 widen4(typename Vec<E>::x4 v) {
-  return __builtin_convertvector(v, floatx4);
 }
 
 template <int T, int NT, class E>
@@ -125,12 +169,15 @@ __device__ inline H<T, NT, E> to_h(S<T, NT> const& s) {
   return h;
 }
 
-// Dense layer on fp16/bf16 MFMA; returns the rounded output tile.  The
-// epilogue of output tile mo-1 runs after the MFMAs of tile mo; A fragments
-// stream through an R-deep ring (1 KB per fragment: 16 B per lane).
-// If `acc0` is given (projection add) it seeds every output tile's accumulator.
-template <int TI, int TO, int NT, class E, class Epi, int D = PONNI_RING_DEPTH>
-__device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restrict__ w, Lane const& L, Epi epi) {
+// Dense layer on fp16/bf16 MFMA; returns the 16-bit output state.
+// init(mo) seeds output tile mo's fp32 accumulator (zero, or a bias that
+// then costs no VALU add); epi(mo, t, o) finishes tile mo: its remaining
+// epilogue steps in fp32 on t, then the 16-bit result into o.  The epilogue
+// of tile mo-1 runs after the MFMAs of tile mo; A fragments stream through an
+// R-deep ring (1 KB per fragment: 16 B per lane).
+template <int TI, int TO, int NT, class E, class Init, class Epi, int D = PONNI_RING_DEPTH>
+__device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restrict__ w, Lane const& L, Init init,
+                                       Epi epi) {
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
   constexpr int TS = (TI + 1) / 2;
@@ -149,8 +196,9 @@ __device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restri
     __syncthreads();
 #endif
     floatx4 acc[NT];
+    floatx4 const seed = init(mo);
 #pragma unroll
-    for (int n = 0; n < NT; n++) acc[n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < NT; n++) acc[n] = seed;
 #pragma unroll
     for (int t = 0; t < TS; t++) {
       int const i = mo * TS + t;
@@ -164,18 +212,225 @@ __device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restri
         acc[n] = Vec<E>::mfma(a, b, acc[n]);
       }
     }
-    if (mo > 0) {
-      epi(mo - 1, prev);
-#pragma unroll
-      for (int n = 0; n < NT; n++) out.v[mo - 1][n] = round4<E>(prev[n]);
-    }
+    if (mo > 0) epi(mo - 1, prev, out.v[mo - 1]);
 #pragma unroll
     for (int n = 0; n < NT; n++) prev[n] = acc[n];
   }
-  epi(TO - 1, prev);
-#pragma unroll
-  for (int n = 0; n < NT; n++) out.v[TO - 1][n] = round4<E>(prev[n]);
+  epi(TO - 1, prev, out.v[TO - 1]);
   return out;
+}
+
+// ---- A fragments staged through LDS -------------------------------------
+// The workgroup's waves share the A fragments of up to CT consecutive output
+// tiles (a "chunk": up to CT * TS 1 KB fragments, contiguous in the packed
+// parameters) in one of two LDS slots.  While a chunk is computed from slot
+// `cur`, every wave loads its share of the next chunk (the next CT tiles of
+// the layer, or the first chunk of the next dense layer) into registers and
+// writes it to the other slot; a workgroup barrier ends the chunk.  Each
+// fragment is read once from L2 per workgroup instead of once per wave, and
+// the next chunk's load has a whole chunk of MFMA work to arrive in.
+#ifndef PONNI_CHUNK_TILES
+#define PONNI_CHUNK_TILES 4
+#endif
+constexpr int kChunkTiles = PONNI_CHUNK_TILES;
+constexpr int kSlotFrags = 8 * kChunkTiles;  // fragments per slot (256 input features)
+#ifndef PONNI_LDS_RING
+#define PONNI_LDS_RING 2
+#endif
+#ifndef PONNI_KSPLIT
+#define PONNI_KSPLIT 1
+#endif
+
+template <class E>
+struct Stage {
+  typename Vec<E>::x8* __restrict__ slots;  // LDS: 2 x kSlotFrags x 64 lanes
+  int cur;
+};
+
+// The NF fragments of a chunk this wave loads: f = wave + WAVES k.
+template <int NF, int WAVES, class E>
+struct ChunkRegs {
+  static constexpr int K = (NF + WAVES - 1) / WAVES;
+  typename Vec<E>::x8 v[K > 0 ? K : 1];
+};
+
+template <int NF, int WAVES, class E>
+__device__ inline ChunkRegs<NF, WAVES, E> chunk_load(E const* __restrict__ chunk, int wave, int lane) {
+  ChunkRegs<NF, WAVES, E> r;
+#pragma unroll
+  for (int k = 0; k < r.K; k++) {
+    int const f = wave + WAVES * k;
+    // (compile-time true when every wave has a k-th fragment: no branch)
+    if (NF >= WAVES * (k + 1) || f < NF)
+      r.v[k] = *reinterpret_cast<typename Vec<E>::x8 const*>(chunk + f * 512 + lane * 8);
+  }
+  return r;
+}
+
+template <int NF, int WAVES, class E>
+__device__ inline void chunk_store(ChunkRegs<NF, WAVES, E> const& r, Stage<E> const& st, int slot, int wave,
+                                   int lane) {
+#pragma unroll
+  for (int k = 0; k < r.K; k++) {
+    int const f = wave + WAVES * k;
+    if (NF >= WAVES * (k + 1) || f < NF) st.slots[(slot * kSlotFrags + f) * 64 + lane] = r.v[k];
+  }
+}
+
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// Dense layer with LDS-staged A fragments.  On entry slot st.cur holds this
+// layer's first chunk; on exit it holds the first chunk of `w_next`, the next
+// dense layer (TSN fragments per tile, TON output tiles).  init / epi as in
+// dense_h.
+template <int TI, int TO, int NT, int WAVES, int TSN, int TON, class E, class Init, class Epi>
+__device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restrict__ w,
+                                        E const* __restrict__ w_next, Stage<E>& st, Lane const& L, Init init,
+                                        Epi epi) {
+  using V8 = typename Vec<E>::x8;
+  using V4 = typename Vec<E>::x4;
+  constexpr int TS = (TI + 1) / 2;
+  constexpr int CT = kChunkTiles;
+  constexpr int NCH = (TO + CT - 1) / CT;
+  constexpr int NFN = cmin(CT, TON) * TSN;  // fragments of the next layer's first chunk
+  static_assert(TS <= 8 && TSN <= 8, "at most 256 input features");
+  int const wave = wave_id();
+  H<TO, NT, E> out;
+  floatx4 prev[NT];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ch++) {
+    int const t0 = ch * CT;
+    bool const last = ch + 1 == NCH;
+    // Next chunk: the next CT tiles of this layer, or the next layer's first chunk.
+    int const nt_next = last ? 0 : cmin(CT, TO - t0 - CT);
+    constexpr int NFX = cmax(CT * TS, NFN);
+    ChunkRegs<NFX, WAVES, E> nx;
+    if (!last) {
+      E const* __restrict__ src = w + (t0 + CT) * TS * 512;
+      if (nt_next == CT) {
+        auto const r = chunk_load<CT * TS, WAVES>(src, wave, L.lane);
+#pragma unroll
+        for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
+      } else {
+        // Partial chunk (the layer's last): only its own fragments.
+#pragma unroll
+        for (int k = 0; k < ChunkRegs<CT * TS, WAVES, E>::K; k++) {
+          int const f = wave + WAVES * k;
+          if (f < nt_next * TS) nx.v[k] = *reinterpret_cast<V8 const*>(src + f * 512 + L.lane * 8);
+        }
+      }
+    } else {
+      auto const r = chunk_load<NFN, WAVES>(w_next, wave, L.lane);
+#pragma unroll
+      for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
+    }
+    V8 const* __restrict__ sl = st.slots + st.cur * (kSlotFrags * 64) + L.lane;
+#pragma unroll
+    for (int tt = 0; tt < CT; tt++) {
+      int const mo = t0 + tt;
+      if (mo < TO) {
+        // A fragments through a small register ring (LDS latency is covered
+        // by the other wave of the SIMD).
+        constexpr int R = TS < PONNI_LDS_RING ? TS : PONNI_LDS_RING;
+        V8 a[R];
+#pragma unroll
+        for (int t = 0; t < R; t++) a[t] = sl[(tt * TS + t) * 64];
+        // KS independent accumulation chains per column tile (even / odd
+        // steps), so the matrix pipe is not bound by one chain's latency.
+        constexpr int KS = TS >= 2 ? PONNI_KSPLIT : 1;
+        floatx4 acc[KS][NT];
+        floatx4 const seed = init(mo);
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+          acc[0][n] = seed;
+#pragma unroll
+          for (int k = 1; k < KS; k++) acc[k][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int t = 0; t < TS; t++) {
+          V8 const at = a[t % R];
+          if (t + R < TS) a[t % R] = sl[(tt * TS + t + R) * 64];
+#pragma unroll
+          for (int n = 0; n < NT; n++) {
+            V4 const lo = in.v[2 * t][n];
+            V4 const hi = (2 * t + 1 < TI) ? in.v[(2 * t + 1 < TI) ? 2 * t + 1 : 2 * t][n]
+                                           : V4{E(0.0f), E(0.0f), E(0.0f), E(0.0f)};
+            acc[t % KS][n] = Vec<E>::mfma(at, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[t % KS][n]);
+          }
+        }
+#pragma unroll
+        for (int k = 1; k < KS; k++)
+#pragma unroll
+          for (int n = 0; n < NT; n++) acc[0][n] += acc[k][n];
+        if (mo > 0) epi(mo - 1, prev, out.v[mo - 1]);
+#pragma unroll
+        for (int n = 0; n < NT; n++) prev[n] = acc[0][n];
+      }
+    }
+    // Slot cur ^ 1 was last read before the previous barrier.
+    if (!last) {
+      if (nt_next == CT) {
+        ChunkRegs<CT * TS, WAVES, E> r;
+#pragma unroll
+        for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
+        chunk_store<CT * TS, WAVES>(r, st, st.cur ^ 1, wave, L.lane);
+      } else {
+        // Partial chunk: store only its fragments (compile-time count after unrolling).
+        ChunkRegs<CT * TS, WAVES, E> r;
+#pragma unroll
+        for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
+#pragma unroll
+        for (int k = 0; k < r.K; k++) {
+          int const f = wave + WAVES * k;
+          if (f < nt_next * TS) st.slots[((st.cur ^ 1) * kSlotFrags + f) * 64 + L.lane] = r.v[k];
+        }
+      }
+    } else {
+      ChunkRegs<NFN, WAVES, E> r;
+#pragma unroll
+      for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
+      chunk_store<NFN, WAVES>(r, st, st.cur ^ 1, wave, L.lane);
+    }
+    __syncthreads();
+    st.cur ^= 1;
+  }
+  epi(TO - 1, prev, out.v[TO - 1]);
+  return out;
+}
+
+// Kernel prologue: the first dense layer's first chunk into slot 0.
+template <int TS, int TO, int WAVES, class E>
+__device__ inline void stage_first(Stage<E>& st, E const* __restrict__ w) {
+  int const wave = wave_id(), lane = threadIdx.x & 63;
+  constexpr int NF = cmin(kChunkTiles, TO) * TS;
+  chunk_store<NF, WAVES>(chunk_load<NF, WAVES>(w, wave, lane), st, 0, wave, lane);
+  st.cur = 0;
+}
+
+// Accumulator seeds for dense_h: zero, or the per-feature vector b.
+struct SeedZero {
+  __device__ floatx4 operator()(int) const { return floatx4{0.0f, 0.0f, 0.0f, 0.0f}; }
+};
+struct SeedRows {
+  float const* __restrict__ b;
+  int g;
+  __device__ floatx4 operator()(int mo) const { return ld4(b + 16 * mo + 4 * g); }
+};
+
+// Final rounding of an epilogue tile to the 16-bit state.
+template <class E, int NT>
+__device__ inline void tile_round(floatx4 const (&t)[NT], typename Vec<E>::x4 (&o)[NT]) {
+#pragma unroll
+  for (int n = 0; n < NT; n++) o[n] = round4<E>(t[n]);
+}
+
+// Stage `bytes` (a multiple of 16) from global memory into LDS, once per
+// workgroup; the caller synchronizes before the first read.
+__device__ inline void stage_bytes(void* __restrict__ lds, void const* __restrict__ src, int bytes) {
+  floatx4* d = reinterpret_cast<floatx4*>(lds);
+  floatx4 const* s4 = reinterpret_cast<floatx4 const*>(src);
+  for (int i = threadIdx.x; i < bytes / 16; i += blockDim.x) d[i] = s4[i];
 }
 
 // Projection add: out = in + round(b + W^T saved) computed in fp32, rounded once.

@@ -49,6 +49,9 @@ __device__ inline float xmin(float v) {
 
 __device__ inline floatx4 ld4(float const* p) { return *reinterpret_cast<floatx4 const*>(p); }
 
+// Wave index within the workgroup as a uniform (scalar) value.
+__device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // p plus an opaque zero: loads through the result cannot be hoisted out of
 // the loop it is taken in, while p's address space (LDS or global) is kept.
 template <class P>
@@ -500,6 +503,12 @@ __device__ inline S<1, NT> reduce(S<T, NT> const& s, Lane const& L) {
     out.v[0][n] = floatx4{L.g == 0 ? r : 0.0f, 0.0f, 0.0f, 0.0f};
   }
   return out;
+}
+
+// Copy n4 float4s of one per-feature vector into LDS (no barrier).
+__device__ inline void stage_vec(floatx4* __restrict__ lds, float const* __restrict__ src, int n4) {
+  floatx4 const* s4 = reinterpret_cast<floatx4 const*>(src);
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) lds[i] = s4[i];
 }
 
 // Stage `count` floats (a multiple of 4) of packed parameters into LDS.

@@ -462,6 +462,19 @@ void lower(ponni_plan_s& p) {
   }
   p.tmp_features[0] = tmp_max[0];
   p.tmp_features[1] = tmp_max[1];
+
+  // FUSED 16-bit plans evaluate a Tanh that ends a dense block by table
+  // lookup (fused_f16.h tile_lut_odd): 32768 16-bit entries after the packed
+  // parameters, 16-byte aligned.
+  p.lut_tanh_off = -1;
+  if (p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16)) {
+    for (Op const& op : p.ops)
+      if (op.code == OP_DENSE && op.epi_count > 0 && p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH) {
+        p.lut_tanh_off = round_up(static_cast<int>(p.packed_elements), 4);
+        p.packed_elements = p.lut_tanh_off + kLutWords;
+        break;
+      }
+  }
 }
 
 bool mfma_supports(ponni_plan_s const& p) {
@@ -573,6 +586,15 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
             h[((int64_t(mo) * TS + t) * 64 + l) * 8 + j] = (k < K && n < N) ? bits16(v) : 0;
           }
   };
+  if (p.lut_tanh_off >= 0) {
+    // tanh of every non-negative 16-bit value, evaluated in double and rounded to the type.
+    auto* h = reinterpret_cast<uint16_t*>(out.data() + p.lut_tanh_off);
+    for (uint32_t b = 0; b < 2 * kLutWords; b++) {
+      double const x = p.dtype == PONNI_F16 ? half_bits_to_float(static_cast<uint16_t>(b))
+                                            : bf16_bits_to_float(static_cast<uint16_t>(b));
+      h[b] = bits16(std::tanh(x));
+    }
+  }
   int const L = static_cast<int>(p.layers.size());
   for (int i = 0; i < L; i++) {
     ponni_layer_desc const& d = p.layers[i];

@@ -359,7 +359,7 @@ def test_c5_plan_is_fused_and_compiles():
     assert "concat<3, 3>" in src and "softmax<10, false>" in src
     plan.compile()
     half = gm.plan("f16")
-    assert half.path == "fused" and half.kernel_source().count("dense_h<") == 4
+    assert half.path == "fused" and half.kernel_source().count("dense_hs<") == 4
     half.compile()
 
 
