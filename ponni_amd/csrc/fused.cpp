@@ -211,15 +211,30 @@ std::string fused_kernel_name(ponni_plan_s const& p) {
     if (op.code == OP_DENSE) widths += "x" + std::to_string(op.n_out);
   char buf[16];
   std::snprintf(buf, sizeof(buf), "%08x", static_cast<unsigned>(fnv(sig) & 0xffffffffu));
-  return "ponni_fused_" + widths + "_" + buf;
+  return std::string(p.path == PONNI_PATH_NARROW ? "ponni_narrow_" : "ponni_fused_") + widths + "_" + buf;
 }
 
+std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg);
+
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
+  if (p.path == PONNI_PATH_NARROW) return narrow_source_of(p, cfg);
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
   std::string const E = p.dtype == PONNI_BF16 ? "__bf16" : "_Float16";
   // 16-column tiles per wave.  16-bit plans run two waves per SIMD (32
   // columns each) with A fragments staged through LDS (fused_f16.h dense_hs).
-  int const NT = 2;
+  int NT = 2;
+  int half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
+  if (half) {
+    if (char const* v = std::getenv("PONNI_HALF_NT")) {  // tuning override
+      int const t = std::atoi(v);
+      if (t == 1 || t == 2) NT = t;
+    }
+    half_wps = NT == 1 ? 4 : 2;
+    if (char const* v = std::getenv("PONNI_HALF_WPS")) {  // tuning override
+      int const t = std::atoi(v);
+      if (t >= 1 && t <= 4) half_wps = t;
+    }
+  }
   int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   // The LDS tanh table is opt-in: its random 2-byte LDS reads contend with
@@ -276,7 +291,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
-  if (half) cfg.waves_per_simd = 2;
+  if (half) cfg.waves_per_simd = half_wps;
   if (p.fused_wps > 0) cfg.waves_per_simd = p.fused_wps;  // measured by fused_compile
   if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
     int const v = std::atoi(w);
@@ -309,7 +324,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   }
   // A workgroup of 16-bit plans is one wave per SIMD per occupancy level: its
   // waves share the staged A fragments and the activation table.
-  if (half) cfg.waves = 4 * std::min(cfg.waves_per_simd, 2);
+  if (half) cfg.waves = 4 * std::min(cfg.waves_per_simd, half_wps);
   cfg.columns_per_block = cfg.waves * 16 * NT;
 
   std::ostringstream o;
@@ -645,6 +660,129 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   return head.str() + o.str();
 }
 
+// ---- generated NARROW kernels ---------------------------------------------
+// A narrow chain (every width <= 16) as straight-line code over
+// narrow_jit.h: one lane owns V consecutive samples, parameters in the NARROW
+// packing at constant offsets, vector row loads and stores.
+namespace {
+
+int narrow_samples_per_lane(ponni_plan_s const& p) {
+  bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
+  if (p.width_class >= 16) return 2;
+  if (p.width_class >= 8) return 4;
+  return half ? 8 : 4;
+}
+
+std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
+  int const W = p.width_class;
+  int const V = narrow_samples_per_lane(p);
+  std::string const S = p.dtype == PONNI_F16 ? "_Float16" : p.dtype == PONNI_BF16 ? "__bf16" : "float";
+  cfg = FusedConfig{};
+  cfg.waves = 4;
+  cfg.waves_per_simd = 4;
+  cfg.columns_per_block = 256 * V;
+  std::string const WV = ", " + std::to_string(W) + ">";
+  auto tv = [&](int n) { return "<" + std::to_string(V) + ", " + std::to_string(n) + WV; };
+  auto finish = [&](int n) { return "    finish<S, " + std::to_string(V) + ", " + std::to_string(n) + WV; };
+  std::ostringstream o;
+  o << "// generated by libponni_hip for one plan (NARROW)\n#include \"narrow_jit.h\"\n";
+  o << "using namespace ponni_hip;\nusing namespace ponni_hip::narrowj;\ntypedef " << S << " S;\n";
+  o << "extern \"C\" __global__ __launch_bounds__(256) void " << fused_kernel_name(p)
+    << "(float const* __restrict__ P, S const* __restrict__ x, int64_t ldx, S* __restrict__ y, int64_t ldy, "
+       "int64_t batch) {\n";
+  o << "  int64_t const b0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * " << V << ";\n";
+  o << "  if (b0 >= batch) return;\n";
+  o << "  bool const vec = b0 + " << V << " <= batch && vec_ok<S, " << V << ">(x, ldx) && vec_ok<S, " << V
+    << ">(y, ldy);\n";
+  o << "  float s[" << W << "][" << V << "];\n";
+  o << "  load<S, " << V << ", " << p.layers.front().n_in << WV << "(s, x, ldx, b0, batch, vec);\n";
+  for (int sl = 0; sl < p.num_slots; sl++)
+    o << "  float sv" << sl << "[" << W << "][" << V << "] = {};\n";
+  int cur_n = p.layers.front().n_in;
+  auto steps = [&](std::string const& a, int n, int begin, int count) {
+    for (int k = 0; k < count; k++) {
+      Step const& st = p.steps[begin + k];
+      if (act_has_param(st.act))
+        o << "    with_vec" << tv(n) << "(" << a << ", P + " << st.off << ", [](float v, float c) { return "
+          << const_expr(st.act) << "; });\n";
+      else
+        o << "    map" << tv(n) << "(" << a << ", [](float v) { return " << act_expr(st) << "; });\n";
+    }
+  };
+  for (Op const& op : p.ops) {
+    o << "  {  // op code " << op.code << "\n";
+    switch (op.code) {
+      case OP_DENSE: {
+        // Pointwise layers keep the width: the Matvec is n_in -> n_out.
+        int const K = op.n_in, N = op.n_out;
+        o << "    float a[" << W << "][" << V << "];\n";
+        o << "    dense<" << V << ", " << K << ", " << N << WV << "(a, s, P + " << op.woff << ");\n";
+        steps("a", N, op.epi_begin, op.epi_count);
+        o << finish(op.n_out) << "(s, a);\n";
+        break;
+      }
+      case OP_POINTWISE:
+        steps("s", cur_n, op.epi_begin, op.epi_count);
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_LAYER_NORM:
+        o << "    layer_norm" << tv(cur_n) << "(s, P + " << op.woff << ", P + " << op.boff << ", " << flit(op.f0)
+          << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_SOFTMAX:
+      case OP_LOG_SOFTMAX:
+        o << "    softmax<" << V << ", " << cur_n << ", " << W << ", " << (op.code == OP_LOG_SOFTMAX ? "true" : "false")
+          << ">(s);\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_MIN_MAX:
+        o << "    min_max" << tv(cur_n) << "(s, " << flit(op.f0) << ", " << flit(op.f1) << ", " << flit(op.f2) << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_SAVE:
+        o << "    copy<" << V << WV << "(sv" << op.slot << ", s);\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_ADD:
+        o << "    for (int f = 0; f < " << W << "; f++) for (int v = 0; v < " << V << "; v++) s[f][v] += sv" << op.slot
+          << "[f][v];\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_CONCAT:
+        if (op.aux)
+          o << "    concat<" << V << ", " << op.n_in << ", " << op.n_out << WV << "(s, s, sv" << op.slot << ");\n";
+        else
+          o << "    concat<" << V << ", " << op.n_out - op.n_in << ", " << op.n_out << WV << "(s, sv" << op.slot
+            << ", s);\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_PROJ_ADD:
+        o << "    proj_add<" << V << ", " << op.n_in << ", " << op.aux << WV << "(s, sv" << op.slot << ", P + " << op.woff
+          << ", P + " << op.boff << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      default:
+        break;
+    }
+    o << "  }\n";
+    cur_n = op.n_out;
+  }
+  o << "  store<S, " << V << ", " << p.layers.back().n_out << WV << "(s, y, ldy, b0, batch, vec);\n}\n";
+  return o.str();
+}
+
+}  // namespace
+
+std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg) { return narrow_source(p, cfg); }
+
+bool narrow_jit_supports(ponni_plan_s const& p) {
+  if (p.path != PONNI_PATH_NARROW || p.width_class <= 0 || p.dtype == PONNI_F64) return false;
+  for (Op const& op : p.ops)
+    if (op.code == OP_LOAD || op.code == OP_BINARY || op.code == OP_REDUCE) return false;
+  return true;
+}
+
 namespace {
 
 std::string cache_key(std::string const& src) {
@@ -691,7 +829,7 @@ int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& c
 // wave fewer, and when it fits the next occupancy's register budget (512 /
 // waves, a multiple of 8) without spills it moves up one.
 int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, std::string& error) {
-  if (p.fused_wps == 0 && std::getenv("PONNI_FUSED_WAVES_PER_SIMD") == nullptr) {
+  if (p.path == PONNI_PATH_FUSED && p.fused_wps == 0 && std::getenv("PONNI_FUSED_WAVES_PER_SIMD") == nullptr) {
     FusedConfig est;
     (void)fused_source(p, est);
     int wps = est.waves_per_simd;

@@ -27,6 +27,8 @@ struct FusedConfig {
 };
 
 bool fused_supports(ponni_plan_s const& p);
+// Can the NARROW plan run as a generated kernel (narrow_jit.h)?
+bool narrow_jit_supports(ponni_plan_s const& p);
 std::string fused_kernel_name(ponni_plan_s const& p);
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg);
 // Compile (or fetch from cache) the plan's kernel; needs no device.  The

@@ -1,0 +1,239 @@
+// NARROW path, generated form: building blocks for per-plan kernels of
+// narrow chains (every width <= 16), compiled at run time by hipRTC with all
+// widths and parameter offsets constant (see fused.cpp, narrow_source).
+//
+// One lane owns V consecutive samples; the state is float s[W][V] (W the
+// plan's padded width class), rows >= the current width held at exactly 0.
+// Inputs and outputs move as V-element vectors (16 B per row for fp32 V = 4)
+// when the views allow it, so each feature row is streamed with full-width
+// coalesced accesses.  Parameters are in the NARROW packing (plan.cpp
+// pack_params): dense weights W x W, [k * W + j] = W(k, j) of the reference's
+// [in, out] Matvec layout, vectors padded to W; uniform addresses, so the
+// compiler reads them with scalar loads.  The arithmetic mirrors the
+// reference's per-sample executor (ponni_Inference.h:412-555) and the
+// interpreted NARROW kernel (kernels_narrow.hip) operation for operation.
+#pragma once
+
+#include "pointwise.h"
+
+namespace ponni_hip {
+namespace narrowj {
+
+template <class S, int V>
+struct VecOf {
+  typedef S type __attribute__((ext_vector_type(V)));
+};
+
+// Rounding of a materialized state to the storage precision.
+template <class S>
+__device__ inline float round_state(float v) {
+  return static_cast<float>(static_cast<S>(v));
+}
+template <>
+__device__ inline float round_state<float>(float v) {
+  return v;
+}
+
+// Can rows of this view be moved as aligned V-element vectors?
+template <class S, int V>
+__device__ inline bool vec_ok(void const* p, int64_t ld) {
+  return (reinterpret_cast<unsigned long long>(p) % (sizeof(S) * V)) == 0 && ld % V == 0;
+}
+
+// s[f][v] = x(f, b0 + v) for f < N; rows >= N and samples >= batch are 0.
+template <class S, int V, int N, int W>
+__device__ inline void load(float (&s)[W][V], S const* __restrict__ x, int64_t ld, int64_t b0, int64_t batch,
+                            bool vec) {
+  typedef typename VecOf<S, V>::type SV;
+#pragma unroll
+  for (int f = 0; f < W; f++)
+#pragma unroll
+    for (int v = 0; v < V; v++) s[f][v] = 0.0f;
+  if (vec) {
+#pragma unroll
+    for (int f = 0; f < N; f++) {
+      SV const r = *reinterpret_cast<SV const*>(x + int64_t(f) * ld + b0);
+#pragma unroll
+      for (int v = 0; v < V; v++) s[f][v] = static_cast<float>(r[v]);
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < N; f++)
+#pragma unroll
+      for (int v = 0; v < V; v++)
+        if (b0 + v < batch) s[f][v] = static_cast<float>(x[int64_t(f) * ld + b0 + v]);
+  }
+}
+
+template <class S, int V, int N, int W>
+__device__ inline void store(float const (&s)[W][V], S* __restrict__ y, int64_t ld, int64_t b0, int64_t batch,
+                             bool vec) {
+  typedef typename VecOf<S, V>::type SV;
+  if (vec) {
+#pragma unroll
+    for (int f = 0; f < N; f++) {
+      SV r;
+#pragma unroll
+      for (int v = 0; v < V; v++) r[v] = static_cast<S>(s[f][v]);
+      *reinterpret_cast<SV*>(y + int64_t(f) * ld + b0) = r;
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < N; f++)
+#pragma unroll
+      for (int v = 0; v < V; v++)
+        if (b0 + v < batch) y[int64_t(f) * ld + b0 + v] = static_cast<S>(s[f][v]);
+  }
+}
+
+// a[j] = sum_k W(k, j) s[k], ascending k (ponni_Matvec.h:70-79); rows >= N are 0.
+template <int V, int K, int N, int W>
+__device__ inline void dense(float (&a)[W][V], float const (&s)[W][V], float const* __restrict__ w) {
+#pragma unroll
+  for (int j = 0; j < W; j++) {
+#pragma unroll
+    for (int v = 0; v < V; v++) a[j][v] = 0.0f;
+    if (j < N) {
+#pragma unroll
+      for (int k = 0; k < K; k++) {
+        float const wk = w[k * W + j];
+#pragma unroll
+        for (int v = 0; v < V; v++) a[j][v] += wk * s[k][v];
+      }
+    }
+  }
+}
+
+// a[j] += c[j] for j < N (ponni_Bias.h:66-68), or f(a[j], c[j]).
+template <int V, int N, int W, class F>
+__device__ inline void with_vec(float (&a)[W][V], float const* __restrict__ c, F f) {
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    float const cj = c[j];
+#pragma unroll
+    for (int v = 0; v < V; v++) a[j][v] = f(a[j][v], cj);
+  }
+}
+
+template <int V, int N, int W, class F>
+__device__ inline void map(float (&a)[W][V], F f) {
+#pragma unroll
+  for (int j = 0; j < N; j++)
+#pragma unroll
+    for (int v = 0; v < V; v++) a[j][v] = f(a[j][v]);
+}
+
+// End of every operation: the state rounded to the storage precision with
+// rows >= N at zero, as every materialization of the reference executor.
+template <class S, int V, int N, int W>
+__device__ inline void finish(float (&s)[W][V], float const (&a)[W][V]) {
+#pragma unroll
+  for (int f = 0; f < W; f++)
+#pragma unroll
+    for (int v = 0; v < V; v++) s[f][v] = f < N ? round_state<S>(a[f][v]) : 0.0f;
+}
+
+template <int V, int W>
+__device__ inline void copy(float (&d)[W][V], float const (&s)[W][V]) {
+#pragma unroll
+  for (int f = 0; f < W; f++)
+#pragma unroll
+    for (int v = 0; v < V; v++) d[f][v] = s[f][v];
+}
+
+// Two-pass LayerNorm, ponni_LayerNorm.h:82-98.
+template <int V, int N, int W>
+__device__ inline void layer_norm(float (&s)[W][V], float const* __restrict__ gamma, float const* __restrict__ beta,
+                                  float eps) {
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float mean = 0.0f;
+#pragma unroll
+    for (int f = 0; f < N; f++) mean += s[f][v];
+    mean /= float(N);
+    float var = 0.0f;
+#pragma unroll
+    for (int f = 0; f < N; f++) {
+      float const d = s[f][v] - mean;
+      var += d * d;
+    }
+    var /= float(N);
+    float const inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int f = 0; f < N; f++) s[f][v] = gamma[f] * ((s[f][v] - mean) * inv_std) + beta[f];
+  }
+}
+
+// Softmax / LogSoftmax, ponni_Softmax.h:45-56, ponni_LogSoftmax.h:46-57.
+template <int V, int N, int W, bool LOG>
+__device__ inline void softmax(float (&s)[W][V]) {
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float mx = s[0][v];
+#pragma unroll
+    for (int f = 1; f < N; f++) mx = s[f][v] > mx ? s[f][v] : mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int f = 0; f < N; f++) sum += expf(s[f][v] - mx);
+    if (!LOG) {
+#pragma unroll
+      for (int f = 0; f < N; f++) s[f][v] = expf(s[f][v] - mx) / sum;
+    } else {
+      float const lse = logf(sum) + mx;
+#pragma unroll
+      for (int f = 0; f < N; f++) s[f][v] = s[f][v] - lse;
+    }
+  }
+}
+
+// MinMaxNorm, ponni_MinMaxNorm.h:68-84.
+template <int V, int N, int W>
+__device__ inline void min_max(float (&s)[W][V], float out_min, float out_max, float eps) {
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float lo = s[0][v], hi = s[0][v];
+#pragma unroll
+    for (int f = 1; f < N; f++) {
+      if (s[f][v] < lo) lo = s[f][v];
+      if (s[f][v] > hi) hi = s[f][v];
+    }
+    float const scale = (out_max - out_min) / ((hi - lo) + eps);
+#pragma unroll
+    for (int f = 0; f < N; f++) s[f][v] = out_min + (s[f][v] - lo) * scale;
+  }
+}
+
+// [lead; trail] with the leading operand's FIRST rows, ponni_Binop_Concatenate.h:63-86.
+template <int V, int FIRST, int NOUT, int W>
+__device__ inline void concat(float (&s)[W][V], float const (&lead)[W][V], float const (&trail)[W][V]) {
+  float o[W][V];
+#pragma unroll
+  for (int f = 0; f < W; f++)
+#pragma unroll
+    for (int v = 0; v < V; v++)
+      o[f][v] = f < FIRST ? lead[f][v] : f < NOUT ? trail[f - FIRST][v] : 0.0f;
+  copy<V, W>(s, o);
+}
+
+// s[i] += b[i] + sum_k W(k, i) saved[k] (bias first), ponni_Binop_Projection_Add.h:81-95.
+template <int V, int NIN, int NSAVE, int W>
+__device__ inline void proj_add(float (&s)[W][V], float const (&sv)[W][V], float const* __restrict__ w,
+                                float const* __restrict__ b) {
+#pragma unroll
+  for (int i = 0; i < NIN; i++) {
+    float proj[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) proj[v] = b[i];
+#pragma unroll
+    for (int k = 0; k < NSAVE; k++) {
+      float const wk = w[k * W + i];
+#pragma unroll
+      for (int v = 0; v < V; v++) proj[v] += wk * sv[k][v];
+    }
+#pragma unroll
+    for (int v = 0; v < V; v++) s[i][v] = s[i][v] + proj[v];
+  }
+}
+
+}  // namespace narrowj
+}  // namespace ponni_hip

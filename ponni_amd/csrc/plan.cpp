@@ -692,7 +692,7 @@ int upload(ponni_plan_s& p) {
       HIP_TRY(hipMemcpy(p.d_params, f.data(), f.size() * 4, hipMemcpyHostToDevice));
     }
   }
-  if (p.path == PONNI_PATH_FUSED && p.fused_fn == nullptr) {
+  if ((p.path == PONNI_PATH_FUSED || p.narrow_jit) && p.fused_fn == nullptr) {
     std::string error;
     int const st = fused_prepare(p, error);
     if (st != PONNI_OK) return fail(st, error);
@@ -807,6 +807,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   p->path = chosen;
   p->width_class = chosen == PONNI_PATH_NARROW ? narrow : chosen == PONNI_PATH_MFMA ? mfma : 0;
   lower(*p);
+  p->narrow_jit = chosen == PONNI_PATH_NARROW && jit_enabled && narrow_jit_supports(*p);
   *out_plan = p;
   return PONNI_OK;
 }
@@ -944,7 +945,10 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_
   }
   hipError_t err = hipSuccess;
   switch (plan->path) {
-    case PONNI_PATH_NARROW: err = launch_narrow(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
+    case PONNI_PATH_NARROW:
+      err = plan->narrow_jit ? fused_launch(*plan, a, stream)
+                             : launch_narrow(plan->dtype, plan->width_class, plan->num_slots, a, stream);
+      break;
     case PONNI_PATH_MFMA: err = launch_mfma(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
     case PONNI_PATH_FUSED: err = fused_launch(*plan, a, stream); break;
     default: err = launch_generic(plan->dtype, a, stream); break;
@@ -958,8 +962,8 @@ int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {
     fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
     return -1;
   }
-  if (plan->path != PONNI_PATH_FUSED) {
-    fail(PONNI_ERR_UNSUPPORTED, "only FUSED plans generate a kernel");
+  if (plan->path != PONNI_PATH_FUSED && !plan->narrow_jit) {
+    fail(PONNI_ERR_UNSUPPORTED, "only FUSED and generated NARROW plans have a kernel source");
     return -1;
   }
   FusedConfig cfg;
@@ -977,7 +981,7 @@ int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {
 
 int ponni_plan_compile(ponni_plan plan) {
   if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
-  if (plan->path != PONNI_PATH_FUSED) return PONNI_OK;
+  if (plan->path != PONNI_PATH_FUSED && !plan->narrow_jit) return PONNI_OK;
   std::string key, error;
   std::vector<char> code;
   int const st = fused_compile(*plan, key, code, error);

@@ -80,7 +80,9 @@ struct ponni_plan_s {
   void* d_scratch[2 + ponni_hip::kMaxSlots] = {};  // tmp1, tmp2, saved slots
   int64_t capacity = 0;
 
-  // FUSED path: the plan's generated kernel (compiled on first forward).
+  // NARROW plans run a generated kernel (narrow_jit.h) unless JIT is off.
+  bool narrow_jit = false;
+  // FUSED path (and generated NARROW): the plan's generated kernel (compiled on first forward).
   hipFunction_t fused_fn = nullptr;
   int fused_blocks_per_cu = 1;
   bool fused_persistent = false;  // grid sized to the resident workgroups

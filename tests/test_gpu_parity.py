@@ -17,7 +17,9 @@ from tests import test_oracle as K
 
 pytestmark = pytest.mark.gpu
 
-PATHS = ["generic", "narrow", "mfma", "fused"]
+# "narrow-aot" is the interpreted NARROW kernel (run-time compilation off);
+# "narrow" is the generated NARROW kernel.
+PATHS = ["generic", "narrow", "narrow-aot", "mfma", "fused"]
 TORCH_DT = {"f32": "float32", "f16": "float16", "bf16": "bfloat16", "f64": "float64"}
 ORACLE_MODE = {"f32": oracle.MODE_F32, "f64": oracle.MODE_F64, "f16": oracle.MODE_F16_OPERANDS,
                "bf16": oracle.MODE_BF16_OPERANDS}
@@ -28,12 +30,29 @@ def _oracle_built():
     oracle.build()
 
 
+def make_model(layers, dtype, path):
+    """Plan for `path`; "narrow-aot" disables run-time compilation (PONNI_JIT=0)."""
+    import os
+
+    if path != "narrow-aot":
+        return P.create_inference_model(*layers, dtype=dtype, path=path)
+    old = os.environ.get("PONNI_JIT")
+    os.environ["PONNI_JIT"] = "0"
+    try:
+        return P.create_inference_model(*layers, dtype=dtype, path="narrow")
+    finally:
+        if old is None:
+            del os.environ["PONNI_JIT"]
+        else:
+            os.environ["PONNI_JIT"] = old
+
+
 def gpu_run(layers, x_np, dtype="f32", path="auto", pad=0, dev="cuda:0"):
     import torch
 
     tdt = getattr(torch, TORCH_DT[dtype])
     try:
-        m = P.create_inference_model(*layers, dtype=dtype, path=path)
+        m = make_model(layers, dtype, path)
     except P.PonniError as e:
         if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
             pytest.skip(f"{path} does not support this chain: {e.message}")
@@ -241,3 +260,22 @@ def test_random_chains_reduced_precision_fused(cuda, dtype, seed):
     x = rng.standard_normal((width, 777))
     got, xg, _ = gpu_run(layers, x, dtype=dtype, path="fused", pad=2)
     check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("B", [4096, 4099, 37])
+def test_narrow_vector_rows(cuda, dtype, B):
+    """Generated NARROW kernel: rows move as aligned vectors (ld a multiple of
+    8), with a partial last vector when B is not; every width class."""
+    rng = np.random.default_rng(B)
+    for w in (3, 6, 12):
+        layers = [P.Matvec(rng.uniform(-0.5, 0.5, (5, w))), P.Bias(rng.uniform(-0.1, 0.1, w)), P.Tanh(w),
+                  P.Save_State(0, w), P.Relu(w), P.Binop_Add(0, w), P.Matvec(rng.uniform(-0.5, 0.5, (w, 2))),
+                  P.Bias(rng.uniform(-0.1, 0.1, 2))]
+        x = rng.normal(size=(5, B))
+        got, xg, m = gpu_run(layers, x, dtype=dtype, path="narrow", pad=(-B) % 8 + 8)
+        assert m.path == "narrow"
+        if dtype == "f32":
+            check_f32(got, oracle.forward(layers, xg))
+        else:
+            check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
