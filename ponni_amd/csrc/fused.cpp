@@ -677,25 +677,25 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   int const W = p.width_class;
   int const V = narrow_samples_per_lane(p);
   std::string const S = p.dtype == PONNI_F16 ? "_Float16" : p.dtype == PONNI_BF16 ? "__bf16" : "float";
+  // U groups of V samples per lane, 256 * V samples apart, so that all of a
+  // lane's input rows are in flight before its first FMA.
+  int U = 1;
+  if (char const* e = std::getenv("PONNI_NARROW_UNROLL")) {  // tuning override
+    int const v = std::atoi(e);
+    if (v >= 1 && v <= 8) U = v;
+  }
   cfg = FusedConfig{};
   cfg.waves = 4;
   cfg.waves_per_simd = 4;
-  cfg.columns_per_block = 256 * V;
+  cfg.columns_per_block = 256 * V * U;
   std::string const WV = ", " + std::to_string(W) + ">";
   auto tv = [&](int n) { return "<" + std::to_string(V) + ", " + std::to_string(n) + WV; };
   auto finish = [&](int n) { return "    finish<S, " + std::to_string(V) + ", " + std::to_string(n) + WV; };
   std::ostringstream o;
   o << "// generated by libponni_hip for one plan (NARROW)\n#include \"narrow_jit.h\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::narrowj;\ntypedef " << S << " S;\n";
-  o << "extern \"C\" __global__ __launch_bounds__(256) void " << fused_kernel_name(p)
-    << "(float const* __restrict__ P, S const* __restrict__ x, int64_t ldx, S* __restrict__ y, int64_t ldy, "
-       "int64_t batch) {\n";
-  o << "  int64_t const b0 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * " << V << ";\n";
-  o << "  if (b0 >= batch) return;\n";
-  o << "  bool const vec = b0 + " << V << " <= batch && vec_ok<S, " << V << ">(x, ldx) && vec_ok<S, " << V
-    << ">(y, ldy);\n";
-  o << "  float s[" << W << "][" << V << "];\n";
-  o << "  load<S, " << V << ", " << p.layers.front().n_in << WV << "(s, x, ldx, b0, batch, vec);\n";
+  // The chain on one group of V samples.
+  o << "__device__ inline void chain(float (&s)[" << W << "][" << V << "], float const* __restrict__ P) {\n";
   for (int sl = 0; sl < p.num_slots; sl++)
     o << "  float sv" << sl << "[" << W << "][" << V << "] = {};\n";
   int cur_n = p.layers.front().n_in;
@@ -768,7 +768,32 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "  }\n";
     cur_n = op.n_out;
   }
-  o << "  store<S, " << V << ", " << p.layers.back().n_out << WV << "(s, y, ldy, b0, batch, vec);\n}\n";
+  o << "}\n";
+  o << "extern \"C\" __global__ __launch_bounds__(256) void " << fused_kernel_name(p)
+    << "(float const* __restrict__ P, S const* __restrict__ x, int64_t ldx, S* __restrict__ y, int64_t ldy, "
+       "int64_t batch) {\n";
+  o << "  constexpr int U = " << U << ", V = " << V << ";\n";
+  o << "  bool const aligned = vec_ok<S, V>(x, ldx) && vec_ok<S, V>(y, ldy);\n";
+  // Workgroups wholly inside the batch (all but the last) with vector-aligned
+  // views take a path with no per-lane predicate, so every load is issued
+  // before the first wait.
+  o << "  if (aligned && (int64_t(blockIdx.x) + 1) * (U * 256 * V) <= batch) {\n";
+  o << "    float s[U][" << W << "][V];\n";
+  o << "#pragma unroll\n    for (int u = 0; u < U; u++)\n      load<S, V, " << p.layers.front().n_in << WV
+    << "(s[u], x, ldx, ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V, batch, true);\n";
+  o << "#pragma unroll\n    for (int u = 0; u < U; u++) chain(s[u], P);\n";
+  o << "#pragma unroll\n    for (int u = 0; u < U; u++)\n      store<S, V, " << p.layers.back().n_out << WV
+    << "(s[u], y, ldy, ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V, batch, true);\n";
+  o << "    return;\n  }\n";
+  o << "  float s[U][" << W << "][V];\n";
+  o << "  int64_t b0[U];\n";
+  o << "#pragma unroll\n  for (int u = 0; u < U; u++) {\n";
+  o << "    b0[u] = ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V;\n";
+  o << "    if (b0[u] < batch) load<S, V, " << p.layers.front().n_in << WV
+    << "(s[u], x, ldx, b0[u], batch, aligned && b0[u] + V <= batch);\n  }\n";
+  o << "#pragma unroll\n  for (int u = 0; u < U; u++)\n    if (b0[u] < batch) chain(s[u], P);\n";
+  o << "#pragma unroll\n  for (int u = 0; u < U; u++)\n    if (b0[u] < batch) store<S, V, " << p.layers.back().n_out
+    << WV << "(s[u], y, ldy, b0[u], batch, aligned && b0[u] + V <= batch);\n}\n";
   return o.str();
 }
 
