@@ -330,9 +330,17 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::ostringstream o;
   std::string const IO = half ? E : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
-  if (char const* d = std::getenv("PONNI_KSPLIT")) {  // tuning override
+  if (char const* d = std::getenv("PONNI_SETPRIO")) {  // tuning override
     int const v = std::atoi(d);
-    if (v >= 1 && v <= 4) o << "#define PONNI_KSPLIT " << v << "\n";
+    if (v == 0 || v == 1) o << "#define PONNI_SETPRIO " << v << "\n";
+  }
+  if (char const* d = std::getenv("PONNI_TILE_GROUP")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 1 && v <= 4) o << "#define PONNI_TILE_GROUP " << v << "\n";
+  }
+  if (char const* d = std::getenv("PONNI_DEFER_EPILOGUE")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v == 0 || v == 1) o << "#define PONNI_DEFER_EPILOGUE " << v << "\n";
   }
   if (char const* d = std::getenv("PONNI_LDS_RING")) {  // tuning override
     int const v = std::atoi(d);
@@ -346,6 +354,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
   }
+  if (half && std::getenv("PONNI_HALF_TILE_BARRIER")) o << "#define PONNI_TILE_BARRIER 1\n";  // tuning override
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
@@ -373,7 +382,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::vector<DenseRef> dense_seq;
   for (Op const& op : p.ops)
     if (op.code == OP_DENSE) dense_seq.push_back({op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
-  if (half && !dense_seq.empty()) {
+  // (tuning override PONNI_HALF_STAGE=0: A fragments straight from L1/L2 per wave)
+  bool const half_staged = !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
+  if (half && half_staged && !dense_seq.empty()) {
     o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
     o << "  Stage<E> st{a_slots, 0};\n";
     o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", " << cfg.waves
@@ -485,7 +496,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         // A 16-bit block ending in Tanh looks the activation up in the LDS table.
         bool const lut_tanh = half && cfg.lut_bytes > 0 && op.epi_count > (seed ? 1 : 0) &&
                               p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH;
-        if (half) {
+        if (half && !half_staged) {
+          std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
+          o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
+            << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, " << init << ", [&](int mo, floatx4 (&t)["
+            << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
+        } else if (half) {
           std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
           auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
           dense_index++;

@@ -237,8 +237,14 @@ constexpr int kSlotFrags = 8 * kChunkTiles;  // fragments per slot (256 input fe
 #ifndef PONNI_LDS_RING
 #define PONNI_LDS_RING 2
 #endif
-#ifndef PONNI_KSPLIT
-#define PONNI_KSPLIT 1
+#ifndef PONNI_SETPRIO
+#define PONNI_SETPRIO 1
+#endif
+#ifndef PONNI_TILE_GROUP
+#define PONNI_TILE_GROUP 2
+#endif
+#ifndef PONNI_DEFER_EPILOGUE
+#define PONNI_DEFER_EPILOGUE 1
 #endif
 
 template <class E>
@@ -295,9 +301,13 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
   constexpr int NCH = (TO + CT - 1) / CT;
   constexpr int NFN = cmin(CT, TON) * TSN;  // fragments of the next layer's first chunk
   static_assert(TS <= 8 && TSN <= 8, "at most 256 input features");
+  // Tiles per group: GT must divide CT and TO (else one at a time); DEFER
+  // runs a group's epilogue after the next group's MFMAs.
+  constexpr int GT = (CT % PONNI_TILE_GROUP == 0 && TO % PONNI_TILE_GROUP == 0) ? PONNI_TILE_GROUP : 1;
+  constexpr bool DEFER = PONNI_DEFER_EPILOGUE != 0;
   int const wave = wave_id();
   H<TO, NT, E> out;
-  floatx4 prev[NT];
+  floatx4 prev[GT][NT];
 #pragma unroll
   for (int ch = 0; ch < NCH; ch++) {
     int const t0 = ch * CT;
@@ -326,46 +336,54 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
       for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
     }
     V8 const* __restrict__ sl = st.slots + st.cur * (kSlotFrags * 64) + L.lane;
+    // GT output tiles at a time: GT * NT independent accumulation chains.
 #pragma unroll
-    for (int tt = 0; tt < CT; tt++) {
-      int const mo = t0 + tt;
-      if (mo < TO) {
-        // A fragments through a small register ring (LDS latency is covered
-        // by the other wave of the SIMD).
-        constexpr int R = TS < PONNI_LDS_RING ? TS : PONNI_LDS_RING;
-        V8 a[R];
+    for (int tt = 0; tt < CT; tt += GT) {
+      int const mo0 = t0 + tt;
+      if (mo0 < TO) {
+        floatx4 acc[GT][NT];
 #pragma unroll
-        for (int t = 0; t < R; t++) a[t] = sl[(tt * TS + t) * 64];
-        // KS independent accumulation chains per column tile (even / odd
-        // steps), so the matrix pipe is not bound by one chain's latency.
-        constexpr int KS = TS >= 2 ? PONNI_KSPLIT : 1;
-        floatx4 acc[KS][NT];
-        floatx4 const seed = init(mo);
+        for (int q = 0; q < GT; q++) {
+          floatx4 const seed = init(mo0 + q < TO ? mo0 + q : mo0);
 #pragma unroll
-        for (int n = 0; n < NT; n++) {
-          acc[0][n] = seed;
-#pragma unroll
-          for (int k = 1; k < KS; k++) acc[k][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int n = 0; n < NT; n++) acc[q][n] = seed;
         }
+        // The wave in its MFMA phase runs at raised priority, so the SIMD's
+        // other wave fills the matrix pipe's shadow with its VALU epilogue
+        // instead of both waves contending in the same phase.
+        if (PONNI_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int t = 0; t < TS; t++) {
-          V8 const at = a[t % R];
-          if (t + R < TS) a[t % R] = sl[(tt * TS + t + R) * 64];
+          V8 a[GT];
+#pragma unroll
+          for (int q = 0; q < GT; q++)
+            if (mo0 + q < TO) a[q] = sl[((tt + q) * TS + t) * 64];
 #pragma unroll
           for (int n = 0; n < NT; n++) {
             V4 const lo = in.v[2 * t][n];
             V4 const hi = (2 * t + 1 < TI) ? in.v[(2 * t + 1 < TI) ? 2 * t + 1 : 2 * t][n]
                                            : V4{E(0.0f), E(0.0f), E(0.0f), E(0.0f)};
-            acc[t % KS][n] = Vec<E>::mfma(at, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[t % KS][n]);
+            V8 const b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int q = 0; q < GT; q++)
+              if (mo0 + q < TO) acc[q][n] = Vec<E>::mfma(a[q], b, acc[q][n]);
           }
         }
+        if (PONNI_SETPRIO) __builtin_amdgcn_s_setprio(0);
+        if (DEFER) {
+          // The previous group's epilogue runs behind this group's MFMAs.
+          if (mo0 > 0)
 #pragma unroll
-        for (int k = 1; k < KS; k++)
+            for (int q = 0; q < GT; q++) epi(mo0 - GT + q, prev[q], out.v[mo0 - GT + q]);
 #pragma unroll
-          for (int n = 0; n < NT; n++) acc[0][n] += acc[k][n];
-        if (mo > 0) epi(mo - 1, prev, out.v[mo - 1]);
+          for (int q = 0; q < GT; q++)
 #pragma unroll
-        for (int n = 0; n < NT; n++) prev[n] = acc[0][n];
+            for (int n = 0; n < NT; n++) prev[q][n] = acc[q][n];
+        } else {
+#pragma unroll
+          for (int q = 0; q < GT; q++)
+            if (mo0 + q < TO) epi(mo0 + q, acc[q], out.v[mo0 + q]);
+        }
       }
     }
     // Slot cur ^ 1 was last read before the previous barrier.
@@ -395,7 +413,9 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
     __syncthreads();
     st.cur ^= 1;
   }
-  epi(TO - 1, prev, out.v[TO - 1]);
+  if (DEFER)
+#pragma unroll
+    for (int q = 0; q < GT; q++) epi(TO - GT + q, prev[q], out.v[TO - GT + q]);
   return out;
 }
 
