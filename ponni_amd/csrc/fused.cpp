@@ -431,6 +431,22 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o.str("");
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
   o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
+  // 16-bit plans request each tile's input rows into LDS one tile ahead
+  // (fused_f16.h prefetch_rows_lds) when the buffer fits next to the staged
+  // A fragments (2 slots x 8 fragments x PONNI_CHUNK_TILES KB) and vectors.
+  int const n_in0 = p.layers.front().n_in;
+  int const in_dma_bytes = cfg.waves * tiles(n_in0) * NT * 4 * 64 * 4;
+  int chunk_tiles = 4;
+  if (char const* d = std::getenv("PONNI_CHUNK_TILES")) chunk_tiles = std::max(1, std::min(8, std::atoi(d)));
+  bool in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + 2 * 8 * 1024 * chunk_tiles + 16 * 1024 <= 160 * 1024;
+  if (char const* v = std::getenv("PONNI_INPUT_DMA"))  // tuning override
+    in_dma = in_dma && std::strcmp(v, "0") != 0;
+  std::string const WCOLS = std::to_string(16 * NT), NW = std::to_string(cfg.waves);
+  if (in_dma) {
+    o << "  __shared__ unsigned in_buf[" << cfg.waves << "][" << in_dma_bytes / 4 / cfg.waves << "];\n";
+    o << "  L.col0 = (int64_t(blockIdx.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
+    o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
+  }
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
   o << "    L.col0 = (tile * " << cfg.waves << " + wave_id()) * " << 16 * NT << ";\n";
   // Register-resident parameters may be hoisted out of the tile loop; otherwise
@@ -440,7 +456,13 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   auto fresh = [&]() { return "s" + std::to_string(var++); };
   std::string cur = fresh();
   int cur_n = p.layers.front().n_in;
-  if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
+  if (in_dma) {
+    o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
+    o << "    wait_lds();\n";
+    o << "    if (tile + gridDim.x < tiles) {\n      Lane Ln = L;\n      Ln.col0 = ((tile + gridDim.x) * " << NW
+      << " + wave_id()) * " << WCOLS << ";\n      prefetch_rows_lds<" << cur_n << ", " << NT
+      << ">(x, ldx, Ln, in_buf[wave_id()]);\n    }\n";
+  } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
   // The logistic family runs on the hardware transcendentals (fused_f32.h).

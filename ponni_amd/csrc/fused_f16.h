@@ -132,6 +132,61 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
   return s;
 }
 
+// ---- input rows prefetched into LDS one tile ahead ----------------------
+// Each lane's input elements (row 16m + 4g + e, column col0 + 16n + c) are
+// requested with global_load_lds_ushort: instruction i = (m NT + n) 4 + e
+// writes lane l's element, zero-extended, to the dword buf[i * 64 + l] (the
+// DMA's per-lane stride is 4 bytes).  The next tile's rows are requested as
+// soon as this tile's are read, so their HBM latency hides behind a whole
+// tile of work.  Lanes outside the rows or the batch issue nothing and read 0.
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+template <int N, int NT, class E>
+__device__ inline void prefetch_rows_lds(E const* __restrict__ x, int64_t ld, Lane const& L,
+                                         unsigned* __restrict__ buf) {
+  constexpr int T = (N + 15) / 16;
+  E const* __restrict__ xl = lane_ptr(x, ld, L);
+  bool const full = L.col0 + 16 * NT <= L.batch;
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+      bool const col_ok = full || L.col0 + 16 * n + L.c < L.batch;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        int const f = 16 * m + 4 * L.g + e;
+        if ((N % 16 == 0 || f < N) && col_ok)
+          __builtin_amdgcn_global_load_lds(static_cast<void const*>(xl + int64_t(16 * m + e) * ld + 16 * n),
+                                           (lds_ptr)(buf + ((m * NT + n) * 4 + e) * 64), 2, 0, 0);
+      }
+    }
+}
+
+template <int N, int NT, class E>
+__device__ inline H<(N + 15) / 16, NT, E> load_rows_lds(unsigned const* __restrict__ buf, Lane const& L) {
+  constexpr int T = (N + 15) / 16;
+  H<T, NT, E> s;
+  bool const full = L.col0 + 16 * NT <= L.batch;
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+      bool const col_ok = full || L.col0 + 16 * n + L.c < L.batch;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        int const f = 16 * m + 4 * L.g + e;
+        unsigned short const bits = static_cast<unsigned short>(buf[((m * NT + n) * 4 + e) * 64 + L.lane]);
+        s.v[m][n][e] = ((N % 16 == 0 || f < N) && col_ok) ? __builtin_bit_cast(E, bits) : E(0.0f);
+      }
+    }
+  return s;
+}
+
+// Waits: every outstanding vector-memory operation of this wave (vmcnt(0)),
+// or every outstanding LDS operation (lgkmcnt(0)).
+__device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 template <int N, int T, int NT, class E>
 __device__ inline void store_rows_h(H<T, NT, E> const& s, E* __restrict__ y, int64_t ld, Lane const& L) {
   E* __restrict__ yl = lane_ptr(y, ld, L);
