@@ -265,6 +265,35 @@ int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len);
  * happens when the application is compiled. */
 int ponni_plan_compile(ponni_plan plan);
 
+/* --- in-kernel (per-sample) inference ------------------------------------- */
+
+/* Device-side description of a plan for application kernels that evaluate
+ * one sample at a time (ponni_amd/include/ponni/device.h, ponni::forward_one):
+ * the op list, epilogue steps and parameters of the plan's GENERIC lowering
+ * (reference parameter layout), in device memory owned by the plan.  Stands
+ * in for the reference's Inference::params (Params{saved_states, layers,
+ * tmp1, tmp2}, ponni_Inference.h:127-149) as passed to
+ * forward_batch_parallel_in_kernel (ponni_Inference.h:394-408, :592-604);
+ * per-sample states live in the calling thread's private memory instead of
+ * the [width, capacity] scratch. */
+typedef struct ponni_device_model {
+  const void* ops;    /* device op list (internal record, program.h) */
+  const void* steps;  /* device epilogue steps */
+  const void* params; /* device parameters, float (double for F64 plans) */
+  int32_t num_ops;
+  int32_t dtype;      /* ponni_dtype of the plan */
+  int32_t num_inputs;
+  int32_t num_outputs;
+  int32_t max_width;  /* widest state of the chain */
+  int32_t tmp_features[2];
+  int32_t saved_features[8];
+} ponni_device_model;
+
+/* Fill *out for `plan` (uploading its GENERIC form on first use and after
+ * parameter changes; the pointers stay valid until the plan is destroyed).
+ * Synchronizes the device when it uploads. */
+int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out);
+
 /* --- synthetic data (bench and tests) ------------------------------------- */
 
 /* Fill n elements of a device buffer of `dtype` with the counter-based

@@ -7,228 +7,32 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include "generic_ops.h"
 #include "plan.h"
-#include "pointwise.h"
 
 namespace ponni_hip {
-namespace {
 
-template <class S> struct Compute { using type = float; };
-template <> struct Compute<double> { using type = double; };
-
-template <class S> __device__ inline typename Compute<S>::type load_as(S const* p) {
-  return static_cast<typename Compute<S>::type>(*p);
-}
 template <> __device__ inline float load_as<__half>(__half const* p) { return __half2float(*p); }
 template <> __device__ inline float load_as<__hip_bfloat16>(__hip_bfloat16 const* p) { return __bfloat162float(*p); }
-
-template <class S, class C> __device__ inline void store_as(S* p, C v) { *p = static_cast<S>(v); }
 template <> __device__ inline void store_as<__half, float>(__half* p, float v) { *p = __float2half_rn(v); }
 template <> __device__ inline void store_as<__hip_bfloat16, float>(__hip_bfloat16* p, float v) {
   *p = __float2bfloat16(v);
 }
 
-struct View2 {
-  char* base;
-  int64_t ld;
-};
-
-template <class S>
-__device__ inline S* at(View2 const& v, int f, int64_t b) {
-  return reinterpret_cast<S*>(v.base) + (int64_t(f) * v.ld + b);
-}
+namespace {
 
 template <class S>
 __global__ __launch_bounds__(256) void generic_forward(LaunchArgs args) {
   using C = typename Compute<S>::type;
   int64_t const b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= args.batch) return;
-  C const* params = static_cast<C const*>(args.params);
   View2 buf[BUF_SAVED + kMaxSlots];
 #pragma unroll
   for (int i = 0; i < BUF_SAVED + kMaxSlots; i++) {
     buf[i].base = static_cast<char*>(args.buffers[i]);
     buf[i].ld = args.buffer_ld[i];
   }
-  for (int o = 0; o < args.num_ops; o++) {
-    Op const op = args.ops[o];
-    View2 const in = buf[op.src];
-    View2 const out = buf[op.dst];
-    switch (op.code) {
-      case OP_DENSE: {
-        // ponni_Inference.h:431-444 with Matvec::compute_output (ponni_Matvec.h:70-79).
-        // A generated Dense seeds the sum with its bias (emitter.py:701-710).
-        C const* w = params + op.woff;
-        int const first = (op.aux & DENSE_BIAS_FIRST) ? 1 : 0;
-        for (int f = 0; f < op.n_out; f++) {
-          C v = first ? params[args.steps[op.epi_begin].off + f] : C(0);
-          for (int k = 0; k < op.n_in; k++) v += w[int64_t(k) * op.n_out + f] * load_as<S>(at<S>(in, k, b));
-          for (int s = first; s < op.epi_count; s++) {
-            Step const st = args.steps[op.epi_begin + s];
-            C const bias = act_has_param(st.act) ? params[st.off + f] : C(0);
-            v = apply_step<C>(st.act, v, bias, C(st.a), C(st.b));
-          }
-          store_as<S, C>(at<S>(out, f, b), v);
-        }
-        break;
-      }
-      case OP_POINTWISE: {
-        Step const st = args.steps[op.epi_begin];
-        for (int f = 0; f < op.n_out; f++) {
-          C const bias = act_has_param(st.act) ? params[st.off + f] : C(0);
-          store_as<S, C>(at<S>(out, f, b), apply_step<C>(st.act, load_as<S>(at<S>(in, f, b)), bias, C(st.a), C(st.b)));
-        }
-        break;
-      }
-      case OP_LAYER_NORM: {  // ponni_LayerNorm.h:76-99
-        int const n = op.n_in;
-        C mean = C(0);
-        for (int f = 0; f < n; f++) mean += load_as<S>(at<S>(in, f, b));
-        mean /= C(n);
-        C var = C(0);
-        for (int f = 0; f < n; f++) {
-          C const d = load_as<S>(at<S>(in, f, b)) - mean;
-          var += d * d;
-        }
-        var /= C(n);
-        C const inv_std = C(1) / d_sqrt(var + C(op.f0));
-        for (int f = 0; f < n; f++) {
-          C const xhat = (load_as<S>(at<S>(in, f, b)) - mean) * inv_std;
-          store_as<S, C>(at<S>(out, f, b), params[op.woff + f] * xhat + params[op.boff + f]);
-        }
-        break;
-      }
-      case OP_SOFTMAX:
-      case OP_LOG_SOFTMAX: {  // ponni_Softmax.h:45-56, ponni_LogSoftmax.h:45-57
-        int const n = op.n_in;
-        C mx = load_as<S>(at<S>(in, 0, b));
-        for (int f = 1; f < n; f++) {
-          C const v = load_as<S>(at<S>(in, f, b));
-          mx = v > mx ? v : mx;
-        }
-        C sum = C(0);
-        for (int f = 0; f < n; f++) sum += d_exp(load_as<S>(at<S>(in, f, b)) - mx);
-        if (op.code == OP_SOFTMAX) {
-          for (int f = 0; f < n; f++)
-            store_as<S, C>(at<S>(out, f, b), d_exp(load_as<S>(at<S>(in, f, b)) - mx) / sum);
-        } else {
-          C const lse = d_log(sum) + mx;
-          for (int f = 0; f < n; f++) store_as<S, C>(at<S>(out, f, b), load_as<S>(at<S>(in, f, b)) - lse);
-        }
-        break;
-      }
-      case OP_MIN_MAX: {  // ponni_MinMaxNorm.h:67-84
-        int const n = op.n_in;
-        C lo = load_as<S>(at<S>(in, 0, b));
-        C hi = lo;
-        for (int f = 1; f < n; f++) {
-          C const v = load_as<S>(at<S>(in, f, b));
-          if (v < lo) lo = v;
-          if (v > hi) hi = v;
-        }
-        C const scale = (C(op.f1) - C(op.f0)) / ((hi - lo) + C(op.f2));
-        for (int f = 0; f < n; f++)
-          store_as<S, C>(at<S>(out, f, b), C(op.f0) + (load_as<S>(at<S>(in, f, b)) - lo) * scale);
-        break;
-      }
-      case OP_SAVE: {  // ponni_Save_State.h:57-67; a leading save also fills tmp1
-        for (int f = 0; f < op.n_out; f++) {
-          S const v = *at<S>(in, f, b);
-          *at<S>(out, f, b) = v;
-          if (op.aux) *at<S>(buf[BUF_TMP1], f, b) = v;
-        }
-        break;
-      }
-      case OP_ADD: {  // ponni_Binop_Add.h:57-68
-        View2 const sv = buf[BUF_SAVED + op.slot];
-        for (int f = 0; f < op.n_out; f++)
-          store_as<S, C>(at<S>(out, f, b), load_as<S>(at<S>(in, f, b)) + load_as<S>(at<S>(sv, f, b)));
-        break;
-      }
-      case OP_CONCAT: {  // ponni_Binop_Concatenate.h:63-86
-        View2 const sv = buf[BUF_SAVED + op.slot];
-        int const n1 = op.n_in;
-        int const n2 = op.n_out - op.n_in;
-        if (op.aux) {
-          // Rows below n1 keep the current state; an in-place write is safe.
-          for (int f = n1; f < op.n_out; f++) *at<S>(out, f, b) = *at<S>(sv, f - n1, b);
-          if (out.base != in.base)
-            for (int f = 0; f < n1; f++) *at<S>(out, f, b) = *at<S>(in, f, b);
-        } else {
-          // [saved; current]: move the current rows up first (descending) so an
-          // in-place write never reads an overwritten row.
-          for (int f = op.n_out - 1; f >= n2; f--) *at<S>(out, f, b) = *at<S>(in, f - n2, b);
-          for (int f = 0; f < n2; f++) *at<S>(out, f, b) = *at<S>(sv, f, b);
-        }
-        break;
-      }
-      case OP_PROJ_ADD: {  // ponni_Binop_Projection_Add.h:81-95
-        View2 const sv = buf[BUF_SAVED + op.slot];
-        int const nsave = op.aux;
-        int const n = op.n_out;
-        C const* w = params + op.woff;
-        for (int i = 0; i < n; i++) {
-          C proj = params[op.boff + i];
-          for (int k = 0; k < nsave; k++) proj += w[int64_t(k) * n + i] * load_as<S>(at<S>(sv, k, b));
-          store_as<S, C>(at<S>(out, i, b), load_as<S>(at<S>(in, i, b)) + proj);
-        }
-        break;
-      }
-      case OP_LOAD: {  // the state becomes a saved one
-        for (int f = 0; f < op.n_out; f++) *at<S>(out, f, b) = *at<S>(in, f, b);
-        break;
-      }
-      case OP_BINARY: {  // emitter.py:735-741 with scalar-or-exact broadcasting
-        View2 const sv = buf[BUF_SAVED + op.slot];
-        int const bop = op.aux & 0xff;
-        bool const saved_left = op.aux & BIN_SAVED_LEFT;
-        C const s0 = load_as<S>(at<S>(in, 0, b));
-        C const v0 = load_as<S>(at<S>(sv, 0, b));
-        for (int f = 0; f < op.n_out; f++) {
-          C const a = (op.aux & BIN_STATE_SCALAR) ? s0 : load_as<S>(at<S>(in, f, b));
-          C const c = (op.aux & BIN_SAVED_SCALAR) ? v0 : load_as<S>(at<S>(sv, f, b));
-          store_as<S, C>(at<S>(out, f, b), saved_left ? apply_binary<C>(bop, c, a) : apply_binary<C>(bop, a, c));
-        }
-        break;
-      }
-      case OP_REDUCE: {  // emitter.py:475-547
-        int const n = op.n_in;
-        C r;
-        if (op.aux == PONNI_REDUCE_MAX || op.aux == PONNI_REDUCE_MIN || op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
-          bool const mn = op.aux == PONNI_REDUCE_MIN;
-          r = load_as<S>(at<S>(in, 0, b));
-          for (int f = 1; f < n; f++) {
-            C const v = load_as<S>(at<S>(in, f, b));
-            r = mn ? (v < r ? v : r) : (v > r ? v : r);
-          }
-          if (op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
-            C sum = C(0);
-            for (int f = 0; f < n; f++) sum += d_exp(load_as<S>(at<S>(in, f, b)) - r);
-            r = isinf(r) ? r : r + d_log(sum);
-          }
-        } else {
-          r = op.aux == PONNI_REDUCE_PROD ? C(1) : C(0);
-          for (int f = 0; f < n; f++) {
-            C const v = load_as<S>(at<S>(in, f, b));
-            switch (op.aux) {
-              case PONNI_REDUCE_L1: r += d_abs(v); break;
-              case PONNI_REDUCE_L2:
-              case PONNI_REDUCE_SUM_SQUARE: r += v * v; break;
-              case PONNI_REDUCE_PROD: r *= v; break;
-              default: r += v; break;
-            }
-          }
-          if (op.aux == PONNI_REDUCE_MEAN) r /= C(n);
-          else if (op.aux == PONNI_REDUCE_L2) r = d_sqrt(r);
-          else if (op.aux == PONNI_REDUCE_LOG_SUM) r = d_log(r);
-        }
-        store_as<S, C>(at<S>(out, 0, b), r);
-        break;
-      }
-      default:
-        break;
-    }
-  }
+  run_ops<S>(args.ops, args.num_ops, args.steps, static_cast<C const*>(args.params), buf, b);
 }
 
 }  // namespace

@@ -814,6 +814,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
 
 void ponni_plan_destroy(ponni_plan plan) {
   if (plan == nullptr) return;
+  if (plan->device_twin) ponni_plan_destroy(plan->device_twin);
   if (plan->device >= 0) {
     int cur = 0;
     if (hipGetDevice(&cur) == hipSuccess && cur != plan->device) (void)hipSetDevice(plan->device);
@@ -873,6 +874,7 @@ int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer, const void* valu
     for (int64_t i = 0; i < count; i++) dst[i] = v[i];
   }
   plan->device_dirty = true;
+  plan->params_version++;
   return PONNI_OK;
 }
 
@@ -986,6 +988,44 @@ int ponni_plan_compile(ponni_plan plan) {
   std::vector<char> code;
   int const st = fused_compile(*plan, key, code, error);
   return st == PONNI_OK ? PONNI_OK : fail(st, error);
+}
+
+int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
+  if (plan == nullptr || out == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or output");
+  if (plan->device_twin == nullptr) {
+    auto* t = new (std::nothrow) ponni_plan_s();
+    if (t == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+    t->layers = plan->layers;
+    t->dtype = plan->dtype;
+    t->num_slots = plan->num_slots;
+    t->max_width = plan->max_width;
+    for (int s = 0; s < kMaxSlots; s++) t->saved_features[s] = plan->saved_features[s];
+    t->path = PONNI_PATH_GENERIC;
+    t->width_class = 0;
+    lower(*t);
+    plan->device_twin = t;
+  }
+  ponni_plan_s& t = *plan->device_twin;
+  if (plan->twin_version != plan->params_version || t.device_dirty) {
+    t.params = plan->params;
+    t.device_dirty = true;
+    int const st = upload(t);
+    if (st != PONNI_OK) return st;
+    plan->twin_version = plan->params_version;
+  }
+  std::memset(out, 0, sizeof(*out));
+  out->ops = t.d_ops;
+  out->steps = t.d_steps;
+  out->params = t.d_params;
+  out->num_ops = static_cast<int32_t>(t.ops.size());
+  out->dtype = t.dtype;
+  out->num_inputs = t.layers.front().n_in;
+  out->num_outputs = t.layers.back().n_out;
+  out->max_width = t.max_width;
+  out->tmp_features[0] = t.tmp_features[0];
+  out->tmp_features[1] = t.tmp_features[1];
+  for (int s = 0; s < kMaxSlots; s++) out->saved_features[s] = t.saved_features[s];
+  return PONNI_OK;
 }
 
 int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed, uint64_t tag, int32_t dist, double a,

@@ -80,6 +80,11 @@ struct ponni_plan_s {
   void* d_scratch[2 + ponni_hip::kMaxSlots] = {};  // tmp1, tmp2, saved slots
   int64_t capacity = 0;
 
+  // GENERIC twin of this plan for ponni_plan_device_model (created on first
+  // use), and the parameter version it last uploaded.
+  ponni_plan_s* device_twin = nullptr;
+  uint64_t params_version = 1;
+  uint64_t twin_version = 0;
   // NARROW plans run a generated kernel (narrow_jit.h) unless JIT is off.
   bool narrow_jit = false;
   // FUSED path (and generated NARROW): the plan's generated kernel (compiled on first forward).

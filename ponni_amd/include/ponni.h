@@ -46,6 +46,7 @@
 #include <utility>
 #include <vector>
 
+#include "ponni/device.h"
 #include "ponni/ponni_file.h"
 #include "ponni_hip.h"
 
@@ -137,6 +138,21 @@ template <class real> constexpr int dtype_of() {
 
 struct LayoutRight {};
 
+// Trivially copyable handle of a View for device code (kernel arguments,
+// lambda captures): the same accessors, no ownership.
+template <class T>
+struct DeviceView {
+  using value_type = T;
+  using array_layout = LayoutRight;
+  static constexpr int rank = 2;
+  T* data_;
+  std::int64_t rows_, cols_, ld_;
+  __host__ __device__ T* data() const { return data_; }
+  __host__ __device__ std::int64_t extent(int d) const { return d == 0 ? rows_ : cols_; }
+  __host__ __device__ std::int64_t stride(int d) const { return d == 0 ? ld_ : 1; }
+  __host__ __device__ T& operator()(std::int64_t r, std::int64_t c) const { return data_[r * ld_ + c]; }
+};
+
 // A rank-2 LayoutRight [rows, cols] array in device memory; element (r, c)
 // at data()[r * stride(0) + c].  Copies share the allocation (as Kokkos::View).
 template <class T>
@@ -176,9 +192,11 @@ class View {
     return v;
   }
 
-  T* data() const { return data_; }
-  std::int64_t extent(int d) const { return d == 0 ? rows_ : cols_; }
-  std::int64_t stride(int d) const { return d == 0 ? ld_ : 1; }
+  __host__ __device__ T* data() const { return data_; }
+  __host__ __device__ std::int64_t extent(int d) const { return d == 0 ? rows_ : cols_; }
+  __host__ __device__ std::int64_t stride(int d) const { return d == 0 ? ld_ : 1; }
+  __host__ __device__ T& operator()(std::int64_t r, std::int64_t c) const { return data_[r * ld_ + c]; }
+  DeviceView<T> device() const { return DeviceView<T>{data_, rows_, cols_, ld_}; }
   std::int64_t size() const { return rows_ * cols_; }
   bool is_allocated() const { return data_ != nullptr; }
   std::string const& label() const { return label_; }
@@ -207,6 +225,20 @@ class View {
   std::shared_ptr<void> owner_;
   T* data_ = nullptr;
   std::int64_t rows_ = 0, cols_ = 0, ld_ = 0;
+};
+
+// Fixed-size per-thread array (ponni::SArray of the reference, used by the
+// in-kernel SArray form of forward_batch_parallel_in_kernel).
+template <class T, int N>
+struct SArray {
+  T v[N > 0 ? N : 1];
+  __host__ __device__ T& operator()(int i) { return v[i]; }
+  __host__ __device__ T const& operator()(int i) const { return v[i]; }
+  __host__ __device__ T& operator[](int i) { return v[i]; }
+  __host__ __device__ T const& operator[](int i) const { return v[i]; }
+  __host__ __device__ T* data() { return v; }
+  __host__ __device__ T const* data() const { return v; }
+  static constexpr int size() { return N; }
 };
 
 // LayoutRight check of the View contract (ponni_kokkos_utils.h:11-25).
@@ -796,6 +828,32 @@ class Inference {
     sync();
   }
 
+  // ---- in-kernel inference (ponni_Inference.h:394-408, :592-665) -----------------------
+  // `params` describes the model for application kernels; copy it into the
+  // kernel (`auto const p = model.params;`) and call
+  // Model::forward_batch_parallel_in_kernel(in, out, p, ibatch) per sample.
+  // It is refreshed whenever parameters are pushed (sync()).
+  using Params = ponni_device_model;
+  Params params{};
+
+  // Sample `ibatch` of LayoutRight [features, batch] views (device memory).
+  template <class InputView, class OutputView, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
+  __device__ static void forward_batch_parallel_in_kernel(InputView const& input, OutputView const& output,
+                                                          Params const& p, int ibatch) {
+    static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
+                  "in-kernel inference runs F32 and F64 models");
+    forward_one<real, MAXW, MAXSAVED>(p, input.data() + ibatch, input.stride(0), output.data() + ibatch,
+                                      output.stride(0));
+  }
+  // One sample held in per-thread arrays.
+  template <int NI, int NO, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
+  __device__ static void forward_batch_parallel_in_kernel(SArray<real, NI> const& input, SArray<real, NO>& output,
+                                                          Params const& p) {
+    static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
+                  "in-kernel inference runs F32 and F64 models");
+    forward_one<real, MAXW, MAXSAVED>(p, input.data(), 1, output.data(), 1);
+  }
+
   // Push parameters of layers changed since the last push (set_trainable_parameters,
   // or get_layer<I>() edits followed by mark_modified()).
   void sync() {
@@ -819,6 +877,11 @@ class Inference {
           (one(l), ...);
         },
         layers_);
+    // (Only where a device exists: models are also built on GPU-less hosts.)
+    int devices = 0;
+    if constexpr (std::is_same_v<real, float> || std::is_same_v<real, double>)
+      if (hipGetDeviceCount(&devices) == hipSuccess && devices > 0)
+        check(ponni_plan_device_model(plan_.get(), &params), "ponni_plan_device_model");
   }
 
   // ---- weights files (ponni_Inference.h:270-333) ---------------------------------------------

@@ -1,0 +1,66 @@
+// ponni/device.h -- per-sample inference inside application kernels (HIP).
+//
+// The reference lets code that already runs inside a Kokkos kernel evaluate
+// one sample of a model: Inference::forward_batch_parallel_in_kernel, in a
+// View form (sample `ibatch` of [features, batch] LayoutRight views,
+// src/ponni_Inference.h:394-408) and an SArray form (fixed-size per-thread
+// arrays, :592-665), both given the model's `params`.  Here the model's
+// device description comes from ponni_plan_device_model (include/ponni_hip.h):
+// the plan's GENERIC op list and parameters in device memory.  forward_one
+// walks that op list for one sample -- the same per-sample interpreter the
+// GENERIC batch kernel runs (csrc/generic_ops.h) -- with the intermediate
+// states (tmp1, tmp2, saved slots) in the calling thread's private memory
+// rather than in [width, capacity] HBM scratch.
+//
+// Build: hipcc ... -I<repo>/include -I<repo>/ponni_amd/include
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../../include/ponni_hip.h"
+#include "../../csrc/generic_ops.h"
+
+namespace ponni {
+
+// Thread-private state limits of forward_one: the widest state of the chain
+// (MAXW features) and all saved slots together (MAXSAVED features).
+constexpr int kInKernelMaxWidth = 256;
+constexpr int kInKernelMaxSaved = 512;
+
+// Can forward_one<real, MAXW, MAXSAVED> evaluate this model?
+template <int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
+__host__ __device__ inline bool fits_in_kernel(ponni_device_model const& m) {
+  int saved = 0;
+  for (int s = 0; s < 8; s++) saved += m.saved_features[s];
+  return m.max_width <= MAXW && m.tmp_features[0] <= MAXW && m.tmp_features[1] <= MAXW && saved <= MAXSAVED;
+}
+
+// One sample: out[f * out_ld] = model(in[k * in_ld]) for f < num_outputs.
+// `real` is float for F32 models and double for F64 models.  A model that
+// does not fit the thread-private limits, or of another dtype, writes NaN.
+template <class real, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
+__device__ inline void forward_one(ponni_device_model const& m, real const* in, int64_t in_ld, real* out,
+                                   int64_t out_ld) {
+  constexpr int want = sizeof(real) == 8 ? PONNI_F64 : PONNI_F32;
+  if (m.dtype != want || !fits_in_kernel<MAXW, MAXSAVED>(m)) {
+    for (int f = 0; f < m.num_outputs; f++) out[f * out_ld] = real(__builtin_nan(""));
+    return;
+  }
+  real tmp[2][MAXW];
+  real saved[MAXSAVED];
+  ponni_hip::View2 buf[ponni_hip::BUF_SAVED + ponni_hip::kMaxSlots];
+  buf[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
+  buf[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
+  buf[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp[0]), 1};
+  buf[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp[1]), 1};
+  int off = 0;
+  for (int s = 0; s < ponni_hip::kMaxSlots; s++) {
+    buf[ponni_hip::BUF_SAVED + s] = {reinterpret_cast<char*>(saved + off), 1};
+    off += m.saved_features[s];
+  }
+  ponni_hip::run_ops<real>(static_cast<ponni_hip::Op const*>(m.ops), m.num_ops,
+                           static_cast<ponni_hip::Step const*>(m.steps), static_cast<real const*>(m.params), buf,
+                           0);
+}
+
+}  // namespace ponni

@@ -271,6 +271,84 @@ void test_views_streams_capacity_gpu() {
   (void)m;
 }
 
+// In-kernel inference (ponni_Inference.h:394-408, :592-665): application
+// kernels evaluating samples with the model's `params`.
+template <class Model, class In, class Out>
+__global__ void in_kernel_views(In in, Out out, typename Model::Params p, int n) {
+  int const b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < n) Model::forward_batch_parallel_in_kernel(in, out, p, b);
+}
+
+template <class Model>
+__global__ void in_kernel_sarray(typename Model::Params p, float* result) {
+  ponni::SArray<float, 2> in;
+  ponni::SArray<float, 1> out;
+  in(0) = 1.0f;
+  in(1) = 2.0f;
+  Model::forward_batch_parallel_in_kernel(in, out, p);
+  result[0] = out(0);
+}
+
+void test_in_kernel_gpu() {
+  using namespace ponni;
+  {  // unit/core/test_core_unit.cpp:280-322: the four-block model, batch and in-kernel agree
+    auto m = four_block_model();
+    std::vector<float> xv{1, -2, 0, 0.3f, 2, 0.5f, 0, -1};
+    auto x = device_matrix<float>(2, 4, xv);
+    auto yb = host(m.forward_batch_parallel(x));
+    View<float> yk("yk", 2, 4);
+    auto const params = m.params;
+    using M = decltype(m);
+    hipLaunchKernelGGL((in_kernel_views<M, DeviceView<float>, DeviceView<float>>), dim3(1), dim3(64), 0, 0,
+                       x.device(), yk.device(), params, 4);
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    auto y = host(yk);
+    for (int i = 0; i < 8; i++) CHECK(near(y[i], yb[i], 1e-5));
+    for (int b = 0; b < 4; b++) CHECK(near(y[b], four_block_closed_form(xv[b], xv[4 + b]), 1e-4));
+  }
+  {  // unit/core/test_template_coverage.cpp:359-384: SArray form -> 6
+    auto m = create_inference_model(Matvec<float, 2, 2>(Matrix<float>(2, 2, std::vector<float>{1, 2, 3, 4})),
+                                    Bias<float, 2>(std::vector<float>{0.5f, -1.0f}), Relu<float, 2>(2),
+                                    Matvec<float, 2, 1>(Matrix<float>(2, 1, std::vector<float>{2, -1})));
+    View<float> r("r", 1, 1);
+    using M = decltype(m);
+    hipLaunchKernelGGL((in_kernel_sarray<M>), dim3(1), dim3(1), 0, 0, m.params, r.data());
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    CHECK(near(host(r)[0], 6.0, 1e-6));
+  }
+  {  // saved states and a projection skip (test_template_coverage.cpp:414-500), strided columns
+    auto m = create_inference_model(Save_State<0>(2), Relu<float>(2), Binop_Concatenate<0>(2, 4, true),
+                                    Save_State<1>(4), Relu<float>(4), Binop_Add<1>(4),
+                                    Binop_Concatenate<0>(4, 6, true));
+    View<float> xs("xs", 2, 5);
+    xs.copy_from_host(std::vector<float>{-2, 0, 0, 0, 0, 3, 0, 0, 0, 0});
+    auto x = xs.columns(0, 1);
+    View<float> ys("ys", 6, 3);
+    auto y = ys.columns(0, 1);
+    using M = decltype(m);
+    hipLaunchKernelGGL((in_kernel_views<M, DeviceView<float>, DeviceView<float>>), dim3(1), dim3(64), 0, 0,
+                       x.device(), y.device(), m.params, 1);
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    auto h = host(ys);
+    std::vector<double> want{0, 6, -2, 6, -2, 3};
+    for (int f = 0; f < 6; f++) CHECK(h[f * 3] == want[f]);
+  }
+  {  // a parameter change reaches `params`
+    auto m = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{1, 1}));
+    auto x = device_matrix<float>(2, 1, {1, 2});
+    auto p = m.get_trainable_parameters();
+    for (auto& v : p) v *= 2.0f;
+    m.set_trainable_parameters(p);
+    View<float> yk("yk", 2, 1);
+    using M = decltype(m);
+    hipLaunchKernelGGL((in_kernel_views<M, DeviceView<float>, DeviceView<float>>), dim3(1), dim3(64), 0, 0,
+                       x.device(), yk.device(), m.params, 1);
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    auto y = host(yk);
+    CHECK(near(y[0], 8.0, 1e-6) && near(y[1], 8.0, 1e-6));
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -282,6 +360,7 @@ int main(int argc, char** argv) {
   if (!cpu_only) {
     test_known_answers_gpu();
     test_views_streams_capacity_gpu();
+    test_in_kernel_gpu();
   }
   std::printf("%s: %d checks, %d failures\n", cpu_only ? "cpu" : "cpu+gpu", g_checks, g_failures);
   return g_failures == 0 ? 0 : 1;
