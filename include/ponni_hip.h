@@ -96,8 +96,18 @@ typedef enum ponni_layer_kind {
                                     attr[0] = ponni_reduce_op                           */
   PONNI_LAYER_UNARY = 44,        /* emitter.py:218-258: pointwise; attr[0] = ponni_unary_op,
                                     attr[1] alpha, attr[2] gamma                       */
-  PONNI_LAYER_CONST_BINARY = 45  /* pointwise op(state, c) with a constant c [n_in];
+  PONNI_LAYER_CONST_BINARY = 45, /* pointwise op(state, c) with a constant c [n_in];
                                     attr[0] = ponni_binary_op; flags bit0 = c on the left */
+
+  /* A layer the library does not implement: a user layer of the C++ facade
+   * under the reference's plugin contract (ponni_LayerTraits.h:10-61; its
+   * device functions compute_output / apply_fused / compute_all_outputs run
+   * in the facade's per-sample kernel).  attr[0] = the caller's index for it;
+   * flags: PONNI_FLAG_EXT_* below; slot = ISAVE when it saves or reads a
+   * saved state.  A plan holding one is always GENERIC, is evaluated only
+   * through ponni_plan_device_model with the caller's callback
+   * (ponni_amd/include/ponni/device.h), and ponni_forward rejects it. */
+  PONNI_LAYER_EXTERNAL = 50
 } ponni_layer_kind;
 
 /* Element-wise binary operations of PONNI_LAYER_BINARY / _CONST_BINARY. */
@@ -144,6 +154,9 @@ typedef enum ponni_unary_op {
 #define PONNI_FLAG_DENSE_BIAS 1 /* PONNI_LAYER_DENSE carries a bias     */
 #define PONNI_FLAG_SAVED_LEFT 1 /* PONNI_LAYER_BINARY: saved[slot] op state */
 #define PONNI_FLAG_CONST_LEFT 1 /* PONNI_LAYER_CONST_BINARY: c op state  */
+#define PONNI_FLAG_EXT_SAVE 1     /* PONNI_LAYER_EXTERNAL: output goes to saved[slot] (save = true) */
+#define PONNI_FLAG_EXT_BINOP 2    /* PONNI_LAYER_EXTERNAL: also reads saved[slot] (binop = true)   */
+#define PONNI_FLAG_EXT_IN_PLACE 4 /* PONNI_LAYER_EXTERNAL: overwrite_input = true                 */
 
 /* One layer of the tuple handed to create_inference_model
  * (src/ponni_create_model.h:40-65).  Widths are the runtime extents the

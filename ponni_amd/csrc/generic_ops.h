@@ -33,10 +33,17 @@ __device__ inline S* at(View2 const& v, int f, int64_t b) {
   return reinterpret_cast<S*>(v.base) + (int64_t(f) * v.ld + b);
 }
 
-template <class S>
+// Caller-implemented layers (OP_EXTERNAL) are evaluated by `ext`:
+// ext(index, flags, in, out, saved, n_in, n_out, b) with the state handles of
+// the op; the library's own kernels never see such an op.
+struct NoExternal {
+  __device__ void operator()(int, int, View2 const&, View2 const&, View2 const&, int, int, int64_t) const {}
+};
+
+template <class S, class Ext = NoExternal>
 __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
                                typename Compute<S>::type const* __restrict__ params,
-                               View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b) {
+                               View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext = Ext()) {
   using C = typename Compute<S>::type;
   for (int o = 0; o < num_ops; o++) {
     Op const op = ops[o];
@@ -160,6 +167,12 @@ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step con
           for (int k = 0; k < nsave; k++) proj += w[int64_t(k) * n + i] * load_as<S>(at<S>(sv, k, b));
           store_as<S, C>(at<S>(out, i, b), load_as<S>(at<S>(in, i, b)) + proj);
         }
+        break;
+      }
+      case OP_EXTERNAL: {
+        View2 const sv = buf[BUF_SAVED + op.slot];
+        ext(op.aux, op.boff, in, out, sv, op.n_in, op.n_out, b);
+        if (op.boff & EXT_ALSO_TMP1) ext(op.aux, op.boff, in, buf[BUF_TMP1], sv, op.n_in, op.n_out, b);
         break;
       }
       case OP_LOAD: {  // the state becomes a saved one

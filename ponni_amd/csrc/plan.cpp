@@ -56,11 +56,19 @@ bool is_binop(int kind) {
 bool known_kind(int kind) {
   return kind == PONNI_LAYER_MATVEC || is_pointwise(kind) ||
          (kind >= PONNI_LAYER_SOFTMAX && kind <= PONNI_LAYER_MIN_MAX_NORM) || is_save(kind) ||
-         is_binop(kind) || is_graph_kind(kind);
+         is_binop(kind) || is_graph_kind(kind) || kind == PONNI_LAYER_EXTERNAL;
+}
+
+bool ext_saves(ponni_layer_desc const& d) {
+  return d.kind == PONNI_LAYER_EXTERNAL && (d.flags & PONNI_FLAG_EXT_SAVE);
+}
+bool ext_reads(ponni_layer_desc const& d) {
+  return d.kind == PONNI_LAYER_EXTERNAL && (d.flags & PONNI_FLAG_EXT_BINOP);
 }
 
 char const* label_of(int kind) {
   switch (kind) {
+    case PONNI_LAYER_EXTERNAL: return "External";
     case PONNI_LAYER_MATVEC: return "Matvec";
     case PONNI_LAYER_BIAS: return "Bias";
     case PONNI_LAYER_RELU: return "ReLU";
@@ -117,11 +125,19 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
     if (d.n_in <= 0 || d.n_out <= 0) return fail(PONNI_ERR_INVALID_MODEL, where + "num_inputs and num_outputs must be > 0");
     bool const same_width = !is_dense(d.kind) && d.kind != PONNI_LAYER_BINOP_CONCATENATE &&
                             d.kind != PONNI_LAYER_LOAD_STATE && d.kind != PONNI_LAYER_BINARY &&
-                            d.kind != PONNI_LAYER_REDUCE;
+                            d.kind != PONNI_LAYER_REDUCE && d.kind != PONNI_LAYER_EXTERNAL;
     if (same_width && d.n_in != d.n_out) return fail(PONNI_ERR_INVALID_MODEL, where + "input/output size mismatch");
-    if (is_save(d.kind) || reads_slot(d.kind)) {
+    if (is_save(d.kind) || reads_slot(d.kind) || ext_saves(d) || ext_reads(d)) {
       if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
     }
+    if (ext_saves(d)) {
+      saved_size[d.slot] = d.n_out;
+      saved_seen[d.slot] = true;
+    }
+    if (ext_reads(d) && !saved_seen[d.slot])
+      return fail(PONNI_ERR_INVALID_MODEL, where + "reads saved state " + std::to_string(d.slot) + " before any save wrote it");
+    if (d.kind == PONNI_LAYER_EXTERNAL && (ext_saves(d) && ext_reads(d)))
+      return fail(PONNI_ERR_INVALID_MODEL, where + "a layer cannot both save and read a saved state");
     switch (d.kind) {
       case PONNI_LAYER_ELU:
         if (!(d.attr[0] > 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "ELU alpha must be > 0");
@@ -409,6 +425,11 @@ void lower(ponni_plan_s& p) {
         break;
       }
       case PONNI_LAYER_LOAD_STATE: op.code = OP_LOAD; break;
+      case PONNI_LAYER_EXTERNAL:
+        op.code = OP_EXTERNAL;
+        op.aux = static_cast<int32_t>(d.attr[0]);
+        op.boff = d.flags & (PONNI_FLAG_EXT_SAVE | PONNI_FLAG_EXT_BINOP | PONNI_FLAG_EXT_IN_PLACE);
+        break;
       case PONNI_LAYER_BINARY:
         op.code = OP_BINARY;
         op.aux = static_cast<int>(d.attr[0]) | ((d.flags & PONNI_FLAG_SAVED_LEFT) ? BIN_SAVED_LEFT : 0) |
@@ -439,6 +460,9 @@ void lower(ponni_plan_s& p) {
       if (is_save(d.kind)) {
         op.dst = BUF_SAVED + d.slot;
         op.aux = 1;  // also copy to tmp1
+      } else if (ext_saves(d)) {
+        op.dst = BUF_SAVED + d.slot;
+        op.boff |= EXT_ALSO_TMP1;
       } else {
         op.dst = BUF_TMP1;
       }
@@ -446,9 +470,18 @@ void lower(ponni_plan_s& p) {
       in_tmp1 = true;
     } else if (i < L - 1) {
       // Every built-in barrier declares overwrite_input = true, so the main
-      // state keeps its buffer; a save writes its slot instead.
+      // state keeps its buffer; a save writes its slot instead.  An external
+      // layer without overwrite_input writes the other buffer
+      // (ponni_Inference.h:518-528).
       op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
-      op.dst = is_save(d.kind) ? BUF_SAVED + d.slot : op.src;
+      if (is_save(d.kind) || ext_saves(d)) {
+        op.dst = BUF_SAVED + d.slot;
+      } else if (d.kind == PONNI_LAYER_EXTERNAL && !(d.flags & PONNI_FLAG_EXT_IN_PLACE)) {
+        in_tmp1 = !in_tmp1;
+        op.dst = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
+      } else {
+        op.dst = op.src;
+      }
       tmp_max[in_tmp1 ? 0 : 1] = std::max(tmp_max[in_tmp1 ? 0 : 1], d.n_out);
     } else {
       op.src = in_tmp1 ? BUF_TMP1 : BUF_TMP2;
@@ -760,10 +793,11 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     p->params[i].assign(static_cast<size_t>(param_count(d)), 0.0);
     max_width = std::max({max_width, d.n_in, d.n_out,
                           d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD || d.kind == PONNI_LAYER_BINARY ? d.n_aux : 0});
-    if (is_save(d.kind)) {
+    if (is_save(d.kind) || ext_saves(d)) {
       p->num_slots = std::max(p->num_slots, d.slot + 1);
       p->saved_features[d.slot] = std::max(p->saved_features[d.slot], d.n_out);
     }
+    if (d.kind == PONNI_LAYER_EXTERNAL) p->external = true;
   }
   p->max_width = max_width;
   // LayerNorm defaults are gamma = 1, beta = 0 (ponni_LayerNorm.h:39-45).
@@ -773,6 +807,15 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
 
   bool graph_ops = false;
   for (int i = 0; i < num_layers; i++) graph_ops = graph_ops || is_graph_kind(layers[i].kind);
+  // Caller-implemented layers run only in the caller's per-sample kernel over
+  // the GENERIC op list.
+  if (p->external) {
+    if (path != PONNI_PATH_AUTO && path != PONNI_PATH_GENERIC) {
+      delete p;
+      return fail(PONNI_ERR_UNSUPPORTED, "a chain with external (custom) layers runs on the GENERIC op list only");
+    }
+    path = PONNI_PATH_GENERIC;
+  }
   // NARROW and MFMA interpret layer-template chains only.
   int const narrow = graph_ops ? 0 : narrow_width_class(max_width);
   int const mfma = graph_ops ? 0 : mfma_width_class(dtype, max_width);
@@ -905,6 +948,8 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch) {
 int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
                   hipStream_t stream) {
   if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+  if (plan->external)
+    return fail(PONNI_ERR_UNSUPPORTED, "the plan holds external (custom) layers: run it through ponni_plan_device_model");
   if (batch <= 0) return fail(PONNI_ERR_SHAPE, "Inference requires a nonzero batch size");
   if (batch > INT32_MAX) return fail(PONNI_ERR_SHAPE, "batch exceeds INT_MAX");
   if (x == nullptr || y == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "input or output pointer is null");
@@ -998,6 +1043,7 @@ int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
     t->layers = plan->layers;
     t->dtype = plan->dtype;
     t->num_slots = plan->num_slots;
+    t->external = plan->external;
     t->max_width = plan->max_width;
     for (int s = 0; s < kMaxSlots; s++) t->saved_features[s] = plan->saved_features[s];
     t->path = PONNI_PATH_GENERIC;

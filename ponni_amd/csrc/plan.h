@@ -54,6 +54,7 @@ struct ponni_plan_s {
   int32_t width_class = 0;
   int32_t max_width = 0;
   int32_t num_slots = 0;           // get_num_saved_states()
+  bool external = false;           // holds PONNI_LAYER_EXTERNAL layers
   int32_t num_fused_blocks = 0;
   int32_t tmp_features[2] = {0, 0};
   int32_t saved_features[ponni_hip::kMaxSlots] = {};

@@ -82,8 +82,15 @@ enum OpCode : int32_t {
   // Generated-graph operations (kokkos_nn/emitter.py).
   OP_LOAD = 11,       // state = saved[slot]
   OP_BINARY = 12,     // state = op(state, saved) / op(saved, state); aux = BinaryAux bits
-  OP_REDUCE = 13      // state[0] = reduce(state[0..n_in)); aux = ponni_reduce_op   emitter.py:475-547
+  OP_REDUCE = 13,     // state[0] = reduce(state[0..n_in)); aux = ponni_reduce_op   emitter.py:475-547
+  // A caller-implemented layer (PONNI_LAYER_EXTERNAL): aux = the caller's
+  // index, boff = PONNI_FLAG_EXT_* bits | EXT_ALSO_TMP1.
+  OP_EXTERNAL = 14
 };
+
+// OP_EXTERNAL's boff: a leading saving layer also fills tmp1
+// (ponni_Inference.h:499-514).
+constexpr int32_t EXT_ALSO_TMP1 = 1 << 8;
 
 // OP_BINARY's aux: bits 0-7 ponni_binary_op, then these flags.
 enum BinaryAux : int32_t {

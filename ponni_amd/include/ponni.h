@@ -365,6 +365,59 @@ struct Initializer_He_Normal {
   }
 };
 
+// ---- layer classification (ponni_LayerTraits.h:10-61) ------------------------------------
+
+// Whether a layer may be fused with its neighbours.  A layer without a
+// static constexpr `fusion_kind` is a barrier.  Built-in layers declare it;
+// a user layer (the plugin contract) opts in the same way and then provides
+//   dense:     static real compute_output(input, int feature, int batch, Params const&)
+//   pointwise: static real apply_fused(value, int feature, Params const&)
+//              (or apply(value, Params const&), or apply(value))
+//   barrier:   static void compute_all_outputs(input, output, int batch, Params const&)
+//              (binop layers: compute_all_outputs(input, saved, output, batch, params))
+// as __host__ __device__ functions, a device-copyable nested `Params`, a
+// `params` member, get_num_inputs() / get_num_outputs(), and the flags
+// overwrite_input / save / binop (with `index` = ISAVE) of the reference.
+enum class LayerFusionKind { barrier, dense, pointwise };
+
+template <class Layer, class = void>
+struct LayerTraits {
+  static constexpr LayerFusionKind fusion_kind = LayerFusionKind::barrier;
+};
+template <class Layer>
+struct LayerTraits<Layer, std::void_t<decltype(Layer::fusion_kind)>> {
+  static constexpr LayerFusionKind fusion_kind = Layer::fusion_kind;
+};
+template <class Layer>
+inline constexpr bool is_dense_layer_v = LayerTraits<Layer>::fusion_kind == LayerFusionKind::dense;
+template <class Layer>
+inline constexpr bool is_pointwise_layer_v = LayerTraits<Layer>::fusion_kind == LayerFusionKind::pointwise;
+
+namespace detail {
+template <class L, class R, class P, class = void>
+struct has_apply_fused : std::false_type {};
+template <class L, class R, class P>
+struct has_apply_fused<L, R, P, std::void_t<decltype(L::apply_fused(std::declval<R>(), 0, std::declval<P const&>()))>>
+    : std::true_type {};
+template <class L, class R, class P, class = void>
+struct has_apply_p : std::false_type {};
+template <class L, class R, class P>
+struct has_apply_p<L, R, P, std::void_t<decltype(L::apply(std::declval<R>(), std::declval<P const&>()))>>
+    : std::true_type {};
+}  // namespace detail
+
+// One pointwise layer on one value (the three forms of ponni_LayerTraits.h:49-61).
+template <class Layer, class Real>
+__host__ __device__ inline Real apply_fused_layer(Real value, int feature, typename Layer::Params const& params) {
+  if constexpr (detail::has_apply_fused<Layer, Real, typename Layer::Params>::value) {
+    return Layer::apply_fused(value, feature, params);
+  } else if constexpr (detail::has_apply_p<Layer, Real, typename Layer::Params>::value) {
+    return Layer::apply(value, params);
+  } else {
+    return Layer::apply(value);
+  }
+}
+
 // ---- layers -----------------------------------------------------------------------------
 
 namespace detail {
@@ -434,6 +487,7 @@ std::vector<double> flatten1(V const& v) {
 // num_outputs, trainable, initializer) or (weights [n_in, n_out], trainable).
 template <class real = float, int N_IN = 1, int N_OUT = 1>
 struct Matvec : detail::LayerCore {
+  static constexpr LayerFusionKind fusion_kind = LayerFusionKind::dense;
   static constexpr int INPUT_SIZE = N_IN, OUTPUT_SIZE = N_OUT;
   Matvec() = default;
   template <class INIT = Initializer_Random_Uniform<real>>
@@ -464,6 +518,7 @@ struct Matvec : detail::LayerCore {
 // Bias (ponni_Bias.h): (num_inputs, trainable, initializer) or (weights, trainable).
 template <class real = float, int N = 1>
 struct Bias : detail::LayerCore {
+  static constexpr LayerFusionKind fusion_kind = LayerFusionKind::pointwise;
   static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
   Bias() = default;
   template <class INIT = Initializer_Random_Uniform<real>>
@@ -492,6 +547,10 @@ namespace detail {
 // Parameter-free pointwise / barrier layers share this shape.
 template <int KIND>
 struct Simple : LayerCore {
+  static constexpr LayerFusionKind fusion_kind =
+      (KIND == PONNI_LAYER_SOFTMAX || KIND == PONNI_LAYER_LOG_SOFTMAX || KIND == PONNI_LAYER_MIN_MAX_NORM)
+          ? LayerFusionKind::barrier
+          : LayerFusionKind::pointwise;
   Simple() = default;
   Simple(int n, char const* lbl, int flags = 0, double a0 = 0, double a1 = 0, double a2 = 0) {
     desc = make_desc(KIND, n, n, 0, 0, flags, a0, a1, a2);
@@ -694,21 +753,92 @@ struct Binop_Projection_Add : detail::LayerCore {
 
 // ---- the model ---------------------------------------------------------------------------
 
+namespace detail {
+
+template <class L>
+inline constexpr bool is_builtin_v = std::is_base_of_v<LayerCore, L>;
+
+// Static flags of a layer type with the reference's defaults.
+template <class L, class = void> struct flag_save : std::false_type {};
+template <class L> struct flag_save<L, std::void_t<decltype(L::save)>> : std::bool_constant<L::save> {};
+template <class L, class = void> struct flag_binop : std::false_type {};
+template <class L> struct flag_binop<L, std::void_t<decltype(L::binop)>> : std::bool_constant<L::binop> {};
+template <class L, class = void> struct flag_overwrite : std::false_type {};
+template <class L>
+struct flag_overwrite<L, std::void_t<decltype(L::overwrite_input)>> : std::bool_constant<L::overwrite_input> {};
+template <class L, class = void> struct flag_index : std::integral_constant<int, 0> {};
+template <class L> struct flag_index<L, std::void_t<decltype(L::index)>> : std::integral_constant<int, L::index> {};
+
+// Device parameters of a layer inside a user-layer chain: the layer's own
+// Params for a user layer, nothing for a built-in one (its parameters are in
+// the plan's device copy).
+struct NoParams {};
+template <class L, bool BUILTIN = is_builtin_v<L>>
+struct params_of {
+  using type = NoParams;
+};
+template <class L>
+struct params_of<L, false> {
+  using type = typename L::Params;
+};
+
+// The C-ABI descriptor of tuple element I: built-in layers carry theirs; a
+// user layer is PONNI_LAYER_EXTERNAL with index I.  A user dense layer never
+// runs in place (its outputs read every input feature).
+template <int I, class L>
+ponni_layer_desc layer_desc(L const& layer) {
+  if constexpr (is_builtin_v<L>) {
+    return layer.desc;
+  } else {
+    int flags = 0;
+    if (flag_save<L>::value) flags |= PONNI_FLAG_EXT_SAVE;
+    if (flag_binop<L>::value) flags |= PONNI_FLAG_EXT_BINOP;
+    if (flag_overwrite<L>::value && !is_dense_layer_v<L>) flags |= PONNI_FLAG_EXT_IN_PLACE;
+    return make_desc(PONNI_LAYER_EXTERNAL, layer.get_num_inputs(), layer.get_num_outputs(),
+                     (flag_save<L>::value || flag_binop<L>::value) ? flag_index<L>::value : 0, 0, flags, double(I));
+  }
+}
+
+// A per-sample state for user layers' device functions: element (f, b) of
+// one of the interpreter's state handles.
+template <class real>
+struct StateView {
+  ponni_hip::View2 v;
+  __host__ __device__ real& operator()(int f, int b) const {
+    return reinterpret_cast<real*>(v.base)[static_cast<std::int64_t>(f) * v.ld + b];
+  }
+};
+
+// Batch pass of a chain holding user layers: one sample per thread.
+template <class Model, class real>
+__global__ __launch_bounds__(256) void user_chain_forward(typename Model::Params p, real const* __restrict__ x,
+                                                          std::int64_t ldx, real* __restrict__ y, std::int64_t ldy,
+                                                          std::int64_t batch) {
+  std::int64_t const b = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b < batch) Model::run_sample(p, x + b, ldx, y + b, ldy);
+}
+
+}  // namespace detail
+
 template <class real, class... Layers>
 class Inference {
   static_assert(sizeof...(Layers) > 0, "a model needs at least one layer");
-  static_assert((std::is_base_of_v<detail::LayerCore, Layers> && ...),
-                "Inference layers must be PONNI layer templates");
 
  public:
   using real_type = real;
   using TUPLE = std::tuple<Layers...>;
   static constexpr int num_layers = static_cast<int>(sizeof...(Layers));
+  // A chain holding user layers (the plugin contract) runs one sample per
+  // thread through the plan's GENERIC op list, with the user layers' device
+  // functions called at their place in it.
+  static constexpr bool has_user_layers = !(detail::is_builtin_v<Layers> && ...);
+  static_assert(!has_user_layers || std::is_same_v<real, float> || std::is_same_v<real, double>,
+                "chains with user layers run in F32 or F64");
 
   explicit Inference(TUPLE const& layers, hipStream_t stream = nullptr, int path = PONNI_PATH_AUTO)
       : layers_(layers), stream_(stream) {
     std::vector<ponni_layer_desc> descs;
-    std::apply([&](auto const&... l) { (descs.push_back(l.desc), ...); }, layers_);
+    collect_descs(descs, std::make_index_sequence<num_layers>{});
     ponni_plan p = nullptr;
     check(ponni_plan_create(descs.data(), num_layers, dtype_of<real>(), path, &p), "create_inference_model");
     plan_ = std::shared_ptr<ponni_plan_s>(p, [](ponni_plan q) { ponni_plan_destroy(q); });
@@ -732,7 +862,8 @@ class Inference {
     return inf;
   }
   // Scratch planning queries of ponni_Inference.h:92-122, :204-223.
-  int get_num_fused_dense_blocks() const { return info().num_fused_dense_blocks; }
+  // Dense layers (built-in or user) each start one fused block (ponni_Inference.h:66-85).
+  static constexpr int get_num_fused_dense_blocks() { return (int(is_dense_layer_v<Layers>) + ...); }
   int get_num_saved_states() const { return info().num_saved_states; }
   template <int REQUESTED_BUFFER>
   int get_planned_temporary_size() const {
@@ -784,9 +915,17 @@ class Inference {
   int internal_state_capacity() const { return static_cast<int>(info().internal_state_capacity); }
 
   // ---- parameters -----------------------------------------------------------------------
+  // Built-in layers' parameters (a user layer keeps its own `params`).
   int get_num_trainable_parameters() const {
     int n = 0;
-    std::apply([&](auto const&... l) { ((n += l.get_num_trainable_parameters()), ...); }, layers_);
+    std::apply(
+        [&](auto const&... l) {
+          auto one = [&](auto const& layer) {
+            if constexpr (detail::is_builtin_v<std::decay_t<decltype(layer)>>) n += layer.get_num_trainable_parameters();
+          };
+          (one(l), ...);
+        },
+        layers_);
     return n;
   }
   // Flattened in tuple order (ponni_Inference.h:688-716).
@@ -795,6 +934,7 @@ class Inference {
     std::apply(
         [&](auto const&... l) {
           auto one = [&](auto const& layer) {
+            if constexpr (detail::is_builtin_v<std::decay_t<decltype(layer)>>)
             for (double v : layer.get_trainable_parameters()) {
               if constexpr (std::is_same_v<real, double>) out.push_back(v);
               else out.push_back(static_cast<real>(static_cast<float>(v)));
@@ -811,6 +951,8 @@ class Inference {
     std::apply(
         [&](auto&... l) {
           auto one = [&](auto& layer) {
+            if constexpr (!detail::is_builtin_v<std::decay_t<decltype(layer)>>) return;
+            else {
             std::size_t const n = static_cast<std::size_t>(layer.get_num_trainable_parameters());
             if (n == 0) return;
             if (in.size() < off + n) abort(std::string("ERROR: ") + layer.get_label() + " trainable input too small");
@@ -821,6 +963,7 @@ class Inference {
             }
             layer.set_trainable_parameters(part);
             off += n;
+            }
           };
           (one(l), ...);
         },
@@ -833,25 +976,67 @@ class Inference {
   // kernel (`auto const p = model.params;`) and call
   // Model::forward_batch_parallel_in_kernel(in, out, p, ibatch) per sample.
   // It is refreshed whenever parameters are pushed (sync()).
-  using Params = ponni_device_model;
+  struct UserChainParams {
+    ponni_device_model model;
+    std::tuple<typename detail::params_of<Layers>::type...> layers;
+  };
+  using Params = std::conditional_t<has_user_layers, UserChainParams, ponni_device_model>;
   Params params{};
+
+  // Calls user layer `index` of the chain on one sample (the GENERIC
+  // interpreter's OP_EXTERNAL callback).
+  struct UserLayers {
+    Params const* p;
+    template <int I>
+    __device__ void call(ponni_hip::View2 const& in, ponni_hip::View2 const& out, ponni_hip::View2 const& sv,
+                         int n_out, int b) const {
+      using L = std::tuple_element_t<I, TUPLE>;
+      if constexpr (!detail::is_builtin_v<L>) {
+        auto const& lp = std::get<I>(p->layers);
+        detail::StateView<real> const iv{in}, ov{out}, svv{sv};
+        if constexpr (is_dense_layer_v<L>) {
+          for (int f = 0; f < n_out; f++) ov(f, b) = L::compute_output(iv, f, b, lp);
+        } else if constexpr (is_pointwise_layer_v<L>) {
+          for (int f = 0; f < n_out; f++) ov(f, b) = apply_fused_layer<L, real>(iv(f, b), f, lp);
+        } else if constexpr (detail::flag_binop<L>::value) {
+          L::compute_all_outputs(iv, svv, ov, b, lp);
+        } else {
+          L::compute_all_outputs(iv, ov, b, lp);
+        }
+      }
+    }
+    template <std::size_t... I>
+    __device__ void dispatch(int index, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
+                             ponni_hip::View2 const& sv, int n_out, int b, std::index_sequence<I...>) const {
+      ((index == static_cast<int>(I) ? (call<static_cast<int>(I)>(in, out, sv, n_out, b), 0) : 0), ...);
+    }
+    __device__ void operator()(int index, int, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
+                               ponni_hip::View2 const& sv, int, int n_out, std::int64_t b) const {
+      dispatch(index, in, out, sv, n_out, static_cast<int>(b), std::make_index_sequence<num_layers>{});
+    }
+  };
+
+  // One sample: column pointers with row strides (thread-private states).
+  template <int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
+  __device__ static void run_sample(Params const& p, real const* in, std::int64_t in_ld, real* out,
+                                    std::int64_t out_ld) {
+    static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
+                  "in-kernel inference runs F32 and F64 models");
+    if constexpr (has_user_layers) forward_one<real, MAXW, MAXSAVED>(p.model, in, in_ld, out, out_ld, UserLayers{&p});
+    else forward_one<real, MAXW, MAXSAVED>(p, in, in_ld, out, out_ld);
+  }
 
   // Sample `ibatch` of LayoutRight [features, batch] views (device memory).
   template <class InputView, class OutputView, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
   __device__ static void forward_batch_parallel_in_kernel(InputView const& input, OutputView const& output,
                                                           Params const& p, int ibatch) {
-    static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
-                  "in-kernel inference runs F32 and F64 models");
-    forward_one<real, MAXW, MAXSAVED>(p, input.data() + ibatch, input.stride(0), output.data() + ibatch,
-                                      output.stride(0));
+    run_sample<MAXW, MAXSAVED>(p, input.data() + ibatch, input.stride(0), output.data() + ibatch, output.stride(0));
   }
   // One sample held in per-thread arrays.
   template <int NI, int NO, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
   __device__ static void forward_batch_parallel_in_kernel(SArray<real, NI> const& input, SArray<real, NO>& output,
                                                           Params const& p) {
-    static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
-                  "in-kernel inference runs F32 and F64 models");
-    forward_one<real, MAXW, MAXSAVED>(p, input.data(), 1, output.data(), 1);
+    run_sample<MAXW, MAXSAVED>(p, input.data(), 1, output.data(), 1);
   }
 
   // Push parameters of layers changed since the last push (set_trainable_parameters,
@@ -861,6 +1046,10 @@ class Inference {
     std::apply(
         [&](auto const&... l) {
           auto one = [&](auto const& layer) {
+            if constexpr (!detail::is_builtin_v<std::decay_t<decltype(layer)>>) {
+              i++;
+              return;
+            } else {
             if (pushed_[i] != layer.version && !layer.params.empty()) {
               std::vector<float> f;
               void const* src = layer.params.data();
@@ -873,15 +1062,23 @@ class Inference {
             }
             pushed_[i] = layer.version;
             i++;
+            }
           };
           (one(l), ...);
         },
         layers_);
     // (Only where a device exists: models are also built on GPU-less hosts.)
     int devices = 0;
-    if constexpr (std::is_same_v<real, float> || std::is_same_v<real, double>)
-      if (hipGetDeviceCount(&devices) == hipSuccess && devices > 0)
-        check(ponni_plan_device_model(plan_.get(), &params), "ponni_plan_device_model");
+    if constexpr (std::is_same_v<real, float> || std::is_same_v<real, double>) {
+      if (hipGetDeviceCount(&devices) == hipSuccess && devices > 0) {
+        if constexpr (has_user_layers) {
+          check(ponni_plan_device_model(plan_.get(), &params.model), "ponni_plan_device_model");
+          collect_user_params(std::make_index_sequence<num_layers>{});
+        } else {
+          check(ponni_plan_device_model(plan_.get(), &params), "ponni_plan_device_model");
+        }
+      }
+    }
   }
 
   // ---- weights files (ponni_Inference.h:270-333) ---------------------------------------------
@@ -966,9 +1163,19 @@ class Inference {
     if (static_cast<int>(output.extent(0)) != get_num_outputs() || output.extent(1) != input.extent(1))
       abort("Error: Provided output dimensions do not match the model and input batch");
     sync();
-    check(ponni_forward(plan_.get(), input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
-                        static_cast<std::int64_t>(output.stride(0)), batch, stream_),
-          "forward_batch_parallel");
+    if constexpr (has_user_layers) {
+      if (!fits_in_kernel(params.model)) abort("Error: a chain with user layers is limited to 256-feature states");
+      unsigned const blocks = static_cast<unsigned>((batch + 255) / 256);
+      hipLaunchKernelGGL((detail::user_chain_forward<Inference, real>), dim3(blocks), dim3(256), 0, stream_, params,
+                         input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
+                         static_cast<std::int64_t>(output.stride(0)), batch);
+      hipError_t const e = hipGetLastError();
+      if (e != hipSuccess) abort(std::string("forward_batch_parallel: ") + hipGetErrorString(e));
+    } else {
+      check(ponni_forward(plan_.get(), input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
+                          static_cast<std::int64_t>(output.stride(0)), batch, stream_),
+            "forward_batch_parallel");
+    }
   }
 
  private:
@@ -995,6 +1202,20 @@ class Inference {
   template <class L>
   static constexpr bool has_member_binop(long) {
     return false;
+  }
+
+  template <std::size_t... I>
+  void collect_descs(std::vector<ponni_layer_desc>& descs, std::index_sequence<I...>) const {
+    (descs.push_back(detail::layer_desc<static_cast<int>(I)>(std::get<I>(layers_))), ...);
+  }
+  template <std::size_t... I>
+  void collect_user_params(std::index_sequence<I...>) {
+    auto one = [&](auto idx) {
+      constexpr std::size_t k = decltype(idx)::value;
+      if constexpr (!detail::is_builtin_v<std::tuple_element_t<k, TUPLE>>)
+        std::get<k>(params.layers) = std::get<k>(layers_).params;
+    };
+    (one(std::integral_constant<std::size_t, I>{}), ...);
   }
 
   TUPLE layers_;

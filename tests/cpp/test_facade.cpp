@@ -271,6 +271,157 @@ void test_views_streams_capacity_gpu() {
   (void)m;
 }
 
+// User layers under the plugin contract (unit/core/test_template_coverage.cpp:82-270):
+// a fixed non-diagonal dense layer, an indexed pointwise layer and a
+// feature-swapping barrier without fusion metadata.
+template <class Real = float, int N = 2>
+struct TestDense {
+  static constexpr bool overwrite_input = false, binop = false, save = false;
+  static constexpr ponni::LayerFusionKind fusion_kind = ponni::LayerFusionKind::dense;
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    int num_inputs = N;
+    Real m00 = 2, m01 = 1, m10 = 1, m11 = -1;
+  };
+  Params params;
+  char const* get_label() const { return "TestDense"; }
+  int get_num_inputs() const { return params.num_inputs; }
+  int get_num_outputs() const { return params.num_inputs; }
+  int get_num_trainable_parameters() const { return 0; }
+  void validate() const {}
+  template <class InputView>
+  __host__ __device__ static Real compute_output(InputView const& input, int feature, int batch, Params const& p) {
+    return feature == 0 ? p.m00 * input(0, batch) + p.m01 * input(1, batch)
+                        : p.m10 * input(0, batch) + p.m11 * input(1, batch);
+  }
+};
+
+template <class Real = float, int N = 2>
+struct TestIndexedPointwise {
+  static constexpr bool overwrite_input = true, binop = false, save = false;
+  static constexpr ponni::LayerFusionKind fusion_kind = ponni::LayerFusionKind::pointwise;
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    int num_inputs = N;
+    Real offset = 0.5;
+  };
+  Params params;
+  char const* get_label() const { return "TestIndexedPointwise"; }
+  int get_num_inputs() const { return params.num_inputs; }
+  int get_num_outputs() const { return params.num_inputs; }
+  int get_num_trainable_parameters() const { return 0; }
+  void validate() const {}
+  __host__ __device__ static Real apply_fused(Real value, int feature, Params const& p) {
+    return value + p.offset * static_cast<Real>(feature + 1);
+  }
+};
+
+template <class Real = float, int N = 2>
+struct TestBarrier {
+  static constexpr bool overwrite_input = false, binop = false, save = false;
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    int num_inputs = N;
+    Real scale = 1;
+  };
+  Params params;
+  char const* get_label() const { return "TestBarrier"; }
+  int get_num_inputs() const { return params.num_inputs; }
+  int get_num_outputs() const { return params.num_inputs; }
+  int get_num_trainable_parameters() const { return 0; }
+  void validate() const {}
+  template <class InputView, class OutputView>
+  __host__ __device__ static void compute_all_outputs(InputView const& input, OutputView const& output, int batch,
+                                                      Params const& p) {
+    output(0, batch) = p.scale * input(1, batch);
+    output(1, batch) = p.scale * input(0, batch);
+  }
+};
+
+// A binop user layer: out = in * saved (reads saved state ISAVE).
+template <int ISAVE, class Real = float, int N = 2>
+struct TestMultiplySaved {
+  static constexpr bool overwrite_input = true, binop = true, save = false;
+  static constexpr int index = ISAVE;
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    int num_inputs = N;
+  };
+  Params params;
+  char const* get_label() const { return "TestMultiplySaved"; }
+  int get_num_inputs() const { return params.num_inputs; }
+  int get_num_outputs() const { return params.num_inputs; }
+  int get_num_trainable_parameters() const { return 0; }
+  void validate(int) const {}
+  template <class InputView, class SavedView, class OutputView>
+  __host__ __device__ static void compute_all_outputs(InputView const& input, SavedView const& saved,
+                                                      OutputView const& output, int batch, Params const& p) {
+    for (int f = 0; f < p.num_inputs; f++) output(f, batch) = input(f, batch) * saved(f, batch);
+  }
+};
+
+void test_user_layers_cpu() {
+  using namespace ponni;
+  static_assert(LayerTraits<TestBarrier<float, 2>>::fusion_kind == LayerFusionKind::barrier);
+  static_assert(is_dense_layer_v<TestDense<float, 2>>);
+  static_assert(is_pointwise_layer_v<TestIndexedPointwise<float, 2>>);
+  static_assert(is_dense_layer_v<Matvec<float>> && is_pointwise_layer_v<Relu<float>> &&
+                LayerTraits<Softmax<float>>::fusion_kind == LayerFusionKind::barrier);
+  using Model = decltype(create_inference_model(TestDense<float, 2>(), TestIndexedPointwise<float, 2>(),
+                                                TestBarrier<float, 2>(), TestDense<float, 2>()));
+  static_assert(Model::has_user_layers && Model::get_num_fused_dense_blocks() == 2);
+  auto m = create_inference_model(TestDense<float, 2>(), TestIndexedPointwise<float, 2>(), TestBarrier<float, 2>(),
+                                  TestDense<float, 2>());
+  CHECK(m.get_num_inputs() == 2 && m.get_num_outputs() == 2 && m.get_num_trainable_parameters() == 0);
+}
+
+template <class Model>
+__global__ void in_kernel_sarray2(typename Model::Params p, float* result) {
+  ponni::SArray<float, 2> in;
+  ponni::SArray<float, 2> out;
+  in(0) = 1.0f;
+  in(1) = 2.0f;
+  Model::forward_batch_parallel_in_kernel(in, out, p);
+  result[0] = out(0);
+  result[1] = out(1);
+}
+
+void test_user_layers_gpu() {
+  using namespace ponni;
+  {  // test_template_coverage.cpp:740-790: dense, indexed pointwise, barrier, dense -> (4.5, -4.5)
+    auto m = create_inference_model(TestDense<float, 2>(), TestIndexedPointwise<float, 2>(), TestBarrier<float, 2>(),
+                                    TestDense<float, 2>());
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {1, 2})));
+    CHECK(near(y[0], 4.5, 1e-6) && near(y[1], -4.5, 1e-6));
+    View<float> r("r", 1, 2);
+    using M = decltype(m);
+    hipLaunchKernelGGL((in_kernel_sarray2<M>), dim3(1), dim3(1), 0, 0, m.params, r.data());
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    auto h = host(r);
+    CHECK(near(h[0], 4.5, 1e-6) && near(h[1], -4.5, 1e-6));
+  }
+  {  // user layers among built-in ones, saved states included, over a batch
+    Matrix<float> w(2, 2, std::vector<float>{0.5f, -1.0f, 2.0f, 0.25f});
+    auto m = create_inference_model(Matvec<float>(w), Bias<float>(std::vector<float>{0.1f, -0.2f}),
+                                    TestIndexedPointwise<float, 2>(), Save_State<0>(2), Relu<float>(2),
+                                    TestBarrier<float, 2>(), TestMultiplySaved<0, float, 2>(), Binop_Add<0>(2),
+                                    Tanh<float>(2));
+    int const B = 1000;
+    std::vector<float> xv(2 * B);
+    for (int i = 0; i < 2 * B; i++) xv[i] = std::sin(0.37f * i) * 2.0f;
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, B, xv)));
+    for (int b = 0; b < B; b++) {
+      double const x0 = xv[b], x1 = xv[B + b];
+      double const d0 = 0.5 * x0 + 2.0 * x1 + 0.1 + 0.5;
+      double const d1 = -1.0 * x0 + 0.25 * x1 - 0.2 + 1.0;
+      double const r0 = std::max(0.0, d0), r1 = std::max(0.0, d1);
+      double const s0 = r1, s1 = r0;                    // barrier swaps
+      double const m0 = s0 * d0 + d0, m1 = s1 * d1 + d1;  // * saved, + saved
+      CHECK(near(y[b], std::tanh(m0), 2e-5) && near(y[B + b], std::tanh(m1), 2e-5));
+    }
+  }
+}
+
 // In-kernel inference (ponni_Inference.h:394-408, :592-665): application
 // kernels evaluating samples with the model's `params`.
 template <class Model, class In, class Out>
@@ -357,7 +508,9 @@ int main(int argc, char** argv) {
   test_parameters_and_fingerprint();
   test_weights_files();
   test_sixteen_bit_types();
+  test_user_layers_cpu();
   if (!cpu_only) {
+    test_user_layers_gpu();
     test_known_answers_gpu();
     test_views_streams_capacity_gpu();
     test_in_kernel_gpu();
