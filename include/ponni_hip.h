@@ -278,6 +278,23 @@ int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len);
  * happens when the application is compiled. */
 int ponni_plan_compile(ponni_plan plan);
 
+/* Launch configuration of the kernel generated for a FUSED or generated
+ * NARROW plan (compiling it if needed; no device required): threads per
+ * workgroup, batch columns per workgroup, and whether the grid is persistent
+ * (at most the resident workgroups, each looping over tiles) or one
+ * workgroup per tile.  With ponni_plan_kernel_source and
+ * ponni_plan_device_params it lets a generated model header compile the
+ * kernel ahead of time and launch it itself -- the counterpart of the
+ * per-model kernel the reference's emitter writes into the header
+ * (kokkos_nn/emitter.py:1537-1573). */
+int ponni_plan_kernel_config(ponni_plan plan, int32_t* threads, int32_t* columns_per_block,
+                             int32_t* persistent);
+
+/* Device pointer to the plan's packed parameters in its kernel's layout
+ * (uploading them first if they changed; synchronizes the device then):
+ * the first argument of the generated kernel. */
+int ponni_plan_device_params(ponni_plan plan, const void** params);
+
 /* --- in-kernel (per-sample) inference ------------------------------------- */
 
 /* Device-side description of a plan for application kernels that evaluate

@@ -114,6 +114,14 @@ class PonniError(RuntimeError):
         self.message = message
 
 
+class DeviceModel(ctypes.Structure):
+    """ponni_device_model (include/ponni_hip.h)."""
+    _fields_ = [("ops", ctypes.c_void_p), ("steps", ctypes.c_void_p), ("params", ctypes.c_void_p),
+                ("num_ops", ctypes.c_int32), ("dtype", ctypes.c_int32), ("num_inputs", ctypes.c_int32),
+                ("num_outputs", ctypes.c_int32), ("max_width", ctypes.c_int32),
+                ("tmp_features", ctypes.c_int32 * 2), ("saved_features", ctypes.c_int32 * 8)]
+
+
 def lib() -> ctypes.CDLL:
     """Load the in-tree libponni_hip.so; fail loudly when it is missing."""
     global _lib
@@ -148,6 +156,12 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_kernel_source.argtypes = [vp, ctypes.c_char_p, i64]
     L.ponni_plan_compile.restype = ctypes.c_int
     L.ponni_plan_compile.argtypes = [vp]
+    L.ponni_plan_kernel_config.restype = ctypes.c_int
+    L.ponni_plan_kernel_config.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)]
+    L.ponni_plan_device_params.restype = ctypes.c_int
+    L.ponni_plan_device_params.argtypes = [vp, ctypes.POINTER(vp)]
+    L.ponni_plan_device_model.restype = ctypes.c_int
+    L.ponni_plan_device_model.argtypes = [vp, ctypes.POINTER(DeviceModel)]
     L.ponni_fill_synthetic.restype = ctypes.c_int
     L.ponni_fill_synthetic.argtypes = [vp, i32, i64, u64, u64, i32, ctypes.c_double, ctypes.c_double, vp]
     L.ponni_fnv1a64.restype = u64

@@ -1035,6 +1035,33 @@ int ponni_plan_compile(ponni_plan plan) {
   return st == PONNI_OK ? PONNI_OK : fail(st, error);
 }
 
+int ponni_plan_kernel_config(ponni_plan plan, int32_t* threads, int32_t* columns_per_block, int32_t* persistent) {
+  if (plan == nullptr || threads == nullptr || columns_per_block == nullptr || persistent == nullptr)
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "null argument");
+  if (plan->path != PONNI_PATH_FUSED && !plan->narrow_jit)
+    return fail(PONNI_ERR_UNSUPPORTED, "only FUSED and generated NARROW plans have a generated kernel");
+  std::string key, error;
+  std::vector<char> code;
+  int const st = fused_compile(*plan, key, code, error);
+  if (st != PONNI_OK) return fail(st, error);
+  FusedConfig cfg;
+  (void)fused_source(*plan, cfg);
+  *threads = 64 * cfg.waves;
+  *columns_per_block = cfg.columns_per_block;
+  *persistent = (cfg.lds_bytes > 0 || cfg.lut_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers) ? 1 : 0;
+  return PONNI_OK;
+}
+
+int ponni_plan_device_params(ponni_plan plan, const void** params) {
+  if (plan == nullptr || params == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null argument");
+  if (plan->device_dirty) {
+    int const st = upload(*plan);
+    if (st != PONNI_OK) return st;
+  }
+  *params = plan->d_params;
+  return PONNI_OK;
+}
+
 int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
   if (plan == nullptr || out == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or output");
   if (plan->device_twin == nullptr) {

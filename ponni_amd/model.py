@@ -206,6 +206,13 @@ class Inference:
         A.lib().ponni_plan_kernel_source(self._plan, buf, n)
         return buf.value.decode()
 
+    def kernel_config(self) -> tuple[int, int, bool]:
+        """(threads per workgroup, batch columns per workgroup, persistent grid) of the
+        generated kernel (FUSED or generated NARROW plans)."""
+        t, c, p = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        A.check(A.lib().ponni_plan_kernel_config(self._plan, ctypes.byref(t), ctypes.byref(c), ctypes.byref(p)))
+        return t.value, c.value, bool(p.value)
+
     def compile(self) -> None:
         A.check(A.lib().ponni_plan_compile(self._plan))
 

@@ -1,0 +1,67 @@
+// The generated-model header of the c5 graph (tests/cpp/gen/c5_model.h,
+// written by ponni_amd.emitter): load the weights file Python saved, run
+// infer_batch (the header's ahead-of-time FUSED kernel), infer_batch_half2
+// and infer_one (an application kernel over device()), and write the three
+// outputs for tests/test_cpp.py to compare.
+//   test_generated <weights.ponni> <x.f32 [24, B]> <B> <out_dir>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "gen/c5_model.h"
+
+using Model = ponni::generated::C5Model;
+
+__global__ void infer_one_kernel(Model::Device m, float const* x, std::int64_t ldx, float* y, std::int64_t ldy,
+                                 int batch) {
+  int const b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  ponni::SArray<float, Model::num_inputs> in;
+  ponni::SArray<float, Model::num_outputs> out;
+  for (int f = 0; f < Model::num_inputs; f++) in(f) = x[f * ldx + b];
+  m.infer_one(in, out);
+  for (int f = 0; f < Model::num_outputs; f++) y[f * ldy + b] = out(f);
+}
+
+static std::vector<float> read_f32(char const* path, std::size_t n) {
+  std::vector<float> v(n);
+  FILE* f = std::fopen(path, "rb");
+  if (!f || std::fread(v.data(), sizeof(float), n, f) != n) ponni::abort(std::string("cannot read ") + path);
+  std::fclose(f);
+  return v;
+}
+
+static void write_f32(std::string const& path, std::vector<float> const& v) {
+  FILE* f = std::fopen(path.c_str(), "wb");
+  if (!f || std::fwrite(v.data(), sizeof(float), v.size(), f) != v.size()) ponni::abort("cannot write " + path);
+  std::fclose(f);
+}
+
+int main(int argc, char** argv) {
+  if (argc != 5) {
+    std::fprintf(stderr, "usage: %s weights.ponni x.f32 batch out_dir\n", argv[0]);
+    return 2;
+  }
+  int const B = std::atoi(argv[3]);
+  std::string const dir = argv[4];
+  Model m;
+  std::string err;
+  if (!m.load_weights(argv[1], &err)) {
+    std::fprintf(stderr, "load_weights: %s\n", err.c_str());
+    return 1;
+  }
+  ponni::View<float> x("x", Model::num_inputs, B);
+  x.copy_from_host(read_f32(argv[2], std::size_t(Model::num_inputs) * B));
+  ponni::View<float> y("y", Model::num_outputs, B), yh("yh", Model::num_outputs, B), y1("y1", Model::num_outputs, B);
+  m.infer_batch(x, y);
+  m.infer_batch_half2(x, yh);
+  hipLaunchKernelGGL(infer_one_kernel, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(), x.stride(0),
+                     y1.data(), y1.stride(0), B);
+  if (hipDeviceSynchronize() != hipSuccess) return 1;
+  write_f32(dir + "/y_batch.f32", y.copy_to_host());
+  write_f32(dir + "/y_half.f32", yh.copy_to_host());
+  write_f32(dir + "/y_one.f32", y1.copy_to_host());
+  std::printf("test_generated: wrote %d samples (%s)\n", B, Model::model_fingerprint().c_str());
+  return 0;
+}

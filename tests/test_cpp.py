@@ -24,3 +24,102 @@ def test_facade_host_only():
 @pytest.mark.gpu
 def test_facade_on_gpu(cuda):
     _run([])
+
+
+# ---- generated-model header (ponni_amd/emitter.py) ---------------------------------
+
+GEN_BIN = os.path.join(os.path.dirname(BIN), "test_generated")
+
+
+def _apply_gather(table, literals, storage):
+    import numpy as np
+
+    return np.array([storage[g] if g >= 0 else literals[-g - 1] for g in table], dtype=np.float64)
+
+
+@pytest.mark.parametrize("which", ["c5", "random0", "random1", "random2", "random5"])
+def test_emitted_gather_tables_rebuild_layer_params(which):
+    """The header's per-layer gather tables, applied to the weights storage,
+    give exactly the parameter vectors the Python model pushes to its plans
+    (the tables are found by tracing the builders on index-valued constants)."""
+    import numpy as np
+
+    from ponni_amd import configs as C
+    from ponni_amd import emitter as E
+    from ponni_amd import graph as G
+    from tests.test_graph import random_graph
+
+    gr = C.c5_graph(True) if which == "c5" else random_graph(int(which[6:]), aligned=True)
+    gm = G.GeneratedModel(gr)
+    gm.storage = np.random.default_rng(7).standard_normal(gm.storage.size)
+    tables, literals = E._gather_tables(gm)
+    want = gm.lowered.layer_params(gm._constants("f64"))
+    assert len(tables) == len(want)
+    for t, v in zip(tables, want):
+        v = np.asarray(v, dtype=np.float64).reshape(-1)
+        assert len(t) == v.size
+        np.testing.assert_array_equal(_apply_gather(t, literals, gm.storage), v)
+
+
+def test_emitted_header_text(tmp_path):
+    from ponni_amd import configs as C
+    from ponni_amd import emitter as E
+    from ponni_amd import graph as G
+
+    gm = G.GeneratedModel(C.c5_graph(True))
+    text = E.emit_cpp_header(C.c5_graph(True), str(tmp_path / "m.h"), class_name="M5")
+    assert "class M5 {" in text and "namespace ponni { namespace generated {" in text
+    assert f'return "{gm.model_fingerprint()}"' in text
+    assert "static constexpr int num_inputs = 24;" in text and "static constexpr int num_outputs = 10;" in text
+    for dt in ("f32", "f16"):
+        gm.plan(dt).kernel_config()  # settles the occupancy the source carries
+        src = gm.plan(dt).kernel_source()
+        name = E._kernel_name(src)
+        assert f"M5_kernels::k_{dt}::{name}" in text  # infer_batch / infer_batch_half2 launch it
+        assert E._kernel_text(src) in text  # the library's own kernel text, compiled ahead of time
+    assert "#include" not in text.split("namespace M5_kernels")[1]
+
+
+@pytest.mark.gpu
+def test_generated_header_on_gpu(cuda, tmp_path):
+    """tests/cpp/test_generated.cpp over the emitted c5 header: infer_batch
+    (ahead-of-time FUSED kernel), infer_batch_half2 and infer_one (an
+    application kernel over device()) against the CPU oracle, on a weights
+    file saved by the Python model.  fp32 bar: relative L2 <= 1e-5 and
+    max-abs <= 1e-4; fp16: relative L2 <= 2e-3 against fp16 operands."""
+    import numpy as np
+
+    import oracle
+    from ponni_amd import configs as C
+    from ponni_amd import graph as G
+    from tests.test_gpu_parity import check_f32, check_half
+
+    if not os.path.exists(GEN_BIN):
+        pytest.fail(f"{GEN_BIN} is missing: build with `python -c 'import __graft_entry__ as g; g.build()'`")
+    oracle.build()
+    gm = G.GeneratedModel(C.c5_graph(True))
+    gm.storage = gm.storage * 0.5 + np.random.default_rng(11).uniform(-0.05, 0.05, gm.storage.size)
+    weights = tmp_path / "c5.ponni"
+    gm.save_parameters(str(weights))
+    B = 4099
+    x = np.random.default_rng(12).standard_normal((24, B)).astype(np.float32)
+    x.tofile(tmp_path / "x.f32")
+    r = subprocess.run([GEN_BIN, str(weights), str(tmp_path / "x.f32"), str(B), str(tmp_path)], capture_output=True,
+                       text=True, timeout=300)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+    def out(name):
+        return np.fromfile(tmp_path / name, dtype=np.float32).reshape(10, B).astype(np.float64)
+
+    gm32 = G.GeneratedModel(C.c5_graph(True))
+    gm32.load_weights(str(weights))  # the values the file holds (fp32)
+    layers = gm32.lowered.layers
+    for l, v in zip(layers, gm32.lowered.layer_params(gm32._constants("f64"))):
+        if v.size:
+            l.params = v
+    want = oracle.forward(layers, x.astype(np.float64))
+    check_f32(out("y_batch.f32"), want, scale_tol=False)
+    check_f32(out("y_one.f32"), want, scale_tol=False)
+    xh = x.astype(np.float16).astype(np.float64)
+    check_half(out("y_half.f32"), oracle.forward(layers, xh, oracle.MODE_F16_OPERANDS))
