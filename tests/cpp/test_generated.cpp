@@ -1,8 +1,9 @@
 // The generated-model header of the c5 graph (tests/cpp/gen/c5_model.h,
 // written by ponni_amd.emitter): load the weights file Python saved, run
 // infer_batch (the header's ahead-of-time FUSED kernel), infer_batch_half2
-// and infer_one (an application kernel over device()), and write the three
-// outputs for tests/test_cpp.py to compare.
+// and infer_one (an application kernel over device()); then read the learned
+// parameters, halve them through a device view, run infer_batch and infer_one
+// again and save the parameters.  tests/test_cpp.py compares every output.
 //   test_generated <weights.ponni> <x.f32 [24, B]> <B> <out_dir>
 #include <cstdio>
 #include <cstdlib>
@@ -47,6 +48,14 @@ int main(int argc, char** argv) {
   std::string const dir = argv[4];
   Model m;
   std::string err;
+  if (m.weights_loaded() || m.parameters_are_finite() || m.save_parameters(dir + "/early.ponni", &err)) {
+    std::fprintf(stderr, "a model without weights must report them missing\n");
+    return 1;
+  }
+  if (m.load_weights(dir + "/missing.ponni", &err) || err.empty()) {
+    std::fprintf(stderr, "loading a missing file must fail with a message\n");
+    return 1;
+  }
   if (!m.load_weights(argv[1], &err)) {
     std::fprintf(stderr, "load_weights: %s\n", err.c_str());
     return 1;
@@ -62,6 +71,25 @@ int main(int argc, char** argv) {
   write_f32(dir + "/y_batch.f32", y.copy_to_host());
   write_f32(dir + "/y_half.f32", yh.copy_to_host());
   write_f32(dir + "/y_one.f32", y1.copy_to_host());
+  if (!m.weights_loaded() || !m.parameters_are_finite() || !m.parameters_synchronized()) return 1;
+
+  std::vector<float> p(Model::get_num_parameters());
+  m.get_parameters(p);
+  write_f32(dir + "/params.f32", p);
+  for (float& v : p) v *= 0.5f;
+  ponni::View<float> pv("p", 1, Model::get_num_parameters());
+  pv.copy_from_host(p);
+  m.set_parameters(pv);
+  m.infer_batch(x, y);
+  hipLaunchKernelGGL(infer_one_kernel, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(), x.stride(0),
+                     y1.data(), y1.stride(0), B);
+  if (hipDeviceSynchronize() != hipSuccess) return 1;
+  write_f32(dir + "/y_batch_scaled.f32", y.copy_to_host());
+  write_f32(dir + "/y_one_scaled.f32", y1.copy_to_host());
+  if (!m.save_parameters(dir + "/saved.ponni", &err)) {
+    std::fprintf(stderr, "save_parameters: %s\n", err.c_str());
+    return 1;
+  }
   std::printf("test_generated: wrote %d samples (%s)\n", B, Model::model_fingerprint().c_str());
   return 0;
 }

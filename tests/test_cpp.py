@@ -85,8 +85,10 @@ def test_generated_header_on_gpu(cuda, tmp_path):
     """tests/cpp/test_generated.cpp over the emitted c5 header: infer_batch
     (ahead-of-time FUSED kernel), infer_batch_half2 and infer_one (an
     application kernel over device()) against the CPU oracle, on a weights
-    file saved by the Python model.  fp32 bar: relative L2 <= 1e-5 and
-    max-abs <= 1e-4; fp16: relative L2 <= 2e-3 against fp16 operands."""
+    file saved by the Python model; then the parameter API (get, set from a
+    device view, save) against the Python model.  fp32 bar: relative L2 <=
+    1e-5 and max-abs <= 1e-4; fp16: relative L2 <= 2e-3 against fp16
+    operands."""
     import numpy as np
 
     import oracle
@@ -114,12 +116,26 @@ def test_generated_header_on_gpu(cuda, tmp_path):
 
     gm32 = G.GeneratedModel(C.c5_graph(True))
     gm32.load_weights(str(weights))  # the values the file holds (fp32)
-    layers = gm32.lowered.layers
-    for l, v in zip(layers, gm32.lowered.layer_params(gm32._constants("f64"))):
-        if v.size:
-            l.params = v
-    want = oracle.forward(layers, x.astype(np.float64))
+
+    def oracle_layers(model):
+        layers = model.lowered.layers
+        for l, v in zip(layers, model.lowered.layer_params(model._constants("f64"))):
+            if v.size:
+                l.params = v
+        return layers
+
+    want = oracle.forward(oracle_layers(gm32), x.astype(np.float64))
     check_f32(out("y_batch.f32"), want, scale_tol=False)
     check_f32(out("y_one.f32"), want, scale_tol=False)
     xh = x.astype(np.float16).astype(np.float64)
-    check_half(out("y_half.f32"), oracle.forward(layers, xh, oracle.MODE_F16_OPERANDS))
+    check_half(out("y_half.f32"), oracle.forward(oracle_layers(gm32), xh, oracle.MODE_F16_OPERANDS))
+
+    learned = gm32.get_parameters()
+    np.testing.assert_array_equal(np.fromfile(tmp_path / "params.f32", dtype=np.float32), learned.astype(np.float32))
+    gm32.set_parameters(learned * 0.5)
+    want = oracle.forward(oracle_layers(gm32), x.astype(np.float64))
+    check_f32(out("y_batch_scaled.f32"), want, scale_tol=False)
+    check_f32(out("y_one_scaled.f32"), want, scale_tol=False)
+    saved = G.GeneratedModel(C.c5_graph(False))
+    saved.load_weights(str(tmp_path / "saved.ponni"))
+    np.testing.assert_array_equal(saved.storage, gm32.storage)
