@@ -324,6 +324,23 @@ typedef struct ponni_device_model {
  * Synchronizes the device when it uploads. */
 int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out);
 
+/* Host execution-space models (create_inference_model(host execution space,
+ * HostSpace, layers...), tests/unit/test_core_unit.cpp:380-404): the same
+ * description with host pointers (the GENERIC op list and the parameters in
+ * the compute type), for per-sample evaluation on the host with
+ * ponni::forward_one.  Touches no device.  The pointers stay valid until the
+ * plan's parameters change or the plan is destroyed.  F32 and F64 plans. */
+int ponni_plan_host_model(ponni_plan plan, ponni_device_model* out);
+
+/* forward_batch_parallel of a host execution-space model
+ * (src/ponni_Inference.h:352-389 over a host execution space): x [num_inputs,
+ * batch] and y [num_outputs, batch] in host memory with row strides ld_in and
+ * ld_out, evaluated on the calling host by `threads` threads (0: one per
+ * hardware thread) through the plan's GENERIC op list, synchronously.  F32
+ * and F64 plans without external layers; the shape errors of ponni_forward. */
+int ponni_forward_host(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                       int32_t threads);
+
 /* --- synthetic data (bench and tests) ------------------------------------- */
 
 /* Fill n elements of a device buffer of `dtype` with the counter-based

@@ -162,6 +162,10 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_device_params.argtypes = [vp, ctypes.POINTER(vp)]
     L.ponni_plan_device_model.restype = ctypes.c_int
     L.ponni_plan_device_model.argtypes = [vp, ctypes.POINTER(DeviceModel)]
+    L.ponni_plan_host_model.restype = ctypes.c_int
+    L.ponni_plan_host_model.argtypes = [vp, ctypes.POINTER(DeviceModel)]
+    L.ponni_forward_host.restype = ctypes.c_int
+    L.ponni_forward_host.argtypes = [vp, vp, i64, vp, i64, i64, ctypes.c_int32]
     L.ponni_fill_synthetic.restype = ctypes.c_int
     L.ponni_fill_synthetic.argtypes = [vp, i32, i64, u64, u64, i32, ctypes.c_double, ctypes.c_double, vp]
     L.ponni_fnv1a64.restype = u64

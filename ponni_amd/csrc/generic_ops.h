@@ -2,7 +2,8 @@
 // writing states through View2 handles: element (f, b) of a handle is
 // base[f * ld + b].  The GENERIC kernel runs it per lane over the plan's HBM
 // scratch (b = the lane's sample); the in-kernel per-sample API
-// (ponni/device.h) runs it over thread-private arrays (ld = 1, b = 0).
+// (ponni/device.h) runs it over thread-private arrays (ld = 1, b = 0), in
+// device code and, for host execution-space models, on the host.
 // Each case follows the reference layer it cites.
 #pragma once
 
@@ -17,11 +18,11 @@ namespace ponni_hip {
 template <class S> struct Compute { using type = float; };
 template <> struct Compute<double> { using type = double; };
 
-template <class S> __device__ inline typename Compute<S>::type load_as(S const* p) {
+template <class S> __host__ __device__ inline typename Compute<S>::type load_as(S const* p) {
   return static_cast<typename Compute<S>::type>(*p);
 }
 
-template <class S, class C> __device__ inline void store_as(S* p, C v) { *p = static_cast<S>(v); }
+template <class S, class C> __host__ __device__ inline void store_as(S* p, C v) { *p = static_cast<S>(v); }
 
 struct View2 {
   char* base;
@@ -29,7 +30,7 @@ struct View2 {
 };
 
 template <class S>
-__device__ inline S* at(View2 const& v, int f, int64_t b) {
+__host__ __device__ inline S* at(View2 const& v, int f, int64_t b) {
   return reinterpret_cast<S*>(v.base) + (int64_t(f) * v.ld + b);
 }
 
@@ -37,11 +38,11 @@ __device__ inline S* at(View2 const& v, int f, int64_t b) {
 // ext(index, flags, in, out, saved, n_in, n_out, b) with the state handles of
 // the op; the library's own kernels never see such an op.
 struct NoExternal {
-  __device__ void operator()(int, int, View2 const&, View2 const&, View2 const&, int, int, int64_t) const {}
+  __host__ __device__ void operator()(int, int, View2 const&, View2 const&, View2 const&, int, int, int64_t) const {}
 };
 
 template <class S, class Ext = NoExternal>
-__device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
+__host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
                                typename Compute<S>::type const* __restrict__ params,
                                View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext = Ext()) {
   using C = typename Compute<S>::type;
@@ -205,7 +206,7 @@ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step con
           if (op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
             C sum = C(0);
             for (int f = 0; f < n; f++) sum += d_exp(load_as<S>(at<S>(in, f, b)) - r);
-            r = isinf(r) ? r : r + d_log(sum);
+            r = __builtin_isinf(r) ? r : r + d_log(sum);
           }
         } else {
           r = op.aux == PONNI_REDUCE_PROD ? C(1) : C(0);

@@ -12,10 +12,10 @@
 
 namespace ponni_hip {
 
-template <> __device__ inline float load_as<__half>(__half const* p) { return __half2float(*p); }
-template <> __device__ inline float load_as<__hip_bfloat16>(__hip_bfloat16 const* p) { return __bfloat162float(*p); }
-template <> __device__ inline void store_as<__half, float>(__half* p, float v) { *p = __float2half_rn(v); }
-template <> __device__ inline void store_as<__hip_bfloat16, float>(__hip_bfloat16* p, float v) {
+template <> __host__ __device__ inline float load_as<__half>(__half const* p) { return __half2float(*p); }
+template <> __host__ __device__ inline float load_as<__hip_bfloat16>(__hip_bfloat16 const* p) { return __bfloat162float(*p); }
+template <> __host__ __device__ inline void store_as<__half, float>(__half* p, float v) { *p = __float2half_rn(v); }
+template <> __host__ __device__ inline void store_as<__hip_bfloat16, float>(__hip_bfloat16* p, float v) {
   *p = __float2bfloat16(v);
 }
 

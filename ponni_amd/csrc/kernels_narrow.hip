@@ -38,7 +38,7 @@ __device__ inline void apply_step_rows(Step const& sp, float const* __restrict__
     }
     return;
   }
-  map_activation<float>(sp.act, sp.a, sp.b, [&](auto&& f) {
+  map_activation<float>(sp.act, float(sp.a), float(sp.b), [&](auto&& f) {
 #pragma unroll
     for (int j = 0; j < W; j++)
 #pragma unroll
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void narrow_forward(LaunchArgs a) {
               var += d * d;
             }
           var /= float(n);
-          float const inv_std = 1.0f / sqrtf(var + op.f0);
+          float const inv_std = 1.0f / sqrtf(var + float(op.f0));
 #pragma unroll
           for (int f = 0; f < W; f++) st[f][p] = prm[op.woff + f] * ((st[f][p] - mean) * inv_std) + prm[op.boff + f];
         }
@@ -160,9 +160,9 @@ __global__ __launch_bounds__(256) void narrow_forward(LaunchArgs a) {
               if (st[f][p] < lo) lo = st[f][p];
               if (st[f][p] > hi) hi = st[f][p];
             }
-          float const scale = (op.f1 - op.f0) / ((hi - lo) + op.f2);
+          float const scale = (float(op.f1) - float(op.f0)) / ((hi - lo) + float(op.f2));
 #pragma unroll
-          for (int f = 0; f < W; f++) st[f][p] = op.f0 + (st[f][p] - lo) * scale;
+          for (int f = 0; f < W; f++) st[f][p] = float(op.f0) + (st[f][p] - lo) * scale;
         }
         break;
       }

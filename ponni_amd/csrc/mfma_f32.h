@@ -86,7 +86,7 @@ __device__ inline void apply_step_tiles(Step const& sp, float const* __restrict_
       }
     return;
   }
-  map_activation<float>(sp.act, sp.a, sp.b, [&](auto&& f) {
+  map_activation<float>(sp.act, float(sp.a), float(sp.b), [&](auto&& f) {
 #pragma unroll
     for (int mo = 0; mo < MT; mo++)
       if (mo < mt) {
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void mfma_forward_f32(LaunchArgs a) {
                 q += d * d;
               }
           float const var = xor_sum(q) / float(nf);
-          float const inv_std = 1.0f / sqrtf(var + op.f0);
+          float const inv_std = 1.0f / sqrtf(var + float(op.f0));
 #pragma unroll
           for (int m = 0; m < MT; m++) {
             if (m < mt_out) {
@@ -255,11 +255,11 @@ __global__ __launch_bounds__(256) void mfma_forward_f32(LaunchArgs a) {
               }
           lo = xor_min(lo);
           hi = xor_max(hi);
-          float const scale = (op.f1 - op.f0) / ((hi - lo) + op.f2);
+          float const scale = (float(op.f1) - float(op.f0)) / ((hi - lo) + float(op.f2));
 #pragma unroll
           for (int m = 0; m < MT; m++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) st[m][n][v] = op.f0 + (st[m][n][v] - lo) * scale;
+            for (int v = 0; v < 4; v++) st[m][n][v] = float(op.f0) + (st[m][n][v] - lo) * scale;
         }
         break;
       }

@@ -227,21 +227,21 @@ Step make_step(ponni_layer_desc const& d) {
   switch (d.kind) {
     case PONNI_LAYER_BIAS: s.act = ACT_BIAS; break;
     case PONNI_LAYER_RELU: s.act = ACT_RELU; break;
-    case PONNI_LAYER_LEAKY_RELU: s.act = ACT_LEAKY_RELU; s.a = float(d.attr[0]); break;
-    case PONNI_LAYER_ELU: s.act = ACT_ELU; s.a = float(d.attr[0]); break;
+    case PONNI_LAYER_LEAKY_RELU: s.act = ACT_LEAKY_RELU; s.a = d.attr[0]; break;
+    case PONNI_LAYER_ELU: s.act = ACT_ELU; s.a = d.attr[0]; break;
     case PONNI_LAYER_SELU: s.act = ACT_SELU; break;
     case PONNI_LAYER_GELU: s.act = (d.flags & PONNI_FLAG_GELU_APPROXIMATE) ? ACT_GELU_TANH : ACT_GELU_ERF; break;
     case PONNI_LAYER_SILU: s.act = ACT_SILU; break;
     case PONNI_LAYER_SIGMOID: s.act = ACT_SIGMOID; break;
     case PONNI_LAYER_TANH: s.act = ACT_TANH; break;
-    case PONNI_LAYER_SOFTPLUS: s.act = ACT_SOFTPLUS; s.a = float(d.attr[0]); break;
-    case PONNI_LAYER_HARD_SIGMOID: s.act = ACT_HARD_SIGMOID; s.a = float(d.attr[0]); s.b = float(d.attr[1]); break;
+    case PONNI_LAYER_SOFTPLUS: s.act = ACT_SOFTPLUS; s.a = d.attr[0]; break;
+    case PONNI_LAYER_HARD_SIGMOID: s.act = ACT_HARD_SIGMOID; s.a = d.attr[0]; s.b = d.attr[1]; break;
     case PONNI_LAYER_HARD_SWISH: s.act = ACT_HARD_SWISH; break;
     case PONNI_LAYER_MISH: s.act = ACT_MISH; break;
     case PONNI_LAYER_UNARY:
       s.act = ACT_ABS + static_cast<int>(d.attr[0]);  // ponni_unary_op order
-      s.a = float(d.attr[1]);
-      s.b = float(d.attr[2]);
+      s.a = d.attr[1];
+      s.b = d.attr[2];
       break;
     case PONNI_LAYER_CONST_BINARY: {
       bool const left = d.flags & PONNI_FLAG_CONST_LEFT;
@@ -402,15 +402,15 @@ void lower(ponni_plan_s& p) {
         op.code = OP_LAYER_NORM;
         vec_stride_ln = static_cast<int>(packed_size(p, d) / 2);
         op.boff = op.woff + vec_stride_ln;
-        op.f0 = static_cast<float>(d.attr[0]);
+        op.f0 = d.attr[0];
         break;
       case PONNI_LAYER_SOFTMAX: op.code = OP_SOFTMAX; break;
       case PONNI_LAYER_LOG_SOFTMAX: op.code = OP_LOG_SOFTMAX; break;
       case PONNI_LAYER_MIN_MAX_NORM:
         op.code = OP_MIN_MAX;
-        op.f0 = static_cast<float>(d.attr[0]);
-        op.f1 = static_cast<float>(d.attr[1]);
-        op.f2 = static_cast<float>(d.attr[2]);
+        op.f0 = d.attr[0];
+        op.f1 = d.attr[1];
+        op.f2 = d.attr[2];
         break;
       case PONNI_LAYER_SAVE_STATE: op.code = OP_SAVE; break;
       case PONNI_LAYER_BINOP_ADD: op.code = OP_ADD; break;
@@ -1062,22 +1062,49 @@ int ponni_plan_device_params(ponni_plan plan, const void** params) {
   return PONNI_OK;
 }
 
-int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
-  if (plan == nullptr || out == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or output");
-  if (plan->device_twin == nullptr) {
+}  // extern "C"
+
+namespace ponni_hip {
+
+ponni_plan_s* generic_twin(ponni_plan_s& plan) {
+  if (plan.device_twin == nullptr) {
     auto* t = new (std::nothrow) ponni_plan_s();
-    if (t == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
-    t->layers = plan->layers;
-    t->dtype = plan->dtype;
-    t->num_slots = plan->num_slots;
-    t->external = plan->external;
-    t->max_width = plan->max_width;
-    for (int s = 0; s < kMaxSlots; s++) t->saved_features[s] = plan->saved_features[s];
+    if (t == nullptr) return nullptr;
+    t->layers = plan.layers;
+    t->dtype = plan.dtype;
+    t->num_slots = plan.num_slots;
+    t->external = plan.external;
+    t->max_width = plan.max_width;
+    for (int s = 0; s < kMaxSlots; s++) t->saved_features[s] = plan.saved_features[s];
     t->path = PONNI_PATH_GENERIC;
     t->width_class = 0;
     lower(*t);
-    plan->device_twin = t;
+    plan.device_twin = t;
   }
+  return plan.device_twin;
+}
+
+int host_twin(ponni_plan_s& plan, ponni_plan_s*& twin) {
+  twin = generic_twin(plan);
+  if (twin == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+  if (plan.host_version != plan.params_version) {
+    std::vector<double> packed;
+    twin->params = plan.params;
+    pack_params(*twin, packed);
+    if (twin->dtype == PONNI_F64) twin->host_params_f64 = std::move(packed);
+    else twin->host_params_f32.assign(packed.begin(), packed.end());
+    plan.host_version = plan.params_version;
+  }
+  return PONNI_OK;
+}
+
+}  // namespace ponni_hip
+
+extern "C" {
+
+int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
+  if (plan == nullptr || out == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or output");
+  if (generic_twin(*plan) == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
   ponni_plan_s& t = *plan->device_twin;
   if (plan->twin_version != plan->params_version || t.device_dirty) {
     t.params = plan->params;

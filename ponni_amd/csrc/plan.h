@@ -10,6 +10,8 @@
 #include "../../include/ponni_hip.h"
 #include "program.h"
 
+struct ponni_plan_s;
+
 namespace ponni_hip {
 
 // Device launch entry points, one per kernel family (kernels_*.hip).
@@ -38,6 +40,12 @@ hipError_t launch_mfma(int dtype, int width_class, int num_slots, LaunchArgs con
                        hipStream_t stream);
 hipError_t launch_fill(void* x, int dtype, int64_t n, uint64_t seed, uint64_t tag, int dist,
                        double a, double b, hipStream_t stream);
+
+// The plan's GENERIC twin (created on first use; owned by the plan), and the
+// same with its host parameter copy brought up to date.
+ponni_plan_s* generic_twin(ponni_plan_s& plan);
+int set_error(int status, std::string const& message);  // ponni_last_error(); returns status
+int host_twin(ponni_plan_s& plan, ponni_plan_s*& twin);
 
 // Width classes each register path is instantiated for.
 int narrow_width_class(int max_width);      // 0 if too wide
@@ -86,6 +94,11 @@ struct ponni_plan_s {
   ponni_plan_s* device_twin = nullptr;
   uint64_t params_version = 1;
   uint64_t twin_version = 0;
+  // Host execution (ponni_forward_host, ponni_plan_host_model): the twin's
+  // packed parameters in the compute type, and the version they were made at.
+  std::vector<double> host_params_f64;
+  std::vector<float> host_params_f32;
+  uint64_t host_version = 0;
   // NARROW plans run a generated kernel (narrow_jit.h) unless JIT is off.
   bool narrow_jit = false;
   // FUSED path (and generated NARROW): the plan's generated kernel (compiled on first forward).

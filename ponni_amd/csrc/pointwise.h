@@ -12,77 +12,77 @@
 
 namespace ponni_hip {
 
-__device__ inline float d_exp(float x) { return expf(x); }
-__device__ inline double d_exp(double x) { return exp(x); }
-__device__ inline float d_log(float x) { return logf(x); }
-__device__ inline double d_log(double x) { return log(x); }
-__device__ inline float d_tanh(float x) { return tanhf(x); }
-__device__ inline double d_tanh(double x) { return tanh(x); }
-__device__ inline float d_erf(float x) { return erff(x); }
-__device__ inline double d_erf(double x) { return erf(x); }
-__device__ inline float d_sqrt(float x) { return sqrtf(x); }
-__device__ inline double d_sqrt(double x) { return sqrt(x); }
-__device__ inline float d_pow(float x, float y) { return powf(x, y); }
-__device__ inline double d_pow(double x, double y) { return pow(x, y); }
-__device__ inline float d_abs(float x) { return fabsf(x); }
-__device__ inline double d_abs(double x) { return fabs(x); }
+__host__ __device__ inline float d_exp(float x) { return expf(x); }
+__host__ __device__ inline double d_exp(double x) { return exp(x); }
+__host__ __device__ inline float d_log(float x) { return logf(x); }
+__host__ __device__ inline double d_log(double x) { return log(x); }
+__host__ __device__ inline float d_tanh(float x) { return tanhf(x); }
+__host__ __device__ inline double d_tanh(double x) { return tanh(x); }
+__host__ __device__ inline float d_erf(float x) { return erff(x); }
+__host__ __device__ inline double d_erf(double x) { return erf(x); }
+__host__ __device__ inline float d_sqrt(float x) { return sqrtf(x); }
+__host__ __device__ inline double d_sqrt(double x) { return sqrt(x); }
+__host__ __device__ inline float d_pow(float x, float y) { return powf(x, y); }
+__host__ __device__ inline double d_pow(double x, double y) { return pow(x, y); }
+__host__ __device__ inline float d_abs(float x) { return fabsf(x); }
+__host__ __device__ inline double d_abs(double x) { return fabs(x); }
 
 // ponni_Relu.h:49-51
-template <class T> __device__ inline T act_relu(T x) { return x > T(0) ? x : T(0); }
+template <class T> __host__ __device__ inline T act_relu(T x) { return x > T(0) ? x : T(0); }
 // ponni_LeakyRelu.h:53-55
-template <class T> __device__ inline T act_leaky_relu(T x, T slope) { return x > T(0) ? x : slope * x; }
+template <class T> __host__ __device__ inline T act_leaky_relu(T x, T slope) { return x > T(0) ? x : slope * x; }
 // ponni_Elu.h:48-50
-template <class T> __device__ inline T act_elu(T x, T alpha) { return x > T(0) ? x : alpha * (d_exp(x) - T(1)); }
+template <class T> __host__ __device__ inline T act_elu(T x, T alpha) { return x > T(0) ? x : alpha * (d_exp(x) - T(1)); }
 // ponni_Selu.h:45-49
-template <class T> __device__ inline T act_selu(T x) {
+template <class T> __host__ __device__ inline T act_selu(T x) {
   T const alpha = T(1.6732632423543772848);
   T const scale = T(1.0507009873554804934);
   return x > T(0) ? scale * x : scale * alpha * (d_exp(x) - T(1));
 }
 // ponni_Gelu.h:55-56
-template <class T> __device__ inline T act_gelu_erf(T x) {
+template <class T> __host__ __device__ inline T act_gelu_erf(T x) {
   return T(0.5) * x * (T(1) + d_erf(x / T(1.4142135623730950488)));
 }
 // ponni_Gelu.h:48-53
-template <class T> __device__ inline T act_gelu_tanh(T x) {
+template <class T> __host__ __device__ inline T act_gelu_tanh(T x) {
   T const x3 = x * x * x;
   return T(0.5) * x * (T(1) + d_tanh(T(0.79788456080286535588) * (x + T(0.044715) * x3)));
 }
 // ponni_Silu.h:45-49
-template <class T> __device__ inline T act_silu(T x) {
+template <class T> __host__ __device__ inline T act_silu(T x) {
   if (x >= T(0)) return x / (T(1) + d_exp(-x));
   T const e = d_exp(x);
   return x * e / (T(1) + e);
 }
 // ponni_Sigmoid.h:45-49
-template <class T> __device__ inline T act_sigmoid(T x) {
+template <class T> __host__ __device__ inline T act_sigmoid(T x) {
   if (x >= T(0)) return T(1) / (T(1) + d_exp(-x));
   T const e = d_exp(x);
   return e / (T(1) + e);
 }
 // ponni_Tanh.h:44
-template <class T> __device__ inline T act_tanh(T x) { return d_tanh(x); }
+template <class T> __host__ __device__ inline T act_tanh(T x) { return d_tanh(x); }
 // ponni_Softplus.h:44-50
-template <class T> __device__ inline T act_softplus(T x, T beta) {
+template <class T> __host__ __device__ inline T act_softplus(T x, T beta) {
   T const s = beta * x;
   if (s > T(0)) return (s + d_log(T(1) + d_exp(-s))) / beta;
   return d_log(T(1) + d_exp(s)) / beta;
 }
 // ponni_HardSigmoid.h:52-56
-template <class T> __device__ inline T act_hard_sigmoid(T x, T alpha, T beta) {
+template <class T> __host__ __device__ inline T act_hard_sigmoid(T x, T alpha, T beta) {
   T v = alpha * x + beta;
   v = v < T(0) ? T(0) : v;
   return v > T(1) ? T(1) : v;
 }
 // ponni_HardSwish.h:42-47
-template <class T> __device__ inline T act_hard_swish(T x) {
+template <class T> __host__ __device__ inline T act_hard_swish(T x) {
   T r = x + T(3);
   r = r < T(0) ? T(0) : r;
   r = r > T(6) ? T(6) : r;
   return x * r / T(6);
 }
 // ponni_Mish.h:44-52
-template <class T> __device__ inline T act_mish(T x) {
+template <class T> __host__ __device__ inline T act_mish(T x) {
   T sp;
   if (x > T(0)) sp = x + d_log(T(1) + d_exp(-x));
   else sp = d_log(T(1) + d_exp(x));
@@ -90,17 +90,17 @@ template <class T> __device__ inline T act_mish(T x) {
 }
 
 // Unary operations of generated graphs, kokkos_nn/emitter.py:218-258.
-template <class T> __device__ inline T act_softsign(T x) { return x / (T(1) + d_abs(x)); }
-template <class T> __device__ inline T act_celu(T x, T alpha) {
+template <class T> __host__ __device__ inline T act_softsign(T x) { return x / (T(1) + d_abs(x)); }
+template <class T> __host__ __device__ inline T act_celu(T x, T alpha) {
   return x > T(0) ? x : alpha * (d_exp(x / alpha) - T(1));
 }
-template <class T> __device__ inline T act_thresholded_relu(T x, T alpha) { return x > alpha ? x : T(0); }
-template <class T> __device__ inline T act_selu_ag(T x, T alpha, T gamma) {
+template <class T> __host__ __device__ inline T act_thresholded_relu(T x, T alpha) { return x > alpha ? x : T(0); }
+template <class T> __host__ __device__ inline T act_selu_ag(T x, T alpha, T gamma) {
   return gamma * (x > T(0) ? x : alpha * (d_exp(x) - T(1)));
 }
 
 // Element-wise op of the state v with a constant c, emitter.py:261-275.
-template <class T> __device__ inline T act_const(int act, T v, T c) {
+template <class T> __host__ __device__ inline T act_const(int act, T v, T c) {
   switch (act) {
     case ACT_BIAS: return v + c;
     case ACT_SUB_C: return v - c;
@@ -119,7 +119,7 @@ template <class T> __device__ inline T act_const(int act, T v, T c) {
 }
 
 // Tensor-tensor binary operation of generated graphs, emitter.py:261-275.
-template <class T> __device__ inline T apply_binary(int op, T l, T r) {
+template <class T> __host__ __device__ inline T apply_binary(int op, T l, T r) {
   switch (op) {
     case 0: return l + r;
     case 1: return l - r;
@@ -136,7 +136,7 @@ template <class T> __device__ inline T apply_binary(int op, T l, T r) {
 // template chains only).  The switch sits outside the element loop so each case is
 // one straight-line loop.  `each(f)` must call f(float&) on every element.
 template <class T, class Each>
-__device__ inline void map_activation(int act, T a, T b, Each&& each) {
+__host__ __device__ inline void map_activation(int act, T a, T b, Each&& each) {
   switch (act) {
     case ACT_RELU: each([](T& v) { v = act_relu(v); }); break;
     case ACT_LEAKY_RELU: each([a](T& v) { v = act_leaky_relu(v, a); }); break;
@@ -158,7 +158,7 @@ __device__ inline void map_activation(int act, T a, T b, Each&& each) {
 // Scalar form for the per-sample generic kernel; `bias` is the step's
 // parameter element (bias or constant operand) for the feature.
 template <class T>
-__device__ inline T apply_step(int act, T x, T bias, T a, T b) {
+__host__ __device__ inline T apply_step(int act, T x, T bias, T a, T b) {
   switch (act) {
     case ACT_BIAS: return x + bias;  // ponni_Bias.h:66-68
     case ACT_ABS: return d_abs(x);

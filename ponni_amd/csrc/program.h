@@ -64,8 +64,8 @@ constexpr bool act_has_param(int act) { return act == ACT_BIAS || (act >= ACT_SU
 struct Step {
   int32_t act;   // Act
   int32_t off;   // parameter offset of the bias vector (ACT_BIAS only)
-  float a;       // scalar attribute (slope, alpha, beta)
-  float b;       // second scalar attribute
+  double a;      // scalar attribute (slope, alpha, beta), exact for F64 plans
+  double b;      // second scalar attribute
 };
 
 enum OpCode : int32_t {
@@ -126,7 +126,7 @@ struct Op {
   int32_t epi_count;  // number of Steps
   int32_t src;        // generic path: input buffer
   int32_t dst;        // generic path: output buffer
-  float f0, f1, f2;   // scalar attributes (epsilon, out_min, out_max)
+  double f0, f1, f2;  // scalar attributes (epsilon, out_min, out_max), exact for F64 plans
 };
 
 constexpr int kMaxSlots = 8;  // saved-state slots a plan may use

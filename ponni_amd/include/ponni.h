@@ -17,7 +17,9 @@
 //
 // What changes underneath: the per-sample Kokkos RangePolicy executor is
 // replaced by one call of ponni_forward(), which runs a gfx950 kernel chosen
-// (and, for wide models, generated) for the whole layer chain.  Layers hold
+// (and, for wide models, generated) for the whole layer chain.  Models bound
+// to the host execution space (create_inference_model(Host(), HostSpace(),
+// ...)) run on host threads through ponni_forward_host instead, on host Views.  Layers hold
 // their parameters on the host; the plan owns the packed device copy and is
 // refreshed whenever parameters change.  A View here is any type with
 // data(), extent(0), extent(1), stride(0) and a LayoutRight array_layout:
@@ -153,14 +155,61 @@ struct DeviceView {
   __host__ __device__ T& operator()(std::int64_t r, std::int64_t c) const { return data_[r * ld_ + c]; }
 };
 
-// A rank-2 LayoutRight [rows, cols] array in device memory; element (r, c)
-// at data()[r * stride(0) + c].  Copies share the allocation (as Kokkos::View).
-template <class T>
+// ---- execution and memory spaces ---------------------------------------------------------
+// The reference selects where a model runs with a Kokkos execution space and
+// memory space (src/ponni_create_model.h:21-90).  Here:
+//   HIP  (memory HIPSpace)   the GPU; holds the stream the model launches on
+//                            (the default execution space);
+//   Host (memory HostSpace)  the calling host, `threads` host threads (0: one
+//                            per hardware thread) through the library's host
+//                            executor (ponni_forward_host); the default host
+//                            execution space.
+struct HostSpace {};
+struct HIPSpace {};
+struct HIP {
+  using memory_space = HIPSpace;
+  hipStream_t stream = nullptr;
+  HIP() = default;
+  explicit HIP(hipStream_t s) : stream(s) {}
+};
+struct Host {
+  using memory_space = HostSpace;
+  int threads = 0;
+  Host() = default;
+  explicit Host(int n) : threads(n) {}
+};
+using DefaultExecutionSpace = HIP;
+using DefaultHostExecutionSpace = Host;
+
+template <class E> struct is_execution_space : std::false_type {};
+template <> struct is_execution_space<HIP> : std::true_type {};
+template <> struct is_execution_space<Host> : std::true_type {};
+template <class E> inline constexpr bool is_execution_space_v = is_execution_space<std::decay_t<E>>::value;
+template <class M> struct is_memory_space : std::false_type {};
+template <> struct is_memory_space<HIPSpace> : std::true_type {};
+template <> struct is_memory_space<HostSpace> : std::true_type {};
+template <class M> inline constexpr bool is_memory_space_v = is_memory_space<std::decay_t<M>>::value;
+
+// The memory space a view type declares (HIPSpace when it declares none: a
+// device pointer is what forward_batch_parallel has always taken).
+template <class V, class = void> struct view_memory_space { using type = HIPSpace; };
+template <class V> struct view_memory_space<V, std::void_t<typename V::memory_space>> {
+  using type = std::conditional_t<std::is_same_v<typename V::memory_space, HostSpace>, HostSpace, HIPSpace>;
+};
+
+// A rank-2 LayoutRight [rows, cols] array in device memory (HIPSpace, the
+// default) or host memory (HostSpace); element (r, c) at
+// data()[r * stride(0) + c].  Copies share the allocation (as Kokkos::View).
+template <class T, class Space = HIPSpace>
 class View {
+  static_assert(is_memory_space_v<Space>, "ponni::View memory space must be HIPSpace or HostSpace");
+  static constexpr bool on_host = std::is_same_v<Space, HostSpace>;
+
  public:
   using value_type = T;
   using non_const_value_type = std::remove_const_t<T>;
   using array_layout = LayoutRight;
+  using memory_space = Space;
   static constexpr int rank = 2;
 
   View() = default;
@@ -168,14 +217,21 @@ class View {
       : label_(std::move(label)), rows_(rows), cols_(cols), ld_(cols) {
     if (rows < 0 || cols < 0) abort("ponni::View extents must be nonnegative");
     if (rows * cols > 0) {
+      std::size_t const bytes = sizeof(T) * static_cast<std::size_t>(rows * cols);
       void* p = nullptr;
-      check_hip(hipMalloc(&p, sizeof(T) * static_cast<std::size_t>(rows * cols)), "hipMalloc");
-      if (zero) check_hip(hipMemset(p, 0, sizeof(T) * static_cast<std::size_t>(rows * cols)), "hipMemset");
-      owner_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+      if constexpr (on_host) {
+        p = std::calloc(static_cast<std::size_t>(rows * cols), sizeof(T));
+        if (p == nullptr) abort("ponni::View host allocation failed");
+        owner_ = std::shared_ptr<void>(p, [](void* q) { std::free(q); });
+      } else {
+        check_hip(hipMalloc(&p, bytes), "hipMalloc");
+        if (zero) check_hip(hipMemset(p, 0, bytes), "hipMemset");
+        owner_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+      }
       data_ = static_cast<T*>(p);
     }
   }
-  // Wrap caller-owned device memory (no ownership).
+  // Wrap caller-owned memory of this space (no ownership).
   static View wrap(T* data, std::int64_t rows, std::int64_t cols, std::int64_t ld) {
     View v;
     v.data_ = data;
@@ -201,19 +257,29 @@ class View {
   bool is_allocated() const { return data_ != nullptr; }
   std::string const& label() const { return label_; }
 
-  // Host <-> device copies of a row-major [rows, cols] host array.
+  // Copies from / to a row-major [rows, cols] host array.
   void copy_from_host(std::vector<non_const_value_type> const& h) const {
     if (static_cast<std::int64_t>(h.size()) != size()) abort("ponni::View::copy_from_host size mismatch");
-    check_hip(hipMemcpy2D(data_, sizeof(T) * ld_, h.data(), sizeof(T) * cols_, sizeof(T) * cols_, rows_,
-                          hipMemcpyHostToDevice),
-              "hipMemcpy2D");
+    if (size() == 0) return;
+    if constexpr (on_host) {
+      for (std::int64_t r = 0; r < rows_; r++)
+        std::memcpy(const_cast<non_const_value_type*>(data_) + r * ld_, h.data() + r * cols_, sizeof(T) * cols_);
+    } else {
+      check_hip(hipMemcpy2D(data_, sizeof(T) * ld_, h.data(), sizeof(T) * cols_, sizeof(T) * cols_, rows_,
+                            hipMemcpyHostToDevice),
+                "hipMemcpy2D");
+    }
   }
   std::vector<non_const_value_type> copy_to_host() const {
     std::vector<non_const_value_type> h(static_cast<std::size_t>(size()));
-    if (size() > 0)
+    if (size() == 0) return h;
+    if constexpr (on_host) {
+      for (std::int64_t r = 0; r < rows_; r++) std::memcpy(h.data() + r * cols_, data_ + r * ld_, sizeof(T) * cols_);
+    } else {
       check_hip(hipMemcpy2D(h.data(), sizeof(T) * cols_, data_, sizeof(T) * ld_, sizeof(T) * cols_, rows_,
                             hipMemcpyDeviceToHost),
                 "hipMemcpy2D");
+    }
     return h;
   }
 
@@ -820,12 +886,20 @@ __global__ __launch_bounds__(256) void user_chain_forward(typename Model::Params
 
 }  // namespace detail
 
-template <class real, class... Layers>
-class Inference {
+// A model bound to an execution space (HIP: the GPU; Host: host threads);
+// Inference<real, Layers...> is the HIP form.
+template <class real, class Exec, class... Layers>
+class BasicInference {
   static_assert(sizeof...(Layers) > 0, "a model needs at least one layer");
+  static_assert(is_execution_space_v<Exec>, "create_inference_model requires an execution space (HIP or Host)");
 
  public:
   using real_type = real;
+  using execution_space = Exec;
+  using memory_space = typename Exec::memory_space;
+  static constexpr bool runs_on_host = std::is_same_v<memory_space, HostSpace>;
+  static_assert(!runs_on_host || std::is_same_v<real, float> || std::is_same_v<real, double>,
+                "host execution-space models run in F32 or F64");
   using TUPLE = std::tuple<Layers...>;
   static constexpr int num_layers = static_cast<int>(sizeof...(Layers));
   // A chain holding user layers (the plugin contract) runs one sample per
@@ -835,8 +909,8 @@ class Inference {
   static_assert(!has_user_layers || std::is_same_v<real, float> || std::is_same_v<real, double>,
                 "chains with user layers run in F32 or F64");
 
-  explicit Inference(TUPLE const& layers, hipStream_t stream = nullptr, int path = PONNI_PATH_AUTO)
-      : layers_(layers), stream_(stream) {
+  explicit BasicInference(TUPLE const& layers, Exec const& exec = Exec(), int path = PONNI_PATH_AUTO)
+      : layers_(layers), exec_(exec) {
     std::vector<ponni_layer_desc> descs;
     collect_descs(descs, std::make_index_sequence<num_layers>{});
     ponni_plan p = nullptr;
@@ -853,7 +927,11 @@ class Inference {
   auto& get_layer() { return std::get<I>(layers_); }
   template <int I>
   auto const& get_layer() const { return std::get<I>(layers_); }
-  hipStream_t stream() const { return stream_; }
+  hipStream_t stream() const {
+    if constexpr (runs_on_host) return nullptr;
+    else return exec_.stream;
+  }
+  Exec const& execution_space_instance() const { return exec_; }
   ponni_plan plan() const { return plan_.get(); }
 
   ponni_plan_info info() const {
@@ -988,7 +1066,7 @@ class Inference {
   struct UserLayers {
     Params const* p;
     template <int I>
-    __device__ void call(ponni_hip::View2 const& in, ponni_hip::View2 const& out, ponni_hip::View2 const& sv,
+    __host__ __device__ void call(ponni_hip::View2 const& in, ponni_hip::View2 const& out, ponni_hip::View2 const& sv,
                          int n_out, int b) const {
       using L = std::tuple_element_t<I, TUPLE>;
       if constexpr (!detail::is_builtin_v<L>) {
@@ -1006,11 +1084,11 @@ class Inference {
       }
     }
     template <std::size_t... I>
-    __device__ void dispatch(int index, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
+    __host__ __device__ void dispatch(int index, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
                              ponni_hip::View2 const& sv, int n_out, int b, std::index_sequence<I...>) const {
       ((index == static_cast<int>(I) ? (call<static_cast<int>(I)>(in, out, sv, n_out, b), 0) : 0), ...);
     }
-    __device__ void operator()(int index, int, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
+    __host__ __device__ void operator()(int index, int, ponni_hip::View2 const& in, ponni_hip::View2 const& out,
                                ponni_hip::View2 const& sv, int, int n_out, std::int64_t b) const {
       dispatch(index, in, out, sv, n_out, static_cast<int>(b), std::make_index_sequence<num_layers>{});
     }
@@ -1018,7 +1096,7 @@ class Inference {
 
   // One sample: column pointers with row strides (thread-private states).
   template <int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
-  __device__ static void run_sample(Params const& p, real const* in, std::int64_t in_ld, real* out,
+  __host__ __device__ static void run_sample(Params const& p, real const* in, std::int64_t in_ld, real* out,
                                     std::int64_t out_ld) {
     static_assert(std::is_same_v<real, float> || std::is_same_v<real, double>,
                   "in-kernel inference runs F32 and F64 models");
@@ -1028,13 +1106,13 @@ class Inference {
 
   // Sample `ibatch` of LayoutRight [features, batch] views (device memory).
   template <class InputView, class OutputView, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
-  __device__ static void forward_batch_parallel_in_kernel(InputView const& input, OutputView const& output,
+  __host__ __device__ static void forward_batch_parallel_in_kernel(InputView const& input, OutputView const& output,
                                                           Params const& p, int ibatch) {
     run_sample<MAXW, MAXSAVED>(p, input.data() + ibatch, input.stride(0), output.data() + ibatch, output.stride(0));
   }
   // One sample held in per-thread arrays.
   template <int NI, int NO, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
-  __device__ static void forward_batch_parallel_in_kernel(SArray<real, NI> const& input, SArray<real, NO>& output,
+  __host__ __device__ static void forward_batch_parallel_in_kernel(SArray<real, NI> const& input, SArray<real, NO>& output,
                                                           Params const& p) {
     run_sample<MAXW, MAXSAVED>(p, input.data(), 1, output.data(), 1);
   }
@@ -1067,9 +1145,17 @@ class Inference {
           (one(l), ...);
         },
         layers_);
-    // (Only where a device exists: models are also built on GPU-less hosts.)
+    // Host models describe the plan in host memory; device models do so only
+    // where a device exists (models are also built on GPU-less hosts).
     int devices = 0;
-    if constexpr (std::is_same_v<real, float> || std::is_same_v<real, double>) {
+    if constexpr (runs_on_host) {
+      if constexpr (has_user_layers) {
+        check(ponni_plan_host_model(plan_.get(), &params.model), "ponni_plan_host_model");
+        collect_user_params(std::make_index_sequence<num_layers>{});
+      } else {
+        check(ponni_plan_host_model(plan_.get(), &params), "ponni_plan_host_model");
+      }
+    } else if constexpr (std::is_same_v<real, float> || std::is_same_v<real, double>) {
       if (hipGetDeviceCount(&devices) == hipSuccess && devices > 0) {
         if constexpr (has_user_layers) {
           check(ponni_plan_device_model(plan_.get(), &params.model), "ponni_plan_device_model");
@@ -1140,20 +1226,23 @@ class Inference {
   // ---- inference --------------------------------------------------------------------------
   // Allocates and zero-fills the output, then runs (ponni_Inference.h:338-346).
   template <class InputView>
-  View<real> forward_batch_parallel(InputView const& input) {
+  View<real, memory_space> forward_batch_parallel(InputView const& input) {
     require_layout_right_views<InputView>();
     std::int64_t const batch = static_cast<std::int64_t>(input.extent(1));
     if (batch == 0) abort("Inference requires a nonzero batch size");
-    View<real> output("output", get_num_outputs(), batch, true);
+    View<real, memory_space> output("output", get_num_outputs(), batch, true);
     forward_batch_parallel(input, output);
     return output;
   }
 
-  // Into caller-provided storage; asynchronous on the model's stream
-  // (ponni_Inference.h:352-389).
+  // Into caller-provided storage (ponni_Inference.h:352-389): asynchronous on
+  // the model's stream for HIP models, synchronous for host models.
   template <class InputView, class OutputView>
   void forward_batch_parallel(InputView const& input, OutputView const& output) {
     require_layout_right_views<InputView, OutputView>();
+    static_assert(std::is_same_v<typename view_memory_space<InputView>::type, memory_space> &&
+                      std::is_same_v<typename view_memory_space<OutputView>::type, memory_space>,
+                  "Inference Views must live in the model's memory space");
     static_assert(!std::is_const_v<std::remove_pointer_t<decltype(output.data())>>,
                   "Inference output View must be writable");
     std::int64_t const batch = static_cast<std::int64_t>(input.extent(1));
@@ -1163,17 +1252,28 @@ class Inference {
     if (static_cast<int>(output.extent(0)) != get_num_outputs() || output.extent(1) != input.extent(1))
       abort("Error: Provided output dimensions do not match the model and input batch");
     sync();
-    if constexpr (has_user_layers) {
+    if constexpr (runs_on_host) {
+      if constexpr (has_user_layers) {
+        if (!fits_in_kernel(params.model)) abort("Error: a chain with user layers is limited to 256-feature states");
+        for (std::int64_t b = 0; b < batch; b++)
+          run_sample(params, input.data() + b, static_cast<std::int64_t>(input.stride(0)), output.data() + b,
+                     static_cast<std::int64_t>(output.stride(0)));
+      } else {
+        check(ponni_forward_host(plan_.get(), input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
+                                 static_cast<std::int64_t>(output.stride(0)), batch, exec_.threads),
+              "forward_batch_parallel");
+      }
+    } else if constexpr (has_user_layers) {
       if (!fits_in_kernel(params.model)) abort("Error: a chain with user layers is limited to 256-feature states");
       unsigned const blocks = static_cast<unsigned>((batch + 255) / 256);
-      hipLaunchKernelGGL((detail::user_chain_forward<Inference, real>), dim3(blocks), dim3(256), 0, stream_, params,
+      hipLaunchKernelGGL((detail::user_chain_forward<BasicInference, real>), dim3(blocks), dim3(256), 0, stream(), params,
                          input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
                          static_cast<std::int64_t>(output.stride(0)), batch);
       hipError_t const e = hipGetLastError();
       if (e != hipSuccess) abort(std::string("forward_batch_parallel: ") + hipGetErrorString(e));
     } else {
       check(ponni_forward(plan_.get(), input.data(), static_cast<std::int64_t>(input.stride(0)), output.data(),
-                          static_cast<std::int64_t>(output.stride(0)), batch, stream_),
+                          static_cast<std::int64_t>(output.stride(0)), batch, stream()),
             "forward_batch_parallel");
     }
   }
@@ -1219,23 +1319,48 @@ class Inference {
   }
 
   TUPLE layers_;
-  hipStream_t stream_ = nullptr;
+  Exec exec_;
   std::shared_ptr<ponni_plan_s> plan_;
   std::vector<std::uint64_t> pushed_;
 };
 
 // ---- factories (ponni_create_model.h:40-98) ------------------------------------------------
 
-// Layers are copied into the model (parameters live in the plan's device
-// buffer), as the reference deep-copies them when the memory space differs.
-template <class... Layers>
-inline auto create_inference_model(Layers const&... layers) {
-  return Inference<float, Layers...>(std::make_tuple(layers...));
+template <class real, class... Layers>
+using Inference = BasicInference<real, HIP, Layers...>;
+
+namespace detail {
+template <class real, class Exec, class Mem, class... Layers>
+inline auto create_model(Exec const& exec, Mem const&, Layers const&... layers) {
+  static_assert(is_execution_space_v<Exec>, "create_inference_model requires an execution space (HIP or Host)");
+  static_assert(is_memory_space_v<Mem>, "create_inference_model requires a memory space (HIPSpace or HostSpace)");
+  static_assert(std::is_same_v<typename Exec::memory_space, Mem>,
+                "create_inference_model execution space cannot access its memory space");
+  return BasicInference<real, Exec, Layers...>(std::make_tuple(layers...), exec);
 }
-// The execution-space-instance overload: a HIP stream.
+}  // namespace detail
+
+// Layers are copied into the model (parameters live in the plan's buffers),
+// as the reference deep-copies them when the memory space differs.
+template <class First, class... Rest,
+          std::enable_if_t<!is_execution_space_v<First> && !std::is_same_v<std::decay_t<First>, hipStream_t>, int> = 0>
+inline auto create_inference_model(First const& first, Rest const&... rest) {
+  return Inference<float, First, Rest...>(std::make_tuple(first, rest...));
+}
+// The execution-space-instance overloads (ponni_create_model.h:52-78).
+template <class Exec, class... Layers, std::enable_if_t<is_execution_space_v<Exec>, int> = 0>
+inline auto create_inference_model(Exec const& exec, Layers const&... layers) {
+  return detail::create_model<float>(exec, typename Exec::memory_space(), layers...);
+}
+template <class Exec, class Mem, class... Layers,
+          std::enable_if_t<is_execution_space_v<Exec> && is_memory_space_v<Mem>, int> = 0>
+inline auto create_inference_model(Exec const& exec, Mem const& mem, Layers const&... layers) {
+  return detail::create_model<float>(exec, mem, layers...);
+}
+// A HIP stream is the HIP execution-space instance.
 template <class... Layers>
 inline auto create_inference_model(hipStream_t stream, Layers const&... layers) {
-  return Inference<float, Layers...>(std::make_tuple(layers...), stream);
+  return Inference<float, Layers...>(std::make_tuple(layers...), HIP(stream));
 }
 template <class... Layers>
 inline auto create_inference_model_single_precision(Layers const&... layers) {

@@ -36,13 +36,15 @@ __host__ __device__ inline bool fits_in_kernel(ponni_device_model const& m) {
 }
 
 // One sample: out[f * out_ld] = model(in[k * in_ld]) for f < num_outputs.
+// Device code passes the description ponni_plan_device_model gives; host
+// code (host execution-space models) the one ponni_plan_host_model gives.
 // `real` is float for F32 models and double for F64 models.  A model that
 // does not fit the thread-private limits, or of another dtype, writes NaN.
 // `ext` evaluates the chain's caller-implemented layers (PONNI_LAYER_EXTERNAL),
 // see ponni_hip::run_ops; the facade supplies it for user layer types.
 template <class real, int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved,
           class Ext = ponni_hip::NoExternal>
-__device__ inline void forward_one(ponni_device_model const& m, real const* in, int64_t in_ld, real* out,
+__host__ __device__ inline void forward_one(ponni_device_model const& m, real const* in, int64_t in_ld, real* out,
                                    int64_t out_ld, Ext const& ext = Ext()) {
   constexpr int want = sizeof(real) == 8 ? PONNI_F64 : PONNI_F32;
   if (m.dtype != want || !fits_in_kernel<MAXW, MAXSAVED>(m)) {

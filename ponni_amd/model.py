@@ -273,6 +273,23 @@ class Inference:
     def forward_raw(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int, stream: int = 0) -> None:
         A.check(A.lib().ponni_forward(self._plan, x_ptr, ld_in, y_ptr, ld_out, batch, stream))
 
+    def forward_host(self, x, threads: int = 0):
+        """Host execution space: x a numpy array [n_in, B] of the plan's dtype
+        (F32 or F64 plans), evaluated on the host by the GENERIC op list
+        (ponni_forward_host).  Returns y [n_out, B]."""
+        import numpy as np
+
+        want = {"f32": np.float32, "f64": np.float64}.get(self.dtype)
+        if want is None:
+            raise ValueError("host execution runs f32 and f64 models")
+        x = np.ascontiguousarray(x, dtype=want)
+        if x.ndim != 2:
+            raise ValueError("input must be rank two [features, batch]")
+        y = np.empty((self.get_num_outputs(), x.shape[1]), dtype=want)
+        A.check(A.lib().ponni_forward_host(self._plan, x.ctypes.data, x.shape[1], y.ctypes.data, y.shape[1],
+                                           x.shape[1], threads))
+        return y
+
     def forward_batch_parallel(self, x, y=None):
         """x: torch tensor [n_in, B] on the GPU (row-contiguous).  Returns y [n_out, B]."""
         import torch

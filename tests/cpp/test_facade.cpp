@@ -13,6 +13,7 @@
 //   unit/core/test_template_coverage.cpp:414-500  multi-slot save -> {0,6,-2,6,-2,3}
 //   unit/core/test_template_coverage.cpp:503-525  half / bhalf factories -> 5
 //   unit/performance_benchmark/performance_benchmark.cpp:21-53  mean 15.4
+//   unit/core/test_core_unit.cpp:380-404   host execution/memory space model -> (4, 4)
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -375,6 +376,99 @@ void test_user_layers_cpu() {
   CHECK(m.get_num_inputs() == 2 && m.get_num_outputs() == 2 && m.get_num_trainable_parameters() == 0);
 }
 
+// Host execution-space models (test_core_unit.cpp:380-404): the same
+// chains on the host, through the library's host executor or, with user
+// layers, the per-sample interpreter on the host.
+template <class Exec>
+auto four_block_model_on(Exec const& exec) {
+  using namespace ponni;
+  return create_inference_model(
+      exec, Matvec<float>(ones(2, 5)), Bias<float>(std::vector<float>(5, 0.5f)), Relu<float>(5), Tanh<float>(5),
+      Matvec<float>(ones(5, 3)), Bias<float>(std::vector<float>(3, -0.25f)), Sigmoid<float>(3),
+      Matvec<float>(ones(3, 7)), Bias<float>(std::vector<float>(7, 0.1f)), LeakyRelu<float>(7, 0.2f),
+      Matvec<float>(ones(7, 2)), Bias<float>(std::vector<float>(2, -0.2f)), HardSwish<float>(2));
+}
+
+void test_host_models_cpu() {
+  using namespace ponni;
+  {  // test_core_unit.cpp:380-404
+    auto host_model = create_inference_model(DefaultHostExecutionSpace(), HostSpace(), Matvec<float>(ones(2, 2)),
+                                             Bias<float>(std::vector<float>(2, 1.0f)), LeakyRelu<float>(2, 0.1f));
+    static_assert(std::is_same_v<typename decltype(host_model)::execution_space, DefaultHostExecutionSpace>);
+    static_assert(std::is_same_v<typename decltype(host_model)::memory_space, HostSpace>);
+    static_assert(std::is_same_v<typename decltype(create_inference_model(Relu<float>(2)))::memory_space, HIPSpace>);
+    View<float, HostSpace> host_input("host_input", 2, 1), host_output("host_output", 2, 1);
+    host_input(0, 0) = 1.0f;
+    host_input(1, 0) = 2.0f;
+    host_model.forward_batch_parallel(host_input, host_output);
+    CHECK(near(host_output(0, 0), 4.0, 1e-6) && near(host_output(1, 0), 4.0, 1e-6));
+  }
+  {  // the four-block closed form over a batch, 3 host threads, strided views
+    auto m = four_block_model_on(Host(3));
+    int const B = 1000;
+    View<float, HostSpace> x("x", 2, B + 7);
+    for (int b = 0; b < B; b++) {
+      x(0, b) = std::sin(0.1f * b);
+      x(1, b) = std::cos(0.3f * b);
+    }
+    auto y = m.forward_batch_parallel(x.columns(0, B));
+    static_assert(std::is_same_v<typename decltype(y)::memory_space, HostSpace>);
+    bool ok = true;
+    for (int b = 0; b < B; b++)
+      for (int o = 0; o < 2; o++) ok = ok && near(y(o, b), four_block_closed_form(x(0, b), x(1, b)), 2e-5);
+    CHECK(ok);
+    // one sample through the in-kernel form, here called on the host
+    SArray<float, 2> in;
+    SArray<float, 2> out;
+    in(0) = 0.25f;
+    in(1) = -0.5f;
+    decltype(m)::forward_batch_parallel_in_kernel(in, out, m.params);
+    CHECK(near(out(0), four_block_closed_form(0.25, -0.5), 2e-5) && near(out(1), out(0), 0.0));
+  }
+  {  // user layers on the host: test_template_coverage.cpp:740-790 -> (4.5, -4.5), and a mixed chain
+    auto m = create_inference_model(Host(), TestDense<float, 2>(), TestIndexedPointwise<float, 2>(),
+                                    TestBarrier<float, 2>(), TestDense<float, 2>());
+    View<float, HostSpace> x("x", 2, 1);
+    x(0, 0) = 1.0f;
+    x(1, 0) = 2.0f;
+    auto y = m.forward_batch_parallel(x);
+    CHECK(near(y(0, 0), 4.5, 1e-6) && near(y(1, 0), -4.5, 1e-6));
+    Matrix<float> w(2, 2, std::vector<float>{0.5f, -1.0f, 2.0f, 0.25f});
+    auto mixed = create_inference_model(Host(), HostSpace(), Matvec<float>(w),
+                                        Bias<float>(std::vector<float>{0.1f, -0.2f}), TestIndexedPointwise<float, 2>(),
+                                        Save_State<0>(2), Relu<float>(2), TestBarrier<float, 2>(),
+                                        TestMultiplySaved<0, float, 2>(), Binop_Add<0>(2), Tanh<float>(2));
+    int const B = 300;
+    View<float, HostSpace> xs("xs", 2, B);
+    for (int i = 0; i < 2 * B; i++) xs(i / B, i % B) = std::sin(0.37f * i) * 2.0f;
+    auto ys = mixed.forward_batch_parallel(xs);
+    bool ok = true;
+    for (int b = 0; b < B; b++) {
+      double const x0 = xs(0, b), x1 = xs(1, b);
+      double const d0 = 0.5 * x0 + 2.0 * x1 + 0.1 + 0.5;
+      double const d1 = -1.0 * x0 + 0.25 * x1 - 0.2 + 1.0;
+      double const r0 = std::max(0.0, d0), r1 = std::max(0.0, d1);
+      double const m0 = r1 * d0 + d0, m1 = r0 * d1 + d1;
+      ok = ok && near(ys(0, b), std::tanh(m0), 2e-5) && near(ys(1, b), std::tanh(m1), 2e-5);
+    }
+    CHECK(ok);
+  }
+  {  // an F64 host model; parameter updates reach it
+    auto m = detail::create_model<double>(Host(), HostSpace(), Matvec<double>(Matrix<double>(3, 2, 1.0)),
+                                          LeakyRelu<double>(2, 0.1));
+    View<double, HostSpace> x("x", 3, 2);
+    x(0, 0) = 1.0;
+    x(1, 0) = 2.0;
+    x(2, 0) = -4.5;
+    x(0, 1) = x(1, 1) = x(2, 1) = 1.0;
+    auto y = m.forward_batch_parallel(x);
+    CHECK(y(0, 0) == -0.1 * 1.5 && y(1, 0) == -0.1 * 1.5 && y(0, 1) == 3.0);
+    m.set_trainable_parameters(std::vector<double>(6, 2.0));
+    y = m.forward_batch_parallel(x);
+    CHECK(y(0, 0) == -0.1 * 3.0 && y(1, 1) == 6.0);
+  }
+}
+
 template <class Model>
 __global__ void in_kernel_sarray2(typename Model::Params p, float* result) {
   ponni::SArray<float, 2> in;
@@ -509,6 +603,7 @@ int main(int argc, char** argv) {
   test_weights_files();
   test_sixteen_bit_types();
   test_user_layers_cpu();
+  test_host_models_cpu();
   if (!cpu_only) {
     test_user_layers_gpu();
     test_known_answers_gpu();

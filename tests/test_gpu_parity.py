@@ -153,10 +153,12 @@ def test_reduced_precision_paths(cuda, dtype, path):
     check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
 
 
-def test_f64_generic(cuda):
-    rng = np.random.default_rng(12)
-    layers = K.random_chain(rng, 20, 3)
-    x = rng.standard_normal((20, 500))
+@pytest.mark.parametrize("seed,width,blocks", [(12, 20, 3), (502, 13, 4), (507, 64, 3)])
+def test_f64_generic(cuda, seed, width, blocks):
+    # Layer attributes (slopes, epsilons, ranges) stay exact in F64 plans.
+    rng = np.random.default_rng(seed)
+    layers = K.random_chain(rng, width, blocks)
+    x = rng.standard_normal((width, 500))
     got, xg, _ = gpu_run(layers, x, dtype="f64", path="generic")
     want = oracle.forward(layers, xg, oracle.MODE_F64)
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
