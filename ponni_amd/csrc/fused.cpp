@@ -227,7 +227,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (half) {
     if (char const* v = std::getenv("PONNI_HALF_NT")) {  // tuning override
       int const t = std::atoi(v);
-      if (t == 1 || t == 2) NT = t;
+      if (t == 1 || t == 2 || t == 4) NT = t;
     }
     half_wps = NT == 1 ? 4 : 2;
     if (char const* v = std::getenv("PONNI_HALF_WPS")) {  // tuning override
