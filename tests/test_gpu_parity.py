@@ -221,6 +221,32 @@ def test_configs_full_size_columns(cuda, name):
         check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
 
 
+@pytest.mark.parametrize("name,B", [("c1", 1_100_000_004), ("c2", 140_000_003), ("c4", 34_000_001)])
+def test_more_than_2_31_elements(cuda, name, B):
+    """Tensors of more than 2^31 elements (the batch stays below INT_MAX, as
+    the reference requires): every kernel offset must be 64-bit.  Columns at
+    both ends and spread over the batch are checked against the oracle."""
+    import torch
+
+    cfg = C.CONFIGS[name]
+    layers = cfg.layers(True)
+    assert max(cfg.n_in, cfg.n_out) * B > 2**31
+    x = config_input(cfg, B)
+    m = P.create_inference_model(*layers, dtype=cfg.dtype)
+    y = m.forward_batch_parallel(x)
+    torch.cuda.synchronize()
+    cols = torch.cat([torch.arange(0, 700), torch.arange(B // 2 - 300, B // 2 + 300), torch.arange(B - 700, B),
+                      torch.from_numpy(np.random.default_rng(1).integers(0, B, 500))]).to(x.device)
+    xg = x.index_select(1, cols).double().cpu().numpy()
+    got = y.index_select(1, cols).double().cpu().numpy()
+    del x, y
+    torch.cuda.empty_cache()
+    if cfg.dtype == "f32":
+        check_f32(got, oracle.forward(layers, xg), scale_tol=False)
+    else:
+        check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
