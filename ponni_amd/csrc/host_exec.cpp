@@ -8,6 +8,7 @@
 // lands here.
 #include <algorithm>
 #include <cstring>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -55,10 +56,17 @@ void run_all(ponni_plan_s const& t, real const* params, void const* x, int64_t l
   }
   std::vector<std::thread> pool;
   pool.reserve(static_cast<size_t>(n));
+  int64_t done = n;  // slices from here on run on the calling thread
   for (int64_t i = 0; i < n; i++) {
     int64_t const b0 = batch * i / n, b1 = batch * (i + 1) / n;
-    pool.emplace_back([&, b0, b1] { run_range<real>(t, params, xr, ldx, yr, ldy, b0, b1); });
+    try {
+      pool.emplace_back([&, b0, b1] { run_range<real>(t, params, xr, ldx, yr, ldy, b0, b1); });
+    } catch (std::system_error const&) {  // no more threads: finish here
+      done = i;
+      break;
+    }
   }
+  if (done < n) run_range<real>(t, params, xr, ldx, yr, ldy, batch * done / n, batch);
   for (auto& th : pool) th.join();
 }
 
