@@ -1,5 +1,6 @@
 """Writes the generated-model headers the C++ tests compile
-(tests/cpp/gen/*.h): the c5 graph with nonzero biases as class C5Model."""
+(tests/cpp/gen/*.h): the c5 graph with nonzero biases as class C5Model and
+the tiny 3 -> 4 -> 2 graph of tests/golden as class TinyModel."""
 import os
 import sys
 
@@ -11,12 +12,14 @@ sys.path.insert(0, ROOT)
 def main() -> None:
     from ponni_amd import configs as C
     from ponni_amd.emitter import emit_cpp_header
+    from tests.golden.make_generated_fixtures import tiny_graph
 
     os.makedirs(os.path.join(HERE, "gen"), exist_ok=True)
-    out = os.path.join(HERE, "gen", "c5_model.h")
-    tmp = out + ".tmp"
-    emit_cpp_header(C.c5_graph(True), tmp, namespace="ponni::generated", class_name="C5Model")
-    os.replace(tmp, out)
+    for name, graph, cls in [("c5_model.h", C.c5_graph(True), "C5Model"), ("tiny_model.h", tiny_graph(), "TinyModel")]:
+        out = os.path.join(HERE, "gen", name)
+        tmp = out + ".tmp"
+        emit_cpp_header(graph, tmp, namespace="ponni::generated", class_name=cls)
+        os.replace(tmp, out)
 
 
 if __name__ == "__main__":

@@ -1,21 +1,22 @@
-// The generated-model header of the c5 graph (tests/cpp/gen/c5_model.h,
-// written by ponni_amd.emitter): load the weights file Python saved, run
-// infer_batch (the header's ahead-of-time FUSED kernel), infer_batch_half2
-// and infer_one (an application kernel over device()); then read the learned
-// parameters, halve them through a device view, run infer_batch and infer_one
-// again and save the parameters.  tests/test_cpp.py compares every output.
-//   test_generated <weights.ponni> <x.f32 [24, B]> <B> <out_dir>
+// Generated-model headers (tests/cpp/gen/*.h, written by ponni_amd.emitter):
+// C5Model (the c5 graph) and TinyModel (a 3 -> 4 -> 2 graph).  For the chosen model: load the weights file, run infer_batch
+// (the header's ahead-of-time kernel), infer_batch_half2 and infer_one (an
+// application kernel over device()); then read the learned parameters, halve
+// them through a device view, run infer_batch and infer_one again and save
+// the parameters.  tests/test_cpp.py compares every output.
+//   test_generated <c5|tiny> <weights.ponni> <x.f32 [num_inputs, B]> <B> <out_dir>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <string>
 #include <vector>
 
 #include "gen/c5_model.h"
+#include "gen/tiny_model.h"
 
-using Model = ponni::generated::C5Model;
-
-__global__ void infer_one_kernel(Model::Device m, float const* x, std::int64_t ldx, float* y, std::int64_t ldy,
-                                 int batch) {
+template <class Model>
+__global__ void infer_one_kernel(typename Model::Device m, float const* x, std::int64_t ldx, float* y,
+                                 std::int64_t ldy, int batch) {
   int const b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
   ponni::SArray<float, Model::num_inputs> in;
@@ -39,13 +40,8 @@ static void write_f32(std::string const& path, std::vector<float> const& v) {
   std::fclose(f);
 }
 
-int main(int argc, char** argv) {
-  if (argc != 5) {
-    std::fprintf(stderr, "usage: %s weights.ponni x.f32 batch out_dir\n", argv[0]);
-    return 2;
-  }
-  int const B = std::atoi(argv[3]);
-  std::string const dir = argv[4];
+template <class Model>
+int run(char const* weights, char const* xpath, int B, std::string const& dir) {
   Model m;
   std::string err;
   if (m.weights_loaded() || m.parameters_are_finite() || m.save_parameters(dir + "/early.ponni", &err)) {
@@ -56,18 +52,21 @@ int main(int argc, char** argv) {
     std::fprintf(stderr, "loading a missing file must fail with a message\n");
     return 1;
   }
-  if (!m.load_weights(argv[1], &err)) {
+  if (!m.load_weights(weights, &err)) {
     std::fprintf(stderr, "load_weights: %s\n", err.c_str());
     return 1;
   }
   ponni::View<float> x("x", Model::num_inputs, B);
-  x.copy_from_host(read_f32(argv[2], std::size_t(Model::num_inputs) * B));
+  x.copy_from_host(read_f32(xpath, std::size_t(Model::num_inputs) * B));
   ponni::View<float> y("y", Model::num_outputs, B), yh("yh", Model::num_outputs, B), y1("y1", Model::num_outputs, B);
+  auto one = [&] {
+    hipLaunchKernelGGL(infer_one_kernel<Model>, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(),
+                       x.stride(0), y1.data(), y1.stride(0), B);
+    return hipDeviceSynchronize() == hipSuccess;
+  };
   m.infer_batch(x, y);
   m.infer_batch_half2(x, yh);
-  hipLaunchKernelGGL(infer_one_kernel, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(), x.stride(0),
-                     y1.data(), y1.stride(0), B);
-  if (hipDeviceSynchronize() != hipSuccess) return 1;
+  if (!one()) return 1;
   write_f32(dir + "/y_batch.f32", y.copy_to_host());
   write_f32(dir + "/y_half.f32", yh.copy_to_host());
   write_f32(dir + "/y_one.f32", y1.copy_to_host());
@@ -81,9 +80,7 @@ int main(int argc, char** argv) {
   pv.copy_from_host(p);
   m.set_parameters(pv);
   m.infer_batch(x, y);
-  hipLaunchKernelGGL(infer_one_kernel, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(), x.stride(0),
-                     y1.data(), y1.stride(0), B);
-  if (hipDeviceSynchronize() != hipSuccess) return 1;
+  if (!one()) return 1;
   write_f32(dir + "/y_batch_scaled.f32", y.copy_to_host());
   write_f32(dir + "/y_one_scaled.f32", y1.copy_to_host());
   if (!m.save_parameters(dir + "/saved.ponni", &err)) {
@@ -92,4 +89,16 @@ int main(int argc, char** argv) {
   }
   std::printf("test_generated: wrote %d samples (%s)\n", B, Model::model_fingerprint().c_str());
   return 0;
+}
+
+int main(int argc, char** argv) {
+  if (argc != 6) {
+    std::fprintf(stderr, "usage: %s c5|tiny weights.ponni x.f32 batch out_dir\n", argv[0]);
+    return 2;
+  }
+  int const B = std::atoi(argv[4]);
+  if (std::strcmp(argv[1], "c5") == 0) return run<ponni::generated::C5Model>(argv[2], argv[3], B, argv[5]);
+  if (std::strcmp(argv[1], "tiny") == 0) return run<ponni::generated::TinyModel>(argv[2], argv[3], B, argv[5]);
+  std::fprintf(stderr, "unknown model %s\n", argv[1]);
+  return 2;
 }

@@ -81,61 +81,68 @@ def test_emitted_header_text(tmp_path):
 
 
 @pytest.mark.gpu
-def test_generated_header_on_gpu(cuda, tmp_path):
-    """tests/cpp/test_generated.cpp over the emitted c5 header: infer_batch
-    (ahead-of-time FUSED kernel), infer_batch_half2 and infer_one (an
+@pytest.mark.parametrize("model", ["c5", "tiny"])
+def test_generated_header_on_gpu(cuda, tmp_path, model):
+    """tests/cpp/test_generated.cpp over an emitted header: infer_batch
+    (the ahead-of-time kernel), infer_batch_half2 and infer_one (an
     application kernel over device()) against the CPU oracle, on a weights
-    file saved by the Python model; then the parameter API (get, set from a
-    device view, save) against the Python model.  fp32 bar: relative L2 <=
-    1e-5 and max-abs <= 1e-4; fp16: relative L2 <= 2e-3 against fp16
-    operands."""
+    file saved by the Python model (c5) or written by the reference
+    generator (tiny, tests/golden/tiny_generated.ponni); then the parameter
+    API (get, set from a device view, save) against the Python model.  fp32
+    bar: relative L2 <= 1e-5 and max-abs <= 1e-4; fp16: relative L2 <= 2e-3
+    against fp16 operands."""
     import numpy as np
 
     import oracle
     from ponni_amd import configs as C
     from ponni_amd import graph as G
+    from tests.golden.make_generated_fixtures import tiny_graph
     from tests.test_gpu_parity import check_f32, check_half
 
     if not os.path.exists(GEN_BIN):
         pytest.fail(f"{GEN_BIN} is missing: build with `python -c 'import __graft_entry__ as g; g.build()'`")
     oracle.build()
-    gm = G.GeneratedModel(C.c5_graph(True))
-    gm.storage = gm.storage * 0.5 + np.random.default_rng(11).uniform(-0.05, 0.05, gm.storage.size)
-    weights = tmp_path / "c5.ponni"
-    gm.save_parameters(str(weights))
+    make_graph = (lambda: C.c5_graph(True)) if model == "c5" else tiny_graph
+    if model == "c5":
+        gm = G.GeneratedModel(make_graph())
+        gm.storage = gm.storage * 0.5 + np.random.default_rng(11).uniform(-0.05, 0.05, gm.storage.size)
+        weights = tmp_path / "c5.ponni"
+        gm.save_parameters(str(weights))
+    else:
+        weights = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_generated.ponni")
+    ref = G.GeneratedModel(make_graph())
+    ref.load_weights(str(weights))  # the values the file holds (fp32)
+    n_in, n_out = ref.num_inputs, ref.num_outputs
     B = 4099
-    x = np.random.default_rng(12).standard_normal((24, B)).astype(np.float32)
+    x = np.random.default_rng(12).standard_normal((n_in, B)).astype(np.float32)
     x.tofile(tmp_path / "x.f32")
-    r = subprocess.run([GEN_BIN, str(weights), str(tmp_path / "x.f32"), str(B), str(tmp_path)], capture_output=True,
-                       text=True, timeout=300)
+    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.f32"), str(B), str(tmp_path)],
+                       capture_output=True, text=True, timeout=300)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
 
     def out(name):
-        return np.fromfile(tmp_path / name, dtype=np.float32).reshape(10, B).astype(np.float64)
+        return np.fromfile(tmp_path / name, dtype=np.float32).reshape(n_out, B).astype(np.float64)
 
-    gm32 = G.GeneratedModel(C.c5_graph(True))
-    gm32.load_weights(str(weights))  # the values the file holds (fp32)
-
-    def oracle_layers(model):
-        layers = model.lowered.layers
-        for l, v in zip(layers, model.lowered.layer_params(model._constants("f64"))):
+    def oracle_layers(m):
+        layers = m.lowered.layers
+        for l, v in zip(layers, m.lowered.layer_params(m._constants("f64"))):
             if v.size:
                 l.params = v
         return layers
 
-    want = oracle.forward(oracle_layers(gm32), x.astype(np.float64))
+    want = oracle.forward(oracle_layers(ref), x.astype(np.float64))
     check_f32(out("y_batch.f32"), want, scale_tol=False)
     check_f32(out("y_one.f32"), want, scale_tol=False)
     xh = x.astype(np.float16).astype(np.float64)
-    check_half(out("y_half.f32"), oracle.forward(oracle_layers(gm32), xh, oracle.MODE_F16_OPERANDS))
+    check_half(out("y_half.f32"), oracle.forward(oracle_layers(ref), xh, oracle.MODE_F16_OPERANDS))
 
-    learned = gm32.get_parameters()
+    learned = ref.get_parameters()
     np.testing.assert_array_equal(np.fromfile(tmp_path / "params.f32", dtype=np.float32), learned.astype(np.float32))
-    gm32.set_parameters(learned * 0.5)
-    want = oracle.forward(oracle_layers(gm32), x.astype(np.float64))
+    ref.set_parameters(learned * 0.5)
+    want = oracle.forward(oracle_layers(ref), x.astype(np.float64))
     check_f32(out("y_batch_scaled.f32"), want, scale_tol=False)
     check_f32(out("y_one_scaled.f32"), want, scale_tol=False)
-    saved = G.GeneratedModel(C.c5_graph(False))
+    saved = G.GeneratedModel(make_graph())
     saved.load_weights(str(tmp_path / "saved.ponni"))
-    np.testing.assert_array_equal(saved.storage, gm32.storage)
+    np.testing.assert_array_equal(saved.storage, ref.storage)
