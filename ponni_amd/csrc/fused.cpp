@@ -134,6 +134,17 @@ std::string act_expr(Step const& s) {
   }
 }
 
+// The generated kernels' form: the logistic family on the hardware 2^x and 1/x.
+std::string act_fast_expr(Step const& s) {
+  switch (s.act) {
+    case ACT_TANH: return "act_tanh_fast(v)";
+    case ACT_SIGMOID: return "act_sigmoid_fast(v)";
+    case ACT_SILU: return "act_silu_fast(v)";
+    case ACT_GELU_TANH: return "act_gelu_tanh_fast(v)";
+    default: return act_expr(s);
+  }
+}
+
 uint64_t fnv(std::string const& s) {
   uint64_t h = 0xcbf29ce484222325ull;
   for (unsigned char ch : s) {
@@ -466,15 +477,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
   // The logistic family runs on the hardware transcendentals (fused_f32.h).
-  auto act = [&](Step const& st) {
-    switch (st.act) {
-      case ACT_TANH: return std::string("act_tanh_fast(v)");
-      case ACT_SIGMOID: return std::string("act_sigmoid_fast(v)");
-      case ACT_SILU: return std::string("act_silu_fast(v)");
-      case ACT_GELU_TANH: return std::string("act_gelu_tanh_fast(v)");
-      default: return act_expr(st);
-    }
-  };
+  auto act = [&](Step const& st) { return act_fast_expr(st); };
   // fp32 view of the state for barrier ops: the state itself (fp32 path) or a
   // widened copy that is rounded back afterwards (16-bit path).
   auto open32 = [&]() -> std::string {
@@ -744,21 +747,39 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         o << "    with_vec" << tv(n) << "(" << a << ", P + " << st.off << ", [](float v, float c) { return "
           << const_expr(st.act) << "; });\n";
       else
-        o << "    map" << tv(n) << "(" << a << ", [](float v) { return " << act_expr(st) << "; });\n";
+        o << "    map" << tv(n) << "(" << a << ", [](float v) { return " << act_fast_expr(st) << "; });\n";
     }
   };
   for (Op const& op : p.ops) {
     o << "  {  // op code " << op.code << "\n";
     switch (op.code) {
       case OP_DENSE: {
-        // Pointwise layers keep the width: the Matvec is n_in -> n_out.
+        // Pointwise layers keep the width: the Matvec is n_in -> n_out.  A
+        // generated Dense's bias (its first step) seeds the sum.
         int const K = op.n_in, N = op.n_out;
+        bool const seed = op.aux & DENSE_BIAS_FIRST;
         o << "    float a[" << W << "][" << V << "];\n";
-        o << "    dense<" << V << ", " << K << ", " << N << WV << "(a, s, P + " << op.woff << ");\n";
-        steps("a", N, op.epi_begin, op.epi_count);
+        if (seed)
+          o << "    dense_bias<" << V << ", " << K << ", " << N << WV << "(a, s, P + " << op.woff << ", P + "
+            << p.steps[op.epi_begin].off << ");\n";
+        else
+          o << "    dense<" << V << ", " << K << ", " << N << WV << "(a, s, P + " << op.woff << ");\n";
+        steps("a", N, op.epi_begin + (seed ? 1 : 0), op.epi_count - (seed ? 1 : 0));
         o << finish(op.n_out) << "(s, a);\n";
         break;
       }
+      case OP_LOAD:
+        o << "    copy<" << V << WV << "(s, sv" << op.slot << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_BINARY:
+        o << "    binary<" << V << ", " << op.n_out << ", " << W << ", " << op.aux << ">(s, sv" << op.slot << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      case OP_REDUCE:
+        o << "    reduce<" << V << ", " << cur_n << ", " << W << ", " << op.aux << ">(s);\n";
+        o << finish(1) << "(s, s);\n";
+        break;
       case OP_POINTWISE:
         steps("s", cur_n, op.epi_begin, op.epi_count);
         o << finish(op.n_out) << "(s, s);\n";
@@ -841,8 +862,9 @@ std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg) { return n
 
 bool narrow_jit_supports(ponni_plan_s const& p) {
   if (p.path != PONNI_PATH_NARROW || p.width_class <= 0 || p.dtype == PONNI_F64) return false;
+  if (p.num_slots > kNarrowJitMaxSlots) return false;
   for (Op const& op : p.ops)
-    if (op.code == OP_LOAD || op.code == OP_BINARY || op.code == OP_REDUCE) return false;
+    if (op.code == OP_EXTERNAL) return false;
   return true;
 }
 

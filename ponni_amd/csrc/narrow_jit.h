@@ -104,6 +104,29 @@ __device__ inline void dense(float (&a)[W][V], float const (&s)[W][V], float con
   }
 }
 
+// Generated Dense: a[j] = c[j] + sum_k W(k, j) s[k], the bias seeding the
+// sum and k ascending (emitter.py:701-710); rows >= N are 0.
+template <int V, int K, int N, int W>
+__device__ inline void dense_bias(float (&a)[W][V], float const (&s)[W][V], float const* __restrict__ w,
+                                  float const* __restrict__ c) {
+#pragma unroll
+  for (int j = 0; j < W; j++) {
+#pragma unroll
+    for (int v = 0; v < V; v++) a[j][v] = 0.0f;
+    if (j < N) {
+      float const cj = c[j];
+#pragma unroll
+      for (int v = 0; v < V; v++) a[j][v] = cj;
+#pragma unroll
+      for (int k = 0; k < K; k++) {
+        float const wk = w[k * W + j];
+#pragma unroll
+        for (int v = 0; v < V; v++) a[j][v] += wk * s[k][v];
+      }
+    }
+  }
+}
+
 // a[j] += c[j] for j < N (ponni_Bias.h:66-68), or f(a[j], c[j]).
 template <int V, int N, int W, class F>
 __device__ inline void with_vec(float (&a)[W][V], float const* __restrict__ c, F f) {
@@ -232,6 +255,60 @@ __device__ inline void proj_add(float (&s)[W][V], float const (&sv)[W][V], float
     }
 #pragma unroll
     for (int v = 0; v < V; v++) s[i][v] = s[i][v] + proj[v];
+  }
+}
+
+// Tensor-tensor operation of the state with saved state `sv` (emitter.py:735-741):
+// operands of one feature broadcast (BinaryAux flags in AUX), the saved one
+// on the left when BIN_SAVED_LEFT.
+template <int V, int NOUT, int W, int AUX>
+__device__ inline void binary(float (&s)[W][V], float const (&sv)[W][V]) {
+  constexpr int bop = AUX & 0xff;
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float const s0 = s[0][v], v0 = sv[0][v];
+#pragma unroll
+    for (int f = 0; f < NOUT; f++) {
+      float const a = (AUX & BIN_STATE_SCALAR) ? s0 : s[f][v];
+      float const c = (AUX & BIN_SAVED_SCALAR) ? v0 : sv[f][v];
+      s[f][v] = (AUX & BIN_SAVED_LEFT) ? apply_binary<float>(bop, c, a) : apply_binary<float>(bop, a, c);
+    }
+  }
+}
+
+// Reduction over the N features into feature 0 (emitter.py:475-547); OP is
+// a ponni_reduce_op value: 0 sum, 1 mean, 2 max, 3 min, 4 L1, 5 L2,
+// 6 sum of squares, 7 log-sum, 8 log-sum-exp, 9 product.
+template <int V, int N, int W, int OP>
+__device__ inline void reduce(float (&s)[W][V]) {
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    float r;
+    if (OP == 2 || OP == 3 || OP == 8) {
+      r = s[0][v];
+#pragma unroll
+      for (int f = 1; f < N; f++) r = OP == 3 ? (s[f][v] < r ? s[f][v] : r) : (s[f][v] > r ? s[f][v] : r);
+      if (OP == 8) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int f = 0; f < N; f++) sum += d_exp(s[f][v] - r);
+        r = __builtin_isinf(r) ? r : r + d_log(sum);
+      }
+    } else {
+      r = OP == 9 ? 1.0f : 0.0f;
+#pragma unroll
+      for (int f = 0; f < N; f++) {
+        float const x = s[f][v];
+        if (OP == 4) r += d_abs(x);
+        else if (OP == 5 || OP == 6) r += x * x;
+        else if (OP == 9) r *= x;
+        else r += x;
+      }
+      if (OP == 1) r /= float(N);
+      else if (OP == 5) r = d_sqrt(r);
+      else if (OP == 7) r = d_log(r);
+    }
+    s[0][v] = r;
   }
 }
 

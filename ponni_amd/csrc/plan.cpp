@@ -816,23 +816,44 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     }
     path = PONNI_PATH_GENERIC;
   }
-  // NARROW and MFMA interpret layer-template chains only.
-  int const narrow = graph_ops ? 0 : narrow_width_class(max_width);
+  // The interpreted NARROW and MFMA kernels run layer-template chains only;
+  // generated NARROW kernels (run-time compilation) also run graph operations.
+  int const narrow_w = narrow_width_class(max_width);
+  int const narrow = graph_ops ? 0 : narrow_w;
   int const mfma = graph_ops ? 0 : mfma_width_class(dtype, max_width);
   char const* jit_env = std::getenv("PONNI_JIT");
   bool const jit_enabled = jit_env == nullptr || std::strcmp(jit_env, "0") != 0;
+  bool const narrow_interp_ok = dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots;
+  bool const narrow_gen_ok = jit_enabled && dtype != PONNI_F64 && narrow_w > 0 && !p->external &&
+                             p->num_slots <= kNarrowJitMaxSlots;
+  // Between widths 9 and 16 the generated NARROW kernel (scalar FMAs, one
+  // lane per sample group) beats FUSED (16-wide MFMA tiles) while the chain
+  // does fewer than 10 multiply-adds per byte of input and output; beyond
+  // that the matrix cores win (measured on chains of 16-wide layers).
+  double macs = 0.0;
+  for (int i = 0; i < num_layers; i++) {
+    auto const& d = layers[i];
+    if (is_dense(d.kind)) macs += double(d.n_in) * d.n_out;
+    if (d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD) macs += double(d.n_aux) * d.n_in;
+  }
+  double const io_bytes = double(layers[0].n_in + layers[num_layers - 1].n_out) * (dtype == PONNI_F32 ? 4 : 2);
+  bool const narrow_light = macs < 10.0 * io_bytes;
+  bool const narrow_jit_ok = jit_enabled && narrow_light && (graph_ops ? narrow_gen_ok : narrow_interp_ok);
   int chosen = path;
   if (chosen == PONNI_PATH_AUTO) {
-    if (dtype != PONNI_F64 && narrow > 0 && max_width <= 8 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    if (narrow_interp_ok && max_width <= 8) chosen = PONNI_PATH_NARROW;
+    else if (narrow_jit_ok) chosen = PONNI_PATH_NARROW;
     else if (jit_enabled && fused_supports(*p)) chosen = PONNI_PATH_FUSED;
-    else if (dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots) chosen = PONNI_PATH_NARROW;
+    else if (graph_ops && narrow_gen_ok) chosen = PONNI_PATH_NARROW;
+    else if (narrow_interp_ok) chosen = PONNI_PATH_NARROW;
     else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
     else chosen = PONNI_PATH_GENERIC;
   } else if (chosen == PONNI_PATH_NARROW) {
-    if (dtype == PONNI_F64 || narrow == 0 || p->num_slots > kNarrowMaxSlots) {
+    if (!narrow_interp_ok && !(graph_ops && narrow_gen_ok)) {
       delete p;
       return fail(PONNI_ERR_UNSUPPORTED,
-                  "NARROW path needs a layer-template chain in F32/F16/BF16, width <= 16 and at most 2 saved states");
+                  "NARROW path needs F32/F16/BF16, width <= 16, and a layer-template chain with at most 2 saved "
+                  "states or (with run-time compilation) a generated graph with at most 4");
     }
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {
@@ -848,7 +869,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     }
   }
   p->path = chosen;
-  p->width_class = chosen == PONNI_PATH_NARROW ? narrow : chosen == PONNI_PATH_MFMA ? mfma : 0;
+  p->width_class = chosen == PONNI_PATH_NARROW ? narrow_w : chosen == PONNI_PATH_MFMA ? mfma : 0;
   lower(*p);
   p->narrow_jit = chosen == PONNI_PATH_NARROW && jit_enabled && narrow_jit_supports(*p);
   *out_plan = p;

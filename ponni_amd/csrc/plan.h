@@ -50,7 +50,8 @@ int host_twin(ponni_plan_s& plan, ponni_plan_s*& twin);
 // Width classes each register path is instantiated for.
 int narrow_width_class(int max_width);      // 0 if too wide
 int mfma_width_class(int dtype, int max_width);  // tiles of 16 features; 0 if too wide
-constexpr int kNarrowMaxSlots = 2;
+constexpr int kNarrowMaxSlots = 2;     // interpreted NARROW kernels
+constexpr int kNarrowJitMaxSlots = 4;  // generated NARROW kernels (one register state per slot)
 constexpr int kMfmaMaxSlots = 2;
 
 }  // namespace ponni_hip

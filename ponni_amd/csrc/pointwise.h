@@ -189,4 +189,33 @@ __host__ __device__ inline T apply_step(int act, T x, T bias, T a, T b) {
   }
 }
 
+// ---- activations on the hardware transcendentals -------------------------
+// The generated FUSED and NARROW kernels evaluate the logistic family through
+// v_exp_f32 and v_rcp_f32 (2^x and 1/x, about 1 ulp each), branch-free.  Each is the same
+// function as the reference formula it replaces, rewritten with
+// sigmoid(t) = 1 / (1 + 2^(-t log2 e)); the results differ from the
+// reference's libm-based evaluation by a few fp32 ulp relative to the
+// quantities that are summed later (tanh near 0 carries ~1e-7 absolute,
+// not relative, error, which is what 1 + tanh, the GELU and the next dense
+// layer see).  Saturation comes out of 2^x -> inf / 0 and 1/inf = 0.
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ inline float fast_sigmoid(float t) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * t));
+}
+// ponni_Sigmoid.h:45-49
+__device__ inline float act_sigmoid_fast(float x) { return fast_sigmoid(x); }
+// ponni_Silu.h:45-49: x * sigmoid(x)
+__device__ inline float act_silu_fast(float x) { return x * fast_sigmoid(x); }
+// ponni_Tanh.h:44: tanh(x) = 1 - 2 / (1 + 2^(2 x log2 e))
+__device__ inline float act_tanh_fast(float x) {
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.0f * kLog2e * x)), 1.0f);
+}
+// ponni_Gelu.h:48-53: 0.5 x (1 + tanh(u)) = x sigmoid(2u),
+// u = sqrt(2/pi) (x + 0.044715 x^3)
+__device__ inline float act_gelu_tanh_fast(float x) {
+  float const u = 0.79788456080286535588f * (x + 0.044715f * (x * x * x));
+  return x * fast_sigmoid(2.0f * u);
+}
+
 }  // namespace ponni_hip

@@ -158,7 +158,10 @@ class Inference:
     def __del__(self):
         plan = getattr(self, "_plan", None)
         if plan is not None and plan.value:
-            A.lib().ponni_plan_destroy(plan)
+            try:
+                A.lib().ponni_plan_destroy(plan)
+            except (AttributeError, TypeError):  # interpreter shutdown: the module is gone
+                pass
             self._plan = None
 
     # -- parameters -----------------------------------------------------------

@@ -93,3 +93,27 @@ def test_random_graphs_half(cuda, seed):
     got, xg = run_model(gm, x, half=True)
     xh = xg.astype(np.float16).astype(np.float64)
     check_half(got, oracle.forward(lowered_with_params(gr), xh, oracle.MODE_F16_OPERANDS), 4e-3)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("seed", range(12))
+def test_random_narrow_graphs(cuda, seed, dtype):
+    """Generated graphs of width <= 16 on generated NARROW kernels (graph
+    operations inline, one lane per sample group) against the oracle."""
+    gr = random_graph(200 + seed, narrow=True)
+    gm = G.GeneratedModel(gr, path="narrow")
+    try:
+        plan = gm.plan(dtype)
+    except P.PonniError as e:
+        if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+            pytest.skip(e.message)
+        raise
+    assert plan.path == "narrow"
+    B = [1, 63, 1025, 4096, 4099, 777][seed % 6]
+    x = np.random.default_rng(300 + seed).standard_normal((gr.size(gr.inputs[0]), B))
+    got, xg = run_model(gm, x, half=dtype == "f16")
+    if dtype == "f32":
+        check_f32(got, oracle.forward(lowered_with_params(gr), xg))
+    else:
+        xh = xg.astype(np.float16).astype(np.float64)
+        check_half(got, oracle.forward(lowered_with_params(gr), xh, oracle.MODE_F16_OPERANDS), 4e-3)

@@ -153,11 +153,13 @@ ELEMENTWISE = ["Relu", "Sigmoid", "Tanh", "LeakyRelu", "Elu", "Gelu", "Silu", "S
                "HardSwish", "Mish", "Abs", "Neg", "Softsign", "Celu", "Erf", "Selu", "ThresholdedRelu"]
 
 
-def random_graph(seed: int, aligned: bool = False, n_in: int | None = None, nodes: int = 14, dtype="float32"):
+def random_graph(seed: int, aligned: bool = False, n_in: int | None = None, nodes: int = 14, dtype="float32",
+                 narrow: bool = False):
     """A random DAG over the supported operations.  aligned: every width a
-    multiple of 16 (what the FUSED concatenation needs)."""
+    multiple of 16 (what the FUSED concatenation needs); narrow: every width
+    at most 16 (what the NARROW kernels take)."""
     rng = np.random.default_rng(seed)
-    widths = [16, 32, 48] if aligned else [1, 3, 5, 8, 13, 16, 24, 33]
+    widths = [16, 32, 48] if aligned else [1, 3, 5, 8, 12, 16] if narrow else [1, 3, 5, 8, 13, 16, 24, 33]
     n_in = n_in or int(rng.choice(widths[1:] if aligned else widths[2:]))
     g = G.GraphBuilder(n_in, dtype=dtype)
     pool = [g.input]
@@ -197,7 +199,7 @@ def random_graph(seed: int, aligned: bool = False, n_in: int | None = None, node
             parts = [t, others[int(rng.integers(len(others)))]]
             if rng.random() < 0.5:
                 parts.reverse()
-            if sum(g.size(p) for p in parts) > (256 if aligned else 96):
+            if sum(g.size(p) for p in parts) > (256 if aligned else 16 if narrow else 96):
                 continue
             out = g.concat(*parts)
         elif r < 0.87:
@@ -389,3 +391,23 @@ def test_dead_nodes_dropped():
     g.dense(g.input, np.ones((7, 4)), None, name="unused")
     lw = G.lower_graph(g.finish(y))
     assert [l.label for l in lw.layers] == ["ReLU"]
+
+
+def test_narrow_generated_graphs_take_the_narrow_path():
+    """Generated graphs of width <= 16 run generated NARROW kernels (one lane
+    per sample group, graph operations inline); wider ones stay FUSED."""
+    from tests.golden.make_generated_fixtures import tiny_graph
+
+    src = G.GeneratedModel(tiny_graph()).plan("f32").kernel_source()
+    assert "ponni_narrow_3x4x2" in src and src.count("dense_bias<") == 2
+    seen = set()
+    for seed in range(12):
+        gm = G.GeneratedModel(random_graph(seed, narrow=True))
+        plan = gm.plan("f32")
+        assert plan.path in ("narrow", "fused"), plan.path
+        if plan.path == "narrow":
+            text = plan.kernel_source()
+            seen.update(op for op in ("binary<", "reduce<", "copy<", "softmax<", "layer_norm<", "concat<")
+                        if op in text)
+    assert {"binary<", "reduce<"} <= seen, seen
+    assert G.GeneratedModel(C.c5_graph(False)).plan("f32").path == "fused"
