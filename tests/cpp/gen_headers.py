@@ -1,6 +1,7 @@
 """Writes the generated-model headers the C++ tests compile
-(tests/cpp/gen/*.h): the c5 graph with nonzero biases as class C5Model and
-the tiny 3 -> 4 -> 2 graph of tests/golden as class TinyModel."""
+(tests/cpp/gen/*.h): the c5 graph with nonzero biases as class C5Model
+(FUSED kernels) and the tiny 3 -> 4 -> 2 graph of tests/golden as class
+TinyModel (generated NARROW kernels)."""
 import os
 import sys
 
