@@ -43,6 +43,13 @@ std::string flit(float v) {
   return std::string(buf) + "f";
 }
 
+// A double literal, exact (F64 plans keep every attribute in double).
+std::string dlit(double v) {
+  char buf[64];
+  std::snprintf(buf, sizeof(buf), "%a", v);
+  return buf;
+}
+
 // Steps that keep a zero padding row at zero (padded parameter entries are 0).
 bool zero_at_zero(int act) {
   switch (act) {
@@ -86,8 +93,8 @@ std::string const_expr(int act) {
     case ACT_RMIN_C: return "c < v ? c : v";
     case ACT_MAX_C: return "v > c ? v : c";
     case ACT_RMAX_C: return "c > v ? c : v";
-    case ACT_POW_C: return "powf(v, c)";
-    default: return "powf(c, v)";
+    case ACT_POW_C: return "d_pow(v, c)";
+    default: return "d_pow(c, v)";
   }
 }
 
@@ -104,32 +111,35 @@ std::string binary_expr(int op) {
   }
 }
 
-std::string act_expr(Step const& s) {
+// The step's activation on v (float, or double when dbl), in the reference
+// formulas of pointwise.h.
+std::string act_expr(Step const& s, bool dbl = false) {
+  auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
   switch (s.act) {
     case ACT_RELU: return "act_relu(v)";
-    case ACT_LEAKY_RELU: return "act_leaky_relu(v, " + flit(s.a) + ")";
-    case ACT_ELU: return "act_elu(v, " + flit(s.a) + ")";
+    case ACT_LEAKY_RELU: return "act_leaky_relu(v, " + lit(s.a) + ")";
+    case ACT_ELU: return "act_elu(v, " + lit(s.a) + ")";
     case ACT_SELU: return "act_selu(v)";
     case ACT_GELU_ERF: return "act_gelu_erf(v)";
     case ACT_GELU_TANH: return "act_gelu_tanh(v)";
     case ACT_SILU: return "act_silu(v)";
     case ACT_SIGMOID: return "act_sigmoid(v)";
     case ACT_TANH: return "act_tanh(v)";
-    case ACT_SOFTPLUS: return "act_softplus(v, " + flit(s.a) + ")";
-    case ACT_HARD_SIGMOID: return "act_hard_sigmoid(v, " + flit(s.a) + ", " + flit(s.b) + ")";
+    case ACT_SOFTPLUS: return "act_softplus(v, " + lit(s.a) + ")";
+    case ACT_HARD_SIGMOID: return "act_hard_sigmoid(v, " + lit(s.a) + ", " + lit(s.b) + ")";
     case ACT_HARD_SWISH: return "act_hard_swish(v)";
     case ACT_MISH: return "act_mish(v)";
-    case ACT_ABS: return "fabsf(v)";
+    case ACT_ABS: return "d_abs(v)";
     case ACT_NEG: return "-v";
-    case ACT_EXP: return "expf(v)";
-    case ACT_LOG: return "logf(v)";
-    case ACT_SQRT: return "sqrtf(v)";
-    case ACT_RECIPROCAL: return "1.0f / v";
+    case ACT_EXP: return "d_exp(v)";
+    case ACT_LOG: return "d_log(v)";
+    case ACT_SQRT: return "d_sqrt(v)";
+    case ACT_RECIPROCAL: return "1 / v";
     case ACT_SOFTSIGN: return "act_softsign(v)";
-    case ACT_CELU: return "act_celu(v, " + flit(s.a) + ")";
-    case ACT_THRESHOLDED_RELU: return "act_thresholded_relu(v, " + flit(s.a) + ")";
-    case ACT_ERF: return "erff(v)";
-    case ACT_SELU_AG: return "act_selu_ag(v, " + flit(s.a) + ", " + flit(s.b) + ")";
+    case ACT_CELU: return "act_celu(v, " + lit(s.a) + ")";
+    case ACT_THRESHOLDED_RELU: return "act_thresholded_relu(v, " + lit(s.a) + ")";
+    case ACT_ERF: return "d_erf(v)";
+    case ACT_SELU_AG: return "act_selu_ag(v, " + lit(s.a) + ", " + lit(s.b) + ")";
     default: return "v";
   }
 }
@@ -709,7 +719,7 @@ namespace {
 
 int narrow_samples_per_lane(ponni_plan_s const& p) {
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
-  if (p.width_class >= 16) return 2;
+  if (p.dtype == PONNI_F64 || p.width_class >= 16) return 2;
   if (p.width_class >= 8) return 4;
   return half ? 8 : 4;
 }
@@ -717,7 +727,10 @@ int narrow_samples_per_lane(ponni_plan_s const& p) {
 std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   int const W = p.width_class;
   int const V = narrow_samples_per_lane(p);
-  std::string const S = p.dtype == PONNI_F16 ? "_Float16" : p.dtype == PONNI_BF16 ? "__bf16" : "float";
+  bool const dbl = p.dtype == PONNI_F64;
+  std::string const S = p.dtype == PONNI_F16 ? "_Float16" : p.dtype == PONNI_BF16 ? "__bf16" : dbl ? "double" : "float";
+  std::string const R = dbl ? "double" : "float";  // compute type
+  auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
   // U groups of V samples per lane, 256 * V samples apart, so that all of a
   // lane's input rows are in flight before its first FMA.
   int U = 1;
@@ -734,20 +747,22 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   auto finish = [&](int n) { return "    finish<S, " + std::to_string(V) + ", " + std::to_string(n) + WV; };
   std::ostringstream o;
   o << "// generated by libponni_hip for one plan (NARROW)\n#include \"narrow_jit.h\"\n";
-  o << "using namespace ponni_hip;\nusing namespace ponni_hip::narrowj;\ntypedef " << S << " S;\n";
+  o << "using namespace ponni_hip;\nusing namespace ponni_hip::narrowj;\ntypedef " << S << " S;\ntypedef " << R
+    << " real;\n";
   // The chain on one group of V samples.
-  o << "__device__ inline void chain(float (&s)[" << W << "][" << V << "], float const* __restrict__ P) {\n";
+  o << "__device__ inline void chain(real (&s)[" << W << "][" << V << "], real const* __restrict__ P) {\n";
   for (int sl = 0; sl < p.num_slots; sl++)
-    o << "  float sv" << sl << "[" << W << "][" << V << "] = {};\n";
+    o << "  real sv" << sl << "[" << W << "][" << V << "] = {};\n";
   int cur_n = p.layers.front().n_in;
   auto steps = [&](std::string const& a, int n, int begin, int count) {
     for (int k = 0; k < count; k++) {
       Step const& st = p.steps[begin + k];
       if (act_has_param(st.act))
-        o << "    with_vec" << tv(n) << "(" << a << ", P + " << st.off << ", [](float v, float c) { return "
+        o << "    with_vec" << tv(n) << "(" << a << ", P + " << st.off << ", [](real v, real c) { return "
           << const_expr(st.act) << "; });\n";
       else
-        o << "    map" << tv(n) << "(" << a << ", [](float v) { return " << act_fast_expr(st) << "; });\n";
+        o << "    map" << tv(n) << "(" << a << ", [](real v) { return " << (dbl ? act_expr(st, true) : act_fast_expr(st))
+          << "; });\n";
     }
   };
   for (Op const& op : p.ops) {
@@ -758,7 +773,7 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         // generated Dense's bias (its first step) seeds the sum.
         int const K = op.n_in, N = op.n_out;
         bool const seed = op.aux & DENSE_BIAS_FIRST;
-        o << "    float a[" << W << "][" << V << "];\n";
+        o << "    real a[" << W << "][" << V << "];\n";
         if (seed)
           o << "    dense_bias<" << V << ", " << K << ", " << N << WV << "(a, s, P + " << op.woff << ", P + "
             << p.steps[op.epi_begin].off << ");\n";
@@ -785,8 +800,8 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         o << finish(op.n_out) << "(s, s);\n";
         break;
       case OP_LAYER_NORM:
-        o << "    layer_norm" << tv(cur_n) << "(s, P + " << op.woff << ", P + " << op.boff << ", " << flit(op.f0)
-          << ");\n";
+        o << "    layer_norm" << tv(cur_n) << "(s, P + " << op.woff << ", P + " << op.boff << ", real(" << lit(op.f0)
+          << "));\n";
         o << finish(op.n_out) << "(s, s);\n";
         break;
       case OP_SOFTMAX:
@@ -796,7 +811,8 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         o << finish(op.n_out) << "(s, s);\n";
         break;
       case OP_MIN_MAX:
-        o << "    min_max" << tv(cur_n) << "(s, " << flit(op.f0) << ", " << flit(op.f1) << ", " << flit(op.f2) << ");\n";
+        o << "    min_max" << tv(cur_n) << "(s, real(" << lit(op.f0) << "), real(" << lit(op.f1) << "), real(" << lit(op.f2)
+          << "));\n";
         o << finish(op.n_out) << "(s, s);\n";
         break;
       case OP_SAVE:
@@ -829,7 +845,7 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   }
   o << "}\n";
   o << "extern \"C\" __global__ __launch_bounds__(256) void " << fused_kernel_name(p)
-    << "(float const* __restrict__ P, S const* __restrict__ x, int64_t ldx, S* __restrict__ y, int64_t ldy, "
+    << "(real const* __restrict__ P, S const* __restrict__ x, int64_t ldx, S* __restrict__ y, int64_t ldy, "
        "int64_t batch) {\n";
   o << "  constexpr int U = " << U << ", V = " << V << ";\n";
   o << "  bool const aligned = vec_ok<S, V>(x, ldx) && vec_ok<S, V>(y, ldy);\n";
@@ -837,14 +853,14 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   // views take a path with no per-lane predicate, so every load is issued
   // before the first wait.
   o << "  if (aligned && (int64_t(blockIdx.x) + 1) * (U * 256 * V) <= batch) {\n";
-  o << "    float s[U][" << W << "][V];\n";
+  o << "    real s[U][" << W << "][V];\n";
   o << "#pragma unroll\n    for (int u = 0; u < U; u++)\n      load<S, V, " << p.layers.front().n_in << WV
     << "(s[u], x, ldx, ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V, batch, true);\n";
   o << "#pragma unroll\n    for (int u = 0; u < U; u++) chain(s[u], P);\n";
   o << "#pragma unroll\n    for (int u = 0; u < U; u++)\n      store<S, V, " << p.layers.back().n_out << WV
     << "(s[u], y, ldy, ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V, batch, true);\n";
   o << "    return;\n  }\n";
-  o << "  float s[U][" << W << "][V];\n";
+  o << "  real s[U][" << W << "][V];\n";
   o << "  int64_t b0[U];\n";
   o << "#pragma unroll\n  for (int u = 0; u < U; u++) {\n";
   o << "    b0[u] = ((int64_t(blockIdx.x) * U + u) * 256 + threadIdx.x) * V;\n";
@@ -861,7 +877,7 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
 std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg) { return narrow_source(p, cfg); }
 
 bool narrow_jit_supports(ponni_plan_s const& p) {
-  if (p.path != PONNI_PATH_NARROW || p.width_class <= 0 || p.dtype == PONNI_F64) return false;
+  if (p.path != PONNI_PATH_NARROW || p.width_class <= 0) return false;
   if (p.num_slots > kNarrowJitMaxSlots) return false;
   for (Op const& op : p.ops)
     if (op.code == OP_EXTERNAL) return false;

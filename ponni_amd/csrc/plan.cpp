@@ -817,15 +817,17 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     path = PONNI_PATH_GENERIC;
   }
   // The interpreted NARROW and MFMA kernels run layer-template chains only;
-  // generated NARROW kernels (run-time compilation) also run graph operations.
+  // generated NARROW kernels (run-time compilation) also run graph operations
+  // and F64.
   int const narrow_w = narrow_width_class(max_width);
   int const narrow = graph_ops ? 0 : narrow_w;
   int const mfma = graph_ops ? 0 : mfma_width_class(dtype, max_width);
   char const* jit_env = std::getenv("PONNI_JIT");
   bool const jit_enabled = jit_env == nullptr || std::strcmp(jit_env, "0") != 0;
   bool const narrow_interp_ok = dtype != PONNI_F64 && narrow > 0 && p->num_slots <= kNarrowMaxSlots;
-  bool const narrow_gen_ok = jit_enabled && dtype != PONNI_F64 && narrow_w > 0 && !p->external &&
-                             p->num_slots <= kNarrowJitMaxSlots;
+  bool const narrow_gen_ok = jit_enabled && narrow_w > 0 && !p->external && p->num_slots <= kNarrowJitMaxSlots;
+  // Plans only a generated NARROW kernel can run need run-time compilation.
+  bool const narrow_ok = narrow_interp_ok || ((graph_ops || dtype == PONNI_F64) && narrow_gen_ok);
   // Between widths 9 and 16 the generated NARROW kernel (scalar FMAs, one
   // lane per sample group) beats FUSED (16-wide MFMA tiles) while the chain
   // does fewer than 10 multiply-adds per byte of input and output; beyond
@@ -838,22 +840,20 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   }
   double const io_bytes = double(layers[0].n_in + layers[num_layers - 1].n_out) * (dtype == PONNI_F32 ? 4 : 2);
   bool const narrow_light = macs < 10.0 * io_bytes;
-  bool const narrow_jit_ok = jit_enabled && narrow_light && (graph_ops ? narrow_gen_ok : narrow_interp_ok);
   int chosen = path;
   if (chosen == PONNI_PATH_AUTO) {
     if (narrow_interp_ok && max_width <= 8) chosen = PONNI_PATH_NARROW;
-    else if (narrow_jit_ok) chosen = PONNI_PATH_NARROW;
+    else if (jit_enabled && narrow_ok && narrow_light) chosen = PONNI_PATH_NARROW;
     else if (jit_enabled && fused_supports(*p)) chosen = PONNI_PATH_FUSED;
-    else if (graph_ops && narrow_gen_ok) chosen = PONNI_PATH_NARROW;
-    else if (narrow_interp_ok) chosen = PONNI_PATH_NARROW;
+    else if (narrow_ok) chosen = PONNI_PATH_NARROW;
     else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
     else chosen = PONNI_PATH_GENERIC;
   } else if (chosen == PONNI_PATH_NARROW) {
-    if (!narrow_interp_ok && !(graph_ops && narrow_gen_ok)) {
+    if (!narrow_ok) {
       delete p;
       return fail(PONNI_ERR_UNSUPPORTED,
-                  "NARROW path needs F32/F16/BF16, width <= 16, and a layer-template chain with at most 2 saved "
-                  "states or (with run-time compilation) a generated graph with at most 4");
+                  "NARROW path needs width <= 16 and a layer-template chain in F32/F16/BF16 with at most 2 saved "
+                  "states, or (with run-time compilation) F64 or a generated graph with at most 4");
     }
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {

@@ -117,3 +117,23 @@ def test_random_narrow_graphs(cuda, seed, dtype):
     else:
         xh = xg.astype(np.float16).astype(np.float64)
         check_half(got, oracle.forward(lowered_with_params(gr), xh, oracle.MODE_F16_OPERANDS), 4e-3)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_narrow_graphs_f64(cuda, seed):
+    """F64 generated graphs of width <= 16 on generated NARROW kernels (double
+    state) against the oracle's fp64 mode."""
+    import torch
+
+    gr = random_graph(400 + seed, narrow=True, dtype="float64")
+    gm = G.GeneratedModel(gr)
+    assert gm.plan().path == "narrow"
+    B = [1, 63, 1025, 4096, 4099, 777][seed]
+    x = np.random.default_rng(500 + seed).standard_normal((gr.size(gr.inputs[0]), B))
+    xt = torch.from_numpy(x).cuda()
+    y = torch.full((gm.num_outputs, B), float("nan"), dtype=torch.float64, device="cuda:0")
+    gm.infer_batch(xt, y)
+    torch.cuda.synchronize()
+    want = oracle.forward(lowered_with_params(gr), x, oracle.MODE_F64)
+    got = y.cpu().numpy()
+    assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * max(1.0, np.abs(want).max())), np.abs(got - want).max()

@@ -164,6 +164,26 @@ def test_f64_generic(cuda, seed, width, blocks):
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_f64_narrow(cuda, seed):
+    """F64 chains of width <= 16 on the generated NARROW kernel (double state,
+    exact attributes) against the oracle's fp64 mode."""
+    rng = np.random.default_rng(700 + seed)
+    width = [3, 8, 13, 16, 5, 7, 12, 16][seed]
+    layers = K.random_chain(rng, width, 2 + seed % 3)
+    try:
+        m = P.create_inference_model(*layers, dtype="f64", path="narrow")
+    except P.PonniError as e:
+        if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+            pytest.skip(e.message)
+        raise
+    assert m.path == "narrow"
+    B = [1, 257, 4099, 1000, 64, 3001, 4096, 77][seed]
+    got, xg, _ = gpu_run(layers, rng.standard_normal((width, B)), dtype="f64", path="narrow", pad=seed % 2)
+    want = oracle.forward(layers, xg, oracle.MODE_F64)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * max(1.0, np.abs(want).max())), np.abs(got - want).max()
+
+
 def config_input(cfg, B, dev="cuda:0"):
     import torch
 
