@@ -1,10 +1,12 @@
 // Generated-model headers (tests/cpp/gen/*.h, written by ponni_amd.emitter):
-// C5Model (the c5 graph) and TinyModel (a 3 -> 4 -> 2 graph).  For the chosen model: load the weights file, run infer_batch
+// C5Model (the c5 graph), TinyModel (a 3 -> 4 -> 2 graph) and F64Model (a
+// double-precision narrow graph).  For the chosen model: load the weights file, run infer_batch
 // (the header's ahead-of-time kernel), infer_batch_half2 and infer_one (an
 // application kernel over device()); then read the learned parameters, halve
 // them through a device view, run infer_batch and infer_one again and save
 // the parameters.  tests/test_cpp.py compares every output.
-//   test_generated <c5|tiny> <weights.ponni> <x.f32 [num_inputs, B]> <B> <out_dir>
+// Arrays on disk are raw Model::Scalar values (float, or double for F64Model).
+//   test_generated <c5|tiny|f64> <weights.ponni> <x.bin [num_inputs, B]> <B> <out_dir>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -12,36 +14,40 @@
 #include <vector>
 
 #include "gen/c5_model.h"
+#include "gen/f64_model.h"
 #include "gen/tiny_model.h"
 
 template <class Model>
-__global__ void infer_one_kernel(typename Model::Device m, float const* x, std::int64_t ldx, float* y,
-                                 std::int64_t ldy, int batch) {
+__global__ void infer_one_kernel(typename Model::Device m, typename Model::Scalar const* x, std::int64_t ldx,
+                                 typename Model::Scalar* y, std::int64_t ldy, int batch) {
   int const b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
-  ponni::SArray<float, Model::num_inputs> in;
-  ponni::SArray<float, Model::num_outputs> out;
+  ponni::SArray<typename Model::Scalar, Model::num_inputs> in;
+  ponni::SArray<typename Model::Scalar, Model::num_outputs> out;
   for (int f = 0; f < Model::num_inputs; f++) in(f) = x[f * ldx + b];
   m.infer_one(in, out);
   for (int f = 0; f < Model::num_outputs; f++) y[f * ldy + b] = out(f);
 }
 
-static std::vector<float> read_f32(char const* path, std::size_t n) {
-  std::vector<float> v(n);
+template <class T>
+static std::vector<T> read_raw(char const* path, std::size_t n) {
+  std::vector<T> v(n);
   FILE* f = std::fopen(path, "rb");
-  if (!f || std::fread(v.data(), sizeof(float), n, f) != n) ponni::abort(std::string("cannot read ") + path);
+  if (!f || std::fread(v.data(), sizeof(T), n, f) != n) ponni::abort(std::string("cannot read ") + path);
   std::fclose(f);
   return v;
 }
 
-static void write_f32(std::string const& path, std::vector<float> const& v) {
+template <class T>
+static void write_raw(std::string const& path, std::vector<T> const& v) {
   FILE* f = std::fopen(path.c_str(), "wb");
-  if (!f || std::fwrite(v.data(), sizeof(float), v.size(), f) != v.size()) ponni::abort("cannot write " + path);
+  if (!f || std::fwrite(v.data(), sizeof(T), v.size(), f) != v.size()) ponni::abort("cannot write " + path);
   std::fclose(f);
 }
 
 template <class Model>
 int run(char const* weights, char const* xpath, int B, std::string const& dir) {
+  using T = typename Model::Scalar;
   Model m;
   std::string err;
   if (m.weights_loaded() || m.parameters_are_finite() || m.save_parameters(dir + "/early.ponni", &err)) {
@@ -56,9 +62,9 @@ int run(char const* weights, char const* xpath, int B, std::string const& dir) {
     std::fprintf(stderr, "load_weights: %s\n", err.c_str());
     return 1;
   }
-  ponni::View<float> x("x", Model::num_inputs, B);
-  x.copy_from_host(read_f32(xpath, std::size_t(Model::num_inputs) * B));
-  ponni::View<float> y("y", Model::num_outputs, B), yh("yh", Model::num_outputs, B), y1("y1", Model::num_outputs, B);
+  ponni::View<T> x("x", Model::num_inputs, B);
+  x.copy_from_host(read_raw<T>(xpath, std::size_t(Model::num_inputs) * B));
+  ponni::View<T> y("y", Model::num_outputs, B), yh("yh", Model::num_outputs, B), y1("y1", Model::num_outputs, B);
   auto one = [&] {
     hipLaunchKernelGGL(infer_one_kernel<Model>, dim3((B + 127) / 128), dim3(128), 0, 0, m.device(), x.data(),
                        x.stride(0), y1.data(), y1.stride(0), B);
@@ -67,22 +73,22 @@ int run(char const* weights, char const* xpath, int B, std::string const& dir) {
   m.infer_batch(x, y);
   m.infer_batch_half2(x, yh);
   if (!one()) return 1;
-  write_f32(dir + "/y_batch.f32", y.copy_to_host());
-  write_f32(dir + "/y_half.f32", yh.copy_to_host());
-  write_f32(dir + "/y_one.f32", y1.copy_to_host());
+  write_raw(dir + "/y_batch.bin", y.copy_to_host());
+  write_raw(dir + "/y_half.bin", yh.copy_to_host());
+  write_raw(dir + "/y_one.bin", y1.copy_to_host());
   if (!m.weights_loaded() || !m.parameters_are_finite() || !m.parameters_synchronized()) return 1;
 
-  std::vector<float> p(Model::get_num_parameters());
+  std::vector<T> p(Model::get_num_parameters());
   m.get_parameters(p);
-  write_f32(dir + "/params.f32", p);
-  for (float& v : p) v *= 0.5f;
-  ponni::View<float> pv("p", 1, Model::get_num_parameters());
+  write_raw(dir + "/params.bin", p);
+  for (T& v : p) v *= T(0.5);
+  ponni::View<T> pv("p", 1, Model::get_num_parameters());
   pv.copy_from_host(p);
   m.set_parameters(pv);
   m.infer_batch(x, y);
   if (!one()) return 1;
-  write_f32(dir + "/y_batch_scaled.f32", y.copy_to_host());
-  write_f32(dir + "/y_one_scaled.f32", y1.copy_to_host());
+  write_raw(dir + "/y_batch_scaled.bin", y.copy_to_host());
+  write_raw(dir + "/y_one_scaled.bin", y1.copy_to_host());
   if (!m.save_parameters(dir + "/saved.ponni", &err)) {
     std::fprintf(stderr, "save_parameters: %s\n", err.c_str());
     return 1;
@@ -93,12 +99,13 @@ int run(char const* weights, char const* xpath, int B, std::string const& dir) {
 
 int main(int argc, char** argv) {
   if (argc != 6) {
-    std::fprintf(stderr, "usage: %s c5|tiny weights.ponni x.f32 batch out_dir\n", argv[0]);
+    std::fprintf(stderr, "usage: %s c5|tiny|f64 weights.ponni x.bin batch out_dir\n", argv[0]);
     return 2;
   }
   int const B = std::atoi(argv[4]);
   if (std::strcmp(argv[1], "c5") == 0) return run<ponni::generated::C5Model>(argv[2], argv[3], B, argv[5]);
   if (std::strcmp(argv[1], "tiny") == 0) return run<ponni::generated::TinyModel>(argv[2], argv[3], B, argv[5]);
+  if (std::strcmp(argv[1], "f64") == 0) return run<ponni::generated::F64Model>(argv[2], argv[3], B, argv[5]);
   std::fprintf(stderr, "unknown model %s\n", argv[1]);
   return 2;
 }

@@ -81,48 +81,50 @@ def test_emitted_header_text(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("model", ["c5", "tiny"])
+@pytest.mark.parametrize("model", ["c5", "tiny", "f64"])
 def test_generated_header_on_gpu(cuda, tmp_path, model):
     """tests/cpp/test_generated.cpp over an emitted header: infer_batch
     (the ahead-of-time kernel), infer_batch_half2 and infer_one (an
     application kernel over device()) against the CPU oracle, on a weights
-    file saved by the Python model (c5) or written by the reference
+    file saved by the Python model (c5, f64) or written by the reference
     generator (tiny, tests/golden/tiny_generated.ponni); then the parameter
     API (get, set from a device view, save) against the Python model.  fp32
-    bar: relative L2 <= 1e-5 and max-abs <= 1e-4; fp16: relative L2 <= 2e-3
-    against fp16 operands."""
+    bar: relative L2 <= 1e-5 and max-abs <= 1e-4; fp64: 1e-11; fp16: relative
+    L2 <= 2e-3 against fp16 operands."""
     import numpy as np
 
     import oracle
     from ponni_amd import configs as C
     from ponni_amd import graph as G
+    from tests.cpp.gen_headers import f64_graph
     from tests.golden.make_generated_fixtures import tiny_graph
     from tests.test_gpu_parity import check_f32, check_half
 
     if not os.path.exists(GEN_BIN):
         pytest.fail(f"{GEN_BIN} is missing: build with `python -c 'import __graft_entry__ as g; g.build()'`")
     oracle.build()
-    make_graph = (lambda: C.c5_graph(True)) if model == "c5" else tiny_graph
-    if model == "c5":
+    make_graph = {"c5": lambda: C.c5_graph(True), "tiny": tiny_graph, "f64": f64_graph}[model]
+    if model == "tiny":
+        weights = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_generated.ponni")
+    else:
         gm = G.GeneratedModel(make_graph())
         gm.storage = gm.storage * 0.5 + np.random.default_rng(11).uniform(-0.05, 0.05, gm.storage.size)
-        weights = tmp_path / "c5.ponni"
+        weights = tmp_path / "w.ponni"
         gm.save_parameters(str(weights))
-    else:
-        weights = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_generated.ponni")
     ref = G.GeneratedModel(make_graph())
-    ref.load_weights(str(weights))  # the values the file holds (fp32)
+    ref.load_weights(str(weights))  # the values the file holds
+    dt = np.float64 if ref.scalar == "f64" else np.float32
     n_in, n_out = ref.num_inputs, ref.num_outputs
     B = 4099
-    x = np.random.default_rng(12).standard_normal((n_in, B)).astype(np.float32)
-    x.tofile(tmp_path / "x.f32")
-    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.f32"), str(B), str(tmp_path)],
+    x = np.random.default_rng(12).standard_normal((n_in, B)).astype(dt)
+    x.tofile(tmp_path / "x.bin")
+    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.bin"), str(B), str(tmp_path)],
                        capture_output=True, text=True, timeout=300)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
 
     def out(name):
-        return np.fromfile(tmp_path / name, dtype=np.float32).reshape(n_out, B).astype(np.float64)
+        return np.fromfile(tmp_path / name, dtype=dt).reshape(n_out, B).astype(np.float64)
 
     def oracle_layers(m):
         layers = m.lowered.layers
@@ -131,18 +133,26 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
                 l.params = v
         return layers
 
-    want = oracle.forward(oracle_layers(ref), x.astype(np.float64))
-    check_f32(out("y_batch.f32"), want, scale_tol=False)
-    check_f32(out("y_one.f32"), want, scale_tol=False)
-    xh = x.astype(np.float16).astype(np.float64)
-    check_half(out("y_half.f32"), oracle.forward(oracle_layers(ref), xh, oracle.MODE_F16_OPERANDS))
+    def check(got, want):
+        if dt == np.float64:
+            assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * max(1.0, np.abs(want).max()))
+        else:
+            check_f32(got, want, scale_tol=False)
+
+    mode = oracle.MODE_F64 if dt == np.float64 else oracle.MODE_F32
+    want = oracle.forward(oracle_layers(ref), x.astype(np.float64), mode)
+    check(out("y_batch.bin"), want)
+    check(out("y_one.bin"), want)
+    if model != "f64":  # (the random F64 graph's Exp / Div leave the fp16 range)
+        xh = x.astype(np.float16).astype(np.float64)
+        check_half(out("y_half.bin"), oracle.forward(oracle_layers(ref), xh, oracle.MODE_F16_OPERANDS), 4e-3)
 
     learned = ref.get_parameters()
-    np.testing.assert_array_equal(np.fromfile(tmp_path / "params.f32", dtype=np.float32), learned.astype(np.float32))
+    np.testing.assert_array_equal(np.fromfile(tmp_path / "params.bin", dtype=dt), learned.astype(dt))
     ref.set_parameters(learned * 0.5)
-    want = oracle.forward(oracle_layers(ref), x.astype(np.float64))
-    check_f32(out("y_batch_scaled.f32"), want, scale_tol=False)
-    check_f32(out("y_one_scaled.f32"), want, scale_tol=False)
+    want = oracle.forward(oracle_layers(ref), x.astype(np.float64), mode)
+    check(out("y_batch_scaled.bin"), want)
+    check(out("y_one_scaled.bin"), want)
     saved = G.GeneratedModel(make_graph())
     saved.load_weights(str(tmp_path / "saved.ponni"))
     np.testing.assert_array_equal(saved.storage, ref.storage)
