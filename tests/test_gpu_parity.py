@@ -267,6 +267,41 @@ def test_more_than_2_31_elements(cuda, name, B):
         check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
 
 
+@pytest.mark.parametrize("path", ["narrow", "fused", "generic", "mfma"])
+def test_hip_graph_capture_and_replay(cuda, path):
+    """After its first call for a batch size, a forward pass is one kernel
+    launch with no allocation, copy or memset, so callers can capture it in a
+    HIP graph.  Every replay, with new inputs written between replays, must
+    equal the eager result on the same inputs."""
+    import torch
+
+    rng = np.random.default_rng(21)
+    layers = C.c2_layers(True) if path != "narrow" else [P.Matvec(rng.uniform(-1, 1, (16, 12))),
+                                                         P.Bias(rng.uniform(-0.1, 0.1, 12)), P.Tanh(12),
+                                                         P.Matvec(rng.uniform(-1, 1, (12, 8)))]
+    m = make_model(layers, "f32", path)
+    B = 5003
+    x = torch.empty((16, B), device="cuda:0")
+    y = torch.empty((m.get_num_outputs(), B), device="cuda:0")
+    x.copy_(torch.from_numpy(rng.standard_normal((16, B))).float())
+    m.forward_batch_parallel(x, y)  # warm-up: upload, compile, scratch
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        m.forward_batch_parallel(x, y)
+    for r in range(3):
+        x.copy_(torch.from_numpy(rng.standard_normal((16, B))).float())
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = y.clone()
+        y.zero_()
+        m.forward_batch_parallel(x, y)
+        torch.cuda.synchronize()
+        assert torch.equal(got, y), f"replay {r} differs from the eager pass"
+    check_f32(got.double().cpu().numpy(), oracle.forward(layers, x.double().cpu().numpy()), scale_tol=False)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
