@@ -210,7 +210,6 @@ bool compile(std::string const& source, std::vector<char>& code, std::string& lo
 
 // Can the FUSED generator express this chain?
 bool fused_supports(ponni_plan_s const& p) {
-  if (p.dtype == PONNI_F64) return false;
   if (p.max_width > 256) return false;
   for (auto const& d : p.layers) {
     if (d.kind == PONNI_LAYER_BINOP_CONCATENATE) {
@@ -240,7 +239,13 @@ std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg);
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (p.path == PONNI_PATH_NARROW) return narrow_source_of(p, cfg);
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
+  bool const dbl = p.dtype == PONNI_F64;  // fp64 tiles (v_mfma_f64_16x16x4f64)
   std::string const E = p.dtype == PONNI_BF16 ? "__bf16" : "_Float16";
+  // Scalar and 4-vector types of the fp32 / fp64 tiles in emitted code (the
+  // 16-bit path's fp32 accumulators stay float).
+  std::string const F = half ? "float" : "real", F4 = half ? "floatx4" : "realx4";
+  int const es = dbl ? 8 : 4;  // packed parameter element bytes
+  auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
   // 16-column tiles per wave.  16-bit plans run two waves per SIMD (32
   // columns each) with A fragments staged through LDS (fused_f16.h dense_hs).
   int NT = 2;
@@ -256,7 +261,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       if (t >= 1 && t <= 4) half_wps = t;
     }
   }
-  int64_t const param_bytes = (p.packed_elements * 4 + 15) / 16 * 16;
+  int64_t const param_bytes = (p.packed_elements * es + 31) / 32 * 32;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   // The LDS tanh table is opt-in: its random 2-byte LDS reads contend with
   // the A-fragment reads of the workgroup's waves (measured slower than the
@@ -270,33 +275,34 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   // and its A-fragment ring.  Parameters small enough to live in registers
   // next to that state are loaded once per wave and reused for every tile.
   int worst = 0, worst_saved_regs = 0;
+  int const tr = dbl ? 16 : 8;  // registers per lane of one fp32 / fp64 tile (2 column tiles)
   {
     int cur = tiles(p.layers.front().n_in);
     std::map<int, int> slots;
     for (Op const& op : p.ops) {
       int saved_regs = 0;
-      for (auto const& kv : slots) saved_regs += kv.second * 8;
+      for (auto const& kv : slots) saved_regs += kv.second * tr;
       worst_saved_regs = std::max(worst_saved_regs, saved_regs);
-      int need = cur * 8;
+      int need = cur * tr;
       switch (op.code) {
         case OP_DENSE:
-          need = (tiles(op.n_in) + tiles(op.n_out)) * 8 + (half ? 16 + 2 * NT * 4 : tiles(op.n_in) * 4);
+          need = (tiles(op.n_in) + tiles(op.n_out)) * tr + (half ? 16 + 2 * NT * 4 : tiles(op.n_in) * tr / 2);
           cur = tiles(op.n_out);
           break;
-        case OP_PROJ_ADD: need = (cur + 2 * tiles(op.n_out)) * 8 + tiles(op.aux) * 4; break;
-        case OP_CONCAT: need = 2 * tiles(op.n_out) * 8; cur = tiles(op.n_out); break;
+        case OP_PROJ_ADD: need = (cur + 2 * tiles(op.n_out)) * tr + tiles(op.aux) * tr / 2; break;
+        case OP_CONCAT: need = 2 * tiles(op.n_out) * tr; cur = tiles(op.n_out); break;
         case OP_SAVE: slots[op.slot] = cur; break;
-        case OP_LOAD: cur = tiles(op.n_out); need = cur * 8; break;
-        case OP_BINARY: need = (cur + 2 * tiles(op.n_out)) * (half ? 16 : 8); cur = tiles(op.n_out); break;
-        case OP_REDUCE: need = cur * (half ? 16 : 8); cur = 1; break;
-        default: need = half ? cur * 16 : cur * 8; break;  // 16-bit states widen to fp32 for barriers
+        case OP_LOAD: cur = tiles(op.n_out); need = cur * tr; break;
+        case OP_BINARY: need = (cur + 2 * tiles(op.n_out)) * (half ? 16 : tr); cur = tiles(op.n_out); break;
+        case OP_REDUCE: need = cur * (half ? 16 : tr); cur = 1; break;
+        default: need = half ? cur * 16 : cur * tr; break;  // 16-bit states widen to fp32 for barriers
       }
       worst = std::max(worst, need + saved_regs);
     }
   }
   int const overhead = 32;
   int64_t const param_regs = (p.packed_elements + 63) / 64;
-  cfg.params_in_registers = !half && worst + overhead + param_regs <= 256;
+  cfg.params_in_registers = !half && !dbl && worst + overhead + param_regs <= 256;
   int regs = worst + overhead + (cfg.params_in_registers ? static_cast<int>(param_regs) : 0);
   if (cfg.params_in_registers) cfg.lds_bytes = 0;
   // Saved residuals move to LDS when that is what it takes to run two waves
@@ -304,7 +310,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (!half) {
     int saved_tiles = 0;
     for (int s = 0; s < kMaxSlots; s++) saved_tiles += tiles(p.saved_features[s]);
-    int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 16 * 4;  // per workgroup (4 waves)
+    int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 4 * es * 4;  // per workgroup (4 waves)
     if (regs + 32 > 256 && worst_saved_regs > 0 && regs - worst_saved_regs <= 224 &&
         cfg.lds_bytes + saved_bytes <= 80 * 1024) {
       cfg.saved_in_lds = true;
@@ -325,7 +331,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   {
     int saved_per_wave = 0;  // bytes of LDS-resident saved states per wave
     if (cfg.saved_in_lds)
-      for (int s = 0; s < kMaxSlots; s++) saved_per_wave += tiles(p.saved_features[s]) * NT * 64 * 16;
+      for (int s = 0; s < kMaxSlots; s++) saved_per_wave += tiles(p.saved_features[s]) * NT * 64 * 4 * es;
     int const target = 4 * cfg.waves_per_simd;  // waves per CU the registers allow
     int best = 0;
     for (int w = 4; w <= 16; w += 4) {
@@ -349,7 +355,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   cfg.columns_per_block = cfg.waves * 16 * NT;
 
   std::ostringstream o;
-  std::string const IO = half ? E : std::string("float");
+  std::string const IO = half ? E : dbl ? std::string("double") : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
   if (char const* d = std::getenv("PONNI_SETPRIO")) {  // tuning override
     int const v = std::atoi(d);
@@ -376,19 +382,20 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
   }
   if (half && std::getenv("PONNI_HALF_TILE_BARRIER")) o << "#define PONNI_TILE_BARRIER 1\n";  // tuning override
+  if (dbl) o << "#define PONNI_REAL double\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
   o << "extern \"C\" __global__ __launch_bounds__(" << 64 * cfg.waves << ", " << cfg.waves_per_simd << ") void "
     << fused_kernel_name(p)
-    << "(float const* __restrict__ gparams, " << IO << " const* __restrict__ x, int64_t ldx, " << IO
+    << "(" << F << " const* __restrict__ gparams, " << IO << " const* __restrict__ x, int64_t ldx, " << IO
     << "* __restrict__ y, int64_t ldy, int64_t batch) {\n";
   if (cfg.lds_bytes > 0) {
-    o << "  __shared__ floatx4 lds_p[" << cfg.lds_bytes / 16 << "];\n";
-    o << "  stage(lds_p, gparams, " << cfg.lds_bytes / 4 << ");\n";
-    o << "  float const* __restrict__ P0 = reinterpret_cast<float const*>(lds_p);\n";
+    o << "  __shared__ " << F4 << " lds_p[" << cfg.lds_bytes / (4 * es) << "];\n";
+    o << "  stage(lds_p, gparams, " << cfg.lds_bytes / es << ");\n";
+    o << "  " << F << " const* __restrict__ P0 = reinterpret_cast<" << F << " const*>(lds_p);\n";
   } else {
-    o << "  float const* __restrict__ P0 = gparams;\n";
+    o << "  " << F << " const* __restrict__ P0 = gparams;\n";
   }
   if (cfg.lut_bytes > 0) {
     o << "  __shared__ unsigned short lut_tanh[" << cfg.lut_bytes / 2 << "];\n";
@@ -413,7 +420,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "  __syncthreads();\n";
   }
   size_t dense_index = 0;
-  std::map<int, int> slot_off;  // slot -> floatx4 offset in the wave's LDS region
+  std::map<int, int> slot_off;  // slot -> 4-vector offset in the wave's LDS region
   if (cfg.saved_in_lds) {
     int off = 0;
     for (int sl = 0; sl < kMaxSlots; sl++)
@@ -421,8 +428,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         slot_off[sl] = off;
         off += tiles(p.saved_features[sl]) * NT * 64;
       }
-    o << "  __shared__ floatx4 lds_saved[" << cfg.waves << "][" << off << "];\n";
-    o << "  floatx4* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
+    o << "  __shared__ " << F4 << " lds_saved[" << cfg.waves << "][" << off << "];\n";
+    o << "  " << F4 << "* __restrict__ SV = lds_saved[threadIdx.x >> 6];\n";
   }
   // Per-feature vectors (biases, LayerNorm gamma / beta, constant operands)
   // of plans whose parameters stream from L2 are staged into LDS once per
@@ -472,7 +479,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o << "    L.col0 = (tile * " << cfg.waves << " + wave_id()) * " << 16 * NT << ";\n";
   // Register-resident parameters may be hoisted out of the tile loop; otherwise
   // pin() hides the pointer's loop invariance so they are re-read per tile.
-  o << (cfg.params_in_registers ? "    float const* __restrict__ P = P0;\n" : "    float const* __restrict__ P = pin(P0);\n");
+  o << "    " << F << " const* __restrict__ P = " << (cfg.params_in_registers ? "P0;\n" : "pin(P0);\n");
   int var = 0;
   auto fresh = [&]() { return "s" + std::to_string(var++); };
   std::string cur = fresh();
@@ -486,8 +493,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
-  // The logistic family runs on the hardware transcendentals (fused_f32.h).
-  auto act = [&](Step const& st) { return act_fast_expr(st); };
+  // The logistic family runs on the hardware transcendentals (pointwise.h),
+  // except in F64 plans, which keep the libm forms.
+  auto act = [&](Step const& st) { return dbl ? act_expr(st, true) : act_fast_expr(st); };
   // fp32 view of the state for barrier ops: the state itself (fp32 path) or a
   // widened copy that is rounded back afterwards (16-bit path).
   auto open32 = [&]() -> std::string {
@@ -505,11 +513,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       if (st.act == ACT_BIAS) {
         o << "    add_rows<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L);\n";
       } else if (act_has_param(st.act)) {
-        o << "    map_const<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L, [](float v, float c) { return "
+        o << "    map_const<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L, [](" << F << " v, " << F << " c) { return "
           << const_expr(st.act) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
       } else {
-        o << "    map<" << tiles(n) << ">(" << v << ", [](float v) { return " << act(st) << "; });\n";
+        o << "    map<" << tiles(n) << ">(" << v << ", [](" << F << " v) { return " << act(st) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
       }
     }
@@ -548,7 +556,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
           std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(" + vec(p.steps[op.epi_begin].off, n) + ", L)"
                                         : "zeros<" + std::to_string(tiles(n)) + ">()";
           o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
-            << op.woff << ", " << init << ", L, [&](int mo, floatx4 (&t)[" << NT << "]) {\n";
+            << op.woff << ", " << init << ", L, [&](int mo, " << F4 << " (&t)[" << NT << "]) {\n";
         }
         int const last = op.epi_count - (lut_tanh ? 1 : 0);
         for (int s = seed ? 1 : 0; s < last; s++) {
@@ -556,11 +564,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
           if (st.act == ACT_BIAS) {
             o << "      tile_add_rows(t, " << vec(st.off, n) << ", mo, L);\n";
           } else if (act_has_param(st.act)) {
-            o << "      tile_const(t, " << vec(st.off, n) << ", mo, L, [](float v, float c) { return " << const_expr(st.act)
+            o << "      tile_const(t, " << vec(st.off, n) << ", mo, L, [](" << F << " v, " << F << " c) { return " << const_expr(st.act)
               << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           } else {
-            o << "      tile_map(t, [](float v) { return " << act(st) << "; });\n";
+            o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
@@ -580,7 +588,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       case OP_LAYER_NORM: {
         std::string const f = open32();
         o << "    layer_norm<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", " << vec(op.woff, cur_n) << ", "
-          << vec(op.boff, cur_n) << ", " << flit(op.f0) << ", L);\n";
+          << vec(op.boff, cur_n) << ", " << lit(op.f0) << ", L);\n";
         close32();
         break;
       }
@@ -594,8 +602,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       }
       case OP_MIN_MAX: {
         std::string const f = open32();
-        o << "    min_max<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", " << flit(op.f0) << ", "
-          << flit(op.f1) << ", " << flit(op.f2) << ", L);\n";
+        o << "    min_max<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", " << lit(op.f0) << ", "
+          << lit(op.f1) << ", " << lit(op.f2) << ", L);\n";
         if (cur_n % 16) o << "    zero_pad<" << cur_n << ", " << tiles(cur_n) << ">(" << f << ", L);\n";
         close32();
         break;
@@ -649,7 +657,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
           o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
           o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", " << vec(op.boff, cur_n) << ", L);\n";
           o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
-            << ", P + " << op.woff << ", " << b << ", L, [](int, floatx4 (&)[" << NT << "]) {});\n";
+            << ", P + " << op.woff << ", " << b << ", L, [](int, " << F4 << " (&)[" << NT << "]) {});\n";
           o << "    add(" << cur << ", " << nv << ");\n";
         }
         break;
@@ -675,7 +683,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         bool const rhs_scalar = saved_left ? state_scalar : saved_scalar;
         std::string call = "binary<" + std::to_string(op.n_out) + ", " + (lhs_scalar ? "true" : "false") + ", " +
                            (rhs_scalar ? "true" : "false") + ">(" + lhs + ", " + rhs +
-                           ", L, [](float x, float y) { return " + binary_expr(op.aux & 0xff) + "; })";
+                           ", L, [](" + F + " x, " + F + " y) { return " + binary_expr(op.aux & 0xff) + "; })";
         if (half) call = "to_h<E>(" + call + ")";
         o << "    auto " << nv << " = " << call << ";\n";
         cur = nv;

@@ -10,8 +10,11 @@
 // which is the D layout of v_mfma_f32_16x16x4f32, and -- contracting the
 // feature set {16m + 4k + e : k = 0..3} -- also its B layout, so a dense
 // layer feeds the next one straight from registers.  Dense weights arrive
-// pre-packed in A-fragment order: 256 floats per (output tile, input tile)
-// pair, lane l holding elements e = 0..3 of W[16m + 4(l/16) + e][16mo + l%16].
+// pre-packed in A-fragment order: 256 values per (output tile, input tile)
+// pair, lane l holding elements e = 0..3 of W[16m + 4(l/16) + e][16mo + l%16]
+// (fp64 tiles: output row 16mo + 4(r%4) + r/4 for r = l%16, because
+// v_mfma_f64_16x16x4f64 returns the 4x4 row blocks transposed; the packing
+// undoes it, so fp64 tiles have the same layout).
 #pragma once
 
 #include "pointwise.h"
@@ -19,13 +22,33 @@
 namespace ponni_hip {
 namespace fused {
 
+// Element type of the tiles: float, or double where the including kernel
+// defines PONNI_REAL as double (F64 plans, v_mfma_f64_16x16x4f64).
+#ifndef PONNI_REAL
+#define PONNI_REAL float
+#endif
+typedef PONNI_REAL real;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+typedef real realx4 __attribute__((ext_vector_type(4)));
+
+// One 16x16x4 MFMA step; fp32 and fp64 share the operand and result layout.
+__device__ inline floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ inline doublex4 mfma4(double a, double b, doublex4 c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+__device__ inline float d_max(float a, float b) { return fmaxf(a, b); }
+__device__ inline double d_max(double a, double b) { return fmax(a, b); }
+__device__ inline float d_min(float a, float b) { return fminf(a, b); }
+__device__ inline double d_min(double a, double b) { return fmin(a, b); }
 
 constexpr int kNT = 2;  // default 16-column tiles per wave (fp32 path)
 
 template <int T, int NT = kNT>
 struct S {
-  floatx4 v[T > 0 ? T : 1][NT];
+  realx4 v[T > 0 ? T : 1][NT];
 };
 
 struct Lane {
@@ -33,21 +56,21 @@ struct Lane {
   int64_t col0, batch;
 };
 
-__device__ inline float xsum(float v) {
+__device__ inline real xsum(real v) {
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
   return v;
 }
-__device__ inline float xmax(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+__device__ inline real xmax(real v) {
+  v = d_max(v, __shfl_xor(v, 16));
+  return d_max(v, __shfl_xor(v, 32));
 }
-__device__ inline float xmin(float v) {
-  v = fminf(v, __shfl_xor(v, 16));
-  return fminf(v, __shfl_xor(v, 32));
+__device__ inline real xmin(real v) {
+  v = d_min(v, __shfl_xor(v, 16));
+  return d_min(v, __shfl_xor(v, 32));
 }
 
-__device__ inline floatx4 ld4(float const* p) { return *reinterpret_cast<floatx4 const*>(p); }
+__device__ inline realx4 ld4(real const* p) { return *reinterpret_cast<realx4 const*>(p); }
 
 // Wave index within the workgroup as a uniform (scalar) value.
 __device__ inline int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
@@ -76,11 +99,11 @@ __device__ inline int64_t lane_offset(Lane const& L, int64_t ld) {
 
 // x [N, batch] (row stride ld) -> tile; rows >= N and columns >= batch read 0.
 template <int N, int NT = kNT>
-__device__ inline S<(N + 15) / 16, NT> load_rows(float const* __restrict__ x, int64_t ld, Lane const& L) {
+__device__ inline S<(N + 15) / 16, NT> load_rows(real const* __restrict__ x, int64_t ld, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   S<T, NT> s;
   // Row 16m + e of the lane's row group 4g: a uniform offset from one per-lane pointer.
-  float const* __restrict__ xl = x + lane_offset(L, ld) + L.col0;
+  real const* __restrict__ xl = x + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -96,8 +119,8 @@ __device__ inline S<(N + 15) / 16, NT> load_rows(float const* __restrict__ x, in
 }
 
 template <int N, int T, int NT>
-__device__ inline void store_rows(S<T, NT> const& s, float* __restrict__ y, int64_t ld, Lane const& L) {
-  float* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
+__device__ inline void store_rows(S<T, NT> const& s, real* __restrict__ y, int64_t ld, Lane const& L) {
+  real* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -117,7 +140,7 @@ __device__ inline S<T, NT> zeros() {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < NT; n++) s.v[m][n] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < NT; n++) s.v[m][n] = realx4{0.0f, 0.0f, 0.0f, 0.0f};
   return s;
 }
 
@@ -127,11 +150,11 @@ __device__ inline S<T, NT> zeros() {
 // R-deep register ring: fragment i + R is requested while fragment i is
 // consumed.  epi(mo, tile) finishes one output tile in place.
 template <int TI, int TO, int NT, class Epi, int D = 4>
-__device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, float const* __restrict__ w, S<TO, NT> acc,
+__device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
                                      Lane const& L, Epi epi) {
   constexpr int NF = TI * TO;
   constexpr int R = D < NF ? D : NF;
-  floatx4 ring[R];
+  realx4 ring[R];
 #pragma unroll
   for (int i = 0; i < R; i++) ring[i] = ld4(w + i * 256 + L.lane * 4);
 #pragma unroll
@@ -139,13 +162,13 @@ __device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, float const* __restric
 #pragma unroll
     for (int m = 0; m < TI; m++) {
       int const i = mo * TI + m;
-      floatx4 const a = ring[i % R];
+      realx4 const a = ring[i % R];
       if (i + R < NF) ring[i % R] = ld4(w + (i + R) * 256 + L.lane * 4);
 #pragma unroll
       for (int e = 0; e < 4; e++)
 #pragma unroll
         for (int n = 0; n < NT; n++)
-          acc.v[mo][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], in.v[m][n][e], acc.v[mo][n], 0, 0, 0);
+          acc.v[mo][n] = mfma4(a[e], in.v[m][n][e], acc.v[mo][n]);
     }
     if (mo > 0) epi(mo - 1, acc.v[mo - 1]);
   }
@@ -155,14 +178,14 @@ __device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, float const* __restric
 
 // Per-tile epilogue helpers (tile = one 16-feature row block, NT columns).
 template <int NT>
-__device__ inline void tile_add_rows(floatx4 (&t)[NT], float const* __restrict__ b, int mo, Lane const& L) {
-  floatx4 const bb = ld4(b + 16 * mo + 4 * L.g);
+__device__ inline void tile_add_rows(realx4 (&t)[NT], real const* __restrict__ b, int mo, Lane const& L) {
+  realx4 const bb = ld4(b + 16 * mo + 4 * L.g);
 #pragma unroll
   for (int n = 0; n < NT; n++) t[n] += bb;
 }
 
 template <int NT, class F>
-__device__ inline void tile_map(floatx4 (&t)[NT], F f) {
+__device__ inline void tile_map(realx4 (&t)[NT], F f) {
 #pragma unroll
   for (int n = 0; n < NT; n++)
 #pragma unroll
@@ -170,7 +193,7 @@ __device__ inline void tile_map(floatx4 (&t)[NT], F f) {
 }
 
 template <int N, int NT>
-__device__ inline void tile_zero_pad(floatx4 (&t)[NT], int mo, Lane const& L) {
+__device__ inline void tile_zero_pad(realx4 (&t)[NT], int mo, Lane const& L) {
 #pragma unroll
   for (int e = 0; e < 4; e++)
     if (16 * mo + 4 * L.g + e >= N)
@@ -180,10 +203,10 @@ __device__ inline void tile_zero_pad(floatx4 (&t)[NT], int mo, Lane const& L) {
 
 // Per-feature vector (bias, gamma, beta) padded to 16*T.
 template <int T, int NT>
-__device__ inline void add_rows(S<T, NT>& s, float const* __restrict__ b, Lane const& L) {
+__device__ inline void add_rows(S<T, NT>& s, real const* __restrict__ b, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++) {
-    floatx4 const bb = ld4(b + 16 * m + 4 * L.g);
+    realx4 const bb = ld4(b + 16 * m + 4 * L.g);
 #pragma unroll
     for (int n = 0; n < NT; n++) s.v[m][n] += bb;
   }
@@ -223,31 +246,31 @@ __device__ inline void add(S<T, NT>& s, S<T, NT> const& o) {
 
 // Two-pass LayerNorm over N features, ponni_LayerNorm.h:82-98.
 template <int N, int T, int NT>
-__device__ inline void layer_norm(S<T, NT>& s, float const* __restrict__ gamma, float const* __restrict__ beta,
-                                  float eps, Lane const& L) {
+__device__ inline void layer_norm(S<T, NT>& s, real const* __restrict__ gamma, real const* __restrict__ beta,
+                                  real eps, Lane const& L) {
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    float sum = 0.0f;
+    real sum = 0.0f;
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += s.v[m][n][e];
-    float const mean = xsum(sum) * (1.0f / float(N));
-    float q = 0.0f;
+    real const mean = xsum(sum) * (1.0f / real(N));
+    real q = 0.0f;
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) {
-          float const d = s.v[m][n][e] - mean;
+          real const d = s.v[m][n][e] - mean;
           q += d * d;
         }
-    float const inv_std = 1.0f / sqrtf(xsum(q) / float(N) + eps);
+    real const inv_std = 1.0f / d_sqrt(xsum(q) / real(N) + eps);
 #pragma unroll
     for (int m = 0; m < T; m++) {
-      floatx4 const gm = ld4(gamma + 16 * m + 4 * L.g);
-      floatx4 const bt = ld4(beta + 16 * m + 4 * L.g);
+      realx4 const gm = ld4(gamma + 16 * m + 4 * L.g);
+      realx4 const bt = ld4(beta + 16 * m + 4 * L.g);
 #pragma unroll
       for (int e = 0; e < 4; e++) s.v[m][n][e] = gm[e] * ((s.v[m][n][e] - mean) * inv_std) + bt[e];
     }
@@ -259,25 +282,25 @@ template <int N, bool LOG, int T, int NT>
 __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    float mx = -__builtin_huge_valf();
+    real mx = -real(__builtin_huge_val());
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = fmaxf(mx, s.v[m][n][e]);
+        if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = d_max(mx, s.v[m][n][e]);
     mx = xmax(mx);
-    float sum = 0.0f;
+    real sum = 0.0f;
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        float const ex = expf(s.v[m][n][e] - mx);
+        real const ex = d_exp(s.v[m][n][e] - mx);
         if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += ex;
         if (!LOG) s.v[m][n][e] = ex;
       }
     sum = xsum(sum);
     if (LOG) {
-      float const lse = logf(sum) + mx;
+      real const lse = d_log(sum) + mx;
 #pragma unroll
       for (int m = 0; m < T; m++)
 #pragma unroll
@@ -293,21 +316,21 @@ __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
 
 // MinMaxNorm over N features, ponni_MinMaxNorm.h:67-84.
 template <int N, int T, int NT>
-__device__ inline void min_max(S<T, NT>& s, float out_min, float out_max, float eps, Lane const& L) {
+__device__ inline void min_max(S<T, NT>& s, real out_min, real out_max, real eps, Lane const& L) {
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    float lo = __builtin_huge_valf(), hi = -__builtin_huge_valf();
+    real lo = real(__builtin_huge_val()), hi = -real(__builtin_huge_val());
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) {
-          lo = fminf(lo, s.v[m][n][e]);
-          hi = fmaxf(hi, s.v[m][n][e]);
+          lo = d_min(lo, s.v[m][n][e]);
+          hi = d_max(hi, s.v[m][n][e]);
         }
     lo = xmin(lo);
     hi = xmax(hi);
-    float const scale = (out_max - out_min) / ((hi - lo) + eps);
+    real const scale = (out_max - out_min) / ((hi - lo) + eps);
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
@@ -333,7 +356,7 @@ __device__ inline S<TA + TB, NT> concat(S<TA, NT> const& a, S<TB, NT> const& b) 
 // Saved residual states may live in LDS instead of registers (one region per
 // wave, lane-contiguous 16-byte chunks, so accesses are bank-conflict free).
 template <int T, int NT>
-__device__ inline void save_lds(S<T, NT> const& s, floatx4* __restrict__ slot, Lane const& L) {
+__device__ inline void save_lds(S<T, NT> const& s, realx4* __restrict__ slot, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -341,7 +364,7 @@ __device__ inline void save_lds(S<T, NT> const& s, floatx4* __restrict__ slot, L
 }
 
 template <int T, int NT = kNT>
-__device__ inline S<T, NT> load_lds(floatx4 const* __restrict__ slot, Lane const& L) {
+__device__ inline S<T, NT> load_lds(realx4 const* __restrict__ slot, Lane const& L) {
   S<T, NT> s;
 #pragma unroll
   for (int m = 0; m < T; m++)
@@ -351,7 +374,7 @@ __device__ inline S<T, NT> load_lds(floatx4 const* __restrict__ slot, Lane const
 }
 
 template <int T, int NT>
-__device__ inline void add_lds(S<T, NT>& s, floatx4 const* __restrict__ slot, Lane const& L) {
+__device__ inline void add_lds(S<T, NT>& s, realx4 const* __restrict__ slot, Lane const& L) {
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
@@ -363,11 +386,11 @@ __device__ inline void add_lds(S<T, NT>& s, floatx4 const* __restrict__ slot, La
 // Per-feature vector b broadcast over the tile's columns (a Dense bias that
 // seeds the accumulator: sum = bias; sum += W x, emitter.py:701-710).
 template <int T, int NT = kNT>
-__device__ inline S<T, NT> bias_rows(float const* __restrict__ b, Lane const& L) {
+__device__ inline S<T, NT> bias_rows(real const* __restrict__ b, Lane const& L) {
   S<T, NT> s;
 #pragma unroll
   for (int m = 0; m < T; m++) {
-    floatx4 const bb = ld4(b + 16 * m + 4 * L.g);
+    realx4 const bb = ld4(b + 16 * m + 4 * L.g);
 #pragma unroll
     for (int n = 0; n < NT; n++) s.v[m][n] = bb;
   }
@@ -376,8 +399,8 @@ __device__ inline S<T, NT> bias_rows(float const* __restrict__ b, Lane const& L)
 
 // Element-wise op with a constant vector c (padded to 16 T): f(v, c).
 template <int NT, class F>
-__device__ inline void tile_const(floatx4 (&t)[NT], float const* __restrict__ c, int mo, Lane const& L, F f) {
-  floatx4 const cc = ld4(c + 16 * mo + 4 * L.g);
+__device__ inline void tile_const(realx4 (&t)[NT], real const* __restrict__ c, int mo, Lane const& L, F f) {
+  realx4 const cc = ld4(c + 16 * mo + 4 * L.g);
 #pragma unroll
   for (int n = 0; n < NT; n++)
 #pragma unroll
@@ -385,7 +408,7 @@ __device__ inline void tile_const(floatx4 (&t)[NT], float const* __restrict__ c,
 }
 
 template <int T, int NT, class F>
-__device__ inline void map_const(S<T, NT>& s, float const* __restrict__ c, Lane const& L, F f) {
+__device__ inline void map_const(S<T, NT>& s, real const* __restrict__ c, Lane const& L, F f) {
 #pragma unroll
   for (int m = 0; m < T; m++) tile_const(s.v[m], c, m, L, f);
 }
@@ -393,7 +416,7 @@ __device__ inline void map_const(S<T, NT>& s, float const* __restrict__ c, Lane 
 // Feature 0 of every column of the wave's tile, in each lane's own column:
 // feature 0 sits in lane c (group 0), element 0.
 template <int T, int NT>
-__device__ inline float feature0(S<T, NT> const& s, int n, Lane const& L) {
+__device__ inline real feature0(S<T, NT> const& s, int n, Lane const& L) {
   return __shfl(s.v[0][n][0], L.c);
 }
 
@@ -405,14 +428,14 @@ __device__ inline S<(N + 15) / 16, NT> binary(S<TA, NT> const& a, S<TB, NT> cons
   S<T, NT> out;
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    float const a0 = SA ? feature0(a, n, L) : 0.0f;
-    float const b0 = SB ? feature0(b, n, L) : 0.0f;
+    real const a0 = SA ? feature0(a, n, L) : 0.0f;
+    real const b0 = SB ? feature0(b, n, L) : 0.0f;
 #pragma unroll
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        float const x = SA ? a0 : a.v[SA ? 0 : m][n][e];
-        float const y = SB ? b0 : b.v[SB ? 0 : m][n][e];
+        real const x = SA ? a0 : a.v[SA ? 0 : m][n][e];
+        real const y = SB ? b0 : b.v[SB ? 0 : m][n][e];
         out.v[m][n][e] = f(x, y);
       }
   }
@@ -420,7 +443,7 @@ __device__ inline S<(N + 15) / 16, NT> binary(S<TA, NT> const& a, S<TB, NT> cons
   return out;
 }
 
-__device__ inline float xprod(float v) {
+__device__ inline real xprod(real v) {
   v *= __shfl_xor(v, 16);
   return v * __shfl_xor(v, 32);
 }
@@ -432,59 +455,59 @@ __device__ inline S<1, NT> reduce(S<T, NT> const& s, Lane const& L) {
   S<1, NT> out;
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    float r;
+    real r;
     if constexpr (OP == 2 || OP == 3 || OP == 8) {  // MAX, MIN, LOG_SUM_EXP
-      float mx = OP == 3 ? __builtin_huge_valf() : -__builtin_huge_valf();
+      real mx = OP == 3 ? real(__builtin_huge_val()) : -real(__builtin_huge_val());
 #pragma unroll
       for (int m = 0; m < T; m++)
 #pragma unroll
         for (int e = 0; e < 4; e++)
-          if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = OP == 3 ? fminf(mx, s.v[m][n][e]) : fmaxf(mx, s.v[m][n][e]);
+          if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = OP == 3 ? d_min(mx, s.v[m][n][e]) : d_max(mx, s.v[m][n][e]);
       mx = OP == 3 ? xmin(mx) : xmax(mx);
       r = mx;
       if constexpr (OP == 8) {
-        float sum = 0.0f;
+        real sum = 0.0f;
 #pragma unroll
         for (int m = 0; m < T; m++)
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += expf(s.v[m][n][e] - mx);
+            if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += d_exp(s.v[m][n][e] - mx);
         sum = xsum(sum);
-        r = __builtin_isinf(mx) ? mx : mx + logf(sum);
+        r = __builtin_isinf(mx) ? mx : mx + d_log(sum);
       }
     } else {
-      float acc = OP == 9 ? 1.0f : 0.0f;
+      real acc = OP == 9 ? 1.0f : 0.0f;
 #pragma unroll
       for (int m = 0; m < T; m++)
 #pragma unroll
         for (int e = 0; e < 4; e++)
           if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) {
-            float const v = s.v[m][n][e];
-            if constexpr (OP == 4) acc += fabsf(v);
+            real const v = s.v[m][n][e];
+            if constexpr (OP == 4) acc += d_abs(v);
             else if constexpr (OP == 5 || OP == 6) acc += v * v;
             else if constexpr (OP == 9) acc *= v;
             else acc += v;
           }
       acc = OP == 9 ? xprod(acc) : xsum(acc);
-      if constexpr (OP == 1) acc = acc / float(N);
-      else if constexpr (OP == 5) acc = sqrtf(acc);
-      else if constexpr (OP == 7) acc = logf(acc);
+      if constexpr (OP == 1) acc = acc / real(N);
+      else if constexpr (OP == 5) acc = d_sqrt(acc);
+      else if constexpr (OP == 7) acc = d_log(acc);
       r = acc;
     }
-    out.v[0][n] = floatx4{L.g == 0 ? r : 0.0f, 0.0f, 0.0f, 0.0f};
+    out.v[0][n] = realx4{L.g == 0 ? r : 0.0f, 0.0f, 0.0f, 0.0f};
   }
   return out;
 }
 
 // Copy n4 float4s of one per-feature vector into LDS (no barrier).
-__device__ inline void stage_vec(floatx4* __restrict__ lds, float const* __restrict__ src, int n4) {
-  floatx4 const* s4 = reinterpret_cast<floatx4 const*>(src);
+__device__ inline void stage_vec(realx4* __restrict__ lds, real const* __restrict__ src, int n4) {
+  realx4 const* s4 = reinterpret_cast<realx4 const*>(src);
   for (int i = threadIdx.x; i < n4; i += blockDim.x) lds[i] = s4[i];
 }
 
-// Stage `count` floats (a multiple of 4) of packed parameters into LDS.
-__device__ inline void stage(floatx4* __restrict__ lds, float const* __restrict__ src, int count) {
-  floatx4 const* s4 = reinterpret_cast<floatx4 const*>(src);
+// Stage `count` values (a multiple of 4) of packed parameters into LDS.
+__device__ inline void stage(realx4* __restrict__ lds, real const* __restrict__ src, int count) {
+  realx4 const* s4 = reinterpret_cast<realx4 const*>(src);
   for (int i = threadIdx.x; i < count / 4; i += blockDim.x) lds[i] = s4[i];
   __syncthreads();
 }

@@ -544,13 +544,18 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
       } else {
         // A fragment of v_mfma_f32_16x16x4f32 for output tile mo and input
         // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16].
+        // v_mfma_f64_16x16x4f64 returns result row 4e + g in element e of
+        // lane group g (fp32: row 4g + e), so fp64 tiles take their A rows in
+        // that transposed order and the result lands in the fp32 tile layout.
+        bool const rows_t = p.dtype == PONNI_F64;
         int const TK = (K + 15) / 16, TN = (N + 15) / 16;
         for (int mo = 0; mo < TN; mo++)
           for (int m = 0; m < TK; m++)
             for (int l = 0; l < 64; l++)
               for (int v = 0; v < 4; v++) {
                 int const k = 16 * m + 4 * (l >> 4) + v;
-                int const n = 16 * mo + (l & 15);
+                int const r = l & 15;
+                int const n = 16 * mo + (rows_t ? (r & 3) * 4 + (r >> 2) : r);
                 double val = (k < K && n < N) ? rnd(w(int64_t(k) * N + n)) : 0.0;
                 o[((int64_t(mo) * TK + m) * 64 + l) * 4 + v] = val;
               }

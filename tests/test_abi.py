@@ -70,9 +70,11 @@ def test_plan_info_and_path_selection():
     assert (inf.num_inputs, inf.num_outputs, inf.num_parameters) == (2, 1, 12)
     assert create(P.configs.CONFIGS["c2"].layers(False)).path == "fused"
     assert create(P.configs.CONFIGS["c3"].layers(False)).path == "fused"
-    # F64: generated NARROW kernels up to width 16, the GENERIC interpreter beyond.
+    # F64: generated NARROW kernels up to width 16, fp64 FUSED kernels up to
+    # 256, the GENERIC interpreter beyond.
     assert create([P.Matvec(np.ones((2, 2)))], dtype="f64").path == "narrow"
-    assert create([P.Matvec(np.ones((40, 40)))], dtype="f64").path == "generic"
+    assert create([P.Matvec(np.ones((40, 40)))], dtype="f64").path == "fused"
+    assert create([P.Matvec(np.ones((300, 8)))], dtype="f64").path == "generic"
 
 
 @pytest.mark.parametrize("seed", range(8))

@@ -137,3 +137,32 @@ def test_random_narrow_graphs_f64(cuda, seed):
     want = oracle.forward(lowered_with_params(gr), x, oracle.MODE_F64)
     got = y.cpu().numpy()
     assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * max(1.0, np.abs(want).max())), np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("case", ["c5", "g0", "g1", "g2"])
+def test_generated_graphs_f64_fused(cuda, case):
+    """F64 generated graphs on the FUSED kernel (fp64 tiles) against the
+    oracle's fp64 mode."""
+    import torch
+
+    gr = C.c5_graph(True) if case == "c5" else random_graph(600 + int(case[1:]), aligned=True, dtype="float64")
+    if case == "c5":
+        gm = G.GeneratedModel(gr, path="fused")
+        plan = gm.plan("f64")
+    else:
+        gm = G.GeneratedModel(gr, path="fused")
+        plan = gm.plan()
+    assert plan.path == "fused"
+    n_in = gr.size(gr.inputs[0])
+    x = np.random.default_rng(7).standard_normal((n_in, 2049))
+    xt = torch.from_numpy(x).cuda()
+    y = torch.full((gm.num_outputs, 2049), float("nan"), dtype=torch.float64, device="cuda:0")
+    plan.forward_batch_parallel(xt, y)
+    torch.cuda.synchronize()
+    layers = gm.lowered.layers
+    for l, v in zip(layers, gm.lowered.layer_params(gm._constants("f64"))):
+        if v.size:
+            l.params = v
+    want = oracle.forward(layers, x, oracle.MODE_F64)
+    got = y.cpu().numpy()
+    assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * max(1.0, np.abs(want).max())), np.abs(got - want).max()

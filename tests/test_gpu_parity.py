@@ -184,6 +184,26 @@ def test_f64_narrow(cuda, seed):
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * max(1.0, np.abs(want).max())), np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("case", ["c2", "c3", "chain0", "chain1", "chain2", "chain3"])
+def test_f64_fused(cuda, case):
+    """F64 models on the FUSED kernel (fp64 tiles, v_mfma_f64_16x16x4f64,
+    exact attributes, libm activations) against the oracle's fp64 mode; the
+    MFMA summation order is the only difference, hence 1e-12."""
+    rng = np.random.default_rng(800 + len(case))
+    if case.startswith("chain"):
+        k = int(case[5:])
+        width = [32, 64, 96, 128][k]
+        layers = K.random_chain(rng, width, 2 + k % 3)
+        x = rng.standard_normal((width, 3001))
+    else:
+        layers = C.CONFIGS[case].layers(True)
+        x = rng.standard_normal((layers[0].n_in, 3001))
+    got, xg, m = gpu_run(layers, x, dtype="f64", path="fused", pad=2)
+    assert m.path == "fused"
+    want = oracle.forward(layers, xg, oracle.MODE_F64)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * max(1.0, np.abs(want).max())), np.abs(got - want).max()
+
+
 def config_input(cfg, B, dev="cuda:0"):
     import torch
 
