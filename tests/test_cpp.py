@@ -37,7 +37,7 @@ def _apply_gather(table, literals, storage):
     return np.array([storage[g] if g >= 0 else literals[-g - 1] for g in table], dtype=np.float64)
 
 
-@pytest.mark.parametrize("which", ["c5", "random0", "random1", "random2", "random5"])
+@pytest.mark.parametrize("which", ["c5"] + [f"random{k}" for k in range(16)] + [f"narrow{k}" for k in range(8)])
 def test_emitted_gather_tables_rebuild_layer_params(which):
     """The header's per-layer gather tables, applied to the weights storage,
     give exactly the parameter vectors the Python model pushes to its plans
@@ -49,7 +49,13 @@ def test_emitted_gather_tables_rebuild_layer_params(which):
     from ponni_amd import graph as G
     from tests.test_graph import random_graph
 
-    gr = C.c5_graph(True) if which == "c5" else random_graph(int(which[6:]), aligned=True)
+    if which == "c5":
+        gr = C.c5_graph(True)
+    elif which.startswith("narrow"):
+        gr = random_graph(200 + int(which[6:]), narrow=True)
+    else:
+        k = int(which[6:])
+        gr = random_graph(k, aligned=k % 2 == 0)
     gm = G.GeneratedModel(gr)
     gm.storage = np.random.default_rng(7).standard_normal(gm.storage.size)
     tables, literals = E._gather_tables(gm)
