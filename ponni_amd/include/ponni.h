@@ -13,7 +13,9 @@
 //                                weight_schema_fingerprint
 //   - the View contract          src/utils/ponni_kokkos_utils.h:11-25: rank-2
 //                                LayoutRight [features, batch] device arrays
-//   - .ponni files               src/utils/ponni_safetensors.h via ponni/ponni_file.h
+//   - .ponni files               src/utils/ponni_safetensors.h via ponni/ponni_file.h,
+//                                load_ponni_tensor and the View copies of
+//                                src/utils/ponni_view_ops.h
 //
 // What changes underneath: the per-sample Kokkos RangePolicy executor is
 // replaced by one call of ponni_forward(), which runs a gfx950 kernel chosen
@@ -245,6 +247,16 @@ class View {
     View v = *this;
     v.data_ = data_ + c0;
     v.cols_ = c1 - c0;
+    return v;
+  }
+  // The same contiguous elements as a [rows, cols] view (shares the allocation).
+  View reshape(std::int64_t rows, std::int64_t cols) const {
+    if (rows * cols != size() || (rows_ > 1 && ld_ != cols_))
+      abort("ponni::View::reshape needs a contiguous view of the same size");
+    View v = *this;
+    v.rows_ = rows;
+    v.cols_ = cols;
+    v.ld_ = cols;
     return v;
   }
 
@@ -547,6 +559,17 @@ std::vector<double> flatten1(V const& v) {
   return out;
 }
 
+// ponni::View arguments (device or host memory) are read through a host copy.
+template <class T, class Space>
+std::vector<double> flatten(View<T, Space> const& m) {
+  auto const h = m.copy_to_host();
+  return std::vector<double>(h.begin(), h.end());
+}
+template <class T, class Space>
+std::vector<double> flatten1(View<T, Space> const& v) {
+  return detail::flatten(v);
+}
+
 }  // namespace detail
 
 // Dense layer, W [n_in, n_out] (ponni_Matvec.h).  Constructors: (num_inputs,
@@ -595,6 +618,11 @@ struct Bias : detail::LayerCore {
   }
   template <class V, class = decltype(std::declval<V const&>()[0]), class = decltype(std::declval<V const&>().size())>
   explicit Bias(V const& weights, bool trainable_ = true) {
+    setup(detail::flatten1(weights), trainable_);
+  }
+  // A [1, n] or [n, 1] View (load_ponni_tensor<1>), in any memory space.
+  template <class T, class Space>
+  explicit Bias(View<T, Space> const& weights, bool trainable_ = true) {
     setup(detail::flatten1(weights), trainable_);
   }
   void setup(std::vector<double> b, bool t) {
@@ -725,6 +753,14 @@ struct LayerNorm : detail::LayerCore {
   }
   template <class V, class = decltype(std::declval<V const&>()[0])>
   LayerNorm(V const& gamma, V const& beta, real epsilon = real(1e-5), bool trainable_ = true) {
+    if (gamma.size() != beta.size()) abort("ERROR: LayerNorm gamma/beta sizes differ");
+    std::vector<double> p = detail::flatten1(gamma), b = detail::flatten1(beta);
+    p.insert(p.end(), b.begin(), b.end());
+    setup(static_cast<int>(gamma.size()), std::move(p), epsilon, trainable_);
+  }
+  template <class T, class Space>
+  LayerNorm(View<T, Space> const& gamma, View<T, Space> const& beta, real epsilon = real(1e-5),
+            bool trainable_ = true) {
     if (gamma.size() != beta.size()) abort("ERROR: LayerNorm gamma/beta sizes differ");
     std::vector<double> p = detail::flatten1(gamma), b = detail::flatten1(beta);
     p.insert(p.end(), b.begin(), b.end());
@@ -1323,6 +1359,66 @@ class BasicInference {
   std::shared_ptr<ponni_plan_s> plan_;
   std::vector<std::uint64_t> pushed_;
 };
+
+// ---- View copies and .ponni tensors (src/utils/ponni_view_ops.h:12-48,
+// src/utils/ponni_safetensors.h:409-444) ------------------------------------------------
+
+// A copy of `v` in memory space Space (LayoutRight, contiguous rows).
+template <class Space, class T, class S>
+View<std::remove_const_t<T>, Space> create_memory_space_copy(View<T, S> const& v, Space = Space()) {
+  View<std::remove_const_t<T>, Space> out(v.label(), v.extent(0), v.extent(1), false);
+  out.copy_from_host(v.copy_to_host());
+  return out;
+}
+template <class T, class S>
+View<std::remove_const_t<T>, HostSpace> create_host_copy(View<T, S> const& v) {
+  return create_memory_space_copy<HostSpace>(v);
+}
+template <class T, class S>
+View<std::remove_const_t<T>, HIPSpace> create_device_copy(View<T, S> const& v) {
+  return create_memory_space_copy<HIPSpace>(v);
+}
+// The elements of a contiguous view as one row, sharing its memory.
+template <class T, class S>
+View<T, S> flatten(View<T, S> const& v) {
+  return v.reshape(1, v.size());
+}
+
+// Tensor `name` of a .ponni file as a float View in Space: rank 2 [rows, cols];
+// rank 1 [1, n] (this View type is rank 2).  F32 or F64 payloads.
+template <int N, class Space = HIPSpace>
+View<float, Space> load_ponni_tensor(PonniFile const& file, std::string const& name) {
+  static_assert(N == 1 || N == 2, "load_ponni_tensor supports ranks one and two");
+  auto const* t = file.find(name);
+  if (t == nullptr) throw std::runtime_error("PONNI file is missing tensor " + name);
+  if (t->shape.size() != static_cast<std::size_t>(N)) throw std::runtime_error("PONNI tensor rank mismatch for " + name);
+  if (t->dtype != "F32" && t->dtype != "F64") throw std::runtime_error("PONNI tensor must use F32 or F64: " + name);
+  std::int64_t const rows = N == 1 ? 1 : static_cast<std::int64_t>(t->shape[0]);
+  std::int64_t const cols = static_cast<std::int64_t>(t->shape[N - 1]);
+  std::vector<float> h(static_cast<std::size_t>(rows * cols));
+  unsigned char const* data = file.tensor_data(*t);
+  for (std::size_t i = 0; i < h.size(); i++) {
+    if (t->dtype == "F32") {
+      float v;
+      std::memcpy(&v, data + 4 * i, 4);
+      h[i] = v;
+    } else {
+      double v;
+      std::memcpy(&v, data + 8 * i, 8);
+      h[i] = static_cast<float>(v);
+    }
+  }
+  View<float, Space> out(name, rows, cols, false);
+  out.copy_from_host(h);
+  return out;
+}
+template <int N, class Space = HIPSpace>
+View<float, Space> load_ponni_tensor(std::string const& path, std::string const& name) {
+  PonniFile file;
+  std::string error;
+  if (!file.load(path, &error)) throw std::runtime_error(error);
+  return load_ponni_tensor<N, Space>(file, name);
+}
 
 // ---- factories (ponni_create_model.h:40-98) ------------------------------------------------
 
