@@ -51,9 +51,27 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
+TORCH_DTYPES = {"f32": "float32", "f64": "float64", "f16": "float16", "bf16": "bfloat16"}
+ELEMENT_BYTES = {"f32": 4, "f64": 8, "f16": 2, "bf16": 2}
+
+
+def with_dtype(cfg, dtype, C):
+    """The configuration computed in another precision (--dtype): same
+    shapes and synthetic inputs, HBM bytes and MFMA peak of that precision."""
+    import dataclasses
+
+    if dtype is None or dtype == cfg.dtype:
+        return cfg
+    scale = ELEMENT_BYTES[dtype] / ELEMENT_BYTES[cfg.dtype]
+    peak = cfg.peak
+    if cfg.bound == "mfma":
+        peak = {"f32": C.FP32_PEAK, "f64": C.FP64_PEAK, "f16": C.FP16_PEAK, "bf16": C.FP16_PEAK}[dtype]
+    return dataclasses.replace(cfg, dtype=dtype, peak=peak, bytes_per_sample=int(cfg.bytes_per_sample * scale))
+
+
 def make_inputs(cfg, torch, P, C):
-    tdt = torch.float16 if cfg.dtype == "f16" else torch.float32
-    es = 2 if cfg.dtype == "f16" else 4
+    tdt = getattr(torch, TORCH_DTYPES[cfg.dtype])
+    es = ELEMENT_BYTES[cfg.dtype]
     per_set = (cfg.n_in + cfg.n_out) * cfg.batch * es
     sets = max(1, -(-ROTATE_BYTES // per_set))
     xs, ys = [], []
@@ -115,7 +133,8 @@ def time_config(cfg, steps, warmup, torch, P, C):
             "peak": round(cfg.peak / scale, 3),
             "unit": unit,
             "frac": round(achieved / cfg.peak, 4),
-            "traffic": pmc_traffic(cfg.name),
+            # (PMC traffic is measured for the configurations' own precision only)
+            "traffic": pmc_traffic(cfg.name) if cfg.dtype == C.CONFIGS[cfg.name].dtype else None,
         },
         "path": model.path,
     }
@@ -131,7 +150,8 @@ def cpu_baseline(cfg, budget_s=10.0):
     oracle.build()
     layers = cfg.layers(False)
     cores = host_cores()
-    mode = oracle.MODE_F16_OPERANDS if cfg.dtype == "f16" else oracle.MODE_F32
+    mode = {"f16": oracle.MODE_F16_OPERANDS, "bf16": oracle.MODE_BF16_OPERANDS, "f64": oracle.MODE_F64}.get(
+        cfg.dtype, oracle.MODE_F32)
 
     def gen(n):
         kind, a, b = cfg.input_dist
@@ -171,6 +191,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c2")
+    ap.add_argument("--dtype", choices=sorted(TORCH_DTYPES), default=None,
+                    help="run the configuration in another precision (not the headline measurement)")
     ap.add_argument("--no-others", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -195,7 +217,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    cfg = C.CONFIGS[args.config]
+    cfg = with_dtype(C.CONFIGS[args.config], args.dtype, C)
     head = time_config(cfg, args.steps, args.warmup, torch, P, C)
     others = {}
     if not args.no_others:
@@ -225,7 +247,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if cfg.dtype == "f32" else "f16",
+        "dtype": cfg.dtype,
         "data": "synthetic",
         "config": {
             "workload": f"{cfg.name}: {cfg.description}",

@@ -86,6 +86,7 @@ class Config:
 
 HBM_PEAK = 8.0e12
 FP32_PEAK = 157.3e12
+FP64_PEAK = 78.6e12
 FP16_PEAK = 2.5e15
 
 INPUT_TAG = 1000  # tag of the input tensor stream
