@@ -474,6 +474,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     o << "  __shared__ unsigned in_buf[" << cfg.waves << "][" << in_dma_bytes / 4 / cfg.waves << "];\n";
     o << "  L.col0 = (int64_t(blockIdx.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
     o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
+    // The LDS writes of these loads complete with vmcnt, which the compiler
+    // does not track for reads of in_buf: each tile's rows are waited for
+    // explicitly, here for the first tile and before the output stores for
+    // the next one (requested at the top of the tile, so long landed).
+    o << "  wait_vmem();\n";
   }
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
   o << "    L.col0 = (tile * " << cfg.waves << " + wave_id()) * " << 16 * NT << ";\n";
@@ -704,6 +709,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         break;
     }
   }
+  if (half && in_dma) o << "    wait_vmem();\n";
   if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";

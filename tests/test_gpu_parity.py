@@ -322,6 +322,25 @@ def test_hip_graph_capture_and_replay(cuda, path):
     check_f32(got.double().cpu().numpy(), oracle.forward(layers, x.double().cpu().numpy()), scale_tol=False)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_half_fused_chain_without_dense_layers(cuda, dtype):
+    """16-bit FUSED kernels stream each tile's input rows into LDS ahead of
+    use; a chain with no dense layer issues no other memory operation, so
+    this pins the explicit wait for those rows (several runs, ragged and
+    multi-tile batches)."""
+    rng = np.random.default_rng(46)
+    layers = [P.Elu(48, 1.0), P.Save_State(0, 48), P.LayerNorm(48), P.Softmax(48), P.Binop_Add(0, 48)]
+    for B in (999, 20011, 257):
+        x = rng.standard_normal((48, B))
+        want = None
+        for _ in range(3):
+            got, xg, m = gpu_run(layers, x, dtype=dtype, path="fused")
+            assert m.path == "fused"
+            if want is None:
+                want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
+            check_half(got, want, 2e-3 if dtype == "f16" else 1.6e-2)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
