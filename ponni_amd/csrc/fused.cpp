@@ -255,6 +255,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       int const t = std::atoi(v);
       if (t == 1 || t == 2 || t == 4) NT = t;
     }
+    if (p.mfma32) NT = 2;  // 32x32 tiles: one 32-column tile per wave
     half_wps = NT == 1 ? 4 : 2;
     if (char const* v = std::getenv("PONNI_HALF_WPS")) {  // tuning override
       int const t = std::atoi(v);
@@ -377,6 +378,10 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v >= 1 && v <= 8) o << "#define PONNI_CHUNK_TILES " << v << "\n";
   }
+  if (char const* d = std::getenv("PONNI_CHUNK_DMA")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v == 0 || v == 1) o << "#define PONNI_CHUNK_DMA " << v << "\n";
+  }
   if (char const* d = std::getenv("PONNI_RING_DEPTH")) {  // tuning override
     int const v = std::atoi(d);
     if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
@@ -408,15 +413,20 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int woff, ts, to;
   };
   std::vector<DenseRef> dense_seq;
+  // (32x32 tiles: 16-feature steps and 32-feature output tiles)
+  bool const m32 = p.mfma32;
   for (Op const& op : p.ops)
-    if (op.code == OP_DENSE) dense_seq.push_back({op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
+    if (op.code == OP_DENSE)
+      dense_seq.push_back(m32 ? DenseRef{op.woff, op.n_in / 16, op.n_out / 32}
+                              : DenseRef{op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
   // (tuning override PONNI_HALF_STAGE=0: A fragments straight from L1/L2 per wave)
-  bool const half_staged = !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
+  bool const half_staged =
+      m32 || !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
   if (half && half_staged && !dense_seq.empty()) {
     o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
     o << "  Stage<E> st{a_slots, 0};\n";
-    o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", " << cfg.waves
-      << ">(st, reinterpret_cast<E const*>(gparams + " << dense_seq[0].woff << "));\n";
+    o << "  " << (m32 ? "stage_first32<" : "stage_first<") << dense_seq[0].ts << ", " << dense_seq[0].to << ", "
+      << cfg.waves << ">(st, reinterpret_cast<E const*>(gparams + " << dense_seq[0].woff << "));\n";
     o << "  __syncthreads();\n";
   }
   size_t dense_index = 0;
@@ -473,7 +483,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (in_dma) {
     o << "  __shared__ unsigned in_buf[" << cfg.waves << "][" << in_dma_bytes / 4 / cfg.waves << "];\n";
     o << "  L.col0 = (int64_t(blockIdx.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
-    o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
+    if (m32) o << "  if (blockIdx.x < tiles) prefetch_rows_lds32<" << n_in0 << ">(x, ldx, L, in_buf[wave_id()]);\n";
+    else o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
     // The LDS writes of these loads complete with vmcnt, which the compiler
     // does not track for reads of in_buf: each tile's rows are waited for
     // explicitly, here for the first tile and before the output stores for
@@ -490,12 +501,15 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::string cur = fresh();
   int cur_n = p.layers.front().n_in;
   if (in_dma) {
-    o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
+    if (m32) o << "    auto " << cur << " = load_rows_lds32<" << cur_n << ", E>(in_buf[wave_id()], L);\n";
+    else o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
     o << "    wait_lds();\n";
     o << "    if (tile + gridDim.x < tiles) {\n      Lane Ln = L;\n      Ln.col0 = ((tile + gridDim.x) * " << NW
-      << " + wave_id()) * " << WCOLS << ";\n      prefetch_rows_lds<" << cur_n << ", " << NT
+      << " + wave_id()) * " << WCOLS << ";\n      "
+      << (m32 ? "prefetch_rows_lds32<" + std::to_string(cur_n) : "prefetch_rows_lds<" + std::to_string(cur_n) + ", " + std::to_string(NT))
       << ">(x, ldx, Ln, in_buf[wave_id()]);\n    }\n";
-  } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
+  } else if (m32) o << "    auto " << cur << " = load_rows_h32<" << cur_n << ">(x, ldx, L);\n";
+  else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
   // The logistic family runs on the hardware transcendentals (pointwise.h),
@@ -542,9 +556,17 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         bool const lead_bias = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
         bool const seed = lead_bias && (half || (op.aux & DENSE_BIAS_FIRST));
         // A 16-bit block ending in Tanh looks the activation up in the LDS table.
-        bool const lut_tanh = half && cfg.lut_bytes > 0 && op.epi_count > (seed ? 1 : 0) &&
+        bool const lut_tanh = half && !m32 && cfg.lut_bytes > 0 && op.epi_count > (seed ? 1 : 0) &&
                               p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH;
-        if (half && !half_staged) {
+        if (m32) {
+          std::string const init = seed ? "SeedRows32{" + vec(p.steps[op.epi_begin].off, n) + ", L.lane >> 5}" : "SeedZero32{}";
+          auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
+          dense_index++;
+          o << "    auto " << nv << " = dense_hs32<" << op.n_in / 32 << ", " << n / 32 << ", " << cfg.waves << ", "
+            << next.ts << ", " << next.to << ">(" << cur << ", reinterpret_cast<E const*>(P + " << op.woff
+            << "), reinterpret_cast<E const*>(P + " << next.woff << "), st, L, " << init
+            << ", [&](int mo, floatx4 (&t)[4], Vec<E>::x4 (&o)[4]) {\n";
+        } else if (half && !half_staged) {
           std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
           o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, " << init << ", [&](int mo, floatx4 (&t)["
@@ -567,17 +589,17 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         for (int s = seed ? 1 : 0; s < last; s++) {
           Step const& st = p.steps[op.epi_begin + s];
           if (st.act == ACT_BIAS) {
-            o << "      tile_add_rows(t, " << vec(st.off, n) << ", mo, L);\n";
+            o << "      " << (m32 ? "t32_add_rows" : "tile_add_rows") << "(t, " << vec(st.off, n) << ", mo, L);\n";
           } else if (act_has_param(st.act)) {
-            o << "      tile_const(t, " << vec(st.off, n) << ", mo, L, [](" << F << " v, " << F << " c) { return " << const_expr(st.act)
-              << "; });\n";
+            o << "      " << (m32 ? "t32_const" : "tile_const") << "(t, " << vec(st.off, n) << ", mo, L, [](" << F
+              << " v, " << F << " c) { return " << const_expr(st.act) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           } else {
             o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
-        if (pad && n % 16) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
+        if (pad && n % 16 && !m32) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
         if (half) o << (lut_tanh ? "      tile_lut_odd<E>(t, o, lut_tanh);\n" : "      tile_round<E>(t, o);\n");
         o << "    });\n";
         cur = nv;
@@ -585,6 +607,22 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         break;
       }
       case OP_POINTWISE: {
+        if (m32) {
+          // Widths are multiples of 32: no padding to restore.
+          o << "    for_tiles32(" << cur << ", [&](int mo, floatx4 (&t)[4]) {\n";
+          for (int s = 0; s < op.epi_count; s++) {
+            Step const& st = p.steps[op.epi_begin + s];
+            if (st.act == ACT_BIAS)
+              o << "      t32_add_rows(t, " << vec(st.off, cur_n) << ", mo, L);\n";
+            else if (act_has_param(st.act))
+              o << "      t32_const(t, " << vec(st.off, cur_n) << ", mo, L, [](" << F << " v, " << F << " c) { return "
+                << const_expr(st.act) << "; });\n";
+            else
+              o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
+          }
+          o << "    });\n";
+          break;
+        }
         std::string const f = open32();
         epilogue(f, cur_n, op.epi_begin, op.epi_count);
         close32();
@@ -710,7 +748,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   if (half && in_dma) o << "    wait_vmem();\n";
-  if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  if (m32) o << "    store_rows_h32<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  else if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";
   if (!vec_lds.empty()) {

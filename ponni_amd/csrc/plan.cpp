@@ -508,6 +508,29 @@ void lower(ponni_plan_s& p) {
         break;
       }
   }
+
+  // 32x32 tiles (opt-in, PONNI_MFMA32=1): a chain of dense layers and
+  // pointwise steps whose every width is a multiple of 32 (then the packed
+  // sizes equal those of the 16x16 layout: K * N / 2 words per dense block).
+  // Per KB of A fragments read from LDS both layouts do the same work (two
+  // 16x16x32 MFMAs over a wave's two column tiles, or one 32x32x16), and the
+  // 32x32 kernel measured slower on c4, so 16x16 stays the default.
+  p.mfma32 = false;
+  char const* m32 = std::getenv("PONNI_MFMA32");
+  if (m32 != nullptr && std::strcmp(m32, "1") == 0 && p.path == PONNI_PATH_FUSED &&
+      (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16)) {
+    bool ok = p.layers.front().n_in % 32 == 0;
+    bool any_dense = false;
+    for (Op const& op : p.ops) {
+      if (op.code == OP_DENSE) {
+        any_dense = true;
+        ok = ok && op.n_in % 32 == 0 && op.n_out % 32 == 0;
+      } else if (op.code != OP_POINTWISE) {
+        ok = false;
+      }
+    }
+    p.mfma32 = ok && any_dense;
+  }
 }
 
 bool mfma_supports(ponni_plan_s const& p) {
@@ -612,8 +635,25 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
     return u;
   };
   auto pack_dense = [&](double const* w, int K, int N, uint32_t* o, bool transposed = false) {
-    int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
     auto* h = reinterpret_cast<uint16_t*>(o);
+    if (p.mfma32) {
+      // v_mfma_f32_32x32x16 A fragment of output tile mo and 16-feature step
+      // s = 2m + u: lane l = 32hh + c, element j holds W[k][32 mo + c] with
+      // k = 32m + 8(2u + j/4) + 4hh + j%4 (fused_f16.h H32).  K, N are
+      // multiples of 32.
+      int const TN = N / 32, TS = K / 16;
+      for (int mo = 0; mo < TN; mo++)
+        for (int s = 0; s < TS; s++)
+          for (int l = 0; l < 64; l++)
+            for (int j = 0; j < 8; j++) {
+              int const k = 32 * (s / 2) + 8 * (2 * (s % 2) + j / 4) + 4 * (l >> 5) + (j & 3);
+              int const n = 32 * mo + (l & 31);
+              double const v = transposed ? w[int64_t(n) * K + k] : w[int64_t(k) * N + n];
+              h[((int64_t(mo) * TS + s) * 64 + l) * 8 + j] = bits16(v);
+            }
+      return;
+    }
+    int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
     for (int mo = 0; mo < TN; mo++)
       for (int t = 0; t < TS; t++)
         for (int l = 0; l < 64; l++)
