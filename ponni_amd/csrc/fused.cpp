@@ -378,6 +378,10 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v >= 1 && v <= 8) o << "#define PONNI_CHUNK_TILES " << v << "\n";
   }
+  if (char const* d = std::getenv("PONNI_FULL_SLOT_CHUNKS")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v == 0 || v == 1) o << "#define PONNI_FULL_SLOT_CHUNKS " << v << "\n";
+  }
   if (char const* d = std::getenv("PONNI_CHUNK_DMA")) {  // tuning override
     int const v = std::atoi(d);
     if (v == 0 || v == 1) o << "#define PONNI_CHUNK_DMA " << v << "\n";

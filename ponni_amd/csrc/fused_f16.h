@@ -283,9 +283,9 @@ __device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restri
 }
 
 // ---- A fragments staged through LDS -------------------------------------
-// The workgroup's waves share the A fragments of up to CT consecutive output
-// tiles (a "chunk": up to CT * TS 1 KB fragments, contiguous in the packed
-// parameters) in one of two LDS slots.  While a chunk is computed from slot
+// The workgroup's waves share the A fragments of CT consecutive output tiles
+// (a "chunk": CT * TS 1 KB fragments, contiguous in the packed parameters, as
+// many tiles as fill a slot) in one of two LDS slots.  While a chunk is computed from slot
 // `cur`, every wave loads its share of the next chunk (the next CT tiles of
 // the layer, or the first chunk of the next dense layer) into registers and
 // writes it to the other slot; a workgroup barrier ends the chunk.  Each
@@ -374,6 +374,14 @@ __device__ inline void chunk_dma(E const* __restrict__ chunk, Stage<E> const& st
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
+// Output tiles per chunk for a layer of TS 32-feature steps: a full slot
+// (a layer of 64 input features takes 16 tiles per chunk, so 4x fewer
+// barriers than 256), or kChunkTiles with PONNI_FULL_SLOT_CHUNKS=0.
+#ifndef PONNI_FULL_SLOT_CHUNKS
+#define PONNI_FULL_SLOT_CHUNKS 1
+#endif
+constexpr int ct16(int ts) { return PONNI_FULL_SLOT_CHUNKS ? kSlotFrags / ts : kChunkTiles; }
+
 // Dense layer with LDS-staged A fragments.  On entry slot st.cur holds this
 // layer's first chunk; on exit it holds the first chunk of `w_next`, the next
 // dense layer (TSN fragments per tile, TON output tiles).  init / epi as in
@@ -385,9 +393,9 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
   constexpr int TS = (TI + 1) / 2;
-  constexpr int CT = kChunkTiles;
+  constexpr int CT = ct16(TS);
   constexpr int NCH = (TO + CT - 1) / CT;
-  constexpr int NFN = cmin(CT, TON) * TSN;  // fragments of the next layer's first chunk
+  constexpr int NFN = cmin(ct16(TSN), TON) * TSN;  // fragments of the next layer's first chunk
   static_assert(TS <= 8 && TSN <= 8, "at most 256 input features");
   // Tiles per group: GT must divide CT and TO (else one at a time); DEFER
   // runs a group's epilogue after the next group's MFMAs.
@@ -517,7 +525,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
 template <int TS, int TO, int WAVES, class E>
 __device__ inline void stage_first(Stage<E>& st, E const* __restrict__ w) {
   int const wave = wave_id(), lane = threadIdx.x & 63;
-  constexpr int NF = cmin(kChunkTiles, TO) * TS;
+  constexpr int NF = cmin(ct16(TS), TO) * TS;
   if (PONNI_CHUNK_DMA) {
     chunk_dma<NF, WAVES>(w, st, 0, wave, lane);
     wait_vmem();
