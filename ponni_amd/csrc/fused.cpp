@@ -378,6 +378,17 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v >= 1 && v <= 8) o << "#define PONNI_CHUNK_TILES " << v << "\n";
   }
+  // fp32 plans whose parameters sit in LDS or registers keep each dense
+  // tile's epilogue among the next tile's MFMAs (fused_f32.h dense_ep; c2
+  // and c5 2.8 / 3.5 % faster).  Plans streaming parameters from L2 keep the
+  // compiler's order: measured neutral at their occupancy (c3), and the
+  // registers it frees would move c3 to two waves per SIMD, 8 % slower.
+  int epi_interleave = (!half && !dbl && (cfg.lds_bytes > 0 || cfg.params_in_registers)) ? 16 : 0;
+  if (char const* d = std::getenv("PONNI_EPI_INTERLEAVE")) {  // tuning override
+    int const v = std::atoi(d);
+    if (v >= 0 && v <= 16) epi_interleave = v;
+  }
+
   if (char const* d = std::getenv("PONNI_FULL_SLOT_CHUNKS")) {  // tuning override
     int const v = std::atoi(d);
     if (v == 0 || v == 1) o << "#define PONNI_FULL_SLOT_CHUNKS " << v << "\n";
@@ -586,7 +597,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         } else {
           std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(" + vec(p.steps[op.epi_begin].off, n) + ", L)"
                                         : "zeros<" + std::to_string(tiles(n)) + ">()";
-          o << "    auto " << nv << " = dense_ep<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
+          o << "    auto " << nv << " = "
+            << (epi_interleave > 0 ? "dense_ep_il<" + std::to_string(epi_interleave) + ", " : std::string("dense_ep<"))
+            << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
             << op.woff << ", " << init << ", L, [&](int mo, " << F4 << " (&t)[" << NT << "]) {\n";
         }
         int const last = op.epi_count - (lut_tanh ? 1 : 0);

@@ -148,10 +148,12 @@ __device__ inline S<T, NT> zeros() {
 // epilogue of output tile mo-1 issued after the MFMAs of tile mo (so its VALU
 // work overlaps the matrix pipe) and the A fragments streamed through an
 // R-deep register ring: fragment i + R is requested while fragment i is
-// consumed.  epi(mo, tile) finishes one output tile in place.
-template <int TI, int TO, int NT, class Epi, int D = 4>
-__device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
-                                     Lane const& L, Epi epi) {
+// consumed.  epi(mo, tile) finishes one output tile in place.  IL > 0 pins
+// each epilogue among the next tile's MFMAs, IL VALU (and as many
+// transcendentals) per input tile of MFMAs.
+template <int IL, int TI, int TO, int NT, class Epi, int D = 4>
+__device__ inline S<TO, NT> dense_ep_il(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
+                                        Lane const& L, Epi epi) {
   constexpr int NF = TI * TO;
   constexpr int R = D < NF ? D : NF;
   realx4 ring[R];
@@ -159,6 +161,8 @@ __device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict
   for (int i = 0; i < R; i++) ring[i] = ld4(w + i * 256 + L.lane * 4);
 #pragma unroll
   for (int mo = 0; mo < TO; mo++) {
+    // (interleaving: one scheduling region per output tile)
+    if (IL > 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < TI; m++) {
       int const i = mo * TI + m;
@@ -170,10 +174,35 @@ __device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict
         for (int n = 0; n < NT; n++)
           acc.v[mo][n] = mfma4(a[e], in.v[m][n][e], acc.v[mo][n]);
     }
-    if (mo > 0) epi(mo - 1, acc.v[mo - 1]);
+    if (mo > 0) {
+      epi(mo - 1, acc.v[mo - 1]);
+      // (pure arithmetic floats to its uses unless something ordered reads it)
+      if (IL > 0)
+#pragma unroll
+        for (int n = 0; n < NT; n++) asm volatile("" : "+v"(acc.v[mo - 1][n]));
+      // Keep that epilogue between this tile's MFMAs: left alone, its pure
+      // arithmetic floats down to its first use (the next layer), so every
+      // tile's epilogue runs after the layer's last MFMA.  The empty asm
+      // above orders the results within this tile's scheduling region (a
+      // sched_barrier at the top of each tile); per input tile (4 NT MFMAs)
+      // up to IL VALU and as many transcendentals follow.
+      if (IL > 0)
+#pragma unroll
+        for (int k = 0; k < TI; k++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 4 * NT, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, IL, 0);
+          __builtin_amdgcn_sched_group_barrier(0x400, IL, 0);
+        }
+    }
   }
   epi(TO - 1, acc.v[TO - 1]);
   return acc;
+}
+
+template <int TI, int TO, int NT, class Epi, int D = 4>
+__device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
+                                     Lane const& L, Epi epi) {
+  return dense_ep_il<0, TI, TO, NT, Epi, D>(in, w, acc, L, epi);
 }
 
 // Per-tile epilogue helpers (tile = one 16-feature row block, NT columns).
