@@ -322,6 +322,28 @@ def test_hip_graph_capture_and_replay(cuda, path):
     check_f32(got.double().cpu().numpy(), oracle.forward(layers, x.double().cpu().numpy()), scale_tol=False)
 
 
+@pytest.mark.skip(reason="open divergence: in this chain one sample's two MinMaxNorm inputs differ by "
+                         "17 fp32 ulps, and the NARROW kernel (FUSED from the next layer on) returns "
+                         "(2.052, -0.987) there instead of (1.999994, -1): its x - min is not exactly 0 "
+                         "for the minimum, so min and x are not the same rounded value; not yet located")
+@pytest.mark.parametrize("path", ["narrow", "fused"])
+def test_state_rounded_before_min_max_norm(cuda, path):
+    """Each layer's state is rounded before the next layer reads it, so
+    MinMaxNorm's x - min is exactly 0 for the minimum.  In this random chain
+    (the random sweep's seed 175) one sample's two MinMaxNorm inputs differ by
+    17 fp32 ulps, which scales any sub-ulp difference by 1 / (max - min)."""
+    rng = np.random.default_rng(10_175)
+    width = int(rng.choice([1, 2, 3, 5, 8, 11, 16, 17, 24, 32, 40, 64, 96, 128, 200, 256]))
+    layers = K.random_chain(rng, width, int(rng.integers(1, 6)))
+    B = int(rng.choice([1, 7, 64, 255, 1000, 4097, 20011]))
+    x = rng.standard_normal((width, B))
+    assert [l.label for l in layers[3:5]] == ["Mish", "MinMaxNorm"] and B == 20011
+    for k in (5, 6, len(layers)):
+        got, xg, m = gpu_run(layers[:k], x, "f32", path)
+        assert m.path == path
+        check_f32(got, oracle.forward(layers[:k], xg, oracle.MODE_F32))
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_half_fused_chain_without_dense_layers(cuda, dtype):
     """16-bit FUSED kernels stream each tile's input rows into LDS ahead of
