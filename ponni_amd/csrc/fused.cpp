@@ -180,17 +180,31 @@ std::string cache_dir() {
   return "";
 }
 
-char const* const kOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-                                "-Xclang", "-packed-fp32-ops"};
+// fp32 / fp64 plans compile with -ffp-contract=on: multiply-adds fuse within
+// one expression (a dot product's terms) but not across statements, so a
+// layer's state is rounded before the next layer reads it, as the reference
+// materializes it.  (Fused across layers, Mish's last product entered
+// MinMaxNorm's x - min unrounded and a sub-ulp difference was scaled by
+// 1 / (max - min).)  16-bit plans round their state to the 16-bit type at
+// every layer, which already stops that, and keep the default.
+std::vector<char const*> jit_options(bool contract) {
+  std::vector<char const*> o{"--offload-arch=gfx950", "-O3", "-std=c++17"};
+  if (contract) o.push_back("-ffp-contract=on");
+  for (char const* x : {"-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"}) o.push_back(x);
+  return o;
+}
 
-bool compile(std::string const& source, std::vector<char>& code, std::string& log) {
+bool contract_on(ponni_plan_s const& p) { return p.dtype == PONNI_F32 || p.dtype == PONNI_F64; }
+
+bool compile(std::string const& source, bool contract, std::vector<char>& code, std::string& log) {
   hiprtcProgram prog = nullptr;
   if (hiprtcCreateProgram(&prog, source.c_str(), "ponni_fused.hip", kJitHeaderCount, kJitHeaderTexts,
                           kJitHeaderNames) != HIPRTC_SUCCESS) {
     log = "hiprtcCreateProgram failed";
     return false;
   }
-  hiprtcResult const r = hiprtcCompileProgram(prog, int(sizeof(kOptions) / sizeof(kOptions[0])), kOptions);
+  std::vector<char const*> const opts = jit_options(contract);
+  hiprtcResult const r = hiprtcCompileProgram(prog, int(opts.size()), opts.data());
   size_t n = 0;
   hiprtcGetProgramLogSize(prog, &n);
   log.assign(n, '\0');
@@ -956,9 +970,9 @@ bool narrow_jit_supports(ponni_plan_s const& p) {
 
 namespace {
 
-std::string cache_key(std::string const& src) {
+std::string cache_key(std::string const& src, bool contract) {
   std::string opts;
-  for (auto const* o : kOptions) opts += std::string(o) + " ";
+  for (auto const* o : jit_options(contract)) opts += std::string(o) + " ";
   std::string hdrs;
   for (int i = 0; i < kJitHeaderCount; i++) hdrs += kJitHeaderTexts[i];
   char buf[32];
@@ -1038,7 +1052,7 @@ namespace {
 int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& code, std::string& error) {
   FusedConfig cfg;
   std::string const src = fused_source(p, cfg);
-  key = cache_key(src);
+  key = cache_key(src, contract_on(p));
   std::lock_guard<std::mutex> lock(g_code_mutex);
   auto it = g_code.find(key);
   if (it != g_code.end()) {
@@ -1054,7 +1068,7 @@ int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& c
   }
   if (code.empty()) {
     std::string log;
-    if (!compile(src, code, log)) {
+    if (!compile(src, contract_on(p), code, log)) {
       error = "hipRTC failed to compile the fused kernel:\n" + log;
       return PONNI_ERR_DEVICE;
     }

@@ -322,10 +322,6 @@ def test_hip_graph_capture_and_replay(cuda, path):
     check_f32(got.double().cpu().numpy(), oracle.forward(layers, x.double().cpu().numpy()), scale_tol=False)
 
 
-@pytest.mark.skip(reason="open divergence: in this chain one sample's two MinMaxNorm inputs differ by "
-                         "17 fp32 ulps, and the NARROW kernel (FUSED from the next layer on) returns "
-                         "(2.052, -0.987) there instead of (1.999994, -1): its x - min is not exactly 0 "
-                         "for the minimum, so min and x are not the same rounded value; not yet located")
 @pytest.mark.parametrize("path", ["narrow", "fused"])
 def test_state_rounded_before_min_max_norm(cuda, path):
     """Each layer's state is rounded before the next layer reads it, so
