@@ -1,25 +1,35 @@
 #!/usr/bin/env python3
 """Benchmark PONNI's batched forward pass on one MI355X.
 
-A step is one forward pass of the headline configuration (BASELINE.json
-configs[1], "c2": fp32 16->64->64->64->8 ReLU MLP, batch 4,194,304) over a
-synthetic input already resident in HBM.  Prints ONE JSON line.
+A step is one forward pass of the headline configuration over a synthetic
+input already resident in HBM.  The headline is "c4", the largest
+configuration of BASELINE.json (fp16 MLP 64->256->256->256->64 with tanh,
+fp16 operands and fp32 accumulation, batch 8,388,608); every other
+configuration is measured the same way and reported under "configs".
+Prints ONE JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--config c2] [--no-others] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--config c4] [--no-others] [--no-cpu]
+  python bench.py --trace-summary run_kernel_trace.csv --skip W   (rocprofv3 output)
 
-`value` is samples/s of the whole job (one GPU).  `roofline` prices the
-dominant kernel (the only kernel of a step) against MI355X's published peak:
-achieved = algorithmic work per sample x batch / mean kernel time, the kernel
-time measured with HIP events recorded on the launch stream around each
-launch.  `cpu_baseline` times the CPU restatement of the reference (oracle/,
-OpenMP over samples, as Kokkos' OpenMP RangePolicy) on a bounded sample on
-this host.  Other configurations are reported under "configs".
+Timing.  W untimed launches, then K timed launches back to back on one stream.
+Each timed launch goes through ponni_forward_timed, whose dispatch stamps two
+HIP events with the kernel's own start and end; two more events bracket the K
+launches.  `ms_per_step` = bracket / K and `value` = batch / ms_per_step.
+`roofline.achieved` = algorithmic work per sample x batch / the kernel's mean
+duration over the same K launches (`frac`); `frac_per_step` prices the same
+work on ms_per_step.  `roofline.traffic` = HBM bytes per launch from the
+committed rocprofv3 PMC runs (profiles/traffic.json).  `cpu_baseline` times the
+CPU restatement of the reference (oracle/, OpenMP over samples as Kokkos'
+OpenMP RangePolicy) on a bounded sample of each configuration on this host.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -27,7 +37,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "samples/sec/GPU for fused MLP forward; % of HBM or MFMA roofline"
+HEADLINE = "c4"
 ROTATE_BYTES = 512 << 20  # rotate buffers so the working set exceeds the 256 MB MALL
+C1_LARGE_BATCH = 64 << 20  # supplementary c1 entry: the same net over 67,108,864 samples
 
 
 def pmc_traffic(config_name: str):
@@ -49,6 +61,49 @@ def host_cores() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:
         return os.cpu_count() or 1
+
+
+class HipEvents:
+    """HIP events through the runtime this process already loaded (torch's)."""
+
+    def __init__(self):
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise RuntimeError("the HIP runtime is not loaded")
+        L = ctypes.CDLL(path)
+        vp = ctypes.c_void_p
+        L.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        L.hipEventDestroy.argtypes = [vp]
+        L.hipEventRecord.argtypes = [vp, vp]
+        L.hipEventSynchronize.argtypes = [vp]
+        L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        self.L = L
+
+    def create(self) -> int:
+        ev = ctypes.c_void_p()
+        self._ok(self.L.hipEventCreate(ctypes.byref(ev)), "hipEventCreate")
+        return ev.value
+
+    def destroy(self, ev: int) -> None:
+        self.L.hipEventDestroy(ev)
+
+    def record(self, ev: int, stream: int) -> None:
+        self._ok(self.L.hipEventRecord(ev, stream), "hipEventRecord")
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        self._ok(self.L.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return float(ms.value)
+
+    @staticmethod
+    def _ok(rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with HIP error {rc}")
 
 
 TORCH_DTYPES = {"f32": "float32", "f64": "float64", "f16": "float16", "bf16": "bfloat16"}
@@ -84,66 +139,72 @@ def make_inputs(cfg, torch, P, C):
     return xs, ys
 
 
-def time_config(cfg, steps, warmup, torch, P, C):
+def time_config(cfg, steps, warmup, torch, P, C, ev):
     layers = cfg.layers(False)
     model = P.create_inference_model(*layers, dtype=cfg.dtype)
     xs, ys = make_inputs(cfg, torch, P, C)
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.current_stream().cuda_stream
     B = cfg.batch
 
-    def launch(i):
+    def args(i):
         x, y = xs[i % len(xs)], ys[i % len(ys)]
-        model.forward_raw(x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), B, stream.cuda_stream)
+        return x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), B, stream
 
     for i in range(warmup):
-        launch(i)
+        model.forward_raw(*args(i))
     torch.cuda.synchronize()
-    # Whole-job timing: K back-to-back launches.
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        launch(i)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    # Per-launch kernel time: events bracket each launch on the launch stream.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        launch(i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    per = sorted(a.elapsed_time(b) for a, b in ev)
-    mean_ms = sum(per) / len(per)
+    starts = [ev.create() for _ in range(steps)]
+    stops = [ev.create() for _ in range(steps)]
+    t0, t1 = ev.create(), ev.create()
+    try:
+        ev.record(t0, stream)
+        # The rotation continues past the warm-up's buffer sets, so no timed
+        # launch finds its input still in the MALL from a recent launch.
+        for i in range(steps):
+            model.forward_raw_timed(*args(warmup + i), starts[i], stops[i])
+        ev.record(t1, stream)
+        torch.cuda.synchronize()
+        total_ms = ev.elapsed_ms(t0, t1)
+        per = [ev.elapsed_ms(a, b) for a, b in zip(starts, stops)]
+    finally:
+        for e in starts + stops + [t0, t1]:
+            ev.destroy(e)
+    ms_per_step = total_ms / steps
+    kernel_ms = sum(per) / len(per)
     work = cfg.flops_per_sample if cfg.bound == "mfma" else cfg.bytes_per_sample
-    achieved = work * B / (mean_ms * 1e-3)
     unit = "TFLOP/s" if cfg.bound == "mfma" else "GB/s"
     scale = 1e12 if cfg.bound == "mfma" else 1e9
+    achieved = work * B / (kernel_ms * 1e-3)
+    per_sorted = sorted(per)
     return {
-        "model": model,
         "layers": layers,
-        "samples_per_s": B * steps / (total_ms * 1e-3),
-        "ms_per_step": total_ms / steps,
-        "kernel_ms_mean": mean_ms,
-        "kernel_ms_min": per[0],
-        "kernel_ms_median": per[len(per) // 2],
+        "samples_per_s": B / (ms_per_step * 1e-3),
+        "ms_per_step": ms_per_step,
+        "kernel_ms_mean": kernel_ms,
+        "kernel_ms_min": per_sorted[0],
+        "kernel_ms_median": statistics.median(per_sorted),
         "roofline": {
             "bound": cfg.bound,
             "achieved": round(achieved / scale, 3),
             "peak": round(cfg.peak / scale, 3),
             "unit": unit,
             "frac": round(achieved / cfg.peak, 4),
-            # (PMC traffic is measured for the configurations' own precision only)
-            "traffic": pmc_traffic(cfg.name) if cfg.dtype == C.CONFIGS[cfg.name].dtype else None,
+            "frac_per_step": round(work * B / (ms_per_step * 1e-3) / cfg.peak, 4),
+            # (PMC traffic is measured for the configurations' own precision and batch only)
+            "traffic": (pmc_traffic(cfg.name)
+                        if cfg.dtype == C.CONFIGS[cfg.name].dtype and cfg.batch == C.CONFIGS[cfg.name].batch
+                        else None),
         },
         "path": model.path,
     }
 
 
-def cpu_baseline(cfg, budget_s=10.0):
-    """Time the oracle (CPU restatement of the reference) on a bounded sample."""
-    import numpy as np
+ORACLE_MODE_NAMES = {"f32": "fp32", "f64": "fp64", "f16": "fp16 operands, fp32 accumulation",
+                     "bf16": "bf16 operands, fp32 accumulation"}
 
+
+def cpu_baseline(cfg, budget_s):
+    """Time the oracle (CPU restatement of the reference) on a bounded sample."""
     import oracle
     from ponni_amd import configs as C
 
@@ -158,10 +219,10 @@ def cpu_baseline(cfg, budget_s=10.0):
         f = C.uniform if kind == "uniform" else C.normal
         return f(cfg.n_in * n, cfg.seed, C.INPUT_TAG, a, b).reshape(cfg.n_in, n)
 
-    # One pass over the first n columns of the workload's input (n sized from a
-    # short probe to take about a tenth of the budget), repeated until the
-    # budget is spent.
-    n = 16384
+    # One pass over n columns drawn from the workload's input distribution (n
+    # sized from a short probe to take about a tenth of the budget), repeated
+    # until the budget is spent.
+    n = 4096
     x = gen(n)
     oracle.forward(layers, x, mode, cores)  # warm the thread pool
     t0 = time.perf_counter()
@@ -180,9 +241,30 @@ def cpu_baseline(cfg, budget_s=10.0):
         "unit": "samples/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{reps} passes over the first {n} columns of {cfg.name} ({cfg.description}), "
-                   f"{total:.1f} s, OpenMP over samples"),
+        "sample": (f"{reps} passes over {n} columns of {cfg.name} ({cfg.description}; same input distribution), "
+                   f"{total:.1f} s, {ORACLE_MODE_NAMES[cfg.dtype]}, OpenMP over samples on {cores} threads"),
     }
+
+
+def summarize_trace(path: str, skip: int) -> int:
+    """Per-kernel statistics of a rocprofv3 kernel trace (CSV), one row per
+    kernel and grid size (one configuration), leaving out the first `skip`
+    dispatches of each (the bench's untimed warm-up)."""
+    rows = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+            rows.setdefault(key, []).append((int(r["Start_Timestamp"]), d))
+    print(f"| Kernel | Grid (work-items) | Dispatches (after skipping {skip}) | Average ns | Median ns | Min ns | "
+          "Max ns |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for (name, grid), v in sorted(rows.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        v.sort()
+        d = [x for _, x in v[skip:]] or [x for _, x in v]
+        print(f"| `{name[:90]}` | {grid:,} | {len(d)} | {sum(d) / len(d):,.0f} | {statistics.median(d):,.0f} | "
+              f"{min(d):,} | {max(d):,} |")
+    return 0
 
 
 def main() -> int:
@@ -190,19 +272,27 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2")
+    ap.add_argument("--config", default=HEADLINE)
+    ap.add_argument("--batch", type=int, default=None, help="override the configuration's batch (not a headline)")
     ap.add_argument("--dtype", choices=sorted(TORCH_DTYPES), default=None,
                     help="run the configuration in another precision (not the headline measurement)")
     ap.add_argument("--no-others", action="store_true", help="skip the other configurations")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU budget of the headline configuration")
+    ap.add_argument("--cpu-seconds-others", type=float, default=6.0, help="CPU budget of each other configuration")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a device copy of 256 MiB (reference for PMC byte counters)")
+    ap.add_argument("--trace-summary", metavar="CSV", help="summarize a rocprofv3 kernel trace and exit")
+    ap.add_argument("--skip", type=int, default=3, help="with --trace-summary: dispatches to drop per kernel")
     args = ap.parse_args()
+    if args.trace_summary:
+        return summarize_trace(args.trace_summary, args.skip)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the forward pass shards over the batch with no "
               "collective, and this build runs and reports a single MI355X.", file=sys.stderr)
         return 2
+
+    import dataclasses
 
     import torch
 
@@ -210,6 +300,7 @@ def main() -> int:
     from ponni_amd import configs as C
 
     torch.cuda.init()
+    ev = HipEvents()
     if args.calibrate_copy:
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0")
         P.fill_synthetic(src, 1, 2, "uniform", 0.0, 1.0)
@@ -218,24 +309,38 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     cfg = with_dtype(C.CONFIGS[args.config], args.dtype, C)
-    head = time_config(cfg, args.steps, args.warmup, torch, P, C)
+    if args.batch:
+        cfg = dataclasses.replace(cfg, batch=args.batch)
+    head = time_config(cfg, args.steps, args.warmup, torch, P, C, ev)
+    torch.cuda.empty_cache()
     others = {}
     if not args.no_others:
-        for name, c in C.CONFIGS.items():
-            if name == cfg.name:
-                continue
-            r = time_config(c, max(5, args.steps // 2), args.warmup, torch, P, C)
+        runs = [(name, c) for name, c in C.CONFIGS.items() if name != cfg.name]
+        runs.append(("c1_large", dataclasses.replace(
+            C.CONFIGS["c1"], batch=C1_LARGE_BATCH,
+            description=C.CONFIGS["c1"].description + ", supplementary batch of 67,108,864 (not a BASELINE config)")))
+        for name, c in runs:
+            r = time_config(c, max(10, args.steps // 2), args.warmup, torch, P, C, ev)
             others[name] = {
-                "samples_per_s": round(r["samples_per_s"], 1),
-                "kernel_ms_mean": round(r["kernel_ms_mean"], 4),
-                "path": r["path"],
+                "workload": c.description,
                 "batch": c.batch,
                 "dtype": c.dtype,
+                "path": r["path"],
+                "samples_per_s": round(r["samples_per_s"], 1),
+                "ms_per_step": round(r["ms_per_step"], 5),
+                "kernel_ms_mean": round(r["kernel_ms_mean"], 5),
+                "kernel_ms_min": round(r["kernel_ms_min"], 5),
+                "kernel_ms_median": round(r["kernel_ms_median"], 5),
                 "roofline": r["roofline"],
             }
             del r
             torch.cuda.empty_cache()
-    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_seconds)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, args.cpu_seconds)
+        for name in others:
+            if name in C.CONFIGS:
+                others[name]["cpu_baseline"] = cpu_baseline(C.CONFIGS[name], args.cpu_seconds_others)
     line = {
         "metric": METRIC,
         "value": round(head["samples_per_s"], 1),
@@ -243,7 +348,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["ms_per_step"], 4),
+        "ms_per_step": round(head["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -253,9 +358,9 @@ def main() -> int:
             "workload": f"{cfg.name}: {cfg.description}",
             "global_batch": cfg.batch,
             "path": head["path"],
-            "kernel_ms_mean": round(head["kernel_ms_mean"], 4),
-            "kernel_ms_min": round(head["kernel_ms_min"], 4),
-            "kernel_ms_median": round(head["kernel_ms_median"], 4),
+            "kernel_ms_mean": round(head["kernel_ms_mean"], 5),
+            "kernel_ms_min": round(head["kernel_ms_min"], 5),
+            "kernel_ms_median": round(head["kernel_ms_median"], 5),
             "parallelism": "single GPU",
         },
         "roofline": head["roofline"],

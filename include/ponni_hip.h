@@ -28,6 +28,7 @@
 
 #ifndef HIP_INCLUDE_HIP_HIP_RUNTIME_API_H
 typedef struct ihipStream_t* hipStream_t;
+typedef struct ihipEvent_t* hipEvent_t;
 #endif
 
 #ifdef __cplusplus
@@ -262,6 +263,16 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch);
  * reference aborts (ponni_Inference.h:366). */
 int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y,
                   int64_t ld_out, int64_t batch, hipStream_t stream);
+
+/* ponni_forward whose kernel dispatch stamps `start` and `stop` (events
+ * created by the caller) with its own start and end, through the runtime's
+ * extended launch, so that stop - start is the kernel's execution time with
+ * no profiler attached.  A measurement aid with no counterpart in the
+ * reference (it times forward_batch_parallel, ponni_Inference.h:352-389);
+ * same arguments, errors and asynchrony as ponni_forward. */
+int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y,
+                        int64_t ld_out, int64_t batch, hipStream_t stream,
+                        hipEvent_t start, hipEvent_t stop);
 
 /* Source text of the kernel generated for a FUSED plan -- the counterpart of
  * the per-model executor the reference instantiates at compile time

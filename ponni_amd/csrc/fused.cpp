@@ -1138,6 +1138,11 @@ hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t 
   void* y = a.y;
   int64_t ldx = a.ld_x, ldy = a.ld_y, batch = a.batch;
   void* args[] = {&params, &x, &ldx, &y, &ldy, &batch};
+  if (a.ev_start != nullptr || a.ev_stop != nullptr) {
+    unsigned const threads = 64u * unsigned(p.fused_waves);
+    return hipExtModuleLaunchKernel(p.fused_fn, static_cast<uint32_t>(grid) * threads, 1, 1, threads, 1, 1, 0, stream,
+                                    args, nullptr, a.ev_start, a.ev_stop, 0);
+  }
   return hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, 64 * p.fused_waves, 1, 1, 0, stream, args,
                                nullptr);
 }

@@ -41,10 +41,10 @@ hipError_t launch_generic(int dtype, LaunchArgs const& args, hipStream_t stream)
   dim3 const block(256);
   dim3 const grid(static_cast<unsigned>((args.batch + 255) / 256));
   switch (dtype) {
-    case PONNI_F64: hipLaunchKernelGGL(generic_forward<double>, grid, block, 0, stream, args); break;
-    case PONNI_F16: hipLaunchKernelGGL(generic_forward<__half>, grid, block, 0, stream, args); break;
-    case PONNI_BF16: hipLaunchKernelGGL(generic_forward<__hip_bfloat16>, grid, block, 0, stream, args); break;
-    default: hipLaunchKernelGGL(generic_forward<float>, grid, block, 0, stream, args); break;
+    case PONNI_F64: launch_kernel(generic_forward<double>, grid, block, 0, stream, args, args); break;
+    case PONNI_F16: launch_kernel(generic_forward<__half>, grid, block, 0, stream, args, args); break;
+    case PONNI_BF16: launch_kernel(generic_forward<__hip_bfloat16>, grid, block, 0, stream, args, args); break;
+    default: launch_kernel(generic_forward<float>, grid, block, 0, stream, args, args); break;
   }
   return hipGetLastError();
 }

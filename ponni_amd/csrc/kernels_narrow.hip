@@ -268,9 +268,9 @@ hipError_t launch_w(int num_slots, LaunchArgs const& a, hipStream_t stream) {
   int64_t const per_block = int64_t(kWaves) * 64 * P;
   dim3 const grid(static_cast<unsigned>((a.batch + per_block - 1) / per_block));
   dim3 const block(kWaves * 64);
-  if (num_slots == 0) hipLaunchKernelGGL((narrow_forward<S, W, P, 0>), grid, block, 0, stream, a);
-  else if (num_slots == 1) hipLaunchKernelGGL((narrow_forward<S, W, P, 1>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((narrow_forward<S, W, P, 2>), grid, block, 0, stream, a);
+  if (num_slots == 0) launch_kernel(narrow_forward<S, W, P, 0>, grid, block, 0, stream, a, a);
+  else if (num_slots == 1) launch_kernel(narrow_forward<S, W, P, 1>, grid, block, 0, stream, a, a);
+  else launch_kernel(narrow_forward<S, W, P, 2>, grid, block, 0, stream, a, a);
   return hipGetLastError();
 }
 

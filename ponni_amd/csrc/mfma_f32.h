@@ -378,10 +378,10 @@ hipError_t launch_ns(LaunchArgs const& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     int64_t const resident = int64_t(cus) * (per_cu > 0 ? per_cu : 1);
     dim3 const grid(static_cast<unsigned>(tiles < resident ? tiles : resident));
-    hipLaunchKernelGGL((mfma_forward_f32<MT, NS, true>), grid, block, bytes, stream, a);
+    launch_kernel(mfma_forward_f32<MT, NS, true>, grid, block, uint32_t(bytes), stream, a, a);
   } else {
     dim3 const grid(static_cast<unsigned>(tiles));
-    hipLaunchKernelGGL((mfma_forward_f32<MT, NS, false>), grid, block, 0, stream, a);
+    launch_kernel(mfma_forward_f32<MT, NS, false>, grid, block, 0, stream, a, a);
   }
   return hipGetLastError();
 }

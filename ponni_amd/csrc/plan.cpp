@@ -1011,8 +1011,10 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch) {
   return reallocate_scratch(*plan, batch);
 }
 
-int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
-                  hipStream_t stream) {
+namespace {
+
+int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                 hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
   if (plan->external)
     return fail(PONNI_ERR_UNSUPPORTED, "the plan holds external (custom) layers: run it through ponni_plan_device_model");
@@ -1056,6 +1058,8 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_
     a.buffers[BUF_TMP1 + b] = plan->d_scratch[b];
     a.buffer_ld[BUF_TMP1 + b] = plan->capacity;
   }
+  a.ev_start = ev_start;
+  a.ev_stop = ev_stop;
   hipError_t err = hipSuccess;
   switch (plan->path) {
     case PONNI_PATH_NARROW:
@@ -1068,6 +1072,19 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_
   }
   if (err != hipSuccess) return fail(PONNI_ERR_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(err));
   return PONNI_OK;
+}
+
+}  // namespace
+
+int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                  hipStream_t stream) {
+  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, nullptr, nullptr);
+}
+
+int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                        hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+  if (start == nullptr || stop == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "timing events are null");
+  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, start, stop);
 }
 
 int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {

@@ -1,6 +1,7 @@
 // Internal plan object behind the ponni_plan handle of include/ponni_hip.h.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -31,7 +32,24 @@ struct LaunchArgs {
   // generic path scratch (unused elsewhere)
   void* buffers[BUF_SAVED + kMaxSlots];
   int64_t buffer_ld[BUF_SAVED + kMaxSlots];
+  // Host side only (kernels ignore them): events the runtime stamps with the
+  // start and end of the kernel's own dispatch (ponni_forward_timed), or null.
+  hipEvent_t ev_start;
+  hipEvent_t ev_stop;
 };
+
+// Launch `kernel` on `stream`; with the timing events of `a` set, through the
+// runtime's extended launch, which stamps them with the dispatch's start and end.
+template <typename... Args, typename F = void (*)(Args...)>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t stream, LaunchArgs const& a,
+                          Args... args) {
+  void* argv[] = {static_cast<void*>(&args)...};
+  auto const fn = reinterpret_cast<void const*>(kernel);
+  if (a.ev_start != nullptr || a.ev_stop != nullptr)
+    (void)hipExtLaunchKernel(fn, grid, block, argv, shmem, stream, a.ev_start, a.ev_stop, 0);
+  else
+    (void)hipLaunchKernel(fn, grid, block, argv, shmem, stream);
+}
 
 hipError_t launch_generic(int dtype, LaunchArgs const& args, hipStream_t stream);
 hipError_t launch_narrow(int dtype, int width_class, int num_slots, LaunchArgs const& args,

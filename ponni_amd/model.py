@@ -276,6 +276,13 @@ class Inference:
     def forward_raw(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int, stream: int = 0) -> None:
         A.check(A.lib().ponni_forward(self._plan, x_ptr, ld_in, y_ptr, ld_out, batch, stream))
 
+    def forward_raw_timed(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int, stream: int,
+                          start_event: int, stop_event: int) -> None:
+        """forward_raw whose kernel dispatch stamps two caller-created HIP events
+        with its own start and end (ponni_forward_timed)."""
+        A.check(A.lib().ponni_forward_timed(self._plan, x_ptr, ld_in, y_ptr, ld_out, batch, stream, start_event,
+                                            stop_event))
+
     def forward_host(self, x, threads: int = 0):
         """Host execution space: x a numpy array [n_in, B] of the plan's dtype
         (F32 or F64 plans), evaluated on the host by the GENERIC op list

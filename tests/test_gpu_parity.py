@@ -80,6 +80,7 @@ def check_f32(got, want, scale_tol=True):
 
 def check_half(got, want, tol=2e-3):
     rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    print(f"16-bit parity: relL2={rel:.3e} (bar {tol:.1e})", flush=True)
     assert np.isfinite(got).all() and rel <= tol, f"relL2={rel:.3e}"
 
 
