@@ -264,6 +264,27 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch);
 int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y,
                   int64_t ld_out, int64_t batch, hipStream_t stream);
 
+/* ponni_forward for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * It has no counterpart in the reference.  It calls no hipMalloc, hipFree or
+ * other allocating routine: a GENERIC plan's state buffers (tmp1, tmp2 and the
+ * saved slots, [features, batch] each) are carved from one fixed device array
+ * of PONNI_NO_ALLOC_SCRATCH_BYTES per GPU, which every GPU the library runs on
+ * holds from the first call on it until the process ends; the other paths
+ * keep their states on chip and need none.  Nothing in the array has to
+ * start at zero (every state is written before it is read).
+ *   - The plan must already be on this device: one ponni_forward or
+ *     ponni_plan_device_params call (which may allocate) puts it there, and
+ *     a parameter change takes it off again; else PONNI_ERR_INVALID_ARGUMENT.
+ *   - A batch whose GENERIC state buffers exceed the array gives
+ *     PONNI_ERR_SHAPE (ponni_forward has no such limit).
+ *   - All calls on one GPU share its array: calls that overlap in time on
+ *     one GPU (different streams, or different plans without ordering) race.
+ * Otherwise the arguments, results and asynchrony of ponni_forward. */
+#define PONNI_NO_ALLOC_SCRATCH_BYTES (64ull << 20)
+int ponni_forward_no_alloc(ponni_plan plan, const void* x, int64_t ld_in, void* y,
+                           int64_t ld_out, int64_t batch, hipStream_t stream);
+
 /* ponni_forward whose kernel dispatch stamps `start` and `stop` (events
  * created by the caller) with its own start and end, through the runtime's
  * extended launch, so that stop - start is the kernel's execution time with

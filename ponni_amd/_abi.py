@@ -152,6 +152,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_reallocate_internal_state.argtypes = [vp, i64]
     L.ponni_forward.restype = ctypes.c_int
     L.ponni_forward.argtypes = [vp, vp, i64, vp, i64, i64, vp]
+    L.ponni_forward_no_alloc.restype = ctypes.c_int
+    L.ponni_forward_no_alloc.argtypes = [vp, vp, i64, vp, i64, i64, vp]
     L.ponni_forward_timed.restype = ctypes.c_int
     L.ponni_forward_timed.argtypes = [vp, vp, i64, vp, i64, i64, vp, vp, vp]
     L.ponni_plan_kernel_source.restype = i64

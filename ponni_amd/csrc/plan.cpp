@@ -1013,8 +1013,24 @@ int ponni_plan_reallocate_internal_state(ponni_plan plan, int64_t batch) {
 
 namespace {
 
+// Bytes of GENERIC state buffers (tmp1, tmp2, saved slots) for `batch`
+// columns when carved from one array, each buffer 256-byte aligned; fills
+// the byte offset of each (-1: not used).
+size_t carved_scratch_bytes(ponni_plan_s const& p, int64_t batch, int64_t (&offset)[2 + kMaxSlots]) {
+  size_t const es = element_size(p.dtype);
+  size_t total = 0;
+  for (int b = 0; b < 2 + kMaxSlots; b++) {
+    int const features = b < 2 ? p.tmp_features[b] : (b - 2 < p.num_slots ? p.saved_features[b - 2] : 0);
+    offset[b] = -1;
+    if (features <= 0) continue;
+    offset[b] = static_cast<int64_t>(total);
+    total += (es * size_t(features) * size_t(batch) + 255) / 256 * 256;
+  }
+  return total;
+}
+
 int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
-                 hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                 hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool no_alloc) {
   if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
   if (plan->external)
     return fail(PONNI_ERR_UNSUPPORTED, "the plan holds external (custom) layers: run it through ponni_plan_device_model");
@@ -1024,6 +1040,10 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   if (ld_in < batch || ld_out < batch)
     return fail(PONNI_ERR_SHAPE, "Error: Provided output dimensions do not match the model and input batch");
   if (plan->device_dirty) {
+    if (no_alloc)
+      return fail(PONNI_ERR_INVALID_ARGUMENT,
+                  "ponni_forward_no_alloc: the plan is not on the device yet (its parameters changed or it never "
+                  "ran); one ponni_forward or ponni_plan_device_params call, which may allocate, puts it there");
     int const st = upload(*plan);
     if (st != PONNI_OK) return st;
   } else {
@@ -1031,11 +1051,31 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(PONNI_ERR_DEVICE, "plan was first used on another device");
   }
-  if (plan->path == PONNI_PATH_GENERIC && batch > plan->capacity) {
-    int const st = reallocate_scratch(*plan, batch);
-    if (st != PONNI_OK) return st;
-  } else if (batch > plan->capacity) {
-    plan->capacity = batch;  // register paths keep no batch scratch
+  void* scratch[2 + kMaxSlots] = {};
+  int64_t scratch_ld = 0;
+  if (no_alloc) {
+    if (plan->path == PONNI_PATH_GENERIC) {
+      int64_t offset[2 + kMaxSlots];
+      size_t const need = carved_scratch_bytes(*plan, batch, offset);
+      if (need > kStaticScratchBytes)
+        return fail(PONNI_ERR_SHAPE, "ponni_forward_no_alloc: batch " + std::to_string(batch) + " needs " +
+                                         std::to_string(need) + " bytes of state buffers; the fixed scratch holds " +
+                                         std::to_string(kStaticScratchBytes) + " bytes (use ponni_forward)");
+      void* base = nullptr;
+      if (need > 0) HIP_TRY(static_scratch(plan->device, &base));
+      for (int b = 0; b < 2 + kMaxSlots; b++)
+        if (offset[b] >= 0) scratch[b] = static_cast<char*>(base) + offset[b];
+      scratch_ld = batch;
+    }
+  } else {
+    if (plan->path == PONNI_PATH_GENERIC && batch > plan->capacity) {
+      int const st = reallocate_scratch(*plan, batch);
+      if (st != PONNI_OK) return st;
+    } else if (batch > plan->capacity) {
+      plan->capacity = batch;  // register paths keep no batch scratch
+    }
+    for (int b = 0; b < 2 + kMaxSlots; b++) scratch[b] = plan->d_scratch[b];
+    scratch_ld = plan->capacity;
   }
   LaunchArgs a{};
   a.ops = plan->d_ops;
@@ -1055,8 +1095,8 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   a.buffers[BUF_OUTPUT] = y;
   a.buffer_ld[BUF_OUTPUT] = ld_out;
   for (int b = 0; b < 2 + kMaxSlots; b++) {
-    a.buffers[BUF_TMP1 + b] = plan->d_scratch[b];
-    a.buffer_ld[BUF_TMP1 + b] = plan->capacity;
+    a.buffers[BUF_TMP1 + b] = scratch[b];
+    a.buffer_ld[BUF_TMP1 + b] = scratch_ld;
   }
   a.ev_start = ev_start;
   a.ev_stop = ev_stop;
@@ -1078,13 +1118,18 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
 
 int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
                   hipStream_t stream) {
-  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, nullptr, nullptr);
+  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, nullptr, nullptr, false);
+}
+
+int ponni_forward_no_alloc(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
+                           hipStream_t stream) {
+  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, nullptr, nullptr, true);
 }
 
 int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
                         hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   if (start == nullptr || stop == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "timing events are null");
-  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, start, stop);
+  return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, start, stop, false);
 }
 
 int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {

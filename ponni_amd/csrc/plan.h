@@ -51,6 +51,12 @@ inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipSt
     (void)hipLaunchKernel(fn, grid, block, argv, shmem, stream);
 }
 
+// Fixed device scratch of ponni_forward_no_alloc (static_scratch.hip): the
+// device address of this device's copy (looked up on the first call with
+// `device` current; no allocation).
+constexpr size_t kStaticScratchBytes = size_t(PONNI_NO_ALLOC_SCRATCH_BYTES);
+hipError_t static_scratch(int device, void** out);
+
 hipError_t launch_generic(int dtype, LaunchArgs const& args, hipStream_t stream);
 hipError_t launch_narrow(int dtype, int width_class, int num_slots, LaunchArgs const& args,
                          hipStream_t stream);

@@ -276,6 +276,12 @@ class Inference:
     def forward_raw(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int, stream: int = 0) -> None:
         A.check(A.lib().ponni_forward(self._plan, x_ptr, ld_in, y_ptr, ld_out, batch, stream))
 
+    def forward_raw_no_alloc(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int,
+                             stream: int = 0) -> None:
+        """forward_raw with no device allocation: GENERIC state buffers come
+        from the library's fixed per-GPU scratch (ponni_forward_no_alloc)."""
+        A.check(A.lib().ponni_forward_no_alloc(self._plan, x_ptr, ld_in, y_ptr, ld_out, batch, stream))
+
     def forward_raw_timed(self, x_ptr: int, ld_in: int, y_ptr: int, ld_out: int, batch: int, stream: int,
                           start_event: int, stop_event: int) -> None:
         """forward_raw whose kernel dispatch stamps two caller-created HIP events
