@@ -17,7 +17,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libponni_oracle.so"
 
-MODE_F32, MODE_F64, MODE_F16_OPERANDS, MODE_BF16_OPERANDS, MODE_F16_CHAIN = 0, 1, 2, 3, 4
+MODE_F32, MODE_F64, MODE_F16_OPERANDS, MODE_BF16_OPERANDS, MODE_F16_CHAIN, MODE_F16_HALF2 = 0, 1, 2, 3, 4, 5
 
 _lib = None
 
@@ -43,6 +43,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_round_half.argtypes = [ctypes.c_float]
         L.oracle_round_bf16.restype = ctypes.c_float
         L.oracle_round_bf16.argtypes = [ctypes.c_float]
+        L.oracle_fma_half.restype = ctypes.c_float
+        L.oracle_fma_half.argtypes = [ctypes.c_float] * 3
+        L.oracle_add_half.restype = ctypes.c_float
+        L.oracle_add_half.argtypes = [ctypes.c_float] * 2
         _lib = L
     return _lib
 
@@ -82,6 +86,14 @@ def round_half(v: float) -> float:
 
 def round_bf16(v: float) -> float:
     return lib().oracle_round_bf16(v)
+
+
+def fma_half(a: float, b: float, c: float) -> float:
+    return lib().oracle_fma_half(a, b, c)
+
+
+def add_half(a: float, b: float) -> float:
+    return lib().oracle_add_half(a, b)
 
 
 def num_threads() -> int:

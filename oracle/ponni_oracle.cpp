@@ -22,7 +22,11 @@
 //                         the same linearized chain the product receives
 //
 // Modes: 0 fp32, 1 fp64, 2 fp16 operands with fp32 arithmetic (state rounded
-// to fp16 at every materialization), 3 the same for bf16, 4 fp16 chain.
+// to fp16 at every materialization), 3 the same for bf16, 4 fp16 chain of the
+// template half model (half_t: v += W * x rounds the product and the sum),
+// 5 fp16 chain of the generated half2 model (each dot-product step one
+// rounded fma, ponni_TwoHalf.h:97-105; activations in fp32 of the half value,
+// rounded, :138-153).
 //
 // Pinning: tests/test_oracle.py checks every function here against the
 // reference's known-answer tests (unit/core/*.cpp, unit/performance_benchmark)
@@ -40,20 +44,23 @@
 namespace {
 
 // ---- binary16 / bfloat16 rounding (IEEE round-to-nearest-even) -------------
-float round_half(float v) {
-  if (std::isnan(v) || std::isinf(v)) return v;
-  float const a = std::fabs(v);
-  if (a >= 65520.0f) return std::copysign(INFINITY, v);  // rounds past max half (65504)
-  if (a < std::ldexp(1.0f, -14)) {
-    // Subnormal range: quantum 2^-24.
-    float const q = std::ldexp(1.0f, -24);
-    return std::copysign(std::nearbyint(a / q) * q, v);
+// One rounding of a double to binary16 (the result is exact in float).
+float round_half_d(double v) {
+  if (std::isnan(v) || std::isinf(v)) return static_cast<float>(v);
+  double const a = std::fabs(v);
+  if (a >= 65520.0) return std::copysign(INFINITY, static_cast<float>(v));  // rounds past max half (65504)
+  double q;
+  if (a < std::ldexp(1.0, -14)) {
+    q = std::ldexp(1.0, -24);  // subnormal range: quantum 2^-24
+  } else {
+    int e = 0;
+    std::frexp(a, &e);        // a = m * 2^e, m in [0.5, 1)
+    q = std::ldexp(1.0, e - 11);  // 10 explicit mantissa bits
   }
-  int e = 0;
-  std::frexp(a, &e);  // a = m * 2^e, m in [0.5, 1)
-  float const q = std::ldexp(1.0f, e - 11);  // 10 explicit mantissa bits
-  return std::copysign(std::nearbyint(a / q) * q, v);
+  return static_cast<float>(std::copysign(std::nearbyint(a / q) * q, v));
 }
+
+float round_half(float v) { return round_half_d(v); }
 
 float round_bf16(float v) {
   if (std::isnan(v) || std::isinf(v)) return v;
@@ -68,19 +75,24 @@ float round_bf16(float v) {
 }
 
 // ---- arithmetic types -------------------------------------------------------
-// H16: every operation on it rounds to binary16, as Kokkos half_t on the host.
+// H16: every operation on it rounds its exact (double) result to binary16
+// once, as half_t arithmetic and the packed-half operations of
+// ponni_TwoHalf.h:97-135 (__hadd2 / __hmul2 / __hfma2) do.
 struct H16 {
   float v = 0.0f;
   H16() = default;
-  H16(double x) : v(round_half(static_cast<float>(x))) {}
+  H16(double x) : v(round_half_d(x)) {}
   explicit operator double() const { return v; }
   explicit operator float() const { return v; }
 };
-inline H16 operator+(H16 a, H16 b) { return H16(a.v + b.v); }
-inline H16 operator-(H16 a, H16 b) { return H16(a.v - b.v); }
-inline H16 operator-(H16 a) { return H16(-a.v); }
-inline H16 operator*(H16 a, H16 b) { return H16(a.v * b.v); }
-inline H16 operator/(H16 a, H16 b) { return H16(a.v / b.v); }
+inline H16 operator+(H16 a, H16 b) { return H16(double(a.v) + double(b.v)); }
+inline H16 operator-(H16 a, H16 b) { return H16(double(a.v) - double(b.v)); }
+inline H16 operator-(H16 a) { return H16(-double(a.v)); }
+inline H16 operator*(H16 a, H16 b) { return H16(double(a.v) * double(b.v)); }
+inline H16 operator/(H16 a, H16 b) { return H16(double(a.v) / double(b.v)); }
+// TwoHalf::fma (ponni_TwoHalf.h:97-105, __hfma2 on the device): a * b + c
+// rounded once (a * b of two halves is exact in double).
+inline H16 fma_half(H16 a, H16 b, H16 c) { return H16(double(a.v) * double(b.v) + double(c.v)); }
 inline H16& operator+=(H16& a, H16 b) { return a = a + b; }
 inline H16& operator/=(H16& a, H16 b) { return a = a / b; }
 inline bool operator>(H16 a, H16 b) { return a.v > b.v; }
@@ -370,6 +382,19 @@ void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_
   }
 }
 
+// One step of a dense dot product, v + w * x.  Mode 5 (the generated half2
+// chain, emitter.py:978-999: sum = TwoHalf::fma(w_splat, x, sum)) rounds it
+// once; every other mode evaluates the reference's `v += W * x`
+// (ponni_Matvec.h:74-78) in its arithmetic type (two roundings in mode 4,
+// half_t).
+template <class T>
+T dense_step(Ctx<T> const& c, T v, T w, T x) {
+  if constexpr (std::is_same_v<T, H16>) {
+    if (c.mode == 5) return fma_half(w, x, v);
+  }
+  return v + w * x;
+}
+
 // traverse_mixed_batch_parallel (ponni_Inference.h:453-555) for one sample.
 template <class T>
 void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, Buf<T> const* saved, int64_t b) {
@@ -397,9 +422,9 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
         T v = T(0);
         if (generated) {  // emitter.py:701-710: sum = bias; sum += W[f][k] x[k]
           if (bias) v = T(w[int64_t(d.n_out) * d.n_in + f]);
-          for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(f) * d.n_in + k]) * in(k, b);
+          for (int k = 0; k < d.n_in; k++) v = dense_step(c, v, T(w[int64_t(f) * d.n_in + k]), in(k, b));
         } else {
-          for (int k = 0; k < d.n_in; k++) v += T(w[int64_t(k) * d.n_out + f]) * in(k, b);
+          for (int k = 0; k < d.n_in; k++) v = dense_step(c, v, T(w[int64_t(k) * d.n_out + f]), in(k, b));
         }
         for (int e = i + 1; e < end; e++) v = pointwise<T>(c.layers[e], c.params[e], v, f);
         out(f, b) = c.store(v);
@@ -494,8 +519,8 @@ extern "C" {
 
 // Per-layer parameters are concatenated in layer order, each in the layer's
 // own layout (Matvec W [n_in, n_out]; LayerNorm gamma, beta; Projection_Add
-// W [NSAVE, n_in], bias; Dense W [n_out, n_in], bias; Const_Binary c [n_in]).  x / y are float for modes 0, 2, 3, 4 and double for
-// mode 1.  Returns 0 on success.
+// W [NSAVE, n_in], bias; Dense W [n_out, n_in], bias; Const_Binary c [n_in]).  x / y are float for modes 0, 2, 3, 4, 5
+// and double for mode 1.  Returns 0 on success.
 int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double const* params, int32_t mode,
                    void const* x, int64_t ld_x, void* y, int64_t ld_y, int64_t batch, int32_t threads) {
   if (!layers || num_layers <= 0 || batch <= 0) return 1;
@@ -534,6 +559,7 @@ int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double co
       return forward<double, double>(ls, ps, mode, static_cast<double const*>(x), ld_x, static_cast<double*>(y),
                                      ld_y, batch, threads);
     case 4:
+    case 5:
       return forward<H16, float>(ls, ps, mode, static_cast<float const*>(x), ld_x, static_cast<float*>(y), ld_y,
                                  batch, threads);
     default:
@@ -552,6 +578,8 @@ void oracle_plan_widths(ponni_layer_desc const* layers, int32_t num_layers, int3
 }
 
 float oracle_round_half(float v) { return round_half(v); }
+float oracle_fma_half(float a, float b, float c) { return fma_half(H16(a), H16(b), H16(c)).v; }
+float oracle_add_half(float a, float b) { return (H16(a) + H16(b)).v; }
 float oracle_round_bf16(float v) { return round_bf16(v); }
 
 }  // extern "C"

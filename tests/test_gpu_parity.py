@@ -151,7 +151,7 @@ def test_reduced_precision_paths(cuda, dtype, path):
               P.Gelu(16, True), P.Binop_Add(0, 16), P.Matvec(rng.standard_normal((16, 6)) * 0.3), P.Softmax(6)]
     x = rng.standard_normal((12, 3000))
     got, xg, _ = gpu_run(layers, x, dtype=dtype, path=path)
-    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
+    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
 
 
 @pytest.mark.parametrize("seed,width,blocks", [(12, 20, 3), (502, 13, 4), (507, 64, 3)])
@@ -357,7 +357,7 @@ def test_half_fused_chain_without_dense_layers(cuda, dtype):
             assert m.path == "fused"
             if want is None:
                 want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
-            check_half(got, want, 2e-3 if dtype == "f16" else 1.6e-2)
+            check_half(got, want, 2e-3)
 
 
 def test_strided_views_and_stream(cuda):
@@ -400,7 +400,7 @@ def test_random_chains_reduced_precision_fused(cuda, dtype, seed):
     layers = K.random_chain(rng, width, 2 + seed % 3)
     x = rng.standard_normal((width, 777))
     got, xg, _ = gpu_run(layers, x, dtype=dtype, path="fused", pad=2)
-    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3 if dtype == "f16" else 1.6e-2)
+    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])

@@ -8,7 +8,7 @@ v_mfma_f32_32x32x16 (fused_f16.h H32, dense_hs32), its weights packed for that
 fragment layout; every other 16-bit plan, and every plan by default, keeps the
 16x16x32 tiles.  CPU tests pin which plans take which layout and that the
 kernels compile; GPU tests check parity with the oracle's fp16-operand /
-fp32-accumulate mode (relative L2 <= 2e-3 for fp16, 1.6e-2 for bf16) and with
+fp32-accumulate mode (relative L2 <= 2e-3 for fp16 and bf16) and with
 the same plan on the default 16x16 tiles.
 """
 import math
@@ -21,7 +21,7 @@ import ponni_amd as P
 from ponni_amd import graph as G
 from tests.test_graph import lowered_with_params
 
-TOL = {"f16": 2e-3, "bf16": 1.6e-2}
+TOL = {"f16": 2e-3, "bf16": 2e-3}
 MODE = {"f16": oracle.MODE_F16_OPERANDS, "bf16": oracle.MODE_BF16_OPERANDS}
 
 

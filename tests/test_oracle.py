@@ -186,6 +186,84 @@ def test_half_rounding_matches_numpy():
     assert np.array_equal(got, want)
 
 
+def test_two_half_known_answers():
+    # unit/core/test_core_unit.cpp:1023-1058: (2, -3) + (4, 5) = (6, 2);
+    # fma((2, -3), (4, 5), (1, 2)) = (9, -13)
+    assert oracle.add_half(2.0, 4.0) == 6.0 and oracle.add_half(-3.0, 5.0) == 2.0
+    assert oracle.fma_half(2.0, 4.0, 1.0) == 9.0 and oracle.fma_half(-3.0, 5.0, 2.0) == -13.0
+
+
+def _f16(v):
+    return np.asarray(v, dtype=np.float64).astype(np.float16).astype(np.float64)
+
+
+def test_fma_half_rounds_once():
+    """TwoHalf::fma is __hfma2 on the device (ponni_TwoHalf.h:97-105): a * b + c
+    rounded once to binary16.  numpy's float64 -> float16 conversion of the
+    exact result is the reference rounding; the set includes cases where
+    rounding to fp32 first and then to fp16 gives a different answer, so a
+    double rounding fails here."""
+    rng = np.random.default_rng(5)
+    a, b, c = (_f16(rng.standard_normal(4000) * 4) for _ in range(3))
+    # 2^-11 (1 + 2^-10) * (1 - 2^-10) + (1 + 2^-10) = 1 + 2^-10 + 2^-11 - 2^-31:
+    # just below the tie between 1 + 2^-10 and 1 + 2^-9, so it rounds down
+    # once; fp32 lands on the tie and then rounds to the even 1 + 2^-9.
+    a = np.concatenate([a, [2.0 ** -11 * (1 + 2.0 ** -10)]])
+    b = np.concatenate([b, [1 - 2.0 ** -10]])
+    c = np.concatenate([c, [1 + 2.0 ** -10]])
+    exact = a * b + c  # exact: a * b has at most 22 significant bits
+    double = exact.astype(np.float32).astype(np.float16).astype(np.float64)
+    want = _f16(exact)
+    assert (double != want).any()
+    got = np.array([oracle.fma_half(float(x), float(y), float(z)) for x, y, z in zip(a, b, c)])
+    assert np.array_equal(got, want)
+
+
+def _half2_chain(layers, x, fused):
+    """Whole-batch numpy evaluation of a Matvec / Bias / Relu chain in binary16
+    arithmetic: fused -> each step of the dot product one rounded fma (the
+    generated half2 chain); else the product and the sum rounded separately
+    (template half_t)."""
+    v = _f16(x)
+    for l in layers:
+        if l.kind == P._abi.LAYER_MATVEC:
+            w = _f16(l.params.reshape(l.n_in, l.n_out))
+            s = np.zeros((l.n_out, v.shape[1]))
+            for k in range(l.n_in):  # ascending k, ponni_Matvec.h:74-78
+                p = w[k][:, None] * v[k][None, :]
+                s = _f16(p + s) if fused else _f16(_f16(p) + s)
+            v = s
+        elif l.kind == P._abi.LAYER_BIAS:
+            v = _f16(v + _f16(l.params)[:, None])
+        else:
+            v = np.maximum(v, 0.0)
+    return v
+
+
+@pytest.mark.parametrize("mode", ["half2", "half_t"])
+def test_fp16_chain_modes_match_numpy_exactly(mode):
+    rng = np.random.default_rng(17)
+    layers = [P.Matvec(rng.standard_normal((12, 24)) * 0.4), P.Bias(rng.uniform(-0.5, 0.5, 24)), P.Relu(24),
+              P.Matvec(rng.standard_normal((24, 7)) * 0.3), P.Bias(rng.uniform(-0.5, 0.5, 7))]
+    x = _f16(rng.standard_normal((12, 300)) * 3)  # fp16 inputs, as the half models take them
+    fused = mode == "half2"
+    got = run(layers, x, oracle.MODE_F16_HALF2 if fused else oracle.MODE_F16_CHAIN)
+    want = _half2_chain(layers, x, fused)
+    assert np.array_equal(got, want)
+    other = _half2_chain(layers, x, not fused)
+    assert not np.array_equal(other, want)  # the two roundings are told apart
+
+
+def test_fp16_chain_tanh_is_fp32_of_the_half_value():
+    # ponni_TwoHalf.h:148-150: tanh of each lane in fp32, rounded to half.
+    x = np.linspace(-6, 6, 4001)
+    got = run([P.Tanh(1)], x[None, :], oracle.MODE_F16_HALF2)[0]
+    want = _f16(np.tanh(_f16(x).astype(np.float32)))
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -14))) - 10)
+    assert (np.abs(got - want) <= ulp).all()
+    assert (got == want).mean() > 0.999
+
+
 def test_bf16_rounding_matches_torch():
     import torch
 
