@@ -245,6 +245,32 @@ int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer);
 int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer,
                                 const void* values, int64_t count);
 
+/* Share one parameter segment of layer `layer` with a caller-owned array
+ * instead of holding a copy: the rebind rule of src/ponni_create_model.h:10-18,
+ * where a layer whose Views already live in the model's memory space is
+ * shared with the model, so writes through the caller's View reach later
+ * forward passes (unit/core/test_core_unit.cpp:516-546).  Segment 0 is the
+ * layer's first View (Matvec / Dense / projection weights, Bias or constant
+ * vector, LayerNorm gamma), segment 1 its second (LayerNorm beta, projection
+ * or Dense bias).  The array holds the segment in the layer's own order as
+ * [rows, cols] with row stride ld (elements; rows * cols = the segment's
+ * parameter count), elements of `dtype` (PONNI_F32 / F64 / F16 / BF16), in
+ * device memory (on_device = 1) or host memory (0).
+ *   - Device arrays: each ponni_forward / ponni_forward_no_alloc /
+ *     ponni_forward_timed first re-reads them on its stream (one small gather
+ *     kernel into the plan's kernel layout), so a write the caller ordered
+ *     before the forward on that stream is seen.
+ *   - Host arrays: read at each forward call (a changed value re-uploads).
+ *   - ponni_plan_get_layer_params reads the arrays; ponni_plan_set_layer_params
+ *     writes into them (the reference deep-copies into the shared View).
+ *   - ponni_plan_device_model / ponni_plan_host_model describe the values
+ *     read at that call.
+ * The array must outlive the sharing.  values = NULL ends the sharing (the
+ * plan keeps the array's current contents).  Reads the array once now. */
+int ponni_plan_share_layer_params(ponni_plan plan, int32_t layer, int32_t segment,
+                                  const void* values, int32_t dtype, int64_t rows,
+                                  int64_t cols, int64_t ld, int32_t on_device);
+
 /* Read one layer's parameters back into host memory (same order and type). */
 int ponni_plan_get_layer_params(ponni_plan plan, int32_t layer,
                                 void* values, int64_t count);

@@ -146,6 +146,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_layer_param_count.argtypes = [vp, i32]
     L.ponni_plan_set_layer_params.restype = ctypes.c_int
     L.ponni_plan_set_layer_params.argtypes = [vp, i32, vp, i64]
+    L.ponni_plan_share_layer_params.restype = ctypes.c_int
+    L.ponni_plan_share_layer_params.argtypes = [vp, i32, i32, vp, i32, i64, i64, i64, i32]
     L.ponni_plan_get_layer_params.restype = ctypes.c_int
     L.ponni_plan_get_layer_params.argtypes = [vp, i32, vp, i64]
     L.ponni_plan_reallocate_internal_state.restype = ctypes.c_int

@@ -543,27 +543,65 @@ bool mfma_supports(ponni_plan_s const& p) {
   return true;
 }
 
-void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
-  out.assign(static_cast<size_t>(p.packed_elements), 0.0);
+// Where each parameter lands in the packed buffer of the plan's path:
+// emit(slot, kind, layer, index) names every packed slot that holds
+// parameter `index` (master-copy order) of layer `layer`; the slots it never
+// names hold zero (padding) or, in 16-bit FUSED plans, the tanh table.
+//   SLOT_VALUE  element `slot` of the packed buffer (fp32, or fp64 for F64
+//               plans): the value rounded to the plan's type
+//   SLOT_HALF   16-bit element `slot` of a 16-bit FUSED buffer: the value's
+//               fp16 / bf16 bits (v_mfma_f32_16x16x32 / 32x32x16 A-fragment
+//               order, see fused_f16.h)
+//   SLOT_WORD   32-bit word `slot` of a 16-bit FUSED buffer: the value
+//               rounded to the plan's 16-bit type, stored as fp32
+template <class Emit>
+void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
+  bool const half_fused = p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16);
+  int const vec_kind = half_fused ? SLOT_WORD : SLOT_VALUE;
   int const L = static_cast<int>(p.layers.size());
   int const W = p.width_class;
   for (int i = 0; i < L; i++) {
     ponni_layer_desc const& d = p.layers[i];
-    std::vector<double> const& src = p.params[i];
-    double* dst = out.data() + p.layer_param_offset[i];
-    auto rnd = [&](double v) { return round_to_dtype(v, p.dtype); };
-    // Dense weights W [K, N] (row k, column o) in the path's layout; a
+    int64_t const base = p.layer_param_offset[i];
+    // Dense weights W [K, N] (row k, column n) starting at parameter src0; a
     // transposed source holds W^T [N, K] (generated Dense, "output_input").
-    auto pack_dense = [&](double const* wsrc, int K, int N, double* o, bool transposed = false) {
-      auto w = [&](int64_t idx) {
-        int64_t const k = idx / N, n = idx % N;
-        return transposed ? wsrc[n * K + k] : wsrc[idx];
-      };
-      if (p.path == PONNI_PATH_GENERIC) {
-        for (int64_t e = 0; e < int64_t(K) * N; e++) o[e] = rnd(w(e));
+    auto dense = [&](int64_t src0, int K, int N, bool transposed) {
+      auto idx = [&](int k, int n) { return src0 + (transposed ? int64_t(n) * K + k : int64_t(k) * N + n); };
+      if (half_fused) {
+        int64_t const hb = 2 * base;  // 16-bit index of the layer's first word
+        if (p.mfma32) {
+          // v_mfma_f32_32x32x16 A fragment of output tile mo and 16-feature step
+          // s = 2m + u: lane l = 32hh + c, element j holds W[k][32 mo + c] with
+          // k = 32m + 8(2u + j/4) + 4hh + j%4 (fused_f16.h H32).  K, N are
+          // multiples of 32.
+          int const TN = N / 32, TS = K / 16;
+          for (int mo = 0; mo < TN; mo++)
+            for (int st = 0; st < TS; st++)
+              for (int l = 0; l < 64; l++)
+                for (int j = 0; j < 8; j++) {
+                  int const k = 32 * (st / 2) + 8 * (2 * (st % 2) + j / 4) + 4 * (l >> 5) + (j & 3);
+                  int const n = 32 * mo + (l & 31);
+                  emit(hb + ((int64_t(mo) * TS + st) * 64 + l) * 8 + j, SLOT_HALF, i, idx(k, n));
+                }
+          return;
+        }
+        // v_mfma_f32_16x16x32 A fragment of output tile mo and 32-feature
+        // step t: lane l, element j holds W[16(2t + j/4) + 4(l/16) + j%4][16 mo + l%16].
+        int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
+        for (int mo = 0; mo < TN; mo++)
+          for (int t = 0; t < TS; t++)
+            for (int l = 0; l < 64; l++)
+              for (int j = 0; j < 8; j++) {
+                int const k = 16 * (2 * t + j / 4) + 4 * (l >> 4) + (j & 3);
+                int const n = 16 * mo + (l & 15);
+                if (k < K && n < N) emit(hb + ((int64_t(mo) * TS + t) * 64 + l) * 8 + j, SLOT_HALF, i, idx(k, n));
+              }
+      } else if (p.path == PONNI_PATH_GENERIC) {
+        for (int k = 0; k < K; k++)
+          for (int n = 0; n < N; n++) emit(base + int64_t(k) * N + n, SLOT_VALUE, i, idx(k, n));
       } else if (p.path == PONNI_PATH_NARROW) {
         for (int k = 0; k < K; k++)
-          for (int n = 0; n < N; n++) o[k * W + n] = rnd(w(int64_t(k) * N + n));
+          for (int n = 0; n < N; n++) emit(base + int64_t(k) * W + n, SLOT_VALUE, i, idx(k, n));
       } else {
         // A fragment of v_mfma_f32_16x16x4f32 for output tile mo and input
         // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16].
@@ -579,44 +617,46 @@ void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
                 int const k = 16 * m + 4 * (l >> 4) + v;
                 int const r = l & 15;
                 int const n = 16 * mo + (rows_t ? (r & 3) * 4 + (r >> 2) : r);
-                double val = (k < K && n < N) ? rnd(w(int64_t(k) * N + n)) : 0.0;
-                o[((int64_t(mo) * TK + m) * 64 + l) * 4 + v] = val;
+                if (k < K && n < N) emit(base + ((int64_t(mo) * TK + m) * 64 + l) * 4 + v, SLOT_VALUE, i, idx(k, n));
               }
       }
     };
+    // n per-feature values starting at parameter src0, from packed slot base + slot0.
+    auto vec = [&](int64_t slot0, int64_t src0, int n) {
+      for (int f = 0; f < n; f++) emit(base + slot0 + f, vec_kind, i, src0 + f);
+    };
+    int64_t const size = packed_size(p, d);
     switch (d.kind) {
       case PONNI_LAYER_MATVEC:
-        pack_dense(src.data(), d.n_in, d.n_out, dst);
+        dense(0, d.n_in, d.n_out, false);
         break;
       case PONNI_LAYER_DENSE:
-        pack_dense(src.data(), d.n_in, d.n_out, dst, true);
-        if (d.flags & PONNI_FLAG_DENSE_BIAS) {
-          double* b = dst + packed_size(p, d) - vec_size(p, d.n_out);
-          for (int f = 0; f < d.n_out; f++) b[f] = rnd(src[int64_t(d.n_out) * d.n_in + f]);
-        }
+        dense(0, d.n_in, d.n_out, true);
+        if (d.flags & PONNI_FLAG_DENSE_BIAS) vec(size - vec_size(p, d.n_out), int64_t(d.n_out) * d.n_in, d.n_out);
         break;
       case PONNI_LAYER_CONST_BINARY:
       case PONNI_LAYER_BIAS:
-        for (int f = 0; f < d.n_in; f++) dst[f] = rnd(src[f]);
+        vec(0, 0, d.n_in);
         break;
-      case PONNI_LAYER_LAYER_NORM: {
-        int64_t const stride = packed_size(p, d) / 2;
-        for (int f = 0; f < d.n_in; f++) {
-          dst[f] = rnd(src[f]);
-          dst[stride + f] = rnd(src[d.n_in + f]);
-        }
+      case PONNI_LAYER_LAYER_NORM:
+        vec(0, 0, d.n_in);
+        vec(size / 2, d.n_in, d.n_in);
         break;
-      }
-      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
-        int64_t const wsize = packed_size(p, d) - vec_size(p, d.n_in);
-        pack_dense(src.data(), d.n_aux, d.n_in, dst);
-        for (int f = 0; f < d.n_in; f++) dst[wsize + f] = rnd(src[int64_t(d.n_aux) * d.n_in + f]);
+      case PONNI_LAYER_BINOP_PROJECTION_ADD:
+        dense(0, d.n_aux, d.n_in, false);
+        vec(size - vec_size(p, d.n_in), int64_t(d.n_aux) * d.n_in, d.n_in);
         break;
-      }
       default:
         break;
     }
   }
+}
+
+void pack_params(ponni_plan_s const& p, std::vector<double>& out) {
+  out.assign(static_cast<size_t>(p.packed_elements), 0.0);
+  visit_param_slots(p, [&](int64_t slot, int, int layer, int64_t idx) {
+    out[slot] = round_to_dtype(p.params[layer][idx], p.dtype);
+  });
 }
 
 // Parameters of FUSED fp16 / bf16 plans as 32-bit words: dense blocks hold
@@ -628,42 +668,6 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
     float const f = static_cast<float>(v);
     return p.dtype == PONNI_F16 ? float_to_half_bits(f) : float_to_bf16_bits(f);
   };
-  auto fbits = [&](double v) {
-    float const f = static_cast<float>(round_to_dtype(v, p.dtype));
-    uint32_t u;
-    std::memcpy(&u, &f, 4);
-    return u;
-  };
-  auto pack_dense = [&](double const* w, int K, int N, uint32_t* o, bool transposed = false) {
-    auto* h = reinterpret_cast<uint16_t*>(o);
-    if (p.mfma32) {
-      // v_mfma_f32_32x32x16 A fragment of output tile mo and 16-feature step
-      // s = 2m + u: lane l = 32hh + c, element j holds W[k][32 mo + c] with
-      // k = 32m + 8(2u + j/4) + 4hh + j%4 (fused_f16.h H32).  K, N are
-      // multiples of 32.
-      int const TN = N / 32, TS = K / 16;
-      for (int mo = 0; mo < TN; mo++)
-        for (int s = 0; s < TS; s++)
-          for (int l = 0; l < 64; l++)
-            for (int j = 0; j < 8; j++) {
-              int const k = 32 * (s / 2) + 8 * (2 * (s % 2) + j / 4) + 4 * (l >> 5) + (j & 3);
-              int const n = 32 * mo + (l & 31);
-              double const v = transposed ? w[int64_t(n) * K + k] : w[int64_t(k) * N + n];
-              h[((int64_t(mo) * TS + s) * 64 + l) * 8 + j] = bits16(v);
-            }
-      return;
-    }
-    int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
-    for (int mo = 0; mo < TN; mo++)
-      for (int t = 0; t < TS; t++)
-        for (int l = 0; l < 64; l++)
-          for (int j = 0; j < 8; j++) {
-            int const k = 16 * (2 * t + j / 4) + 4 * (l >> 4) + (j & 3);
-            int const n = 16 * mo + (l & 15);
-            double const v = (k < K && n < N) ? (transposed ? w[int64_t(n) * K + k] : w[int64_t(k) * N + n]) : 0.0;
-            h[((int64_t(mo) * TS + t) * 64 + l) * 8 + j] = (k < K && n < N) ? bits16(v) : 0;
-          }
-  };
   if (p.lut_tanh_off >= 0) {
     // tanh of every non-negative 16-bit value, evaluated in double and rounded to the type.
     auto* h = reinterpret_cast<uint16_t*>(out.data() + p.lut_tanh_off);
@@ -673,42 +677,16 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
       h[b] = bits16(std::tanh(x));
     }
   }
-  int const L = static_cast<int>(p.layers.size());
-  for (int i = 0; i < L; i++) {
-    ponni_layer_desc const& d = p.layers[i];
-    std::vector<double> const& src = p.params[i];
-    uint32_t* dst = out.data() + p.layer_param_offset[i];
-    switch (d.kind) {
-      case PONNI_LAYER_MATVEC: pack_dense(src.data(), d.n_in, d.n_out, dst); break;
-      case PONNI_LAYER_DENSE:
-        pack_dense(src.data(), d.n_in, d.n_out, dst, true);
-        if (d.flags & PONNI_FLAG_DENSE_BIAS) {
-          uint32_t* b = dst + packed_size(p, d) - round_up(d.n_out, 16);
-          for (int f = 0; f < d.n_out; f++) b[f] = fbits(src[int64_t(d.n_out) * d.n_in + f]);
-        }
-        break;
-      case PONNI_LAYER_CONST_BINARY:
-      case PONNI_LAYER_BIAS:
-        for (int f = 0; f < d.n_in; f++) dst[f] = fbits(src[f]);
-        break;
-      case PONNI_LAYER_LAYER_NORM: {
-        int64_t const stride = packed_size(p, d) / 2;
-        for (int f = 0; f < d.n_in; f++) {
-          dst[f] = fbits(src[f]);
-          dst[stride + f] = fbits(src[d.n_in + f]);
-        }
-        break;
-      }
-      case PONNI_LAYER_BINOP_PROJECTION_ADD: {
-        int64_t const wsize = packed_size(p, d) - round_up(d.n_in, 16);
-        pack_dense(src.data(), d.n_aux, d.n_in, dst);
-        for (int f = 0; f < d.n_in; f++) dst[wsize + f] = fbits(src[int64_t(d.n_aux) * d.n_in + f]);
-        break;
-      }
-      default:
-        break;
+  auto* h = reinterpret_cast<uint16_t*>(out.data());
+  visit_param_slots(p, [&](int64_t slot, int kind, int layer, int64_t idx) {
+    double const v = p.params[layer][idx];
+    if (kind == SLOT_HALF) {
+      h[slot] = bits16(v);
+    } else {
+      float const f = static_cast<float>(round_to_dtype(v, p.dtype));
+      std::memcpy(&out[slot], &f, 4);
     }
-  }
+  });
 }
 
 int element_size(int dtype) {
@@ -729,6 +707,154 @@ int param_element_size(ponni_plan_s const& p) { return p.dtype == PONNI_F64 ? 8 
     if (e_ != hipSuccess)                                                                     \
       return fail(PONNI_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));       \
   } while (0)
+
+// First parameter (master-copy order) and length of parameter segment `seg`
+// of a layer: segment 0 is its first View (Matvec / Dense / projection
+// weights, Bias / constant vector, LayerNorm gamma), segment 1 its second
+// (LayerNorm beta, projection / Dense bias).  False when it has none.
+bool segment_range(ponni_layer_desc const& d, int seg, int64_t& first, int64_t& count) {
+  first = 0;
+  count = 0;
+  switch (d.kind) {
+    case PONNI_LAYER_MATVEC: count = seg == 0 ? int64_t(d.n_in) * d.n_out : 0; break;
+    case PONNI_LAYER_BIAS:
+    case PONNI_LAYER_CONST_BINARY: count = seg == 0 ? d.n_in : 0; break;
+    case PONNI_LAYER_LAYER_NORM:
+      first = seg == 1 ? d.n_in : 0;
+      count = seg <= 1 ? d.n_in : 0;
+      break;
+    case PONNI_LAYER_BINOP_PROJECTION_ADD:
+      first = seg == 1 ? int64_t(d.n_aux) * d.n_in : 0;
+      count = seg == 0 ? int64_t(d.n_aux) * d.n_in : seg == 1 ? d.n_in : 0;
+      break;
+    case PONNI_LAYER_DENSE:
+      first = seg == 1 ? int64_t(d.n_out) * d.n_in : 0;
+      count = seg == 0 ? int64_t(d.n_out) * d.n_in : (seg == 1 && (d.flags & PONNI_FLAG_DENSE_BIAS)) ? d.n_out : 0;
+      break;
+    default: break;
+  }
+  return count > 0;
+}
+
+double load_host_element(void const* ptr, int dtype, int64_t i) {
+  switch (dtype) {
+    case PONNI_F64: return static_cast<double const*>(ptr)[i];
+    case PONNI_F16: return half_bits_to_float(static_cast<uint16_t const*>(ptr)[i]);
+    case PONNI_BF16: return bf16_bits_to_float(static_cast<uint16_t const*>(ptr)[i]);
+    default: return static_cast<float const*>(ptr)[i];
+  }
+}
+
+void store_host_element(void* ptr, int dtype, int64_t i, double v) {
+  switch (dtype) {
+    case PONNI_F64: static_cast<double*>(ptr)[i] = v; break;
+    case PONNI_F16: static_cast<uint16_t*>(ptr)[i] = float_to_half_bits(static_cast<float>(v)); break;
+    case PONNI_BF16: static_cast<uint16_t*>(ptr)[i] = float_to_bf16_bits(static_cast<float>(v)); break;
+    default: static_cast<float*>(ptr)[i] = static_cast<float>(v); break;
+  }
+}
+
+// Read shared segment `seg` of layer `i` (device or host array) into `out`.
+int read_segment(ponni_plan_s const& p, int i, int seg, std::vector<double>& out) {
+  SharedSegment const& s = p.shared[i][seg];
+  int64_t first = 0, count = 0;
+  segment_range(p.layers[i], seg, first, count);
+  out.resize(static_cast<size_t>(count));
+  int64_t const rows = count / s.cols;
+  if (s.on_device) {
+    size_t const es = element_size(s.dtype);
+    std::vector<unsigned char> stage(static_cast<size_t>(count) * es);
+    HIP_TRY(hipMemcpy2D(stage.data(), es * s.cols, s.ptr, es * s.ld, es * s.cols, rows, hipMemcpyDeviceToHost));
+    for (int64_t e = 0; e < count; e++) out[e] = load_host_element(stage.data(), s.dtype, e);
+  } else {
+    for (int64_t e = 0; e < count; e++) out[e] = load_host_element(s.ptr, s.dtype, (e / s.cols) * s.ld + e % s.cols);
+  }
+  return PONNI_OK;
+}
+
+// Write `values` into shared segment `seg` of layer `i`.
+int write_segment(ponni_plan_s const& p, int i, int seg, double const* values) {
+  SharedSegment const& s = p.shared[i][seg];
+  int64_t first = 0, count = 0;
+  segment_range(p.layers[i], seg, first, count);
+  int64_t const rows = count / s.cols;
+  if (s.on_device) {
+    size_t const es = element_size(s.dtype);
+    std::vector<unsigned char> stage(static_cast<size_t>(count) * es);
+    for (int64_t e = 0; e < count; e++) store_host_element(stage.data(), s.dtype, e, values[e]);
+    HIP_TRY(hipMemcpy2D(const_cast<void*>(s.ptr), es * s.ld, stage.data(), es * s.cols, es * s.cols, rows,
+                        hipMemcpyHostToDevice));
+  } else {
+    for (int64_t e = 0; e < count; e++)
+      store_host_element(const_cast<void*>(s.ptr), s.dtype, (e / s.cols) * s.ld + e % s.cols, values[e]);
+  }
+  return PONNI_OK;
+}
+
+// Bring the master copy up to date with the shared arrays (device ones only
+// when `device`); a change bumps the parameter version, so the GENERIC twins
+// are rebuilt, and (host arrays) marks the device copy stale.
+int pull_shared(ponni_plan_s& p, bool device) {
+  if (p.num_shared_device + p.num_shared_host == 0) return PONNI_OK;
+  bool changed = false, host_changed = false;
+  std::vector<double> v;
+  for (size_t i = 0; i < p.shared.size(); i++)
+    for (int seg = 0; seg < 2; seg++) {
+      SharedSegment const& s = p.shared[i][seg];
+      if (s.ptr == nullptr || (s.on_device && !device)) continue;
+      int const st = read_segment(p, static_cast<int>(i), seg, v);
+      if (st != PONNI_OK) return st;
+      int64_t first = 0, count = 0;
+      segment_range(p.layers[i], seg, first, count);
+      double* m = p.params[i].data() + first;
+      if (!std::equal(v.begin(), v.end(), m)) {
+        std::copy(v.begin(), v.end(), m);
+        changed = true;
+        host_changed = host_changed || !s.on_device;
+      }
+    }
+  if (changed) p.params_version++;
+  if (host_changed) p.device_dirty = true;
+  return PONNI_OK;
+}
+
+// The gather map of the device-shared segments in the plan's packed layout.
+int build_gather(ponni_plan_s& p) {
+  if (p.d_gather) (void)hipFree(p.d_gather);
+  if (p.d_gather_src) (void)hipFree(p.d_gather_src);
+  p.d_gather = nullptr;
+  p.d_gather_src = nullptr;
+  p.gather_count = 0;
+  if (p.num_shared_device == 0) return PONNI_OK;
+  std::vector<GatherSource> sources;
+  std::vector<std::array<int32_t, 2>> table(p.layers.size(), {-1, -1});
+  for (size_t i = 0; i < p.shared.size(); i++)
+    for (int seg = 0; seg < 2; seg++) {
+      SharedSegment const& s = p.shared[i][seg];
+      if (s.ptr == nullptr || !s.on_device) continue;
+      table[i][seg] = static_cast<int32_t>(sources.size());
+      sources.push_back(GatherSource{s.ptr, s.dtype, 0});
+    }
+  std::vector<GatherEntry> map;
+  visit_param_slots(p, [&](int64_t slot, int kind, int layer, int64_t idx) {
+    for (int seg = 0; seg < 2; seg++) {
+      int64_t first = 0, count = 0;
+      if (table[layer][seg] < 0 || !segment_range(p.layers[layer], seg, first, count)) continue;
+      if (idx < first || idx >= first + count) continue;
+      SharedSegment const& s = p.shared[layer][seg];
+      int64_t const e = idx - first;
+      map.push_back(GatherEntry{slot, (e / s.cols) * s.ld + e % s.cols, table[layer][seg], kind});
+    }
+  });
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_gather_src), sizeof(GatherSource) * sources.size()));
+  HIP_TRY(hipMemcpy(p.d_gather_src, sources.data(), sizeof(GatherSource) * sources.size(), hipMemcpyHostToDevice));
+  if (!map.empty()) {
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_gather), sizeof(GatherEntry) * map.size()));
+    HIP_TRY(hipMemcpy(p.d_gather, map.data(), sizeof(GatherEntry) * map.size(), hipMemcpyHostToDevice));
+  }
+  p.gather_count = static_cast<int64_t>(map.size());
+  return PONNI_OK;
+}
 
 int upload(ponni_plan_s& p) {
   int dev = 0;
@@ -775,6 +901,8 @@ int upload(ponni_plan_s& p) {
     int const st = fused_prepare(p, error);
     if (st != PONNI_OK) return fail(st, error);
   }
+  int const st = build_gather(p);
+  if (st != PONNI_OK) return st;
   p.device_dirty = false;
   return PONNI_OK;
 }
@@ -832,6 +960,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   p->layers.assign(layers, layers + num_layers);
   p->dtype = dtype;
   p->params.resize(num_layers);
+  p->shared.resize(num_layers);
   int max_width = 0;
   for (int i = 0; i < num_layers; i++) {
     auto const& d = layers[i];
@@ -932,6 +1061,8 @@ void ponni_plan_destroy(ponni_plan plan) {
     if (plan->d_ops) (void)hipFree(plan->d_ops);
     if (plan->d_steps) (void)hipFree(plan->d_steps);
     if (plan->d_params) (void)hipFree(plan->d_params);
+    if (plan->d_gather) (void)hipFree(plan->d_gather);
+    if (plan->d_gather_src) (void)hipFree(plan->d_gather_src);
     if (cur != plan->device) (void)hipSetDevice(cur);
   }
   delete plan;
@@ -982,7 +1113,55 @@ int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer, const void* valu
     auto const* v = static_cast<float const*>(values);
     for (int64_t i = 0; i < count; i++) dst[i] = v[i];
   }
+  // A shared segment is the caller's array: the new values go there too.
+  for (int seg = 0; seg < 2; seg++) {
+    int64_t first = 0, n = 0;
+    if (plan->shared[layer][seg].ptr == nullptr || !segment_range(plan->layers[layer], seg, first, n)) continue;
+    int const st = write_segment(*plan, layer, seg, dst.data() + first);
+    if (st != PONNI_OK) return st;
+  }
   plan->device_dirty = true;
+  plan->params_version++;
+  return PONNI_OK;
+}
+
+int ponni_plan_share_layer_params(ponni_plan plan, int32_t layer, int32_t segment, const void* values,
+                                  int32_t dtype, int64_t rows, int64_t cols, int64_t ld, int32_t on_device) {
+  if (plan == nullptr || layer < 0 || layer >= static_cast<int32_t>(plan->layers.size()))
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "layer index out of range");
+  int64_t first = 0, count = 0;
+  if (segment < 0 || segment > 1 || !segment_range(plan->layers[layer], segment, first, count))
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "layer " + std::to_string(layer) + " has no parameter segment " +
+                                                std::to_string(segment));
+  SharedSegment& s = plan->shared[layer][segment];
+  if (s.ptr != nullptr) {
+    // The plan keeps the array's current contents when the sharing ends or moves.
+    std::vector<double> v;
+    int const st = read_segment(*plan, layer, segment, v);
+    if (st != PONNI_OK) return st;
+    std::copy(v.begin(), v.end(), plan->params[layer].begin() + first);
+    (s.on_device ? plan->num_shared_device : plan->num_shared_host)--;
+    s = SharedSegment{};
+  }
+  if (values != nullptr) {
+    if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
+    if (rows < 0 || cols <= 0 || ld < cols || rows * cols != count)
+      return fail(PONNI_ERR_SHAPE, "layer " + std::to_string(layer) + " segment " + std::to_string(segment) +
+                                       " holds " + std::to_string(count) + " parameters; the array is [" +
+                                       std::to_string(rows) + ", " + std::to_string(cols) + "] with row stride " +
+                                       std::to_string(ld));
+    s = SharedSegment{values, dtype, on_device ? 1 : 0, cols, ld};
+    (s.on_device ? plan->num_shared_device : plan->num_shared_host)++;
+    std::vector<double> v;
+    int const st = read_segment(*plan, layer, segment, v);
+    if (st != PONNI_OK) {
+      (s.on_device ? plan->num_shared_device : plan->num_shared_host)--;
+      s = SharedSegment{};
+      return st;
+    }
+    std::copy(v.begin(), v.end(), plan->params[layer].begin() + first);
+  }
+  plan->device_dirty = true;  // rebuilds the packed copy and the gather map
   plan->params_version++;
   return PONNI_OK;
 }
@@ -990,6 +1169,8 @@ int ponni_plan_set_layer_params(ponni_plan plan, int32_t layer, const void* valu
 int ponni_plan_get_layer_params(ponni_plan plan, int32_t layer, void* values, int64_t count) {
   if (plan == nullptr || layer < 0 || layer >= static_cast<int32_t>(plan->layers.size()))
     return fail(PONNI_ERR_INVALID_ARGUMENT, "layer index out of range");
+  int const st = pull_shared(*plan, true);
+  if (st != PONNI_OK) return st;
   auto const& src = plan->params[layer];
   if (count != static_cast<int64_t>(src.size()))
     return fail(PONNI_ERR_SHAPE, "layer " + std::to_string(layer) + " holds " + std::to_string(src.size()) +
@@ -1039,6 +1220,10 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   if (x == nullptr || y == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "input or output pointer is null");
   if (ld_in < batch || ld_out < batch)
     return fail(PONNI_ERR_SHAPE, "Error: Provided output dimensions do not match the model and input batch");
+  if (plan->num_shared_host > 0) {
+    int const st = pull_shared(*plan, false);
+    if (st != PONNI_OK) return st;
+  }
   if (plan->device_dirty) {
     if (no_alloc)
       return fail(PONNI_ERR_INVALID_ARGUMENT,
@@ -1101,6 +1286,11 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   a.ev_start = ev_start;
   a.ev_stop = ev_stop;
   hipError_t err = hipSuccess;
+  if (plan->gather_count > 0) {
+    err = launch_gather(plan->d_gather, plan->gather_count, plan->d_gather_src, plan->d_params, plan->dtype, stream);
+    if (err != hipSuccess)
+      return fail(PONNI_ERR_DEVICE, std::string("shared-parameter refresh failed: ") + hipGetErrorString(err));
+  }
   switch (plan->path) {
     case PONNI_PATH_NARROW:
       err = plan->narrow_jit ? fused_launch(*plan, a, stream)
@@ -1215,6 +1405,8 @@ ponni_plan_s* generic_twin(ponni_plan_s& plan) {
 int host_twin(ponni_plan_s& plan, ponni_plan_s*& twin) {
   twin = generic_twin(plan);
   if (twin == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+  int const st = pull_shared(plan, plan.num_shared_device > 0);
+  if (st != PONNI_OK) return st;
   if (plan.host_version != plan.params_version) {
     std::vector<double> packed;
     twin->params = plan.params;
@@ -1233,6 +1425,8 @@ extern "C" {
 int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
   if (plan == nullptr || out == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "null plan or output");
   if (generic_twin(*plan) == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+  int const pst = pull_shared(*plan, true);
+  if (pst != PONNI_OK) return pst;
   ponni_plan_s& t = *plan->device_twin;
   if (plan->twin_version != plan->params_version || t.device_dirty) {
     t.params = plan->params;

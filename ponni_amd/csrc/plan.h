@@ -4,6 +4,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -50,6 +51,35 @@ inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipSt
   else
     (void)hipLaunchKernel(fn, grid, block, argv, shmem, stream);
 }
+
+// Kinds of packed parameter slots (plan.cpp visit_param_slots).
+enum SlotKind { SLOT_VALUE = 0, SLOT_HALF = 1, SLOT_WORD = 2 };
+
+// One parameter segment of a layer shared with a caller-owned array
+// (ponni_plan_share_layer_params): element e of the segment lives at element
+// (e / cols) * ld + e % cols of `ptr`, of type `dtype`.
+struct SharedSegment {
+  void const* ptr = nullptr;
+  int32_t dtype = 0;
+  int32_t on_device = 0;
+  int64_t cols = 0;
+  int64_t ld = 0;
+};
+// A packed slot that ponni_forward refreshes from a device-shared array
+// before the forward kernel, and the arrays it reads (kernels_gather.hip).
+struct GatherEntry {
+  int64_t slot;  // packed slot of kind `kind`
+  int64_t src;   // element offset in the shared array
+  int32_t seg;   // index into the GatherSource table
+  int32_t kind;  // SlotKind
+};
+struct GatherSource {
+  void const* ptr;
+  int32_t dtype;
+  int32_t pad;
+};
+hipError_t launch_gather(GatherEntry const* map, int64_t count, GatherSource const* sources, void* packed,
+                         int plan_dtype, hipStream_t stream);
 
 // Fixed device scratch of ponni_forward_no_alloc (static_scratch.hip): the
 // device address of this device's copy (looked up on the first call with
@@ -136,4 +166,13 @@ struct ponni_plan_s {
   int fused_columns_per_block = 128;
   int fused_waves = 4;  // waves per workgroup
   int fused_wps = 0;    // waves per SIMD the kernel is compiled for (0: not settled yet)
+
+  // Parameter segments shared with caller-owned arrays (two per layer at
+  // most), and the gather map that refreshes the device-shared ones.
+  std::vector<std::array<ponni_hip::SharedSegment, 2>> shared;
+  int num_shared_device = 0;
+  int num_shared_host = 0;
+  ponni_hip::GatherEntry* d_gather = nullptr;
+  ponni_hip::GatherSource* d_gather_src = nullptr;
+  int64_t gather_count = 0;
 };

@@ -147,6 +147,7 @@ class Inference:
     def __init__(self, layers: Sequence[Layer], dtype: str = "f32", path: str = "auto"):
         self.layers = list(layers)
         self.dtype = dtype
+        self._shared = {}  # arrays shared with the plan, kept alive here
         L = A.lib()
         self._plan = ctypes.c_void_p()
         A.check(L.ponni_plan_create(descs(self.layers), len(self.layers), _DTYPES[dtype], _PATHS[path],
@@ -173,6 +174,32 @@ class Inference:
         v = np.ascontiguousarray(np.asarray(values, dtype=np.float64).reshape(-1), dtype=npt)
         A.check(A.lib().ponni_plan_set_layer_params(self._plan, i, v.ctypes.data, v.size))
         self.layers[i].params = np.asarray(values, dtype=np.float64).reshape(-1).copy()
+
+    def share_layer_params(self, i: int, segment: int, array) -> None:
+        """Share parameter segment `segment` of layer i with `array` (a 1-D or
+        2-D torch tensor on the GPU or numpy array on the host, with unit
+        column stride; it must outlive the sharing), as the reference shares a
+        layer's Views with a model in the same memory space
+        (ponni_plan_share_layer_params).  None ends the sharing."""
+        if array is None:
+            A.check(A.lib().ponni_plan_share_layer_params(self._plan, i, segment, None, 0, 0, 0, 0, 0))
+            self._shared.pop((i, segment), None)
+            return
+        if hasattr(array, "data_ptr"):  # torch tensor
+            names = {"torch.float32": A.F32, "torch.float64": A.F64, "torch.float16": A.F16,
+                     "torch.bfloat16": A.BF16}
+            dt, ptr, on_device = names[str(array.dtype)], array.data_ptr(), int(array.is_cuda)
+            shape, strides = tuple(array.shape), tuple(array.stride())
+        else:
+            names = {"float32": A.F32, "float64": A.F64, "float16": A.F16}
+            dt, ptr, on_device = names[str(array.dtype)], array.ctypes.data, 0
+            shape, strides = array.shape, tuple(s // array.itemsize for s in array.strides)
+        rows, cols = (1, shape[0]) if len(shape) == 1 else shape
+        ld = cols if len(shape) == 1 else strides[0]
+        if strides[-1] != 1:
+            raise ValueError("shared arrays need unit column stride")
+        A.check(A.lib().ponni_plan_share_layer_params(self._plan, i, segment, ptr, dt, rows, cols, ld, on_device))
+        self._shared[(i, segment)] = array
 
     def get_layer_params(self, i: int) -> np.ndarray:
         npt, _ = self._param_ctype()
