@@ -13,6 +13,7 @@
 //                                weight_schema_fingerprint
 //   - the View contract          src/utils/ponni_kokkos_utils.h:11-25: rank-2
 //                                LayoutRight [features, batch] device arrays
+//   - initializers               src/initializers/ponni_initializer.h (all fifteen)
 //   - .ponni files               src/utils/ponni_safetensors.h via ponni/ponni_file.h,
 //                                load_ponni_tensor and the View copies of
 //                                src/utils/ponni_view_ops.h
@@ -21,11 +22,19 @@
 // replaced by one call of ponni_forward(), which runs a gfx950 kernel chosen
 // (and, for wide models, generated) for the whole layer chain.  Models bound
 // to the host execution space (create_inference_model(Host(), HostSpace(),
-// ...)) run on host threads through ponni_forward_host instead, on host Views.  Layers hold
-// their parameters on the host; the plan owns the packed device copy and is
-// refreshed whenever parameters change.  A View here is any type with
-// data(), extent(0), extent(1), stride(0) and a LayoutRight array_layout:
-// ponni::View below, or a Kokkos::View with Kokkos::LayoutRight.
+// ...)) run on host threads through ponni_forward_host instead, on host
+// Views.  Layers hold their parameters in Views of their memory space
+// (`params.weights`, ...); create_inference_model rebinds every layer to the
+// model's memory space (a copy only when the spaces differ) and the model
+// shares the layers' Views with its plan, which re-reads them at every
+// forward pass into its kernel layout (ponni_plan_share_layer_params), so a
+// write through a layer's View reaches the next pass, as in the reference.
+// A View here is ponni::View<T**, Space> / View<T*, Space> (View<T, Space>
+// is rank 2 too), or any type with data(), extent(), stride(), a
+// memory_space and a LayoutRight array_layout, such as a Kokkos::View with
+// Kokkos::LayoutRight: a foreign view of the layer's element type and memory
+// space is shared, any other one copied through the runtime (device memory
+// is never read on the host).
 //
 // Build: hipcc -std=c++17 -I<repo>/include -I<repo>/ponni_amd/include app.cpp
 //        -L<repo>/ponni_amd -lponni_hip
@@ -142,8 +151,8 @@ template <class real> constexpr int dtype_of() {
 
 struct LayoutRight {};
 
-// Trivially copyable handle of a View for device code (kernel arguments,
-// lambda captures): the same accessors, no ownership.
+// Trivially copyable handle of a rank-2 View for device code (kernel
+// arguments, lambda captures): the same accessors, no ownership.
 template <class T>
 struct DeviceView {
   using value_type = T;
@@ -193,53 +202,81 @@ template <> struct is_memory_space<HostSpace> : std::true_type {};
 template <class M> inline constexpr bool is_memory_space_v = is_memory_space<std::decay_t<M>>::value;
 
 // The memory space a view type declares (HIPSpace when it declares none: a
-// device pointer is what forward_batch_parallel has always taken).
+// device pointer is what forward_batch_parallel has always taken).  Kokkos
+// memory spaces map by accessibility: host-accessible ones are HostSpace.
 template <class V, class = void> struct view_memory_space { using type = HIPSpace; };
 template <class V> struct view_memory_space<V, std::void_t<typename V::memory_space>> {
+#ifdef KOKKOS_VERSION
+  using type = std::conditional_t<
+      std::is_same_v<typename V::memory_space, HostSpace> ||
+          Kokkos::SpaceAccessibility<Kokkos::DefaultHostExecutionSpace, typename V::memory_space>::accessible,
+      HostSpace, HIPSpace>;
+#else
   using type = std::conditional_t<std::is_same_v<typename V::memory_space, HostSpace>, HostSpace, HIPSpace>;
+#endif
 };
 
-// A rank-2 LayoutRight [rows, cols] array in device memory (HIPSpace, the
-// default) or host memory (HostSpace); element (r, c) at
-// data()[r * stride(0) + c].  Copies share the allocation (as Kokkos::View).
-template <class T, class Space = HIPSpace>
+namespace detail {
+// View<T, S> and View<T**, S> are rank 2, View<T*, S> rank 1 (the Kokkos
+// data-type spelling; the plain element type is kept for rank 2).
+template <class D> struct view_data { using value_type = D; static constexpr int rank = 2; };
+template <class T> struct view_data<T*> { using value_type = T; static constexpr int rank = 1; };
+template <class T> struct view_data<T**> { using value_type = T; static constexpr int rank = 2; };
+[[noreturn]] inline void view_abort(std::string const& message) {
+  std::fprintf(stderr, "%s\n", message.c_str());
+  std::fflush(stderr);
+  std::abort();
+}
+inline void view_check(hipError_t e, char const* what) {
+  if (e != hipSuccess) view_abort(std::string(what) + ": " + hipGetErrorString(e));
+}
+}  // namespace detail
+
+// A LayoutRight array in device memory (HIPSpace, the default) or host memory
+// (HostSpace): rank 2 [rows, cols] with element (r, c) at
+// data()[r * stride(0) + c], or rank 1 [n], contiguous.  Copies share the
+// allocation (as Kokkos::View does).
+template <class D, class Space = HIPSpace>
 class View {
   static_assert(is_memory_space_v<Space>, "ponni::View memory space must be HIPSpace or HostSpace");
   static constexpr bool on_host = std::is_same_v<Space, HostSpace>;
+  template <class, class> friend class View;
 
  public:
-  using value_type = T;
+  using value_type = typename detail::view_data<D>::value_type;
+  using T = value_type;
   using non_const_value_type = std::remove_const_t<T>;
   using array_layout = LayoutRight;
   using memory_space = Space;
-  static constexpr int rank = 2;
+  static constexpr int rank = detail::view_data<D>::rank;
 
   View() = default;
-  View(std::string label, std::int64_t rows, std::int64_t cols, bool zero = true)
-      : label_(std::move(label)), rows_(rows), cols_(cols), ld_(cols) {
-    if (rows < 0 || cols < 0) abort("ponni::View extents must be nonnegative");
-    if (rows * cols > 0) {
-      std::size_t const bytes = sizeof(T) * static_cast<std::size_t>(rows * cols);
-      void* p = nullptr;
-      if constexpr (on_host) {
-        p = std::calloc(static_cast<std::size_t>(rows * cols), sizeof(T));
-        if (p == nullptr) abort("ponni::View host allocation failed");
-        owner_ = std::shared_ptr<void>(p, [](void* q) { std::free(q); });
-      } else {
-        check_hip(hipMalloc(&p, bytes), "hipMalloc");
-        if (zero) check_hip(hipMemset(p, 0, bytes), "hipMemset");
-        owner_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
-      }
-      data_ = static_cast<T*>(p);
-    }
+  // rank 2: [rows, cols]; rank 1: View(label, n).  Device arrays start at zero
+  // unless `zero` is false; host arrays always do.
+  View(std::string label, std::int64_t rows, std::int64_t cols, bool zero = true) : label_(std::move(label)) {
+    static_assert(rank == 2, "a rank-1 View takes one extent");
+    allocate(rows, cols, zero);
   }
-  // Wrap caller-owned memory of this space (no ownership).
-  static View wrap(T* data, std::int64_t rows, std::int64_t cols, std::int64_t ld) {
+  View(std::string label, std::int64_t n) : label_(std::move(label)) {
+    static_assert(rank == 1, "a rank-2 View takes two extents");
+    allocate(1, n, true);
+  }
+  // The same array under another spelling of the same rank (View<T> <-> View<T**>).
+  template <class D2, class = std::enable_if_t<!std::is_same_v<D2, D> && detail::view_data<D2>::rank == rank &&
+                                               std::is_same_v<typename detail::view_data<D2>::value_type, T>>>
+  View(View<D2, Space> const& o)
+      : label_(o.label_), owner_(o.owner_), data_(o.data_), rows_(o.rows_), cols_(o.cols_), ld_(o.ld_) {}
+
+  // Caller-owned memory of this space (no ownership; `keep` holds whatever
+  // keeps it alive, e.g. the foreign view it came from).
+  static View wrap(T* data, std::int64_t rows, std::int64_t cols, std::int64_t ld,
+                   std::shared_ptr<void> keep = nullptr) {
     View v;
     v.data_ = data;
     v.rows_ = rows;
     v.cols_ = cols;
     v.ld_ = ld;
+    v.owner_ = std::move(keep);
     return v;
   }
   // Columns [c0, c1) of this view (a LayoutRight subview with stride(0) > extent(1)).
@@ -251,8 +288,8 @@ class View {
   }
   // The same contiguous elements as a [rows, cols] view (shares the allocation).
   View reshape(std::int64_t rows, std::int64_t cols) const {
-    if (rows * cols != size() || (rows_ > 1 && ld_ != cols_))
-      abort("ponni::View::reshape needs a contiguous view of the same size");
+    static_assert(rank == 2, "reshape makes a rank-2 View");
+    if (rows * cols != size() || !contiguous()) detail::view_abort("ponni::View::reshape needs a contiguous view of the same size");
     View v = *this;
     v.rows_ = rows;
     v.cols_ = cols;
@@ -261,25 +298,40 @@ class View {
   }
 
   __host__ __device__ T* data() const { return data_; }
-  __host__ __device__ std::int64_t extent(int d) const { return d == 0 ? rows_ : cols_; }
-  __host__ __device__ std::int64_t stride(int d) const { return d == 0 ? ld_ : 1; }
+  __host__ __device__ std::int64_t extent(int d) const {
+    if constexpr (rank == 1) return d == 0 ? cols_ : 1;
+    else return d == 0 ? rows_ : cols_;
+  }
+  __host__ __device__ std::int64_t stride(int d) const {
+    if constexpr (rank == 1) return 1;
+    else return d == 0 ? ld_ : 1;
+  }
   __host__ __device__ T& operator()(std::int64_t r, std::int64_t c) const { return data_[r * ld_ + c]; }
+  __host__ __device__ T& operator()(std::int64_t i) const {
+    static_assert(rank == 1, "a rank-2 View takes two indices");
+    return data_[i];
+  }
   DeviceView<T> device() const { return DeviceView<T>{data_, rows_, cols_, ld_}; }
   std::int64_t size() const { return rows_ * cols_; }
+  std::int64_t rows() const { return rows_; }  // rank 1: 1
+  std::int64_t cols() const { return cols_; }  // rank 1: n
+  std::int64_t ld() const { return ld_; }
+  bool contiguous() const { return rows_ <= 1 || ld_ == cols_; }
   bool is_allocated() const { return data_ != nullptr; }
   std::string const& label() const { return label_; }
+  std::shared_ptr<void> const& owner() const { return owner_; }
 
-  // Copies from / to a row-major [rows, cols] host array.
+  // Copies from / to a row-major host array of size() elements.
   void copy_from_host(std::vector<non_const_value_type> const& h) const {
-    if (static_cast<std::int64_t>(h.size()) != size()) abort("ponni::View::copy_from_host size mismatch");
+    if (static_cast<std::int64_t>(h.size()) != size()) detail::view_abort("ponni::View::copy_from_host size mismatch");
     if (size() == 0) return;
     if constexpr (on_host) {
       for (std::int64_t r = 0; r < rows_; r++)
         std::memcpy(const_cast<non_const_value_type*>(data_) + r * ld_, h.data() + r * cols_, sizeof(T) * cols_);
     } else {
-      check_hip(hipMemcpy2D(data_, sizeof(T) * ld_, h.data(), sizeof(T) * cols_, sizeof(T) * cols_, rows_,
-                            hipMemcpyHostToDevice),
-                "hipMemcpy2D");
+      detail::view_check(hipMemcpy2D(const_cast<non_const_value_type*>(data_), sizeof(T) * ld_, h.data(),
+                                     sizeof(T) * cols_, sizeof(T) * cols_, rows_, hipMemcpyHostToDevice),
+                         "hipMemcpy2D");
     }
   }
   std::vector<non_const_value_type> copy_to_host() const {
@@ -288,16 +340,32 @@ class View {
     if constexpr (on_host) {
       for (std::int64_t r = 0; r < rows_; r++) std::memcpy(h.data() + r * cols_, data_ + r * ld_, sizeof(T) * cols_);
     } else {
-      check_hip(hipMemcpy2D(h.data(), sizeof(T) * cols_, data_, sizeof(T) * ld_, sizeof(T) * cols_, rows_,
-                            hipMemcpyDeviceToHost),
-                "hipMemcpy2D");
+      detail::view_check(hipMemcpy2D(h.data(), sizeof(T) * cols_, data_, sizeof(T) * ld_, sizeof(T) * cols_, rows_,
+                                     hipMemcpyDeviceToHost),
+                         "hipMemcpy2D");
     }
     return h;
   }
 
  private:
-  static void check_hip(hipError_t e, char const* what) {
-    if (e != hipSuccess) abort(std::string(what) + ": " + hipGetErrorString(e));
+  void allocate(std::int64_t rows, std::int64_t cols, bool zero) {
+    if (rows < 0 || cols < 0) detail::view_abort("ponni::View extents must be nonnegative");
+    rows_ = rows;
+    cols_ = cols;
+    ld_ = cols;
+    if (rows * cols == 0) return;
+    std::size_t const bytes = sizeof(T) * static_cast<std::size_t>(rows * cols);
+    void* p = nullptr;
+    if constexpr (on_host) {
+      p = std::calloc(static_cast<std::size_t>(rows * cols), sizeof(T));
+      if (p == nullptr) detail::view_abort("ponni::View host allocation failed");
+      owner_ = std::shared_ptr<void>(p, [](void* q) { std::free(q); });
+    } else {
+      detail::view_check(hipMalloc(&p, bytes), "hipMalloc");
+      if (zero) detail::view_check(hipMemset(p, 0, bytes), "hipMemset");
+      owner_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+    }
+    data_ = static_cast<T*>(p);
   }
   std::string label_;
   std::shared_ptr<void> owner_;
@@ -338,6 +406,47 @@ constexpr void require_layout_right_views() {
   static_assert((is_layout_right_view_v<Views> && ...), "PONNI Views must use LayoutRight");
 }
 
+// ---- View operations (src/utils/ponni_view_ops.h:12-48) ----------------------------------
+
+// A copy of `v` in memory space Space (LayoutRight, contiguous rows).
+template <class Space, class D, class S>
+View<std::remove_const_t<D>, Space> create_memory_space_copy(View<D, S> const& v, Space = Space()) {
+  using R = View<std::remove_const_t<D>, Space>;
+  R out;
+  if constexpr (R::rank == 1) out = R(v.label(), v.extent(0));
+  else out = R(v.label(), v.extent(0), v.extent(1), false);
+  out.copy_from_host(v.copy_to_host());
+  return out;
+}
+template <class D, class S>
+View<std::remove_const_t<D>, HostSpace> create_host_copy(View<D, S> const& v) {
+  return create_memory_space_copy<HostSpace>(v);
+}
+template <class D, class S>
+View<std::remove_const_t<D>, HIPSpace> create_device_copy(View<D, S> const& v) {
+  return create_memory_space_copy<HIPSpace>(v);
+}
+// The elements of a contiguous rank-2 View as a rank-1 View, sharing its memory.
+template <class D, class S>
+View<typename View<D, S>::value_type*, S> flatten(View<D, S> const& v) {
+  if (!v.contiguous()) detail::view_abort("ponni::flatten needs a contiguous View");
+  return View<typename View<D, S>::value_type*, S>::wrap(v.data(), 1, v.size(), v.size(), v.owner());
+}
+// Every element of `dst` set to `value` (Kokkos::deep_copy(view, scalar)).
+template <class D, class S>
+void deep_copy(View<D, S> const& dst, typename View<D, S>::value_type const& value) {
+  dst.copy_from_host(std::vector<typename View<D, S>::non_const_value_type>(static_cast<std::size_t>(dst.size()), value));
+}
+// Element-wise copy between Views of the same size, in any memory spaces
+// (Kokkos::deep_copy(dst, src); sizes must match).
+template <class D1, class S1, class D2, class S2>
+void deep_copy(View<D1, S1> const& dst, View<D2, S2> const& src) {
+  if (dst.size() != src.size()) detail::view_abort("ponni::deep_copy: Views differ in size");
+  auto h = src.copy_to_host();
+  std::vector<typename View<D1, S1>::non_const_value_type> out(h.begin(), h.end());
+  dst.copy_from_host(out);
+}
+
 // ---- host arrays and initializers ------------------------------------------------------
 
 // A host row-major matrix used to hand weights to layer constructors.
@@ -362,84 +471,270 @@ inline std::uint64_t splitmix64(std::uint64_t z) {
   z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
   return z ^ (z >> 31);
 }
+// A seed of 0 draws a fresh one from the clock (ponni_initializer.h:20-22).
 inline std::uint64_t effective_seed(std::uint64_t seed) {
   return seed == 0 ? static_cast<std::uint64_t>(std::time(nullptr)) : seed;
 }
-// Uniform [0, 1) of element i of a fill (53 random bits).
-inline double unit(std::uint64_t seed, std::uint64_t i) {
-  return static_cast<double>(splitmix64(seed ^ splitmix64(i + 1)) >> 11) * (1.0 / 9007199254740992.0);
+// Draw k of element i's own stream, uniform on [0, 1) (53 random bits); each
+// element has its own stream so a fill does not depend on thread scheduling.
+inline double unit(std::uint64_t seed, std::uint64_t i, std::uint64_t k = 0) {
+  return static_cast<double>(splitmix64(seed ^ splitmix64(splitmix64(i + 1) + k)) >> 11) *
+         (1.0 / 9007199254740992.0);
 }
-inline double normal(std::uint64_t seed, std::uint64_t i) {
-  double const u1 = 1.0 - unit(seed, 2 * i), u2 = unit(seed, 2 * i + 1);
+// Standard normal draw k of element i (Box-Muller on two uniforms).
+inline double normal(std::uint64_t seed, std::uint64_t i, std::uint64_t k = 0) {
+  double const u1 = 1.0 - unit(seed, i, 2 * k), u2 = unit(seed, i, 2 * k + 1);
   return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+}
+inline void require_finite(double v, char const* message) {
+  if (!std::isfinite(v)) throw std::invalid_argument(message);
+}
+// The value as `real` holds it, kept below `ub` when the rounding of a draw
+// just under ub would reach it (bounds are half-open, as drand(lb, ub)).
+template <class real>
+double as_real(double v) {
+  if constexpr (std::is_same_v<real, double>) return v;
+  else return static_cast<double>(static_cast<float>(static_cast<real>(static_cast<float>(v))));
+}
+template <class real>
+double below(double v, double lb, double ub) {
+  if (as_real<real>(v) < ub || !(lb < ub)) return v;
+  if constexpr (std::is_same_v<real, double>) return std::nextafter(ub, lb);
+  float f = static_cast<float>(ub);
+  while (as_real<real>(f) >= ub) f = std::nextafter(f, -INFINITY);
+  return f;
+}
+template <class real>
+void fill_uniform(std::vector<double>& a, double lb, double ub, std::uint64_t seed) {
+  if (a.empty()) return;
+  if (lb == ub) {
+    for (double& v : a) v = lb;
+    return;
+  }
+  std::uint64_t const s = effective_seed(seed);
+  for (std::size_t i = 0; i < a.size(); i++) a[i] = below<real>(lb + (ub - lb) * unit(s, i), lb, ub);
+}
+inline void fill_normal(std::vector<double>& a, double mean, double stdev, std::uint64_t seed) {
+  if (a.empty()) return;
+  std::uint64_t const s = effective_seed(seed);
+  for (std::size_t i = 0; i < a.size(); i++) a[i] = stdev == 0.0 ? mean : mean + stdev * normal(s, i);
+}
+// Normal draws outside mean +- 2 stdev are drawn again (ponni_initializer.h:143-161).
+inline void fill_truncated_normal(std::vector<double>& a, double mean, double stdev, std::uint64_t seed) {
+  if (a.empty()) return;
+  std::uint64_t const s = effective_seed(seed);
+  for (std::size_t i = 0; i < a.size(); i++) {
+    if (stdev == 0.0) {
+      a[i] = mean;
+      continue;
+    }
+    double z = normal(s, i, 0);
+    for (std::uint64_t k = 1; std::abs(z) > 2.0; k++) z = normal(s, i, k);
+    a[i] = mean + stdev * z;
+  }
+}
+// Gram-Schmidt over the columns of a [m, n] array when m >= n, else over its
+// rows, then scaled by `gain` (ponni_initializer.h:313-377).
+inline void orthonormalize(std::vector<double>& a, int m, int n, double gain) {
+  auto at = [&](int i, int j) -> double& { return a[static_cast<std::size_t>(i) * n + j]; };
+  bool const cols = m >= n;
+  int const count = cols ? n : m, len = cols ? m : n;
+  auto el = [&](int vec, int k) -> double& { return cols ? at(k, vec) : at(vec, k); };
+  for (int j = 0; j < count; j++) {
+    for (int k = 0; k < j; k++) {
+      double dot = 0;
+      for (int i = 0; i < len; i++) dot += el(j, i) * el(k, i);
+      for (int i = 0; i < len; i++) el(j, i) -= dot * el(k, i);
+    }
+    double norm = 0;
+    for (int i = 0; i < len; i++) norm += el(j, i) * el(j, i);
+    norm = std::sqrt(norm) + 1e-20;
+    for (int i = 0; i < len; i++) el(j, i) /= norm;
+  }
+  for (double& v : a) v *= gain;
+}
+// fan_in / fan_out of a [n_in, n_out] array (a rank-1 one: its length for
+// both), ponni_initializer.h:89-107.
+template <class V>
+void fans(V const& a, double& fan_in, double& fan_out) {
+  fan_in = static_cast<double>(a.extent(0));
+  fan_out = V::rank >= 2 ? static_cast<double>(a.extent(1)) : fan_in;
+}
+// Apply a flat fill to any View (values made on the host, then copied in).
+template <class V, class F>
+void fill_view(V const& a, F&& fill) {
+  std::vector<double> v(static_cast<std::size_t>(a.size()));
+  fill(v);
+  using T = typename V::non_const_value_type;
+  std::vector<T> out(v.size());
+  for (std::size_t i = 0; i < v.size(); i++) {
+    if constexpr (std::is_same_v<T, double>) out[i] = v[i];
+    else out[i] = static_cast<T>(static_cast<float>(v[i]));
+  }
+  a.copy_from_host(out);
 }
 }  // namespace init_detail
 
-// Initializers of src/initializers/ponni_initializer.h (same parameters and
-// fan conventions: a [n_in, n_out] weight has fan_in = n_in, fan_out = n_out).
-// The random streams are this library's own (splitmix64 per element); the
-// reference's Kokkos XorShift streams are not reproduced.
+// Initializers of src/initializers/ponni_initializer.h: the same names,
+// parameters, validation (std::invalid_argument), fan conventions (a
+// [n_in, n_out] array has fan_in = n_in, fan_out = n_out) and degenerate
+// cases; fill(view) works on a View in either memory space.  The random
+// streams are this library's own (splitmix64, one stream per element; seed 0
+// draws from the clock); the reference's Kokkos XorShift streams are not
+// reproduced, so fills agree with the reference in distribution only.
 template <class real>
-struct Initializer_Random_Uniform {
-  double lb = -0.05, ub = 0.05;
-  std::uint64_t seed = 0;
-  Initializer_Random_Uniform(real lb_ = real(-0.05), real ub_ = real(0.05), std::uint64_t seed_ = 0)
-      : lb(lb_), ub(ub_), seed(seed_) {
-    if (!(lb <= ub)) throw std::invalid_argument("Initializer_Random_Uniform requires lower bound <= upper bound");
-  }
-  void fill(std::vector<double>& a, int, int) const {
-    std::uint64_t const s = init_detail::effective_seed(seed);
-    for (std::size_t i = 0; i < a.size(); i++) a[i] = lb + (ub - lb) * init_detail::unit(s, i);
-  }
+struct Initializer_None {
+  template <class V> void fill(V const&) const { require_layout_right_views<V>(); }
+  void fill(std::vector<double>&, int, int) const {}
 };
 template <class real>
-struct Initializer_Random_Normal {
-  double mean = 0, stdev = 1;
-  std::uint64_t seed = 0;
-  Initializer_Random_Normal(real m = real(0), real s = real(1), std::uint64_t sd = 0) : mean(m), stdev(s), seed(sd) {}
+struct Initializer_Random_Uniform {
+  real lb, ub;
+  std::uint64_t seed;
+  Initializer_Random_Uniform(real lb_ = real(-0.05), real ub_ = real(0.05), std::uint64_t seed_ = 0)
+      : lb(lb_), ub(ub_), seed(seed_) {
+    init_detail::require_finite(static_cast<double>(lb), "Initializer_Random_Uniform lower bound must be finite");
+    init_detail::require_finite(static_cast<double>(ub), "Initializer_Random_Uniform upper bound must be finite");
+    if (static_cast<double>(lb) > static_cast<double>(ub))
+      throw std::invalid_argument("Initializer_Random_Uniform requires lower bound <= upper bound");
+  }
   void fill(std::vector<double>& a, int, int) const {
-    std::uint64_t const s = init_detail::effective_seed(seed);
-    for (std::size_t i = 0; i < a.size(); i++) a[i] = mean + stdev * init_detail::normal(s, i);
+    init_detail::fill_uniform<real>(a, static_cast<double>(lb), static_cast<double>(ub), seed);
+  }
+  template <class V> void fill(V const& a) const {
+    init_detail::fill_view(a, [&](std::vector<double>& v) { fill(v, 0, 0); });
   }
 };
 template <class real>
 struct Initializer_Constant {
-  double value = 0;
+  real value;
   explicit Initializer_Constant(real v = real(0)) : value(v) {}
   void fill(std::vector<double>& a, int, int) const {
-    for (double& v : a) v = value;
+    for (double& v : a) v = static_cast<double>(value);
+  }
+  template <class V> void fill(V const& a) const {
+    init_detail::fill_view(a, [&](std::vector<double>& v) { fill(v, 0, 0); });
   }
 };
 template <class real> struct Initializer_Zeros : Initializer_Constant<real> { Initializer_Zeros() : Initializer_Constant<real>(real(0)) {} };
 template <class real> struct Initializer_Ones : Initializer_Constant<real> { Initializer_Ones() : Initializer_Constant<real>(real(1)) {} };
-struct Initializer_Xavier_Uniform {
-  std::uint64_t seed = 0;
-  explicit Initializer_Xavier_Uniform(std::uint64_t s = 0) : seed(s) {}
-  void fill(std::vector<double>& a, int fan_in, int fan_out) const {
-    double const lim = std::sqrt(6.0 / (fan_in + fan_out));
-    Initializer_Random_Uniform<double>(-lim, lim, seed).fill(a, fan_in, fan_out);
+template <class real>
+struct Initializer_Random_Normal {
+  real mean, stdev;
+  std::uint64_t seed;
+  Initializer_Random_Normal(real m = real(0), real s = real(1), std::uint64_t sd = 0) : mean(m), stdev(s), seed(sd) {
+    init_detail::require_finite(static_cast<double>(mean), "Initializer_Random_Normal mean must be finite");
+    init_detail::require_finite(static_cast<double>(stdev), "Initializer_Random_Normal standard deviation must be finite");
+    if (static_cast<double>(stdev) < 0)
+      throw std::invalid_argument("Initializer_Random_Normal standard deviation must be nonnegative");
+  }
+  void fill(std::vector<double>& a, int, int) const {
+    init_detail::fill_normal(a, static_cast<double>(mean), static_cast<double>(stdev), seed);
+  }
+  template <class V> void fill(V const& a) const {
+    init_detail::fill_view(a, [&](std::vector<double>& v) { fill(v, 0, 0); });
   }
 };
-struct Initializer_Xavier_Normal {
-  std::uint64_t seed = 0;
-  explicit Initializer_Xavier_Normal(std::uint64_t s = 0) : seed(s) {}
-  void fill(std::vector<double>& a, int fan_in, int fan_out) const {
-    Initializer_Random_Normal<double>(0.0, std::sqrt(2.0 / (fan_in + fan_out)), seed).fill(a, fan_in, fan_out);
+template <class real>
+struct Initializer_Truncated_Normal {
+  real mean, stdev;
+  std::uint64_t seed;
+  Initializer_Truncated_Normal(real m = real(0), real s = real(1), std::uint64_t sd = 0)
+      : mean(m), stdev(s), seed(sd) {
+    init_detail::require_finite(static_cast<double>(mean), "Initializer_Truncated_Normal mean must be finite");
+    init_detail::require_finite(static_cast<double>(stdev),
+                                "Initializer_Truncated_Normal standard deviation must be finite");
+    if (static_cast<double>(stdev) < 0)
+      throw std::invalid_argument("Initializer_Truncated_Normal standard deviation must be nonnegative");
+  }
+  void fill(std::vector<double>& a, int, int) const {
+    init_detail::fill_truncated_normal(a, static_cast<double>(mean), static_cast<double>(stdev), seed);
+  }
+  template <class V> void fill(V const& a) const {
+    init_detail::fill_view(a, [&](std::vector<double>& v) { fill(v, 0, 0); });
   }
 };
-struct Initializer_He_Uniform {
-  std::uint64_t seed = 0;
-  explicit Initializer_He_Uniform(std::uint64_t s = 0) : seed(s) {}
+
+namespace init_detail {
+// The fan-scaled initializers: a uniform limit or a normal deviation from
+// (fan_in, fan_out) (ponni_initializer.h:226-311).
+template <class real, class Derived>
+struct FanScaled {
+  std::uint64_t seed;
+  explicit FanScaled(std::uint64_t s) : seed(s) {}
   void fill(std::vector<double>& a, int fan_in, int fan_out) const {
-    double const lim = std::sqrt(6.0 / fan_in);
-    Initializer_Random_Uniform<double>(-lim, lim, seed).fill(a, fan_in, fan_out);
+    if (a.empty()) return;
+    double const fi = fan_in, fo = fan_out;
+    if (Derived::uniform) fill_uniform<real>(a, -Derived::scale(fi, fo), Derived::scale(fi, fo), seed);
+    else fill_normal(a, 0.0, Derived::scale(fi, fo), seed);
+  }
+  template <class V> void fill(V const& a) const {
+    if (a.size() == 0) return;
+    double fi = 0, fo = 0;
+    fans(a, fi, fo);
+    fill_view(a, [&](std::vector<double>& v) { fill(v, static_cast<int>(fi), static_cast<int>(fo)); });
   }
 };
-struct Initializer_He_Normal {
-  std::uint64_t seed = 0;
-  explicit Initializer_He_Normal(std::uint64_t s = 0) : seed(s) {}
-  void fill(std::vector<double>& a, int fan_in, int fan_out) const {
-    Initializer_Random_Normal<double>(0.0, std::sqrt(2.0 / fan_in), seed).fill(a, fan_in, fan_out);
+}  // namespace init_detail
+
+template <class real>
+struct Initializer_Xavier_Uniform : init_detail::FanScaled<real, Initializer_Xavier_Uniform<real>> {
+  static constexpr bool uniform = true;
+  static double scale(double fi, double fo) { return std::sqrt(6.0 / (fi + fo)); }
+  Initializer_Xavier_Uniform(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_Xavier_Uniform>(s) {}
+};
+template <class real>
+struct Initializer_Xavier_Normal : init_detail::FanScaled<real, Initializer_Xavier_Normal<real>> {
+  static constexpr bool uniform = false;
+  static double scale(double fi, double fo) { return std::sqrt(2.0 / (fi + fo)); }
+  Initializer_Xavier_Normal(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_Xavier_Normal>(s) {}
+};
+template <class real>
+struct Initializer_He_Uniform : init_detail::FanScaled<real, Initializer_He_Uniform<real>> {
+  static constexpr bool uniform = true;
+  static double scale(double fi, double) { return std::sqrt(6.0 / fi); }
+  Initializer_He_Uniform(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_He_Uniform>(s) {}
+};
+template <class real>
+struct Initializer_He_Normal : init_detail::FanScaled<real, Initializer_He_Normal<real>> {
+  static constexpr bool uniform = false;
+  static double scale(double fi, double) { return std::sqrt(2.0 / fi); }
+  Initializer_He_Normal(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_He_Normal>(s) {}
+};
+template <class real>
+struct Initializer_Lecun_Uniform : init_detail::FanScaled<real, Initializer_Lecun_Uniform<real>> {
+  static constexpr bool uniform = true;
+  static double scale(double fi, double) { return std::sqrt(3.0 / fi); }
+  Initializer_Lecun_Uniform(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_Lecun_Uniform>(s) {}
+};
+template <class real>
+struct Initializer_Lecun_Normal : init_detail::FanScaled<real, Initializer_Lecun_Normal<real>> {
+  static constexpr bool uniform = false;
+  static double scale(double fi, double) { return std::sqrt(1.0 / fi); }
+  Initializer_Lecun_Normal(std::uint64_t s = 0) : init_detail::FanScaled<real, Initializer_Lecun_Normal>(s) {}
+};
+// Orthonormal rows or columns of a Gaussian draw, times `gain`; rank-1 arrays
+// get the standard normal draw (ponni_initializer.h:313-377).
+template <class real>
+struct Initializer_Orthogonal {
+  real gain;
+  std::uint64_t seed;
+  Initializer_Orthogonal(real g = real(1), std::uint64_t s = 0) : gain(g), seed(s) {
+    init_detail::require_finite(static_cast<double>(gain), "Initializer_Orthogonal gain must be finite");
+  }
+  void fill(std::vector<double>& a, int m, int n) const {
+    if (a.empty()) return;
+    init_detail::fill_normal(a, 0.0, 1.0, seed);
+    if (m > 0 && n > 0 && static_cast<std::size_t>(m) * n == a.size())
+      init_detail::orthonormalize(a, m, n, static_cast<double>(gain));
+  }
+  template <class V> void fill(V const& a) const {
+    require_layout_right_views<V>();
+    if (a.size() == 0) return;
+    init_detail::fill_view(a, [&](std::vector<double>& v) {
+      if constexpr (V::rank == 2) fill(v, static_cast<int>(a.extent(0)), static_cast<int>(a.extent(1)));
+      else init_detail::fill_normal(v, 0.0, 1.0, seed);
+    });
   }
 };
 
@@ -497,35 +792,23 @@ __host__ __device__ inline Real apply_fused_layer(Real value, int feature, typen
 }
 
 // ---- layers -----------------------------------------------------------------------------
+// Each layer template takes the reference's arguments plus a trailing
+// MemorySpace (src/layers/*.h), holds its parameters in Views of that space
+// (`params.weights` ...), and can be rebound: rebind_memory_space<M> names the
+// same layer in M, copy_to_memory_space(M) returns one holding copies of its
+// Views.  A model shares its layers' Views (create_inference_model rebinds
+// every layer to the model's memory space first): each forward pass reads
+// them, so a write through a layer's View reaches the next pass.
 
 namespace detail {
 
-// Common state of every built-in layer: the C-ABI descriptor and the host
-// master copy of its parameters in the layer's own order.
-struct LayerCore {
+// Label and C-ABI descriptor of a built-in layer.
+struct LayerBase {
   ponni_layer_desc desc{};
-  std::vector<double> params;
-  bool trainable = false;
   char const* label = "";
-  std::uint64_t version = 0;  // bumped on every parameter change
-
   int get_num_inputs() const { return desc.n_in; }
   int get_num_outputs() const { return desc.n_out; }
   char const* get_label() const { return label; }
-  int get_num_trainable_parameters() const { return trainable ? static_cast<int>(params.size()) : 0; }
-
-  // Consume the first get_num_trainable_parameters() values (ponni_Matvec.h:103-109).
-  template <class Vec>
-  void set_trainable_parameters(Vec const& in) {
-    if (!trainable) return;
-    if (static_cast<std::int64_t>(in.size()) < static_cast<std::int64_t>(params.size()))
-      abort(std::string("ERROR: ") + label + " trainable input too small");
-    for (std::size_t i = 0; i < params.size(); i++) params[i] = static_cast<double>(in[i]);
-    version++;
-  }
-  std::vector<double> get_trainable_parameters() const { return trainable ? params : std::vector<double>(); }
-  // Call after writing `params` directly.
-  void mark_modified() { version++; }
 };
 
 inline ponni_layer_desc make_desc(int kind, int n_in, int n_out, int slot = 0, int n_aux = 0, int flags = 0,
@@ -543,270 +826,525 @@ inline ponni_layer_desc make_desc(int kind, int n_in, int n_out, int slot = 0, i
   return d;
 }
 
-template <class M>
-std::vector<double> flatten(M const& m) {
-  std::vector<double> v(static_cast<std::size_t>(m.extent(0)) * m.extent(1));
-  for (int i = 0; i < static_cast<int>(m.extent(0)); i++)
-    for (int j = 0; j < static_cast<int>(m.extent(1)); j++)
-      v[static_cast<std::size_t>(i) * m.extent(1) + j] = static_cast<double>(m(i, j));
-  return v;
+// Whether A looks like a view (data(), extent(), stride() and a declared
+// memory space), and the element type it holds.
+template <class A, class = void> struct is_view_like : std::false_type {};
+template <class A>
+struct is_view_like<A, std::void_t<typename A::memory_space, decltype(std::declval<A const&>().data()),
+                                   decltype(std::declval<A const&>().extent(0)),
+                                   decltype(std::declval<A const&>().stride(0))>> : std::true_type {};
+template <class A> struct is_ponni_view : std::false_type {};
+template <class D, class S> struct is_ponni_view<View<D, S>> : std::true_type {};
+
+template <class A, class = void> struct has_call2 : std::false_type {};
+template <class A>
+struct has_call2<A, std::void_t<decltype(std::declval<A const&>()(0, 0)), decltype(std::declval<A const&>().extent(1))>>
+    : std::true_type {};
+template <class A, class = void> struct has_index : std::false_type {};
+template <class A>
+struct has_index<A, std::void_t<decltype(std::declval<A const&>()[0]), decltype(std::declval<A const&>().size())>>
+    : std::true_type {};
+// A rank-2 array argument (view or host matrix) and a rank-1 one (rank-1
+// view, rank-2 view of one row or column, or a host vector).
+template <class A, bool VIEW = is_view_like<A>::value> struct array_rank { static constexpr int value = 0; };
+template <class A> struct array_rank<A, true> { static constexpr int value = static_cast<int>(A::rank); };
+template <class A>
+struct array_rank<A, false> {
+  static constexpr int value = has_call2<A>::value ? 2 : has_index<A>::value ? 1 : 0;
+};
+template <class A>
+inline constexpr bool is_array2d_v = array_rank<A>::value == 2;
+template <class A>
+inline constexpr bool is_array1d_v = array_rank<A>::value == 1 || (is_view_like<A>::value && array_rank<A>::value == 2);
+
+// The elements of a view-like array (any memory space, any row stride) as
+// a row-major host vector of doubles: device memory is copied, never
+// dereferenced on the host.
+template <class A>
+std::vector<double> host_values(A const& a) {
+  if constexpr (is_ponni_view<A>::value) {
+    auto const h = a.copy_to_host();
+    std::vector<double> out(h.size());
+    for (std::size_t i = 0; i < h.size(); i++) out[i] = static_cast<double>(static_cast<float>(h[i]));
+    if constexpr (std::is_same_v<typename A::non_const_value_type, double>)
+      for (std::size_t i = 0; i < h.size(); i++) out[i] = h[i];
+    return out;
+  } else if constexpr (is_view_like<A>::value) {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(a.data())>>;
+    std::int64_t const rows = A::rank >= 2 ? static_cast<std::int64_t>(a.extent(0)) : 1;
+    std::int64_t const cols = static_cast<std::int64_t>(A::rank >= 2 ? a.extent(1) : a.extent(0));
+    std::int64_t const ld = A::rank >= 2 ? static_cast<std::int64_t>(a.stride(0)) : cols;
+    std::vector<T> h(static_cast<std::size_t>(rows * cols));
+    if (rows * cols > 0) {
+      if constexpr (std::is_same_v<typename view_memory_space<A>::type, HostSpace>) {
+        for (std::int64_t r = 0; r < rows; r++)
+          for (std::int64_t c = 0; c < cols; c++) h[r * cols + c] = a.data()[r * ld + c];
+      } else {
+        view_check(hipMemcpy2D(h.data(), sizeof(T) * cols, a.data(), sizeof(T) * ld, sizeof(T) * cols, rows,
+                               hipMemcpyDeviceToHost),
+                   "hipMemcpy2D");
+      }
+    }
+    return std::vector<double>(h.begin(), h.end());
+  } else if constexpr (has_call2<A>::value) {
+    std::vector<double> v(static_cast<std::size_t>(a.extent(0)) * a.extent(1));
+    for (int i = 0; i < static_cast<int>(a.extent(0)); i++)
+      for (int j = 0; j < static_cast<int>(a.extent(1)); j++)
+        v[static_cast<std::size_t>(i) * a.extent(1) + j] = static_cast<double>(a(i, j));
+    return v;
+  } else {
+    std::vector<double> out(a.size());
+    for (std::size_t i = 0; i < out.size(); i++) out[i] = static_cast<double>(a[i]);
+    return out;
+  }
 }
 
-template <class V>
-std::vector<double> flatten1(V const& v) {
-  std::vector<double> out(v.size());
-  for (std::size_t i = 0; i < out.size(); i++) out[i] = static_cast<double>(v[i]);
+// A View<real, Space> of rank R made from values (copied in).
+template <class real, class Space, int R>
+auto view_from_values(char const* label, std::int64_t rows, std::int64_t cols, std::vector<double> const& v) {
+  using V = std::conditional_t<R == 1, View<real*, Space>, View<real**, Space>>;
+  V out;
+  if constexpr (R == 1) out = V(label, cols);
+  else out = V(label, rows, cols, false);
+  std::vector<real> h(v.size());
+  for (std::size_t i = 0; i < v.size(); i++) {
+    if constexpr (std::is_same_v<real, double>) h[i] = v[i];
+    else h[i] = static_cast<real>(static_cast<float>(v[i]));
+  }
+  out.copy_from_host(h);
   return out;
 }
 
-// ponni::View arguments (device or host memory) are read through a host copy.
-template <class T, class Space>
-std::vector<double> flatten(View<T, Space> const& m) {
-  auto const h = m.copy_to_host();
-  return std::vector<double>(h.begin(), h.end());
+// The View a layer holds for a constructor argument: the argument itself when
+// it is already a View of the layer's element type and memory space (or a
+// foreign view of them, wrapped and kept alive), so the layer shares it;
+// otherwise a copy in the layer's memory space.  R is the View's rank; a
+// rank-1 View may come from a rank-2 array of one row or one column.
+template <class real, class Space, int R, class A>
+auto layer_view(char const* label, A const& a) {
+  using V = std::conditional_t<R == 1, View<real*, Space>, View<real**, Space>>;
+  if constexpr (is_view_like<A>::value) {
+    std::int64_t const e0 = static_cast<std::int64_t>(a.extent(0));
+    std::int64_t const e1 = A::rank >= 2 ? static_cast<std::int64_t>(a.extent(1)) : 1;
+    std::int64_t const ld = A::rank >= 2 ? static_cast<std::int64_t>(a.stride(0)) : e0;
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(a.data())>>;
+    if constexpr (std::is_same_v<T, real> && std::is_same_v<typename view_memory_space<A>::type, Space>) {
+      std::shared_ptr<void> keep;
+      if constexpr (is_ponni_view<A>::value) keep = a.owner();
+      else keep = std::make_shared<A>(a);
+      auto* p = const_cast<T*>(a.data());
+      if constexpr (R == 1) {
+        // rank 1, or one row, or one column (stride ld between elements)
+        if (A::rank == 1 || e0 == 1) return V::wrap(p, 1, A::rank == 1 ? e0 : e1, A::rank == 1 ? e0 : e1, keep);
+        if (e1 == 1 && ld == 1) return V::wrap(p, 1, e0, e0, keep);
+      } else if (A::rank == 2) {
+        return V::wrap(p, e0, e1, ld, keep);
+      }
+    }
+    std::int64_t const n = e0 * e1;
+    return view_from_values<real, Space, R>(label, R == 1 ? 1 : e0, R == 1 ? n : e1, host_values(a));
+  } else {
+    std::vector<double> v = host_values(a);
+    std::int64_t rows = 1;
+    if constexpr (has_call2<A>::value) rows = static_cast<std::int64_t>(a.extent(0));
+    std::int64_t const cols = static_cast<std::int64_t>(v.size()) / std::max<std::int64_t>(rows, 1);
+    return view_from_values<real, Space, R>(label, R == 1 ? 1 : rows, R == 1 ? static_cast<std::int64_t>(v.size()) : cols, v);
+  }
 }
-template <class T, class Space>
-std::vector<double> flatten1(View<T, Space> const& v) {
-  return detail::flatten(v);
+
+// Write host values into a View (any space, any row stride), converted.
+template <class V>
+void store_values(V const& v, std::vector<double> const& values) {
+  using T = typename V::non_const_value_type;
+  std::vector<T> h(values.size());
+  for (std::size_t i = 0; i < values.size(); i++) {
+    if constexpr (std::is_same_v<T, double>) h[i] = values[i];
+    else h[i] = static_cast<T>(static_cast<float>(values[i]));
+  }
+  v.copy_from_host(h);
+}
+
+// Trainable input of set_trainable_parameters (a View in any space or a
+// host vector) as host doubles.
+template <class A>
+std::vector<double> trainable_values(A const& in) {
+  return host_values(in);
 }
 
 }  // namespace detail
 
-// Dense layer, W [n_in, n_out] (ponni_Matvec.h).  Constructors: (num_inputs,
-// num_outputs, trainable, initializer) or (weights [n_in, n_out], trainable).
-template <class real = float, int N_IN = 1, int N_OUT = 1>
-struct Matvec : detail::LayerCore {
+// Dense layer, W [n_in, n_out] (ponni_Matvec.h).
+template <class real = float, int N_IN = 1, int N_OUT = 1, class MemorySpace = HIPSpace>
+struct Matvec : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Matvec<real, N_IN, N_OUT, NewMemorySpace>;
+  using real1d = View<real*, MemorySpace>;
+  using real2d = View<real**, MemorySpace>;
+  static constexpr bool overwrite_input = false, binop = false, save = false;
   static constexpr LayerFusionKind fusion_kind = LayerFusionKind::dense;
   static constexpr int INPUT_SIZE = N_IN, OUTPUT_SIZE = N_OUT;
+  struct Params {
+    real2d weights;
+    bool trainable = true;
+  };
+  Params params;
+
   Matvec() = default;
   template <class INIT = Initializer_Random_Uniform<real>>
-  Matvec(int num_inputs, int num_outputs, bool trainable_ = true, INIT init = INIT()) {
-    std::vector<double> w(static_cast<std::size_t>(num_inputs) * num_outputs);
-    init.fill(w, num_inputs, num_outputs);
-    setup(num_inputs, num_outputs, std::move(w), trainable_);
+  Matvec(int num_inputs, int num_outputs, bool trainable = true, INIT initializer = INIT()) {
+    real2d w("Matvec_weights", num_inputs, num_outputs);
+    initializer.fill(w);
+    init(w, trainable);
   }
-  template <class M, class = decltype(std::declval<M const&>()(0, 0))>
-  explicit Matvec(M const& weights, bool trainable_ = true) {
-    setup(static_cast<int>(weights.extent(0)), static_cast<int>(weights.extent(1)), detail::flatten(weights),
-          trainable_);
+  // Weights [n_in, n_out]: a View of this element type and memory space (or a
+  // foreign view of them) is shared; anything else is copied.
+  template <class A, class = std::enable_if_t<detail::is_array2d_v<A>>>
+  explicit Matvec(A const& weights, bool trainable = true) {
+    init(detail::layer_view<real, MemorySpace, 2>("Matvec_weights", weights), trainable);
   }
-  void setup(int n_in, int n_out, std::vector<double> w, bool t) {
-    if (n_in <= 0 || n_out <= 0) abort("ERROR: Matvec weights dimensions must be nonzero");
-    desc = detail::make_desc(PONNI_LAYER_MATVEC, n_in, n_out);
-    params = std::move(w);
-    trainable = t;
+  void init(real2d const& weights, bool trainable = true) {
+    if (!weights.is_allocated()) abort("ERROR: Matvec weights matrix not is_allocated");
+    params.weights = weights;
+    params.trainable = trainable;
+    desc = detail::make_desc(PONNI_LAYER_MATVEC, static_cast<int>(weights.extent(0)), static_cast<int>(weights.extent(1)));
     label = "Matvec";
   }
-  // W(k, j) of the [n_in, n_out] weights.
-  double weight(int k, int j) const { return params[static_cast<std::size_t>(k) * desc.n_out + j]; }
-  void validate() const {
-    if (desc.n_in <= 0 || desc.n_out <= 0) abort("ERROR: Matvec weights dimensions must be nonzero");
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& space = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(create_memory_space_copy(params.weights, space), params.trainable);
   }
+  using detail::LayerBase::get_num_inputs;
+  using detail::LayerBase::get_num_outputs;
+  static int get_num_inputs(Params const& p) { return static_cast<int>(p.weights.extent(0)); }
+  static int get_num_outputs(Params const& p) { return static_cast<int>(p.weights.extent(1)); }
+  int get_num_trainable_parameters() const { return params.trainable ? static_cast<int>(params.weights.size()) : 0; }
+  // Consume the first get_num_trainable_parameters() values (ponni_Matvec.h:103-109).
+  template <class A>
+  void set_trainable_parameters(A const& in) {
+    if (!params.trainable) return;
+    auto v = detail::trainable_values(in);
+    if (static_cast<std::int64_t>(v.size()) < params.weights.size()) abort("ERROR: Matvec trainable input too small");
+    v.resize(static_cast<std::size_t>(params.weights.size()));
+    detail::store_values(params.weights, v);
+  }
+  real1d get_trainable_parameters() const { return params.trainable ? flatten(params.weights) : real1d(); }
+  // W(k, j) of the [n_in, n_out] weights, read from the View.
+  double weight(int k, int j) const {
+    return detail::host_values(params.weights)[static_cast<std::size_t>(k) * desc.n_out + j];
+  }
+  void validate() const {
+    if (!params.weights.is_allocated()) abort("ERROR: weights not is_allocated");
+    if (params.weights.extent(0) == 0 || params.weights.extent(1) == 0)
+      abort("ERROR: Matvec weights dimensions must be nonzero");
+  }
+  template <class F> void for_each_segment(F&& f) const { f(0, params.weights); }
 };
 
-// Bias (ponni_Bias.h): (num_inputs, trainable, initializer) or (weights, trainable).
-template <class real = float, int N = 1>
-struct Bias : detail::LayerCore {
+// Bias (ponni_Bias.h): b [n], added after the dot product.
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Bias : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Bias<real, N, NewMemorySpace>;
+  using real1d = View<real*, MemorySpace>;
+  static constexpr bool overwrite_input = true, binop = false, save = false;
   static constexpr LayerFusionKind fusion_kind = LayerFusionKind::pointwise;
   static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    real1d weights;
+    bool trainable = true;
+  };
+  Params params;
+
   Bias() = default;
   template <class INIT = Initializer_Random_Uniform<real>>
-  Bias(int num_inputs, bool trainable_ = true, INIT init = INIT()) {
-    std::vector<double> b(static_cast<std::size_t>(num_inputs));
-    init.fill(b, num_inputs, num_inputs);
-    setup(std::move(b), trainable_);
+  Bias(int num_inputs, bool trainable = true, INIT initializer = INIT()) {
+    real1d b("Bias_weights", num_inputs);
+    initializer.fill(b);
+    init(b, trainable);
   }
-  template <class V, class = decltype(std::declval<V const&>()[0]), class = decltype(std::declval<V const&>().size())>
-  explicit Bias(V const& weights, bool trainable_ = true) {
-    setup(detail::flatten1(weights), trainable_);
+  // b: a rank-1 View (or one row / column of a rank-2 one) of this element
+  // type and memory space is shared; host vectors and other Views are copied.
+  template <class A, class = std::enable_if_t<detail::is_array1d_v<A>>>
+  explicit Bias(A const& weights, bool trainable = true) {
+    init(detail::layer_view<real, MemorySpace, 1>("Bias_weights", weights), trainable);
   }
-  // A [1, n] or [n, 1] View (load_ponni_tensor<1>), in any memory space.
-  template <class T, class Space>
-  explicit Bias(View<T, Space> const& weights, bool trainable_ = true) {
-    setup(detail::flatten1(weights), trainable_);
-  }
-  void setup(std::vector<double> b, bool t) {
-    int const n = static_cast<int>(b.size());
+  void init(real1d const& weights, bool trainable = true) {
+    if (!weights.is_allocated()) abort("ERROR: Bias weights not is_allocated");
+    params.weights = weights;
+    params.trainable = trainable;
+    int const n = static_cast<int>(weights.extent(0));
     desc = detail::make_desc(PONNI_LAYER_BIAS, n, n);
-    params = std::move(b);
-    trainable = t;
     label = "Bias";
   }
-  void validate() const {
-    if (desc.n_in <= 0) abort("ERROR: Bias weights dimension must be nonzero");
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& space = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(create_memory_space_copy(params.weights, space), params.trainable);
   }
+  using detail::LayerBase::get_num_inputs;
+  using detail::LayerBase::get_num_outputs;
+  static int get_num_inputs(Params const& p) { return static_cast<int>(p.weights.extent(0)); }
+  static int get_num_outputs(Params const& p) { return static_cast<int>(p.weights.extent(0)); }
+  int get_num_trainable_parameters() const { return params.trainable ? static_cast<int>(params.weights.size()) : 0; }
+  template <class A>
+  void set_trainable_parameters(A const& in) {
+    if (!params.trainable) return;
+    auto v = detail::trainable_values(in);
+    if (static_cast<std::int64_t>(v.size()) < params.weights.size()) abort("ERROR: Bias trainable input too small");
+    v.resize(static_cast<std::size_t>(params.weights.size()));
+    detail::store_values(params.weights, v);
+  }
+  real1d get_trainable_parameters() const { return params.trainable ? params.weights : real1d(); }
+  void validate() const {
+    if (!params.weights.is_allocated()) abort("ERROR: weights not is_allocated");
+    if (params.weights.extent(0) == 0) abort("ERROR: Bias weights dimension must be nonzero");
+  }
+  template <class F> void for_each_segment(F&& f) const { f(0, params.weights); }
 };
 
 namespace detail {
-// Parameter-free pointwise / barrier layers share this shape.
-template <int KIND>
-struct Simple : LayerCore {
+// Parameter-free pointwise / barrier layers: one descriptor, rebound freely.
+template <int KIND, template <class, int, class> class Self, class real, int N, class MemorySpace>
+struct SimpleLayer : LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Self<real, N, NewMemorySpace>;
+  static constexpr bool overwrite_input = true, binop = false, save = false;
   static constexpr LayerFusionKind fusion_kind =
       (KIND == PONNI_LAYER_SOFTMAX || KIND == PONNI_LAYER_LOG_SOFTMAX || KIND == PONNI_LAYER_MIN_MAX_NORM)
           ? LayerFusionKind::barrier
           : LayerFusionKind::pointwise;
-  Simple() = default;
-  Simple(int n, char const* lbl, int flags = 0, double a0 = 0, double a1 = 0, double a2 = 0) {
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    int num_inputs = 0;
+  };
+  SimpleLayer() = default;
+  SimpleLayer(int n, char const* lbl, int flags = 0, double a0 = 0, double a1 = 0, double a2 = 0) {
     desc = make_desc(KIND, n, n, 0, 0, flags, a0, a1, a2);
     label = lbl;
   }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& = NewMemorySpace()) const {
+    rebind_memory_space<NewMemorySpace> out;
+    out.desc = desc;
+    out.label = label;
+    return out;
+  }
+  int get_num_trainable_parameters() const { return 0; }
+  template <class A> void set_trainable_parameters(A const&) {}
+  View<real*, MemorySpace> get_trainable_parameters() const { return {}; }
   void validate() const {
     if (desc.n_in <= 0) abort(std::string("ERROR: ") + label + " num_inputs must be > 0");
   }
+  template <class F> void for_each_segment(F&&) const {}
 };
 }  // namespace detail
 
-template <class real = float, int N = 1>
-struct Relu : detail::Simple<PONNI_LAYER_RELU> {
-  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+#define PONNI_SIMPLE_LAYER_BASE(NAME, KIND) detail::SimpleLayer<KIND, NAME, real, N, MemorySpace>
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Relu : PONNI_SIMPLE_LAYER_BASE(Relu, PONNI_LAYER_RELU) {
   Relu() = default;
-  explicit Relu(int n) : Simple(n, "ReLU") {}
+  explicit Relu(int n) : Relu::SimpleLayer(n, "ReLU") {}
 };
-template <class real = float, int N = 1>
-struct LeakyRelu : detail::Simple<PONNI_LAYER_LEAKY_RELU> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct LeakyRelu : PONNI_SIMPLE_LAYER_BASE(LeakyRelu, PONNI_LAYER_LEAKY_RELU) {
   LeakyRelu() = default;
   explicit LeakyRelu(int n, real negative_slope = real(0.01))
-      : Simple(n, "LeakyReLU", 0, static_cast<double>(negative_slope)) {}
+      : LeakyRelu::SimpleLayer(n, "LeakyReLU", 0, static_cast<double>(negative_slope)) {}
 };
-template <class real = float, int N = 1>
-struct Elu : detail::Simple<PONNI_LAYER_ELU> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Elu : PONNI_SIMPLE_LAYER_BASE(Elu, PONNI_LAYER_ELU) {
   Elu() = default;
-  explicit Elu(int n, real alpha = real(1)) : Simple(n, "ELU", 0, static_cast<double>(alpha)) {
+  explicit Elu(int n, real alpha = real(1)) : Elu::SimpleLayer(n, "ELU", 0, static_cast<double>(alpha)) {
     if (!(static_cast<double>(alpha) > 0)) abort("ERROR: ELU alpha must be > 0");
   }
 };
-template <class real = float, int N = 1>
-struct Selu : detail::Simple<PONNI_LAYER_SELU> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Selu : PONNI_SIMPLE_LAYER_BASE(Selu, PONNI_LAYER_SELU) {
   Selu() = default;
-  explicit Selu(int n) : Simple(n, "SELU") {}
+  explicit Selu(int n) : Selu::SimpleLayer(n, "SELU") {}
 };
-template <class real = float, int N = 1>
-struct Gelu : detail::Simple<PONNI_LAYER_GELU> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Gelu : PONNI_SIMPLE_LAYER_BASE(Gelu, PONNI_LAYER_GELU) {
   Gelu() = default;
   explicit Gelu(int n, bool approximate = false)
-      : Simple(n, "GELU", approximate ? PONNI_FLAG_GELU_APPROXIMATE : 0) {}
+      : Gelu::SimpleLayer(n, "GELU", approximate ? PONNI_FLAG_GELU_APPROXIMATE : 0) {}
 };
-template <class real = float, int N = 1>
-struct Silu : detail::Simple<PONNI_LAYER_SILU> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Silu : PONNI_SIMPLE_LAYER_BASE(Silu, PONNI_LAYER_SILU) {
   Silu() = default;
-  explicit Silu(int n) : Simple(n, "SiLU") {}
+  explicit Silu(int n) : Silu::SimpleLayer(n, "SiLU") {}
 };
-template <class real = float, int N = 1>
-struct Sigmoid : detail::Simple<PONNI_LAYER_SIGMOID> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Sigmoid : PONNI_SIMPLE_LAYER_BASE(Sigmoid, PONNI_LAYER_SIGMOID) {
   Sigmoid() = default;
-  explicit Sigmoid(int n) : Simple(n, "Sigmoid") {}
+  explicit Sigmoid(int n) : Sigmoid::SimpleLayer(n, "Sigmoid") {}
 };
-template <class real = float, int N = 1>
-struct Tanh : detail::Simple<PONNI_LAYER_TANH> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Tanh : PONNI_SIMPLE_LAYER_BASE(Tanh, PONNI_LAYER_TANH) {
   Tanh() = default;
-  explicit Tanh(int n) : Simple(n, "Tanh") {}
+  explicit Tanh(int n) : Tanh::SimpleLayer(n, "Tanh") {}
 };
-template <class real = float, int N = 1>
-struct Softplus : detail::Simple<PONNI_LAYER_SOFTPLUS> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Softplus : PONNI_SIMPLE_LAYER_BASE(Softplus, PONNI_LAYER_SOFTPLUS) {
   Softplus() = default;
-  explicit Softplus(int n, real beta = real(1)) : Simple(n, "Softplus", 0, static_cast<double>(beta)) {
+  explicit Softplus(int n, real beta = real(1)) : Softplus::SimpleLayer(n, "Softplus", 0, static_cast<double>(beta)) {
     if (!(static_cast<double>(beta) > 0)) abort("ERROR: Softplus beta must be > 0");
   }
 };
-template <class real = float, int N = 1>
-struct HardSigmoid : detail::Simple<PONNI_LAYER_HARD_SIGMOID> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct HardSigmoid : PONNI_SIMPLE_LAYER_BASE(HardSigmoid, PONNI_LAYER_HARD_SIGMOID) {
   HardSigmoid() = default;
   explicit HardSigmoid(int n, real alpha = real(0.2), real beta = real(0.5))
-      : Simple(n, "HardSigmoid", 0, static_cast<double>(alpha), static_cast<double>(beta)) {}
+      : HardSigmoid::SimpleLayer(n, "HardSigmoid", 0, static_cast<double>(alpha), static_cast<double>(beta)) {}
 };
-template <class real = float, int N = 1>
-struct HardSwish : detail::Simple<PONNI_LAYER_HARD_SWISH> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct HardSwish : PONNI_SIMPLE_LAYER_BASE(HardSwish, PONNI_LAYER_HARD_SWISH) {
   HardSwish() = default;
-  explicit HardSwish(int n) : Simple(n, "HardSwish") {}
+  explicit HardSwish(int n) : HardSwish::SimpleLayer(n, "HardSwish") {}
 };
-template <class real = float, int N = 1>
-struct Mish : detail::Simple<PONNI_LAYER_MISH> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Mish : PONNI_SIMPLE_LAYER_BASE(Mish, PONNI_LAYER_MISH) {
   Mish() = default;
-  explicit Mish(int n) : Simple(n, "Mish") {}
+  explicit Mish(int n) : Mish::SimpleLayer(n, "Mish") {}
 };
-template <class real = float, int N = 1>
-struct Softmax : detail::Simple<PONNI_LAYER_SOFTMAX> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Softmax : PONNI_SIMPLE_LAYER_BASE(Softmax, PONNI_LAYER_SOFTMAX) {
   Softmax() = default;
-  explicit Softmax(int n) : Simple(n, "Softmax") {}
+  explicit Softmax(int n) : Softmax::SimpleLayer(n, "Softmax") {}
 };
-template <class real = float, int N = 1>
-struct LogSoftmax : detail::Simple<PONNI_LAYER_LOG_SOFTMAX> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct LogSoftmax : PONNI_SIMPLE_LAYER_BASE(LogSoftmax, PONNI_LAYER_LOG_SOFTMAX) {
   LogSoftmax() = default;
-  explicit LogSoftmax(int n) : Simple(n, "LogSoftmax") {}
+  explicit LogSoftmax(int n) : LogSoftmax::SimpleLayer(n, "LogSoftmax") {}
 };
-template <class real = float, int N = 1>
-struct MinMaxNorm : detail::Simple<PONNI_LAYER_MIN_MAX_NORM> {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct MinMaxNorm : PONNI_SIMPLE_LAYER_BASE(MinMaxNorm, PONNI_LAYER_MIN_MAX_NORM) {
   MinMaxNorm() = default;
   explicit MinMaxNorm(int n, real out_min = real(0), real out_max = real(1), real epsilon = real(1e-12))
-      : Simple(n, "MinMaxNorm", 0, static_cast<double>(out_min), static_cast<double>(out_max),
-               static_cast<double>(epsilon)) {}
+      : MinMaxNorm::SimpleLayer(n, "MinMaxNorm", 0, static_cast<double>(out_min), static_cast<double>(out_max),
+                                static_cast<double>(epsilon)) {}
 };
+#undef PONNI_SIMPLE_LAYER_BASE
 
 // LayerNorm (ponni_LayerNorm.h): gamma = 1, beta = 0 by default; trainable [gamma; beta].
-template <class real = float, int N = 1>
-struct LayerNorm : detail::LayerCore {
+template <class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct LayerNorm : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = LayerNorm<real, N, NewMemorySpace>;
+  using real1d = View<real*, MemorySpace>;
+  static constexpr bool overwrite_input = true, binop = false, save = false;
+  static constexpr int INPUT_SIZE = N, OUTPUT_SIZE = N;
+  struct Params {
+    real1d gamma;
+    real1d beta;
+    real epsilon = real(1e-5);
+    bool trainable = true;
+  };
+  Params params;
+
   LayerNorm() = default;
-  explicit LayerNorm(int n, real epsilon = real(1e-5), bool trainable_ = true) {
-    std::vector<double> p(2 * static_cast<std::size_t>(n), 0.0);
-    for (int i = 0; i < n; i++) p[i] = 1.0;
-    setup(n, std::move(p), epsilon, trainable_);
+  explicit LayerNorm(int n, real epsilon = real(1e-5), bool trainable = true) {
+    real1d g("LayerNorm_gamma", n), b("LayerNorm_beta", n);
+    deep_copy(g, real(1));
+    init(g, b, epsilon, trainable);
   }
-  template <class V, class = decltype(std::declval<V const&>()[0])>
-  LayerNorm(V const& gamma, V const& beta, real epsilon = real(1e-5), bool trainable_ = true) {
+  template <class A, class B, class = std::enable_if_t<detail::is_array1d_v<A> && detail::is_array1d_v<B>>>
+  LayerNorm(A const& gamma, B const& beta, real epsilon = real(1e-5), bool trainable = true) {
+    init(detail::layer_view<real, MemorySpace, 1>("LayerNorm_gamma", gamma),
+         detail::layer_view<real, MemorySpace, 1>("LayerNorm_beta", beta), epsilon, trainable);
+  }
+  void init(real1d const& gamma, real1d const& beta, real epsilon, bool trainable) {
     if (gamma.size() != beta.size()) abort("ERROR: LayerNorm gamma/beta sizes differ");
-    std::vector<double> p = detail::flatten1(gamma), b = detail::flatten1(beta);
-    p.insert(p.end(), b.begin(), b.end());
-    setup(static_cast<int>(gamma.size()), std::move(p), epsilon, trainable_);
-  }
-  template <class T, class Space>
-  LayerNorm(View<T, Space> const& gamma, View<T, Space> const& beta, real epsilon = real(1e-5),
-            bool trainable_ = true) {
-    if (gamma.size() != beta.size()) abort("ERROR: LayerNorm gamma/beta sizes differ");
-    std::vector<double> p = detail::flatten1(gamma), b = detail::flatten1(beta);
-    p.insert(p.end(), b.begin(), b.end());
-    setup(static_cast<int>(gamma.size()), std::move(p), epsilon, trainable_);
-  }
-  void setup(int n, std::vector<double> p, real epsilon, bool t) {
     if (!(static_cast<double>(epsilon) > 0)) abort("ERROR: LayerNorm epsilon must be > 0");
+    params.gamma = gamma;
+    params.beta = beta;
+    params.epsilon = epsilon;
+    params.trainable = trainable;
+    int const n = static_cast<int>(gamma.extent(0));
     desc = detail::make_desc(PONNI_LAYER_LAYER_NORM, n, n, 0, 0, 0, static_cast<double>(epsilon));
-    params = std::move(p);
-    trainable = t;
     label = "LayerNorm";
   }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& space = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(create_memory_space_copy(params.gamma, space),
+                                               create_memory_space_copy(params.beta, space), params.epsilon,
+                                               params.trainable);
+  }
+  int get_num_trainable_parameters() const { return params.trainable ? static_cast<int>(2 * params.gamma.size()) : 0; }
+  template <class A>
+  void set_trainable_parameters(A const& in) {
+    if (!params.trainable) return;
+    auto v = detail::trainable_values(in);
+    std::size_t const n = static_cast<std::size_t>(params.gamma.size());
+    if (v.size() < 2 * n) abort("ERROR: LayerNorm trainable input too small");
+    detail::store_values(params.gamma, std::vector<double>(v.begin(), v.begin() + n));
+    detail::store_values(params.beta, std::vector<double>(v.begin() + n, v.begin() + 2 * n));
+  }
+  real1d get_trainable_parameters() const {
+    if (!params.trainable) return real1d();
+    auto g = detail::host_values(params.gamma), b = detail::host_values(params.beta);
+    g.insert(g.end(), b.begin(), b.end());
+    return detail::view_from_values<real, MemorySpace, 1>("LayerNorm_trainable", 1, static_cast<std::int64_t>(g.size()), g);
+  }
   void validate() const {}
+  template <class F> void for_each_segment(F&& f) const {
+    f(0, params.gamma);
+    f(1, params.beta);
+  }
 };
 
 // Residual plumbing (ponni_Save_State.h, ponni_Binop_*.h).  ISAVE selects the
 // saved-state slot, as the reference's first template argument.
-template <int ISAVE, class real = float, int N = 1>
-struct Save_State : detail::LayerCore {
-  static constexpr bool save = true, binop = false;
+template <int ISAVE, class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Save_State : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Save_State<ISAVE, real, N, NewMemorySpace>;
+  static constexpr bool overwrite_input = true, save = true, binop = false;
   static constexpr int index = ISAVE;
   Save_State() = default;
   explicit Save_State(int n) {
     desc = detail::make_desc(PONNI_LAYER_SAVE_STATE, n, n, ISAVE);
     label = "Save_State";
   }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(desc.n_in);
+  }
+  int get_num_trainable_parameters() const { return 0; }
+  template <class A> void set_trainable_parameters(A const&) {}
+  View<real*, MemorySpace> get_trainable_parameters() const { return {}; }
   void validate() const {}
+  template <class F> void for_each_segment(F&&) const {}
 };
 
-template <int ISAVE, class real = float, int N = 1>
-struct Binop_Add : detail::LayerCore {
-  static constexpr bool save = false, binop = true;
+template <int ISAVE, class real = float, int N = 1, class MemorySpace = HIPSpace>
+struct Binop_Add : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Binop_Add<ISAVE, real, N, NewMemorySpace>;
+  static constexpr bool overwrite_input = true, save = false, binop = true;
   static constexpr int index = ISAVE;
   Binop_Add() = default;
   explicit Binop_Add(int n) {
     desc = detail::make_desc(PONNI_LAYER_BINOP_ADD, n, n, ISAVE);
     label = "Binop_Add";
   }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(desc.n_in);
+  }
+  int get_num_trainable_parameters() const { return 0; }
+  template <class A> void set_trainable_parameters(A const&) {}
+  View<real*, MemorySpace> get_trainable_parameters() const { return {}; }
   void validate(int saved_n) const {
     if (saved_n != desc.n_in) abort("ERROR: Saved layer num inputs != this layer's num inputs");
   }
+  template <class F> void for_each_segment(F&&) const {}
 };
 
-template <int ISAVE, class real = float, int N1 = 1, int N2 = 1>
-struct Binop_Concatenate : detail::LayerCore {
-  static constexpr bool save = false, binop = true;
+template <int ISAVE, class real = float, int N1 = 1, int N2 = 1, class MemorySpace = HIPSpace>
+struct Binop_Concatenate : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace> using rebind_memory_space = Binop_Concatenate<ISAVE, real, N1, N2, NewMemorySpace>;
+  static constexpr bool overwrite_input = true, save = false, binop = true;
   static constexpr int index = ISAVE;
   Binop_Concatenate() = default;
   Binop_Concatenate(int num_inputs, int num_outputs, bool after = true) {
@@ -814,42 +1352,90 @@ struct Binop_Concatenate : detail::LayerCore {
                              after ? PONNI_FLAG_CONCAT_AFTER : 0);
     label = "Binop_Concatenate";
   }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(desc.n_in, desc.n_out, (desc.flags & PONNI_FLAG_CONCAT_AFTER) != 0);
+  }
+  int get_num_trainable_parameters() const { return 0; }
+  template <class A> void set_trainable_parameters(A const&) {}
+  View<real*, MemorySpace> get_trainable_parameters() const { return {}; }
   void validate(int saved_n) const {
     if (desc.n_out != saved_n + desc.n_in)
       abort("ERROR: this layer's num outputs != this layer's num inputs + saved layer's num inputs");
   }
+  template <class F> void for_each_segment(F&&) const {}
 };
 
 // out = in + (bias + W^T saved), W [NSAVE, NIN] (ponni_Binop_Projection_Add.h).
-template <int ISAVE, class real = float, int NIN = 1, int NSAVE = 1>
-struct Binop_Projection_Add : detail::LayerCore {
-  static constexpr bool save = false, binop = true;
+template <int ISAVE, class real = float, int NIN = 1, int NSAVE = 1, class MemorySpace = HIPSpace>
+struct Binop_Projection_Add : detail::LayerBase {
+  using memory_space = MemorySpace;
+  template <class NewMemorySpace>
+  using rebind_memory_space = Binop_Projection_Add<ISAVE, real, NIN, NSAVE, NewMemorySpace>;
+  using real1d = View<real*, MemorySpace>;
+  using real2d = View<real**, MemorySpace>;
+  static constexpr bool overwrite_input = true, save = false, binop = true;
   static constexpr int index = ISAVE;
+  struct Params {
+    real2d weights;
+    real1d bias;
+    bool trainable = true;
+  };
+  Params params;
+
   Binop_Projection_Add() = default;
   template <class INIT = Initializer_Random_Uniform<real>>
-  Binop_Projection_Add(int num_inputs, int num_saved_inputs, bool trainable_ = true, INIT init = INIT()) {
-    std::vector<double> w(static_cast<std::size_t>(num_saved_inputs) * num_inputs), b(num_inputs);
-    init.fill(w, num_saved_inputs, num_inputs);
-    init.fill(b, num_inputs, num_inputs);
-    w.insert(w.end(), b.begin(), b.end());
-    setup(num_inputs, num_saved_inputs, std::move(w), trainable_);
+  Binop_Projection_Add(int num_inputs, int num_saved_inputs, bool trainable = true, INIT initializer = INIT()) {
+    real2d w("Binop_Projection_Add_weights", num_saved_inputs, num_inputs);
+    real1d b("Binop_Projection_Add_bias", num_inputs);
+    initializer.fill(w);
+    initializer.fill(b);
+    init(w, b, trainable);
   }
-  template <class M, class V, class = decltype(std::declval<M const&>()(0, 0))>
-  Binop_Projection_Add(M const& weights, V const& bias, bool trainable_ = true) {
-    if (static_cast<std::size_t>(weights.extent(1)) != bias.size())
-      abort("ERROR: Binop_Projection_Add incompatible weights/bias shapes");
-    std::vector<double> p = detail::flatten(weights), b = detail::flatten1(bias);
-    p.insert(p.end(), b.begin(), b.end());
-    setup(static_cast<int>(weights.extent(1)), static_cast<int>(weights.extent(0)), std::move(p), trainable_);
+  template <class A, class B, class = std::enable_if_t<detail::is_array2d_v<A> && detail::is_array1d_v<B>>>
+  Binop_Projection_Add(A const& weights, B const& bias, bool trainable = true) {
+    init(detail::layer_view<real, MemorySpace, 2>("Binop_Projection_Add_weights", weights),
+         detail::layer_view<real, MemorySpace, 1>("Binop_Projection_Add_bias", bias), trainable);
   }
-  void setup(int n_in, int n_save, std::vector<double> p, bool t) {
-    desc = detail::make_desc(PONNI_LAYER_BINOP_PROJECTION_ADD, n_in, n_in, ISAVE, n_save);
-    params = std::move(p);
-    trainable = t;
+  void init(real2d const& weights, real1d const& bias, bool trainable) {
+    if (weights.extent(1) != bias.extent(0)) abort("ERROR: Binop_Projection_Add incompatible weights/bias shapes");
+    params.weights = weights;
+    params.bias = bias;
+    params.trainable = trainable;
+    desc = detail::make_desc(PONNI_LAYER_BINOP_PROJECTION_ADD, static_cast<int>(weights.extent(1)),
+                             static_cast<int>(weights.extent(1)), ISAVE, static_cast<int>(weights.extent(0)));
     label = "Binop_Projection_Add";
+  }
+  template <class NewMemorySpace>
+  auto copy_to_memory_space(NewMemorySpace const& space = NewMemorySpace()) const {
+    return rebind_memory_space<NewMemorySpace>(create_memory_space_copy(params.weights, space),
+                                               create_memory_space_copy(params.bias, space), params.trainable);
+  }
+  int get_num_trainable_parameters() const {
+    return params.trainable ? static_cast<int>(params.weights.size() + params.bias.size()) : 0;
+  }
+  template <class A>
+  void set_trainable_parameters(A const& in) {
+    if (!params.trainable) return;
+    auto v = detail::trainable_values(in);
+    std::size_t const nw = static_cast<std::size_t>(params.weights.size()), nb = static_cast<std::size_t>(params.bias.size());
+    if (v.size() < nw + nb) abort("ERROR: Binop_Projection_Add trainable input too small");
+    detail::store_values(params.weights, std::vector<double>(v.begin(), v.begin() + nw));
+    detail::store_values(params.bias, std::vector<double>(v.begin() + nw, v.begin() + nw + nb));
+  }
+  real1d get_trainable_parameters() const {
+    if (!params.trainable) return real1d();
+    auto w = detail::host_values(params.weights), b = detail::host_values(params.bias);
+    w.insert(w.end(), b.begin(), b.end());
+    return detail::view_from_values<real, MemorySpace, 1>("Binop_Projection_Add_trainable", 1,
+                                                         static_cast<std::int64_t>(w.size()), w);
   }
   void validate(int saved_n) const {
     if (saved_n != desc.n_aux) abort("ERROR: saved layer size incompatible with projection weights");
+  }
+  template <class F> void for_each_segment(F&& f) const {
+    f(0, params.weights);
+    f(1, params.bias);
   }
 };
 
@@ -858,7 +1444,7 @@ struct Binop_Projection_Add : detail::LayerCore {
 namespace detail {
 
 template <class L>
-inline constexpr bool is_builtin_v = std::is_base_of_v<LayerCore, L>;
+inline constexpr bool is_builtin_v = std::is_base_of_v<LayerBase, L>;
 
 // Static flags of a layer type with the reference's defaults.
 template <class L, class = void> struct flag_save : std::false_type {};
@@ -937,6 +1523,8 @@ class BasicInference {
   static_assert(!runs_on_host || std::is_same_v<real, float> || std::is_same_v<real, double>,
                 "host execution-space models run in F32 or F64");
   using TUPLE = std::tuple<Layers...>;
+  using real1d = View<real*, memory_space>;
+  using real2d = View<real**, memory_space>;
   static constexpr int num_layers = static_cast<int>(sizeof...(Layers));
   // A chain holding user layers (the plugin contract) runs one sample per
   // thread through the plan's GENERIC op list, with the user layers' device
@@ -952,7 +1540,7 @@ class BasicInference {
     ponni_plan p = nullptr;
     check(ponni_plan_create(descs.data(), num_layers, dtype_of<real>(), path, &p), "create_inference_model");
     plan_ = std::shared_ptr<ponni_plan_s>(p, [](ponni_plan q) { ponni_plan_destroy(q); });
-    pushed_.assign(num_layers, ~std::uint64_t(0));
+    share_views(std::make_index_sequence<num_layers>{});
     sync();
   }
 
@@ -1042,41 +1630,28 @@ class BasicInference {
         layers_);
     return n;
   }
-  // Flattened in tuple order (ponni_Inference.h:688-716).
-  std::vector<real> get_trainable_parameters() const {
-    std::vector<real> out;
-    std::apply(
-        [&](auto const&... l) {
-          auto one = [&](auto const& layer) {
-            if constexpr (detail::is_builtin_v<std::decay_t<decltype(layer)>>)
-            for (double v : layer.get_trainable_parameters()) {
-              if constexpr (std::is_same_v<real, double>) out.push_back(v);
-              else out.push_back(static_cast<real>(static_cast<float>(v)));
-            }
-          };
-          (one(l), ...);
-        },
-        layers_);
-    return out;
+  // Flattened in tuple order, in the model's memory space (ponni_Inference.h:688-716).
+  real1d get_trainable_parameters() const {
+    std::vector<double> v = trainable_values();
+    if (v.empty()) return real1d();
+    return detail::view_from_values<real, memory_space, 1>("trainable_parameters", 1,
+                                                           static_cast<std::int64_t>(v.size()), v);
   }
-  template <class Vec>
-  void set_trainable_parameters(Vec const& in) {
+  // Consumes get_num_trainable_parameters() values (a View in any memory space
+  // or a host vector) into the layers' Views, in tuple order.
+  template <class A>
+  void set_trainable_parameters(A const& in) {
+    std::vector<double> const v = detail::host_values(in);
     std::size_t off = 0;
     std::apply(
         [&](auto&... l) {
           auto one = [&](auto& layer) {
-            if constexpr (!detail::is_builtin_v<std::decay_t<decltype(layer)>>) return;
-            else {
-            std::size_t const n = static_cast<std::size_t>(layer.get_num_trainable_parameters());
-            if (n == 0) return;
-            if (in.size() < off + n) abort(std::string("ERROR: ") + layer.get_label() + " trainable input too small");
-            std::vector<double> part(n);
-            for (std::size_t i = 0; i < n; i++) {
-              if constexpr (std::is_same_v<real, double>) part[i] = static_cast<double>(in[off + i]);
-              else part[i] = static_cast<double>(static_cast<float>(in[off + i]));
-            }
-            layer.set_trainable_parameters(part);
-            off += n;
+            if constexpr (detail::is_builtin_v<std::decay_t<decltype(layer)>>) {
+              std::size_t const n = static_cast<std::size_t>(layer.get_num_trainable_parameters());
+              if (n == 0) return;
+              if (v.size() < off + n) abort(std::string("ERROR: ") + layer.get_label() + " trainable input too small");
+              layer.set_trainable_parameters(std::vector<double>(v.begin() + off, v.begin() + off + n));
+              off += n;
             }
           };
           (one(l), ...);
@@ -1153,34 +1728,11 @@ class BasicInference {
     run_sample<MAXW, MAXSAVED>(p, input.data(), 1, output.data(), 1);
   }
 
-  // Push parameters of layers changed since the last push (set_trainable_parameters,
-  // or get_layer<I>() edits followed by mark_modified()).
+  // Refresh `params` (the in-kernel description, and the user layers'
+  // Params of a chain that has them) from the layers' current Views.  The
+  // batched forward pass reads the Views itself; in-kernel callers call this
+  // after writing a layer's View directly.
   void sync() {
-    int i = 0;
-    std::apply(
-        [&](auto const&... l) {
-          auto one = [&](auto const& layer) {
-            if constexpr (!detail::is_builtin_v<std::decay_t<decltype(layer)>>) {
-              i++;
-              return;
-            } else {
-            if (pushed_[i] != layer.version && !layer.params.empty()) {
-              std::vector<float> f;
-              void const* src = layer.params.data();
-              if constexpr (!std::is_same_v<real, double>) {
-                f.assign(layer.params.begin(), layer.params.end());
-                src = f.data();
-              }
-              check(ponni_plan_set_layer_params(plan_.get(), i, src, static_cast<std::int64_t>(layer.params.size())),
-                    "ponni_plan_set_layer_params");
-            }
-            pushed_[i] = layer.version;
-            i++;
-            }
-          };
-          (one(l), ...);
-        },
-        layers_);
     // Host models describe the plan in host memory; device models do so only
     // where a device exists (models are also built on GPU-less hosts).
     int devices = 0;
@@ -1227,7 +1779,7 @@ class BasicInference {
       if (error) *error = "cannot save weights from a model with no trainable parameters";
       return false;
     }
-    std::vector<real> p = get_trainable_parameters();
+    std::vector<double> const p = trainable_values();
     int st;
     if constexpr (std::is_same_v<real, double>) {
       st = ponni_file_write_parameters(path.c_str(), weight_schema_fingerprint().c_str(), p.data(), n, 8, "template");
@@ -1287,7 +1839,7 @@ class BasicInference {
       abort("Error: Provided # inputs differs from model's # inputs");
     if (static_cast<int>(output.extent(0)) != get_num_outputs() || output.extent(1) != input.extent(1))
       abort("Error: Provided output dimensions do not match the model and input batch");
-    sync();
+    if constexpr (has_user_layers) sync();  // their per-sample kernel reads `params`
     if constexpr (runs_on_host) {
       if constexpr (has_user_layers) {
         if (!fits_in_kernel(params.model)) abort("Error: a chain with user layers is limited to 256-feature states");
@@ -1354,35 +1906,53 @@ class BasicInference {
     (one(std::integral_constant<std::size_t, I>{}), ...);
   }
 
+  // Share every built-in layer's parameter Views with the plan (the layers
+  // were rebound to the model's memory space): the plan reads them at each
+  // forward pass (ponni_plan_share_layer_params).
+  template <std::size_t... I>
+  void share_views(std::index_sequence<I...>) {
+    auto one = [&](auto idx) {
+      constexpr std::size_t k = decltype(idx)::value;
+      using L = std::tuple_element_t<k, TUPLE>;
+      if constexpr (detail::is_builtin_v<L>) {
+        static_assert(std::is_same_v<typename L::memory_space, memory_space>,
+                      "a model's layers live in its memory space (create_inference_model rebinds them)");
+        std::get<k>(layers_).for_each_segment([&](int seg, auto const& v) {
+          using V = std::decay_t<decltype(v)>;
+          check(ponni_plan_share_layer_params(plan_.get(), static_cast<std::int32_t>(k), seg, v.data(),
+                                              dtype_of<typename V::non_const_value_type>(), v.rows(), v.cols(),
+                                              v.ld(), std::is_same_v<typename V::memory_space, HIPSpace> ? 1 : 0),
+                "create_inference_model");
+        });
+      }
+    };
+    (one(std::integral_constant<std::size_t, I>{}), ...);
+  }
+  // Built-in layers' trainable values in tuple order, read from their Views.
+  std::vector<double> trainable_values() const {
+    std::vector<double> out;
+    std::apply(
+        [&](auto const&... l) {
+          auto one = [&](auto const& layer) {
+            if constexpr (detail::is_builtin_v<std::decay_t<decltype(layer)>>) {
+              if (layer.get_num_trainable_parameters() == 0) return;
+              auto const v = detail::host_values(layer.get_trainable_parameters());
+              out.insert(out.end(), v.begin(), v.end());
+            }
+          };
+          (one(l), ...);
+        },
+        layers_);
+    return out;
+  }
+
   TUPLE layers_;
   Exec exec_;
   std::shared_ptr<ponni_plan_s> plan_;
-  std::vector<std::uint64_t> pushed_;
 };
 
 // ---- View copies and .ponni tensors (src/utils/ponni_view_ops.h:12-48,
 // src/utils/ponni_safetensors.h:409-444) ------------------------------------------------
-
-// A copy of `v` in memory space Space (LayoutRight, contiguous rows).
-template <class Space, class T, class S>
-View<std::remove_const_t<T>, Space> create_memory_space_copy(View<T, S> const& v, Space = Space()) {
-  View<std::remove_const_t<T>, Space> out(v.label(), v.extent(0), v.extent(1), false);
-  out.copy_from_host(v.copy_to_host());
-  return out;
-}
-template <class T, class S>
-View<std::remove_const_t<T>, HostSpace> create_host_copy(View<T, S> const& v) {
-  return create_memory_space_copy<HostSpace>(v);
-}
-template <class T, class S>
-View<std::remove_const_t<T>, HIPSpace> create_device_copy(View<T, S> const& v) {
-  return create_memory_space_copy<HIPSpace>(v);
-}
-// The elements of a contiguous view as one row, sharing its memory.
-template <class T, class S>
-View<T, S> flatten(View<T, S> const& v) {
-  return v.reshape(1, v.size());
-}
 
 // Tensor `name` of a .ponni file as a float View in Space: rank 2 [rows, cols];
 // rank 1 [1, n] (this View type is rank 2).  F32 or F64 payloads.
@@ -1426,22 +1996,42 @@ template <class real, class... Layers>
 using Inference = BasicInference<real, HIP, Layers...>;
 
 namespace detail {
+template <class L, class = void> struct has_rebind : std::false_type {};
+template <class L>
+struct has_rebind<L, std::void_t<typename L::memory_space, typename L::template rebind_memory_space<HostSpace>>>
+    : std::true_type {};
+// A layer in the model's memory space (src/ponni_create_model.h:10-18): the
+// layer itself when it already lives there, so the model shares its Views;
+// otherwise copy_to_memory_space.  A user layer without the rebinding
+// members is used as it is.
+template <class Mem, class L>
+auto rebind_layer_memory_space(L const& layer, Mem const& memory_space) {
+  if constexpr (!has_rebind<L>::value) {
+    return layer;
+  } else if constexpr (std::is_same_v<typename L::memory_space, Mem>) {
+    return layer;
+  } else {
+    return layer.template copy_to_memory_space<Mem>(memory_space);
+  }
+}
 template <class real, class Exec, class Mem, class... Layers>
-inline auto create_model(Exec const& exec, Mem const&, Layers const&... layers) {
+inline auto create_model(Exec const& exec, Mem const& mem, Layers const&... layers) {
   static_assert(is_execution_space_v<Exec>, "create_inference_model requires an execution space (HIP or Host)");
   static_assert(is_memory_space_v<Mem>, "create_inference_model requires a memory space (HIPSpace or HostSpace)");
   static_assert(std::is_same_v<typename Exec::memory_space, Mem>,
                 "create_inference_model execution space cannot access its memory space");
-  return BasicInference<real, Exec, Layers...>(std::make_tuple(layers...), exec);
+  return BasicInference<real, Exec, std::decay_t<decltype(rebind_layer_memory_space(layers, mem))>...>(
+      std::make_tuple(rebind_layer_memory_space(layers, mem)...), exec);
 }
 }  // namespace detail
 
-// Layers are copied into the model (parameters live in the plan's buffers),
-// as the reference deep-copies them when the memory space differs.
+// Default model: the GPU, HIPSpace; layers in another space are copied in
+// (ponni_create_model.h:40-98).  Like the reference, the default and the
+// execution-space forms compute in float.
 template <class First, class... Rest,
           std::enable_if_t<!is_execution_space_v<First> && !std::is_same_v<std::decay_t<First>, hipStream_t>, int> = 0>
 inline auto create_inference_model(First const& first, Rest const&... rest) {
-  return Inference<float, First, Rest...>(std::make_tuple(first, rest...));
+  return detail::create_model<float>(HIP(), HIPSpace(), first, rest...);
 }
 // The execution-space-instance overloads (ponni_create_model.h:52-78).
 template <class Exec, class... Layers, std::enable_if_t<is_execution_space_v<Exec>, int> = 0>
@@ -1456,23 +2046,23 @@ inline auto create_inference_model(Exec const& exec, Mem const& mem, Layers cons
 // A HIP stream is the HIP execution-space instance.
 template <class... Layers>
 inline auto create_inference_model(hipStream_t stream, Layers const&... layers) {
-  return Inference<float, Layers...>(std::make_tuple(layers...), HIP(stream));
+  return detail::create_model<float>(HIP(stream), HIPSpace(), layers...);
 }
 template <class... Layers>
 inline auto create_inference_model_single_precision(Layers const&... layers) {
-  return Inference<float, Layers...>(std::make_tuple(layers...));
+  return detail::create_model<float>(HIP(), HIPSpace(), layers...);
 }
 template <class... Layers>
 inline auto create_inference_model_double_precision(Layers const&... layers) {
-  return Inference<double, Layers...>(std::make_tuple(layers...));
+  return detail::create_model<double>(HIP(), HIPSpace(), layers...);
 }
 template <class... Layers>
 inline auto create_inference_model_half_precision(Layers const&... layers) {
-  return Inference<half_t, Layers...>(std::make_tuple(layers...));
+  return detail::create_model<half_t>(HIP(), HIPSpace(), layers...);
 }
 template <class... Layers>
 inline auto create_inference_model_bhalf_precision(Layers const&... layers) {
-  return Inference<bhalf_t, Layers...>(std::make_tuple(layers...));
+  return detail::create_model<bhalf_t>(HIP(), HIPSpace(), layers...);
 }
 
 }  // namespace ponni

@@ -16,6 +16,9 @@
 //   unit/core/test_core_unit.cpp:380-404   host execution/memory space model -> (4, 4)
 #include <cmath>
 #include <cstdio>
+#include <limits>
+#include <stdexcept>
+#include <utility>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -54,14 +57,22 @@ std::vector<double> host(V const& v) {
 
 ponni::Matrix<float> ones(int r, int c) { return ponni::Matrix<float>(r, c, 1.0f); }
 
-auto four_block_model() {
+// The execution space whose memory space is S (host checks build their
+// layers and models in HostSpace, so they need no device).
+template <class S>
+using ExecOf = std::conditional_t<std::is_same_v<S, ponni::HostSpace>, ponni::Host, ponni::HIP>;
+
+template <class S = ponni::HIPSpace>
+auto four_block_model_in(ExecOf<S> const& exec = ExecOf<S>()) {
   using namespace ponni;
   return create_inference_model(
-      Matvec<float>(ones(2, 5)), Bias<float>(std::vector<float>(5, 0.5f)), Relu<float>(5), Tanh<float>(5),
-      Matvec<float>(ones(5, 3)), Bias<float>(std::vector<float>(3, -0.25f)), Sigmoid<float>(3),
-      Matvec<float>(ones(3, 7)), Bias<float>(std::vector<float>(7, 0.1f)), LeakyRelu<float>(7, 0.2f),
-      Matvec<float>(ones(7, 2)), Bias<float>(std::vector<float>(2, -0.2f)), HardSwish<float>(2));
+      exec, S(), Matvec<float, 1, 1, S>(ones(2, 5)), Bias<float, 1, S>(std::vector<float>(5, 0.5f)),
+      Relu<float, 1, S>(5), Tanh<float, 1, S>(5), Matvec<float, 1, 1, S>(ones(5, 3)),
+      Bias<float, 1, S>(std::vector<float>(3, -0.25f)), Sigmoid<float, 1, S>(3), Matvec<float, 1, 1, S>(ones(3, 7)),
+      Bias<float, 1, S>(std::vector<float>(7, 0.1f)), LeakyRelu<float, 1, S>(7, 0.2f),
+      Matvec<float, 1, 1, S>(ones(7, 2)), Bias<float, 1, S>(std::vector<float>(2, -0.2f)), HardSwish<float, 1, S>(2));
 }
+auto four_block_model() { return four_block_model_in<ponni::HIPSpace>(); }
 
 double four_block_closed_form(double x0, double x1) {
   double const s = x0 + x1;
@@ -75,43 +86,48 @@ double four_block_closed_form(double x0, double x1) {
 
 // ---- host-only checks ----------------------------------------------------------------
 
+template <class S>
 void test_structure_and_planning() {
   using namespace ponni;
-  auto first = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{1, 1}),
-                                      LeakyRelu<float>(2, 0.1f));
+  ExecOf<S> const ex;
+  auto first = create_inference_model(ex, S(), Matvec<float, 1, 1, S>(ones(2, 2)),
+                                      Bias<float, 1, S>(std::vector<float>{1, 1}), LeakyRelu<float, 1, S>(2, 0.1f));
   CHECK(first.get_num_inputs() == 2 && first.get_num_outputs() == 2);
-  CHECK(first.get_planned_temporary_size<0>() == 0 && first.get_planned_temporary_size<1>() == 0);
+  CHECK(first.template get_planned_temporary_size<0>() == 0 && first.template get_planned_temporary_size<1>() == 0);
   CHECK(first.get_num_fused_dense_blocks() == 1);
-  auto four = four_block_model();
-  CHECK(four.get_planned_temporary_size<0>() == 7 && four.get_planned_temporary_size<1>() == 3);
+  auto four = four_block_model_in<S>();
+  CHECK(four.template get_planned_temporary_size<0>() == 7 && four.template get_planned_temporary_size<1>() == 3);
   CHECK(four.get_num_fused_dense_blocks() == 4);
   four.validate();
-  auto soft = create_inference_model(Matvec<float>(ones(2, 3)), Bias<float>(std::vector<float>{0, 1, 2}),
-                                     Relu<float>(3), Softmax<float>(3), Matvec<float>(ones(3, 2)),
-                                     Bias<float>(std::vector<float>{0, -1}), Tanh<float>(2));
-  CHECK(soft.get_planned_temporary_size<0>() == 3 && soft.get_planned_temporary_size<1>() == 0);
-  auto res = create_inference_model(Save_State<0>(2), Relu<float>(2), Binop_Concatenate<0>(2, 4, true),
+  auto soft = create_inference_model(ex, S(), Matvec<float, 1, 1, S>(ones(2, 3)),
+                                     Bias<float, 1, S>(std::vector<float>{0, 1, 2}), Relu<float, 1, S>(3),
+                                     Softmax<float, 1, S>(3), Matvec<float, 1, 1, S>(ones(3, 2)),
+                                     Bias<float, 1, S>(std::vector<float>{0, -1}), Tanh<float, 1, S>(2));
+  CHECK(soft.template get_planned_temporary_size<0>() == 3 && soft.template get_planned_temporary_size<1>() == 0);
+  auto res = create_inference_model(ex, S(), Save_State<0>(2), Relu<float>(2), Binop_Concatenate<0>(2, 4, true),
                                     Save_State<1>(4), Relu<float>(4), Binop_Add<1>(4),
                                     Binop_Concatenate<0>(4, 6, true));
   CHECK(res.get_num_saved_states() == 2);
   res.validate();
 }
 
+template <class S>
 void test_parameters_and_fingerprint() {
   using namespace ponni;
   ponni::Matrix<float> w(2, 3, std::vector<float>{1, 2, 3, 4, 5, 6});
-  auto m = create_inference_model(Matvec<float>(w), Bias<float>(std::vector<float>{7, 8, 9}), Relu<float>(3),
-                                  LayerNorm<float>(3), Matvec<float>(ones(3, 1), false));
+  auto m = create_inference_model(ExecOf<S>(), S(), Matvec<float, 1, 1, S>(w),
+                                  Bias<float, 1, S>(std::vector<float>{7, 8, 9}), Relu<float>(3),
+                                  LayerNorm<float, 1, S>(3), Matvec<float, 1, 1, S>(ones(3, 1), false));
   CHECK(m.get_num_trainable_parameters() == 6 + 3 + 6);  // the last Matvec is frozen
-  auto p = m.get_trainable_parameters();
-  std::vector<float> want{1, 2, 3, 4, 5, 6, 7, 8, 9, 1, 1, 1, 0, 0, 0};
-  CHECK(p.size() == want.size() && std::equal(p.begin(), p.end(), want.begin()));
+  auto p = host(m.get_trainable_parameters());
+  std::vector<double> want{1, 2, 3, 4, 5, 6, 7, 8, 9, 1, 1, 1, 0, 0, 0};
+  CHECK(p == want);
   std::vector<float> q(15);
   for (int i = 0; i < 15; i++) q[i] = 0.5f * i;
   m.set_trainable_parameters(q);
-  p = m.get_trainable_parameters();
+  p = host(m.get_trainable_parameters());
   CHECK(std::equal(p.begin(), p.end(), q.begin()));
-  CHECK(m.get_layer<1>().params[0] == 3.0);
+  CHECK(host(m.template get_layer<1>().params.weights)[0] == 3.0);
   // "ponni-template-model-v1\n" + "I\tlabel\tnin\tnout\tntrainable\n" (ponni_Inference.h:270-288)
   std::string text = "ponni-template-model-v1\n0\tMatvec\t2\t3\t6\n1\tBias\t3\t3\t3\n2\tReLU\t3\t3\t0\n"
                      "3\tLayerNorm\t3\t3\t6\n4\tMatvec\t3\t1\t0\n";
@@ -120,26 +136,30 @@ void test_parameters_and_fingerprint() {
   CHECK(m.weight_schema_fingerprint() == fp);
 }
 
+template <class S>
 void test_weights_files() {
   using namespace ponni;
+  ExecOf<S> const ex;
   char const* path = "/tmp/ponni_facade_test.ponni";
-  auto a = create_inference_model(Matvec<float>(ponni::Matrix<float>(2, 2, std::vector<float>{1, 2, 3, 4})),
-                                  Bias<float>(std::vector<float>{5, 6}));
+  auto a = create_inference_model(ex, S(), Matvec<float, 1, 1, S>(ponni::Matrix<float>(2, 2, std::vector<float>{1, 2, 3, 4})),
+                                  Bias<float, 1, S>(std::vector<float>{5, 6}));
   std::string err;
   CHECK(a.save_weights(path, &err));
-  auto b = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{0, 0}));
+  auto b = create_inference_model(ex, S(), Matvec<float, 1, 1, S>(ones(2, 2)), Bias<float, 1, S>(std::vector<float>{0, 0}));
   CHECK(b.load_weights(path, &err));
-  auto p = b.get_trainable_parameters();
+  auto p = host(b.get_trainable_parameters());
   CHECK(p.size() == 6 && p[0] == 1 && p[3] == 4 && p[5] == 6);
-  auto c = create_inference_model(Matvec<float>(ones(2, 2)), Relu<float>(2), Bias<float>(std::vector<float>{0, 0}));
+  auto c = create_inference_model(ex, S(), Matvec<float, 1, 1, S>(ones(2, 2)), Relu<float>(2),
+                                  Bias<float, 1, S>(std::vector<float>{0, 0}));
   CHECK(!c.load_weights(path, &err));
   CHECK(err.find("fingerprint") != std::string::npos);
-  auto d = create_inference_model(Relu<float>(2));
+  auto d = create_inference_model(ex, S(), Relu<float>(2));
   CHECK(!d.load_weights(path, &err));
   CHECK(err == "cannot load weights into a model with no trainable parameters");
   CHECK(!d.save_weights(path, &err));
   CHECK(err == "cannot save weights from a model with no trainable parameters");
-  auto e = create_inference_model_double_precision(Matvec<double>(ones(2, 2)), Bias<double>(std::vector<double>{0, 0}));
+  auto e = detail::create_model<double>(ex, S(), Matvec<double, 1, 1, S>(ones(2, 2)),
+                                        Bias<double, 1, S>(std::vector<double>{0, 0}));
   CHECK(!e.load_weights(path, &err));  // F32 file, F64 model: dtype mismatch
   std::remove(path);
 }
@@ -263,10 +283,9 @@ void test_views_streams_capacity_gpu() {
   ms.reallocate_internal_state(0);
   CHECK(ms.internal_state_capacity() == 0);
   CHECK(hipStreamDestroy(s) == hipSuccess);
-  // Parameter edits through get_layer + mark_modified reach the device.
+  // A write through a layer's View reaches the next forward pass (the model shares it).
   auto one = create_inference_model(Matvec<float>(ones(2, 1)));
-  one.get_layer<0>().params = {3.0, 4.0};
-  one.get_layer<0>().mark_modified();
+  one.get_layer<0>().params.weights.copy_from_host({3.0f, 4.0f});
   auto r = host(one.forward_batch_parallel(device_matrix<float>(2, 1, {1, 1})));
   CHECK(r[0] == 7.0);
   (void)m;
@@ -379,21 +398,13 @@ void test_user_layers_cpu() {
 // Host execution-space models (test_core_unit.cpp:380-404): the same
 // chains on the host, through the library's host executor or, with user
 // layers, the per-sample interpreter on the host.
-template <class Exec>
-auto four_block_model_on(Exec const& exec) {
-  using namespace ponni;
-  return create_inference_model(
-      exec, Matvec<float>(ones(2, 5)), Bias<float>(std::vector<float>(5, 0.5f)), Relu<float>(5), Tanh<float>(5),
-      Matvec<float>(ones(5, 3)), Bias<float>(std::vector<float>(3, -0.25f)), Sigmoid<float>(3),
-      Matvec<float>(ones(3, 7)), Bias<float>(std::vector<float>(7, 0.1f)), LeakyRelu<float>(7, 0.2f),
-      Matvec<float>(ones(7, 2)), Bias<float>(std::vector<float>(2, -0.2f)), HardSwish<float>(2));
-}
-
 void test_host_models_cpu() {
   using namespace ponni;
   {  // test_core_unit.cpp:380-404
-    auto host_model = create_inference_model(DefaultHostExecutionSpace(), HostSpace(), Matvec<float>(ones(2, 2)),
-                                             Bias<float>(std::vector<float>(2, 1.0f)), LeakyRelu<float>(2, 0.1f));
+    auto host_model = create_inference_model(DefaultHostExecutionSpace(), HostSpace(),
+                                             Matvec<float, 1, 1, HostSpace>(ones(2, 2)),
+                                             Bias<float, 1, HostSpace>(std::vector<float>(2, 1.0f)),
+                                             LeakyRelu<float>(2, 0.1f));
     static_assert(std::is_same_v<typename decltype(host_model)::execution_space, DefaultHostExecutionSpace>);
     static_assert(std::is_same_v<typename decltype(host_model)::memory_space, HostSpace>);
     static_assert(std::is_same_v<typename decltype(create_inference_model(Relu<float>(2)))::memory_space, HIPSpace>);
@@ -404,7 +415,7 @@ void test_host_models_cpu() {
     CHECK(near(host_output(0, 0), 4.0, 1e-6) && near(host_output(1, 0), 4.0, 1e-6));
   }
   {  // the four-block closed form over a batch, 3 host threads, strided views
-    auto m = four_block_model_on(Host(3));
+    auto m = four_block_model_in<HostSpace>(Host(3));
     int const B = 1000;
     View<float, HostSpace> x("x", 2, B + 7);
     for (int b = 0; b < B; b++) {
@@ -434,8 +445,9 @@ void test_host_models_cpu() {
     auto y = m.forward_batch_parallel(x);
     CHECK(near(y(0, 0), 4.5, 1e-6) && near(y(1, 0), -4.5, 1e-6));
     Matrix<float> w(2, 2, std::vector<float>{0.5f, -1.0f, 2.0f, 0.25f});
-    auto mixed = create_inference_model(Host(), HostSpace(), Matvec<float>(w),
-                                        Bias<float>(std::vector<float>{0.1f, -0.2f}), TestIndexedPointwise<float, 2>(),
+    auto mixed = create_inference_model(Host(), HostSpace(), Matvec<float, 1, 1, HostSpace>(w),
+                                        Bias<float, 1, HostSpace>(std::vector<float>{0.1f, -0.2f}),
+                                        TestIndexedPointwise<float, 2>(),
                                         Save_State<0>(2), Relu<float>(2), TestBarrier<float, 2>(),
                                         TestMultiplySaved<0, float, 2>(), Binop_Add<0>(2), Tanh<float>(2));
     int const B = 300;
@@ -454,7 +466,7 @@ void test_host_models_cpu() {
     CHECK(ok);
   }
   {  // an F64 host model; parameter updates reach it
-    auto m = detail::create_model<double>(Host(), HostSpace(), Matvec<double>(Matrix<double>(3, 2, 1.0)),
+    auto m = detail::create_model<double>(Host(), HostSpace(), Matvec<double, 1, 1, HostSpace>(Matrix<double>(3, 2, 1.0)),
                                           LeakyRelu<double>(2, 0.1));
     View<double, HostSpace> x("x", 3, 2);
     x(0, 0) = 1.0;
@@ -581,8 +593,8 @@ void test_in_kernel_gpu() {
   {  // a parameter change reaches `params`
     auto m = create_inference_model(Matvec<float>(ones(2, 2)), Bias<float>(std::vector<float>{1, 1}));
     auto x = device_matrix<float>(2, 1, {1, 2});
-    auto p = m.get_trainable_parameters();
-    for (auto& v : p) v *= 2.0f;
+    auto p = host(m.get_trainable_parameters());
+    for (auto& v : p) v *= 2.0;
     m.set_trainable_parameters(p);
     View<float> yk("yk", 2, 1);
     using M = decltype(m);
@@ -594,17 +606,332 @@ void test_in_kernel_gpu() {
   }
 }
 
+// ---- initializers (unit/core/test_core_unit.cpp:874-1017) --------------------------------
+
+struct Stats {
+  double minimum, maximum, mean, variance;
+};
+template <class V>
+Stats stats_of(V const& v) {
+  auto h = host(v);
+  Stats s{h[0], h[0], 0, 0};
+  for (double x : h) {
+    s.minimum = std::min(s.minimum, x);
+    s.maximum = std::max(s.maximum, x);
+    s.mean += x;
+  }
+  s.mean /= h.size();
+  for (double x : h) s.variance += (x - s.mean) * (x - s.mean);
+  s.variance /= h.size();
+  return s;
+}
+template <class Init>
+bool throws_invalid(Init make) {
+  try {
+    make();
+  } catch (std::invalid_argument const&) {
+    return true;
+  }
+  return false;
+}
+
+void test_initializers_cpu() {
+  using namespace ponni;
+  using real2d = View<float**, HostSpace>;
+  int constexpr fan_in = 512, fan_out = 384;
+  real2d values("initializer_values", fan_in, fan_out), repeated("initializer_repeated", fan_in, fan_out);
+  auto variance_ok = [](Stats const& s, double expected) { return std::fabs(s.variance - expected) / expected < 0.05; };
+  auto fill_twice = [&](auto const& init) {
+    init.fill(values);
+    init.fill(repeated);
+    CHECK(host(values) == host(repeated));  // deterministic for a nonzero seed
+    return stats_of(values);
+  };
+  Initializer_Zeros<float>().fill(values);
+  auto st = stats_of(values);
+  CHECK(st.minimum == 0.0 && st.maximum == 0.0);
+  Initializer_Ones<float>().fill(values);
+  st = stats_of(values);
+  CHECK(st.minimum == 1.0 && st.maximum == 1.0);
+  Initializer_Constant<float>(2.5f).fill(values);
+  st = stats_of(values);
+  CHECK(st.minimum == 2.5 && st.maximum == 2.5);
+  st = fill_twice(Initializer_Random_Uniform<float>(-0.2f, 0.3f, 111));
+  CHECK(st.minimum >= -0.2 && st.maximum < 0.3 && std::fabs(st.mean - 0.05) < 0.005);
+  CHECK(variance_ok(st, 0.25 / 12.0));
+  st = fill_twice(Initializer_Random_Normal<float>(0.35f, 0.4f, 222));
+  CHECK(std::fabs(st.mean - 0.35) < 0.01 && variance_ok(st, 0.16));
+  st = fill_twice(Initializer_Truncated_Normal<float>(-0.2f, 0.3f, 333));
+  CHECK(st.minimum >= -0.8 && st.maximum <= 0.4 && std::fabs(st.mean + 0.2) < 0.01);
+  CHECK(variance_ok(st, 0.09 * 0.7737413));  // two-sigma truncation: 1 - 4 phi(2) / (2 Phi(2) - 1)
+  double const xv = 2.0 / (fan_in + fan_out), hv = 2.0 / fan_in, lv = 1.0 / fan_in;
+  st = fill_twice(Initializer_Xavier_Uniform<float>(444));
+  double const xl = std::sqrt(6.0 / (fan_in + fan_out));
+  CHECK(st.minimum >= -xl && st.maximum < xl && variance_ok(st, xv));
+  CHECK(variance_ok(fill_twice(Initializer_Xavier_Normal<float>(555)), xv));
+  st = fill_twice(Initializer_He_Uniform<float>(666));
+  double const hl = std::sqrt(6.0 / fan_in);
+  CHECK(st.minimum >= -hl && st.maximum < hl && variance_ok(st, hv));
+  CHECK(variance_ok(fill_twice(Initializer_He_Normal<float>(777)), hv));
+  st = fill_twice(Initializer_Lecun_Uniform<float>(888));
+  double const ll = std::sqrt(3.0 / fan_in);
+  CHECK(st.minimum >= -ll && st.maximum < ll && variance_ok(st, lv));
+  CHECK(variance_ok(fill_twice(Initializer_Lecun_Normal<float>(999)), lv));
+  // Orthogonal: orthonormal columns of a tall array, rows of a wide one, times the gain.
+  for (auto [m, n] : {std::pair<int, int>{48, 16}, {16, 48}}) {
+    View<double**, HostSpace> q("q", m, n);
+    Initializer_Orthogonal<double>(2.0, 1234).fill(q);
+    int const k = std::min(m, n);
+    bool ortho = true;
+    for (int a = 0; a < k; a++)
+      for (int b = 0; b < k; b++) {
+        double dot = 0;
+        for (int i = 0; i < std::max(m, n); i++) dot += m >= n ? q(i, a) * q(i, b) : q(a, i) * q(b, i);
+        ortho = ortho && std::fabs(dot - (a == b ? 4.0 : 0.0)) < 1e-9;
+      }
+    CHECK(ortho);
+  }
+  // zero-size Views are no-op targets for every initializer
+  real2d empty("initializer_empty", 0, fan_out);
+  Initializer_None<float>().fill(empty);
+  Initializer_Zeros<float>().fill(empty);
+  Initializer_Random_Uniform<float>(-1.0f, 1.0f, 1).fill(empty);
+  Initializer_Random_Normal<float>(0.0f, 1.0f, 2).fill(empty);
+  Initializer_Truncated_Normal<float>(0.0f, 1.0f, 3).fill(empty);
+  Initializer_Xavier_Uniform<float>(4).fill(empty);
+  Initializer_Xavier_Normal<float>(5).fill(empty);
+  Initializer_He_Uniform<float>(6).fill(empty);
+  Initializer_He_Normal<float>(7).fill(empty);
+  Initializer_Lecun_Uniform<float>(8).fill(empty);
+  Initializer_Lecun_Normal<float>(9).fill(empty);
+  Initializer_Orthogonal<float>(1.0f, 10).fill(empty);
+  CHECK(empty.size() == 0);
+  // degenerate distributions fill their exact value
+  Initializer_Random_Uniform<float>(0.75f, 0.75f, 11).fill(values);
+  st = stats_of(values);
+  CHECK(st.minimum == 0.75 && st.maximum == 0.75);
+  Initializer_Random_Normal<float>(-0.5f, 0.0f, 12).fill(values);
+  st = stats_of(values);
+  CHECK(st.minimum == -0.5 && st.maximum == -0.5);
+  Initializer_Truncated_Normal<float>(0.25f, 0.0f, 13).fill(values);
+  st = stats_of(values);
+  CHECK(st.minimum == 0.25 && st.maximum == 0.25);
+  // None leaves values alone
+  Initializer_Constant<float>(3.0f).fill(values);
+  Initializer_None<float>().fill(values);
+  CHECK(stats_of(values).maximum == 3.0);
+  float const inf = std::numeric_limits<float>::infinity(), nan = std::numeric_limits<float>::quiet_NaN();
+  CHECK(throws_invalid([] { Initializer_Random_Uniform<float>(1.0f, -1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Random_Uniform<float>(nan, 1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Random_Uniform<float>(0.0f, inf, 1); }));
+  CHECK(throws_invalid([] { Initializer_Random_Normal<float>(0.0f, -1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Random_Normal<float>(nan, 1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Random_Normal<float>(0.0f, inf, 1); }));
+  CHECK(throws_invalid([] { Initializer_Truncated_Normal<float>(0.0f, -1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Truncated_Normal<float>(nan, 1.0f, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Truncated_Normal<float>(0.0f, inf, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Orthogonal<float>(inf, 1); }));
+  CHECK(throws_invalid([&] { Initializer_Orthogonal<float>(nan, 1); }));
+  // layer constructors take any initializer (ponni_Matvec.h:38-44)
+  Matvec<float, 1, 1, HostSpace> mv(6, 4, true, Initializer_Orthogonal<float>(1.0f, 7));
+  Bias<float, 1, HostSpace> bv(4, true, Initializer_Lecun_Normal<float>(8));
+  CHECK(mv.get_num_inputs() == 6 && mv.get_num_outputs() == 4 && bv.get_num_inputs() == 4);
+  Matvec<float, 1, 1, HostSpace> cv(2, 3, true, Initializer_Constant<float>(2.0f));
+  auto cw = host(cv.params.weights);
+  CHECK(cw.size() == 6 && cw[0] == 2.0 && cw[5] == 2.0);
+}
+
+// ---- layer Views, memory spaces and rebinding (ponni_create_model.h:10-18) -----------------
+
+void test_rebinding_cpu() {
+  using namespace ponni;
+  View<float**, HostSpace> w("w", 2, 3);
+  for (int i = 0; i < 6; i++) w(i / 3, i % 3) = 1.0f + i;
+  Matvec<float, 1, 1, HostSpace> mv(w, true);
+  static_assert(std::is_same_v<Matvec<float>::rebind_memory_space<HostSpace>, Matvec<float, 1, 1, HostSpace>>);
+  static_assert(std::is_same_v<Matvec<float>::memory_space, HIPSpace>);
+  CHECK(mv.params.weights.data() == w.data());  // the layer holds the caller's View
+  using HostMatvec = Matvec<float, 1, 1, HostSpace>;
+  CHECK(HostMatvec::get_num_inputs(mv.params) == 2 && mv.get_num_outputs() == 3);
+  // set_trainable_parameters writes into the View (test_core_unit.cpp:530-538)
+  View<float*, HostSpace> fresh("fresh", 6);
+  for (int i = 0; i < 6; i++) fresh(i) = 10.0f + i;
+  mv.set_trainable_parameters(fresh);
+  CHECK(w(0, 0) == 10.0f && w(1, 2) == 15.0f);
+  auto got = host(mv.get_trainable_parameters());
+  CHECK(got.size() == 6 && got[0] == 10.0 && got[5] == 15.0);
+  // a host model shares the layer's View: a later write through it is seen
+  auto m = create_inference_model(Host(1), HostSpace(), mv);
+  View<float, HostSpace> x("x", 2, 1), y("y", 3, 1);
+  x(0, 0) = 1.0f;
+  x(1, 0) = 2.0f;
+  m.forward_batch_parallel(x, y);
+  CHECK(y(0, 0) == 36.0f && y(1, 0) == 39.0f && y(2, 0) == 42.0f);
+  w(0, 0) = 0.0f;
+  m.forward_batch_parallel(x, y);
+  CHECK(y(0, 0) == 26.0f);
+  // copy_to_memory_space gives an independent copy
+  auto copy = mv.copy_to_memory_space<HostSpace>();
+  static_assert(std::is_same_v<decltype(copy), Matvec<float, 1, 1, HostSpace>>);
+  CHECK(copy.params.weights.data() != w.data() && host(copy.params.weights) == host(w));
+  w(1, 1) = -7.0f;
+  CHECK(host(copy.params.weights)[4] == 14.0);
+  // LayerNorm and Projection_Add hold two Views each
+  View<float*, HostSpace> g("g", 3), b("b", 3);
+  deep_copy(g, 2.0f);
+  LayerNorm<float, 1, HostSpace> ln(g, b);
+  CHECK(ln.params.gamma.data() == g.data() && ln.get_num_trainable_parameters() == 6);
+  Binop_Projection_Add<0, float, 1, 1, HostSpace> pa(Matrix<float>(2, 3, 0.5f), std::vector<float>{1, 2, 3});
+  CHECK(pa.params.weights.extent(0) == 2 && pa.params.bias.extent(0) == 3 && pa.get_num_trainable_parameters() == 9);
+  // deep_copy and flatten
+  View<float**, HostSpace> a("a", 2, 2);
+  deep_copy(a, 1.5f);
+  auto flat = flatten(a);
+  static_assert(decltype(flat)::rank == 1);
+  CHECK(flat.extent(0) == 4 && flat(3) == 1.5f && flat.data() == a.data());
+}
+
+// A view type of another library (as a Kokkos::View of device memory would
+// be): data(), extent(), stride(), a LayoutRight layout and a device memory
+// space.  The facade must copy it through the runtime, never read it on the host.
+struct ForeignDeviceSpace {};
+struct ForeignDeviceMatrix {
+  using value_type = float;
+  using array_layout = ponni::LayoutRight;
+  using memory_space = ForeignDeviceSpace;
+  static constexpr int rank = 2;
+  float* p = nullptr;
+  std::int64_t r = 0, c = 0, ld = 0;
+  float* data() const { return p; }
+  std::int64_t extent(int d) const { return d == 0 ? r : c; }
+  std::int64_t stride(int d) const { return d == 0 ? ld : 1; }
+};
+
+template <class Model>
+__global__ void in_kernel_sarray23(typename Model::Params p, float* result) {
+  ponni::SArray<float, 2> in;
+  ponni::SArray<float, 3> out;
+  in(0) = 1.0f;
+  in(1) = 2.0f;
+  Model::forward_batch_parallel_in_kernel(in, out, p);
+  for (int i = 0; i < 3; i++) result[i] = out(i);
+}
+
+void test_device_views_gpu() {
+  using namespace ponni;
+  using DeviceMatrix = View<float**, HIPSpace>;
+  using DeviceVector = View<float*, HIPSpace>;
+  {  // the README model (README.md:44-67), built from device Views
+    DeviceMatrix weights_1("weights_1", 2, 3);
+    DeviceVector bias_1("bias_1", 3);
+    DeviceMatrix weights_2("weights_2", 3, 1);
+    DeviceVector bias_2("bias_2", 1);
+    deep_copy(weights_1, 0.25f);
+    deep_copy(bias_1, 0.10f);
+    deep_copy(weights_2, 0.50f);
+    deep_copy(bias_2, -0.20f);
+    auto model = create_inference_model(Matvec<float>(weights_1), Bias<float>(bias_1), Relu<float>(3),
+                                        Matvec<float>(weights_2), Bias<float>(bias_2));
+    model.validate();
+    CHECK(model.get_layer<0>().params.weights.data() == weights_1.data());  // shared, not copied
+    int const batch_size = 100000;
+    DeviceMatrix inputs("inputs", 2, batch_size);
+    deep_copy(inputs, 1.0f);
+    auto outputs = model.forward_batch_parallel(inputs);
+    auto const h = host(outputs);
+    CHECK(near(h[0], 0.7, 1e-6) && near(h[batch_size - 1], 0.7, 1e-6));  // 3 x 0.5 x 0.6 - 0.2
+    deep_copy(weights_1, 0.5f);  // a write through the shared View reaches the next pass
+    auto const h2 = host(model.forward_batch_parallel(inputs));
+    CHECK(near(h2[0], 1.45, 1e-6) && near(h2[batch_size / 2], 1.45, 1e-6));
+  }
+  {  // test_core_unit.cpp:516-546 with the weights shared
+    DeviceMatrix mv_w("mv_w", 2, 3);
+    mv_w.copy_from_host({1, 2, 3, 4, 5, 6});
+    Matvec<float> mv(mv_w, true);
+    CHECK(std::string(mv.get_label()) == "Matvec" && mv.get_num_trainable_parameters() == 6);
+    CHECK(Matvec<float>::get_num_inputs(mv.params) == 2 && Matvec<float>::get_num_outputs(mv.params) == 3);
+    DeviceVector mv_new_params("mv_new_params", 6);
+    mv_new_params.copy_from_host({10, 11, 12, 13, 14, 15});
+    mv.set_trainable_parameters(mv_new_params);
+    auto got = host(mv.get_trainable_parameters());
+    CHECK(near(got[0], 10.0, 0) && near(got[5], 15.0, 0));
+    CHECK(host(mv_w)[0] == 10.0);  // the caller's View holds them
+    auto m = create_inference_model(mv);
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {1, 2})));
+    CHECK(y[0] == 36.0 && y[1] == 39.0 && y[2] == 42.0);
+    using StaticMatvec = Matvec<float, 2, 3>;
+    auto ms = create_inference_model(StaticMatvec(mv_w, true));
+    View<float> r("r", 1, 3);
+    using M = decltype(ms);
+    hipLaunchKernelGGL((in_kernel_sarray23<M>), dim3(1), dim3(1), 0, 0, ms.params, r.data());
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    auto hr = host(r);
+    CHECK(near(hr[0], 36.0, 1e-6) && near(hr[2], 42.0, 1e-6));
+    mv_w.copy_from_host({1, 1, 1, 1, 1, 1});  // shared with `m` as well
+    auto y1 = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {1, 2})));
+    CHECK(y1[0] == 3.0 && y1[2] == 3.0);
+  }
+  {  // host layers in a device model are copied (the rebind rule's other branch)
+    View<float**, HostSpace> hw("hw", 2, 1);
+    hw(0, 0) = 2.0f;
+    hw(1, 0) = -1.0f;
+    auto m = create_inference_model(Matvec<float, 1, 1, HostSpace>(hw));
+    static_assert(std::is_same_v<std::decay_t<decltype(m.get_layer<0>())>, Matvec<float, 1, 1, HIPSpace>>);
+    hw(0, 0) = 100.0f;  // not seen: the model holds a device copy
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {3, 1})));
+    CHECK(y[0] == 5.0);
+    // and a device layer in a host model (test_core_unit.cpp:380-404 spelling)
+    auto hm = create_inference_model(DefaultHostExecutionSpace(), HostSpace(), Matvec<float>(ones(2, 2)),
+                                     Bias<float>(std::vector<float>(2, 1.0f)), LeakyRelu<float>(2, 0.1f));
+    View<float, HostSpace> hx("hx", 2, 1);
+    hx(0, 0) = 1.0f;
+    hx(1, 0) = 2.0f;
+    auto hy = hm.forward_batch_parallel(hx);
+    CHECK(near(hy(0, 0), 4.0, 1e-6) && near(hy(1, 0), 4.0, 1e-6));
+  }
+  {  // a foreign device view type: shared through its pointer, or copied by the runtime
+    DeviceMatrix store("store", 2, 5);
+    store.copy_from_host({10, 11, 12, 0, 0, 13, 14, 15, 0, 0});
+    ForeignDeviceMatrix f{store.data(), 2, 3, 5};  // row stride 5
+    Matvec<float> mv(f);
+    CHECK(mv.params.weights.data() == store.data() && mv.params.weights.stride(0) == 5);
+    auto m = create_inference_model(mv);
+    auto y = host(m.forward_batch_parallel(device_matrix<float>(2, 1, {1, 2})));
+    CHECK(y[0] == 36.0 && y[1] == 39.0 && y[2] == 42.0);
+    Matvec<double> md(f);  // another element type: copied through the runtime
+    CHECK((host(md.params.weights) == std::vector<double>{10, 11, 12, 13, 14, 15}));
+    Bias<float> bf(ForeignDeviceMatrix{store.data(), 1, 3, 5});
+    CHECK(bf.params.weights.data() == store.data() && bf.get_num_inputs() == 3);
+  }
+  {  // LayerNorm gamma / beta Views shared with the model
+    DeviceVector g("g", 4), b("b", 4);
+    deep_copy(g, 1.0f);
+    auto m = create_inference_model(LayerNorm<float>(g, b));
+    auto x = device_matrix<float>(4, 1, {1, 2, 3, 4});
+    auto y0 = host(m.forward_batch_parallel(x));
+    deep_copy(b, 2.0f);
+    auto y1 = host(m.forward_batch_parallel(x));
+    for (int i = 0; i < 4; i++) CHECK(near(y1[i] - y0[i], 2.0, 1e-5));
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   bool const cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
-  test_structure_and_planning();
-  test_parameters_and_fingerprint();
-  test_weights_files();
+  test_structure_and_planning<ponni::HostSpace>();
+  test_parameters_and_fingerprint<ponni::HostSpace>();
+  test_weights_files<ponni::HostSpace>();
   test_sixteen_bit_types();
+  test_initializers_cpu();
+  test_rebinding_cpu();
   test_user_layers_cpu();
   test_host_models_cpu();
   if (!cpu_only) {
+    test_structure_and_planning<ponni::HIPSpace>();
+    test_parameters_and_fingerprint<ponni::HIPSpace>();
+    test_weights_files<ponni::HIPSpace>();
+    test_device_views_gpu();
     test_user_layers_gpu();
     test_known_answers_gpu();
     test_views_streams_capacity_gpu();

@@ -15,18 +15,21 @@
 
 namespace {
 
+// Layers live in the model's memory space, so the host run needs no device.
 template <class Space, class Exec>
 auto resnet(ponni::PonniFile const& f, Exec const& exec) {
   using namespace ponni;
+  using Mv = Matvec<float, 1, 1, Space>;
+  using B = Bias<float, 1, Space>;
+  using Act = Silu<float, 1, Space>;
+  using Save = Save_State<0, float, 1, Space>;
+  using Add = Binop_Add<0, float, 1, Space>;
+  auto w = [&](char const* name) { return load_ponni_tensor<2, Space>(f, name); };
   auto v = [&](char const* name) { return load_ponni_tensor<1, Space>(f, name); };
-  return create_inference_model(
-      exec, Space(), Matvec<float>(load_ponni_tensor<2, Space>(f, "fc1.weight")), Bias<float>(v("fc1.bias")), Silu<float>(5),
-      Save_State<0, float>(5), Matvec<float>(load_ponni_tensor<2, Space>(f, "fc2.weight")), Bias<float>(v("fc2.bias")),
-      Silu<float>(5), Binop_Add<0, float>(5), Save_State<0, float>(5),
-      Matvec<float>(load_ponni_tensor<2, Space>(f, "fc3.weight")), Bias<float>(v("fc3.bias")), Silu<float>(5),
-      Binop_Add<0, float>(5), Save_State<0, float>(5), Matvec<float>(load_ponni_tensor<2, Space>(f, "fc4.weight")),
-      Bias<float>(v("fc4.bias")), Silu<float>(5), Binop_Add<0, float>(5),
-      Matvec<float>(load_ponni_tensor<2, Space>(f, "fc5.weight")), Bias<float>(v("fc5.bias")));
+  return create_inference_model(exec, Space(), Mv(w("fc1.weight")), B(v("fc1.bias")), Act(5), Save(5),
+                                Mv(w("fc2.weight")), B(v("fc2.bias")), Act(5), Add(5), Save(5), Mv(w("fc3.weight")),
+                                B(v("fc3.bias")), Act(5), Add(5), Save(5), Mv(w("fc4.weight")), B(v("fc4.bias")),
+                                Act(5), Add(5), Mv(w("fc5.weight")), B(v("fc5.bias")));
 }
 
 template <class Space, class Exec>
@@ -36,8 +39,9 @@ auto projection(ponni::PonniFile const& f, Exec const& exec) {
   auto b_main = load_ponni_tensor<1, Space>(f, "b_main");
   auto w_skip = load_ponni_tensor<2, Space>(f, "w_skip");
   auto b_skip = load_ponni_tensor<1, Space>(f, "b_skip");
-  return create_inference_model(exec, Space(), Relu<float>(2), Save_State<0, float>(2), Matvec<float>(w_main, false),
-                                Bias<float>(b_main, false), Binop_Projection_Add<0, float, 3, 2>(w_skip, b_skip, false));
+  return create_inference_model(exec, Space(), Relu<float, 1, Space>(2), Save_State<0, float, 1, Space>(2),
+                                Matvec<float, 1, 1, Space>(w_main, false), Bias<float, 1, Space>(b_main, false),
+                                Binop_Projection_Add<0, float, 3, 2, Space>(w_skip, b_skip, false));
 }
 
 template <class Space, class Model>
