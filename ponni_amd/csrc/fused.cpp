@@ -186,7 +186,9 @@ std::string cache_dir() {
 // materializes it.  (Fused across layers, Mish's last product entered
 // MinMaxNorm's x - min unrounded and a sub-ulp difference was scaled by
 // 1 / (max - min).)  16-bit plans round their state to the 16-bit type at
-// every layer, which already stops that, and keep the default.
+// every op or block boundary (an epilogue fused into its dense block stays
+// in fp32 until that rounding, within an fp32 ulp of the unfused
+// evaluation), which already stops that, and keep the default.
 std::vector<char const*> jit_options(bool contract) {
   std::vector<char const*> o{"--offload-arch=gfx950", "-O3", "-std=c++17"};
   if (contract) o.push_back("-ffp-contract=on");
@@ -970,9 +972,15 @@ bool narrow_jit_supports(ponni_plan_s const& p) {
 
 namespace {
 
+// Source, options, embedded headers and the run-time compiler's version: a
+// compiler upgrade (whose code generation the kernels' numerics depend on)
+// never picks up an object an older one wrote.
 std::string cache_key(std::string const& src, bool contract) {
   std::string opts;
   for (auto const* o : jit_options(contract)) opts += std::string(o) + " ";
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) == HIPRTC_SUCCESS)
+    opts += "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + " ";
   std::string hdrs;
   for (int i = 0; i < kJitHeaderCount; i++) hdrs += kJitHeaderTexts[i];
   char buf[32];

@@ -3,6 +3,7 @@
 // including its branch structure, so results agree with the reference to
 // rounding.
 #pragma once
+#define PONNI_POINTWISE_H 1
 
 #ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>

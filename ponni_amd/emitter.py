@@ -19,6 +19,13 @@ Build the application with
   hipcc -std=c++17 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops
         -I<repo>/include -I<repo>/ponni_amd/include -I<repo>/ponni_amd/csrc app.cpp
         -L<repo>/ponni_amd -lponni_hip
+
+The header sets `#pragma clang fp contract(on)` before its first include,
+so its kernels (and everything after it in the translation unit) fuse
+multiply-adds only within one expression: each layer's state is rounded
+before the next layer reads it, as in the library's fp32 / fp64 kernels
+(-ffp-contract=on), whatever contraction the application compiles with.  It
+must therefore come before any other include of ponni.h.
 """
 from __future__ import annotations
 
@@ -119,6 +126,16 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("// hipcc -std=c++17 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops")
     w("//       -I<repo>/include -I<repo>/ponni_amd/include -I<repo>/ponni_amd/csrc ... -lponni_hip")
     w("#pragma once")
+    w("")
+    w("// Kernels below and the helpers they inline fuse multiply-adds only within one expression,")
+    w("// so a layer's state is rounded before the next layer reads it (the library compiles its")
+    w("// fp32 / fp64 kernels the same way).  The rule applies from here to the end of the")
+    w("// translation unit; the helpers are compiled at their first include, hence the check.")
+    w("#if defined(PONNI_POINTWISE_H) && !defined(PONNI_GENERATED_CONTRACT_ON)")
+    w('#error "include the generated model header before ponni.h and the library kernel headers"')
+    w("#endif")
+    w("#pragma clang fp contract(on)")
+    w("#define PONNI_GENERATED_CONTRACT_ON 1")
     w("")
     w('#include "ponni.h"')
     if need_fused:

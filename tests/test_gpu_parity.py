@@ -323,7 +323,7 @@ def test_hip_graph_capture_and_replay(cuda, path):
     check_f32(got.double().cpu().numpy(), oracle.forward(layers, x.double().cpu().numpy()), scale_tol=False)
 
 
-@pytest.mark.parametrize("path", ["narrow", "fused"])
+@pytest.mark.parametrize("path", PATHS)
 def test_state_rounded_before_min_max_norm(cuda, path):
     """Each layer's state is rounded before the next layer reads it, so
     MinMaxNorm's x - min is exactly 0 for the minimum.  In this random chain
