@@ -99,6 +99,14 @@ typedef enum ponni_layer_kind {
                                     attr[1] alpha, attr[2] gamma                       */
   PONNI_LAYER_CONST_BINARY = 45, /* pointwise op(state, c) with a constant c [n_in];
                                     attr[0] = ponni_binary_op; flags bit0 = c on the left */
+  PONNI_LAYER_SELECT = 46,       /* interpreter.py:178-183 Where / CompareSelect: cond != 0 ?
+                                    a : b over n_out features.  Each operand comes from
+                                    the state, a saved slot or a constant (flags: 2 bits
+                                    per operand, PONNI_SELECT_*); the first slot operand
+                                    is saved[slot], the second saved[attr[1]]; a one-
+                                    feature operand broadcasts (flags bits 6-8); constant
+                                    a, then constant b, are the layer's parameters
+                                    [n_out] each.  The condition is never a constant. */
 
   /* A layer the library does not implement: a user layer of the C++ facade
    * under the reference's plugin contract (ponni_LayerTraits.h:10-61; its
@@ -119,7 +127,18 @@ typedef enum ponni_binary_op {
   PONNI_BINARY_DIV = 3,
   PONNI_BINARY_MIN = 4, /* a < b ? a : b */
   PONNI_BINARY_MAX = 5, /* a > b ? a : b */
-  PONNI_BINARY_POW = 6
+  PONNI_BINARY_POW = 6,
+  /* comparisons and logic give 1 or 0 (interpreter.py:132-162; a boolean is
+   * 1 / 0 in the state, anything nonzero is true) */
+  PONNI_BINARY_EQUAL = 7,
+  PONNI_BINARY_GREATER = 8,
+  PONNI_BINARY_GREATER_EQUAL = 9,
+  PONNI_BINARY_LESS = 10,
+  PONNI_BINARY_LESS_EQUAL = 11,
+  PONNI_BINARY_AND = 12,
+  PONNI_BINARY_OR = 13,
+  PONNI_BINARY_XOR = 14,
+  PONNI_BINARY_PRELU = 15 /* a >= 0 ? a : a * b (interpreter.py:164-165) */
 } ponni_binary_op;
 
 /* Feature reductions of PONNI_LAYER_REDUCE (emitter.py:475-512). */
@@ -149,8 +168,36 @@ typedef enum ponni_unary_op {
   PONNI_UNARY_CELU = 7,             /* attr[1] alpha */
   PONNI_UNARY_THRESHOLDED_RELU = 8, /* attr[1] alpha */
   PONNI_UNARY_ERF = 9,
-  PONNI_UNARY_SELU = 10             /* attr[1] alpha, attr[2] gamma: gamma * (x > 0 ? x : alpha*(e^x - 1)) */
+  PONNI_UNARY_SELU = 10,            /* attr[1] alpha, attr[2] gamma: gamma * (x > 0 ? x : alpha*(e^x - 1)) */
+  PONNI_UNARY_ACOS = 11,
+  PONNI_UNARY_ACOSH = 12,
+  PONNI_UNARY_ASIN = 13,
+  PONNI_UNARY_ASINH = 14,
+  PONNI_UNARY_ATAN = 15,
+  PONNI_UNARY_ATANH = 16,
+  PONNI_UNARY_CEIL = 17,
+  PONNI_UNARY_COS = 18,
+  PONNI_UNARY_COSH = 19,
+  PONNI_UNARY_FLOOR = 20,
+  PONNI_UNARY_SIN = 21,
+  PONNI_UNARY_SINH = 22,
+  PONNI_UNARY_TAN = 23,
+  PONNI_UNARY_ROUND = 24,           /* to nearest, ties to even (numpy round) */
+  PONNI_UNARY_SIGN = 25,            /* -1, 0, 1; NaN stays NaN */
+  PONNI_UNARY_IS_NAN = 26,          /* 1 / 0 */
+  PONNI_UNARY_IS_INF = 27,          /* 1 / 0; attr[1] detect_negative, attr[2] detect_positive */
+  PONNI_UNARY_NOT = 28,             /* x == 0 ? 1 : 0 */
+  PONNI_UNARY_NONZERO = 29          /* Cast to bool: x != 0 ? 1 : 0 */
 } ponni_unary_op;
+
+/* Operand sources of PONNI_LAYER_SELECT (2 bits each in flags: cond bits 0-1,
+ * a bits 2-3, b bits 4-5), and its one-feature (broadcast) operand flags. */
+#define PONNI_SELECT_STATE 0
+#define PONNI_SELECT_SLOT 1
+#define PONNI_SELECT_CONST 2
+#define PONNI_SELECT_COND_SCALAR 64
+#define PONNI_SELECT_A_SCALAR 128
+#define PONNI_SELECT_B_SCALAR 256
 
 #define PONNI_FLAG_DENSE_BIAS 1 /* PONNI_LAYER_DENSE carries a bias     */
 #define PONNI_FLAG_SAVED_LEFT 1 /* PONNI_LAYER_BINARY: saved[slot] op state */

@@ -98,6 +98,9 @@ inline H16& operator/=(H16& a, H16 b) { return a = a / b; }
 inline bool operator>(H16 a, H16 b) { return a.v > b.v; }
 inline bool operator<(H16 a, H16 b) { return a.v < b.v; }
 inline bool operator>=(H16 a, H16 b) { return a.v >= b.v; }
+inline bool operator<=(H16 a, H16 b) { return a.v <= b.v; }
+inline bool operator==(H16 a, H16 b) { return a.v == b.v; }
+inline bool operator!=(H16 a, H16 b) { return a.v != b.v; }
 inline H16 o_exp(H16 x) { return H16(std::exp(x.v)); }
 inline H16 o_log(H16 x) { return H16(std::log(x.v)); }
 inline H16 o_tanh(H16 x) { return H16(std::tanh(x.v)); }
@@ -123,9 +126,56 @@ inline double o_abs(double x) { return std::fabs(x); }
 inline double o_pow(double x, double y) { return std::pow(x, y); }
 inline bool o_isinf(double x) { return std::isinf(x); }
 
-// emitter.py:261-275
+// Unary math of generated graphs (emitter.py:218-258; interpreter.py:15-117)
+// in the arithmetic of T: float overloads for fp32, double for fp64, and the
+// fp32 value of a half rounded back to half (a half chain's activations,
+// ponni_TwoHalf.h:138-153).  Round is ties-to-even (emitter.py:1659-1667).
+double math_op(int op, double x) {
+  switch (op) {
+    case PONNI_UNARY_ACOS: return std::acos(x);
+    case PONNI_UNARY_ACOSH: return std::acosh(x);
+    case PONNI_UNARY_ASIN: return std::asin(x);
+    case PONNI_UNARY_ASINH: return std::asinh(x);
+    case PONNI_UNARY_ATAN: return std::atan(x);
+    case PONNI_UNARY_ATANH: return std::atanh(x);
+    case PONNI_UNARY_CEIL: return std::ceil(x);
+    case PONNI_UNARY_COS: return std::cos(x);
+    case PONNI_UNARY_COSH: return std::cosh(x);
+    case PONNI_UNARY_FLOOR: return std::floor(x);
+    case PONNI_UNARY_SIN: return std::sin(x);
+    case PONNI_UNARY_SINH: return std::sinh(x);
+    case PONNI_UNARY_TAN: return std::tan(x);
+    default: return std::nearbyint(x);  // PONNI_UNARY_ROUND, default rounding mode: ties to even
+  }
+}
+float math_op(int op, float x) {
+  switch (op) {
+    case PONNI_UNARY_ACOS: return std::acos(x);
+    case PONNI_UNARY_ACOSH: return std::acosh(x);
+    case PONNI_UNARY_ASIN: return std::asin(x);
+    case PONNI_UNARY_ASINH: return std::asinh(x);
+    case PONNI_UNARY_ATAN: return std::atan(x);
+    case PONNI_UNARY_ATANH: return std::atanh(x);
+    case PONNI_UNARY_CEIL: return std::ceil(x);
+    case PONNI_UNARY_COS: return std::cos(x);
+    case PONNI_UNARY_COSH: return std::cosh(x);
+    case PONNI_UNARY_FLOOR: return std::floor(x);
+    case PONNI_UNARY_SIN: return std::sin(x);
+    case PONNI_UNARY_SINH: return std::sinh(x);
+    case PONNI_UNARY_TAN: return std::tan(x);
+    default: return std::nearbyint(x);
+  }
+}
+H16 math_op(int op, H16 x) { return H16(math_op(op, x.v)); }
+inline bool o_isnan(H16 x) { return std::isnan(x.v); }
+inline bool o_isnan(float x) { return std::isnan(x); }
+inline bool o_isnan(double x) { return std::isnan(x); }
+
+// emitter.py:261-275; comparisons and logic (interpreter.py:132-162,
+// emitter.py:397-424) give 1 / 0 and read any nonzero operand as true.
 template <class T>
 T binary_op(int op, T l, T r) {
+  T const one = T(1), zero = T(0);
   switch (op) {
     case PONNI_BINARY_ADD: return l + r;
     case PONNI_BINARY_SUB: return l - r;
@@ -133,6 +183,15 @@ T binary_op(int op, T l, T r) {
     case PONNI_BINARY_DIV: return l / r;
     case PONNI_BINARY_MIN: return l < r ? l : r;
     case PONNI_BINARY_MAX: return l > r ? l : r;
+    case PONNI_BINARY_EQUAL: return l == r ? one : zero;
+    case PONNI_BINARY_GREATER: return l > r ? one : zero;
+    case PONNI_BINARY_GREATER_EQUAL: return l >= r ? one : zero;
+    case PONNI_BINARY_LESS: return l < r ? one : zero;
+    case PONNI_BINARY_LESS_EQUAL: return l <= r ? one : zero;
+    case PONNI_BINARY_AND: return (l != zero && r != zero) ? one : zero;
+    case PONNI_BINARY_OR: return (l != zero || r != zero) ? one : zero;
+    case PONNI_BINARY_XOR: return ((l != zero) != (r != zero)) ? one : zero;
+    case PONNI_BINARY_PRELU: return l >= zero ? l : l * r;  // interpreter.py:164-165
     default: return o_pow(l, r);
   }
 }
@@ -202,7 +261,18 @@ T pointwise(ponni_layer_desc const& d, double const* p, T x, int f) {
         case PONNI_UNARY_CELU: return x > T(0) ? x : alpha * (o_exp(x / alpha) - T(1));
         case PONNI_UNARY_THRESHOLDED_RELU: return x > alpha ? x : T(0);
         case PONNI_UNARY_SELU: return T(d.attr[2]) * (x > T(0) ? x : alpha * (o_exp(x) - T(1)));
-        default: return o_erf(x);
+        case PONNI_UNARY_ERF: return o_erf(x);
+        case PONNI_UNARY_SIGN:  // emitter.py:1669-1674
+          return o_isnan(x) ? x : x > T(0) ? T(1) : x < T(0) ? T(-1) : T(0);
+        case PONNI_UNARY_IS_NAN: return o_isnan(x) ? T(1) : T(0);
+        case PONNI_UNARY_IS_INF: {  // interpreter.py:171-177
+          bool const neg = o_isinf(x) && x < T(0) && d.attr[1] != 0.0;
+          bool const pos = o_isinf(x) && x > T(0) && d.attr[2] != 0.0;
+          return neg || pos ? T(1) : T(0);
+        }
+        case PONNI_UNARY_NOT: return x == T(0) ? T(1) : T(0);
+        case PONNI_UNARY_NONZERO: return x != T(0) ? T(1) : T(0);
+        default: return math_op(static_cast<int>(d.attr[0]), x);
       }
     }
     case PONNI_LAYER_CONST_BINARY: {  // binary op with a constant operand
@@ -223,7 +293,15 @@ bool is_dense(int k) { return k == PONNI_LAYER_MATVEC || k == PONNI_LAYER_DENSE;
 
 bool reads_slot(int k) {
   return k == PONNI_LAYER_BINOP_ADD || k == PONNI_LAYER_BINOP_CONCATENATE || k == PONNI_LAYER_BINOP_PROJECTION_ADD ||
-         k == PONNI_LAYER_LOAD_STATE || k == PONNI_LAYER_BINARY;
+         k == PONNI_LAYER_LOAD_STATE || k == PONNI_LAYER_BINARY || k == PONNI_LAYER_SELECT;
+}
+
+// Constant operands of a Select layer (the operands whose 2-bit source field
+// in flags is PONNI_SELECT_CONST).
+int select_constants(ponni_layer_desc const& d) {
+  int n = 0;
+  for (int k = 0; k < 3; k++) n += ((d.flags >> (2 * k)) & 3) == PONNI_SELECT_CONST;
+  return n;
 }
 
 // ---- buffers ------------------------------------------------------------------
@@ -252,7 +330,7 @@ struct Ctx {
 
 // Barrier layer compute_all_outputs(in[, saved], out) for one sample.
 template <class T>
-void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_t b) {
+void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_t b, Buf<T> const* slots) {
   ponni_layer_desc const& d = c.layers[i];
   double const* p = c.params[i];
   int const n = d.n_in;
@@ -346,6 +424,34 @@ void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_
       }
       return;
     }
+    case PONNI_LAYER_SELECT: {  // interpreter.py:178-183 Where / CompareSelect
+      // Operand k (cond, a, b) is the state, a saved slot (the first saved
+      // operand reads d.slot, the second attr[1]) or a constant vector (the
+      // constants' values follow one another in p); a one-feature operand
+      // broadcasts.  All are read before the first write.
+      std::vector<T> v[3];
+      int slots_used = 0, consts_used = 0;
+      for (int k = 0; k < 3; k++) {
+        int const src = (d.flags >> (2 * k)) & 3;
+        if (src == PONNI_SELECT_STATE) {
+          for (int f = 0; f < d.n_in; f++) v[k].push_back(in(f, b));
+        } else if (src == PONNI_SELECT_SLOT) {
+          int const s = slots_used++ == 0 ? d.slot : static_cast<int>(d.attr[1]);
+          int const width = (d.flags & (PONNI_SELECT_COND_SCALAR << k)) ? 1 : d.n_out;
+          for (int f = 0; f < width; f++) v[k].push_back(slots[s](f, b));
+        } else {
+          double const* cv = p + int64_t(consts_used++) * d.n_out;
+          for (int f = 0; f < d.n_out; f++) v[k].push_back(T(cv[f]));
+        }
+      }
+      for (int f = 0; f < d.n_out; f++) {
+        T const cond = v[0][v[0].size() == 1 ? 0 : f];
+        T const a = v[1][v[1].size() == 1 ? 0 : f];
+        T const bb = v[2][v[2].size() == 1 ? 0 : f];
+        out(f, b) = c.store(cond != T(0) ? a : bb);
+      }
+      return;
+    }
     case PONNI_LAYER_REDUCE: {  // emitter.py:475-547
       int const op = static_cast<int>(d.attr[0]);
       T r;
@@ -434,17 +540,17 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
     }
     Buf<T> const sv = reads_slot(d.kind) ? saved[d.slot] : Buf<T>{};
     if (i == 0 && L == 1) {
-      barrier(c, i, x, sv, y, b);
+      barrier(c, i, x, sv, y, b, saved);
     } else if (i == 0) {
-      if (d.kind == PONNI_LAYER_SAVE_STATE) barrier(c, i, x, sv, saved[d.slot], b);
-      barrier(c, i, x, sv, tmp1, b);
+      if (d.kind == PONNI_LAYER_SAVE_STATE) barrier(c, i, x, sv, saved[d.slot], b, saved);
+      barrier(c, i, x, sv, tmp1, b, saved);
       in_tmp1 = true;
     } else if (i < L - 1) {
       Buf<T> const in = in_tmp1 ? tmp1 : tmp2;
       Buf<T> const out = d.kind == PONNI_LAYER_SAVE_STATE ? saved[d.slot] : in;
-      barrier(c, i, in, sv, out, b);
+      barrier(c, i, in, sv, out, b, saved);
     } else {
-      barrier(c, i, in_tmp1 ? tmp1 : tmp2, sv, y, b);
+      barrier(c, i, in_tmp1 ? tmp1 : tmp2, sv, y, b, saved);
     }
     i++;
   }
@@ -519,7 +625,8 @@ extern "C" {
 
 // Per-layer parameters are concatenated in layer order, each in the layer's
 // own layout (Matvec W [n_in, n_out]; LayerNorm gamma, beta; Projection_Add
-// W [NSAVE, n_in], bias; Dense W [n_out, n_in], bias; Const_Binary c [n_in]).  x / y are float for modes 0, 2, 3, 4, 5
+// W [NSAVE, n_in], bias; Dense W [n_out, n_in], bias; Const_Binary c [n_in];
+// Select: its constant operands, n_out values each).  x / y are float for modes 0, 2, 3, 4, 5
 // and double for mode 1.  Returns 0 on success.
 int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double const* params, int32_t mode,
                    void const* x, int64_t ld_x, void* y, int64_t ld_y, int64_t batch, int32_t threads) {
@@ -539,6 +646,7 @@ int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double co
         off += int64_t(d.n_out) * d.n_in + ((d.flags & PONNI_FLAG_DENSE_BIAS) ? d.n_out : 0);
         break;
       case PONNI_LAYER_CONST_BINARY: off += d.n_in; break;
+      case PONNI_LAYER_SELECT: off += int64_t(select_constants(d)) * d.n_out; break;
       default: break;
     }
   }

@@ -51,11 +51,17 @@ LAYER_REDUCE = 43
 LAYER_UNARY = 44
 LAYER_CONST_BINARY = 45
 
-BINARY_OPS = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Min": 4, "Max": 5, "Pow": 6}
+LAYER_SELECT = 46
+BINARY_OPS = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Min": 4, "Max": 5, "Pow": 6, "Equal": 7, "Greater": 8,
+              "GreaterOrEqual": 9, "Less": 10, "LessOrEqual": 11, "And": 12, "Or": 13, "Xor": 14, "PRelu": 15}
+SELECT_STATE, SELECT_SLOT, SELECT_CONST = 0, 1, 2
+SELECT_COND_SCALAR, SELECT_A_SCALAR, SELECT_B_SCALAR = 64, 128, 256
 REDUCE_OPS = {"ReduceSum": 0, "ReduceMean": 1, "ReduceMax": 2, "ReduceMin": 3, "ReduceL1": 4, "ReduceL2": 5,
               "ReduceSumSquare": 6, "ReduceLogSum": 7, "ReduceLogSumExp": 8, "ReduceProd": 9}
 UNARY_OPS = {"Abs": 0, "Neg": 1, "Exp": 2, "Log": 3, "Sqrt": 4, "Reciprocal": 5, "Softsign": 6, "Celu": 7,
-             "ThresholdedRelu": 8, "Erf": 9, "Selu": 10}
+             "ThresholdedRelu": 8, "Erf": 9, "Selu": 10, "Acos": 11, "Acosh": 12, "Asin": 13, "Asinh": 14,
+             "Atan": 15, "Atanh": 16, "Ceil": 17, "Cos": 18, "Cosh": 19, "Floor": 20, "Sin": 21, "Sinh": 22,
+             "Tan": 23, "Round": 24, "Sign": 25, "IsNaN": 26, "IsInf": 27, "Not": 28, "NonZero": 29}
 
 FLAG_GELU_APPROXIMATE = 1
 FLAG_CONCAT_AFTER = 1

@@ -72,6 +72,20 @@ bool zero_at_zero(int act) {
     case ACT_ERF:
     case ACT_SELU_AG:
     case ACT_MUL_C:
+    case ACT_ASIN:
+    case ACT_ASINH:
+    case ACT_ATAN:
+    case ACT_ATANH:
+    case ACT_CEIL:
+    case ACT_FLOOR:
+    case ACT_SIN:
+    case ACT_SINH:
+    case ACT_TAN:
+    case ACT_ROUND:
+    case ACT_SIGN:
+    case ACT_IS_NAN:
+    case ACT_IS_INF:
+    case ACT_NONZERO:
       return true;
     case ACT_THRESHOLDED_RELU:
       return true;  // 0 > a ? 0 : 0
@@ -80,9 +94,25 @@ bool zero_at_zero(int act) {
   }
 }
 
+// Binary operation (ponni_binary_op) on operand expressions l and r.
+std::string binary_expr(int op, std::string const& l = "x", std::string const& r = "y") {
+  switch (op) {
+    case PONNI_BINARY_ADD: return l + " + " + r;
+    case PONNI_BINARY_SUB: return l + " - " + r;
+    case PONNI_BINARY_MUL: return l + " * " + r;
+    case PONNI_BINARY_DIV: return l + " / " + r;
+    case PONNI_BINARY_MIN: return l + " < " + r + " ? " + l + " : " + r;
+    case PONNI_BINARY_MAX: return l + " > " + r + " ? " + l + " : " + r;
+    case PONNI_BINARY_POW: return "d_pow(" + l + ", " + r + ")";
+    default: return "apply_binary(" + std::to_string(op) + ", " + l + ", " + r + ")";
+  }
+}
+
 // f(v, c) of a step with a constant vector operand.
-std::string const_expr(int act) {
-  switch (act) {
+std::string const_expr(Step const& st) {
+  if (st.act == ACT_CBIN) return st.b != 0 ? binary_expr(static_cast<int>(st.a), "c", "v")
+                                           : binary_expr(static_cast<int>(st.a), "v", "c");
+  switch (st.act) {
     case ACT_BIAS: return "v + c";
     case ACT_SUB_C: return "v - c";
     case ACT_RSUB_C: return "c - v";
@@ -95,19 +125,6 @@ std::string const_expr(int act) {
     case ACT_RMAX_C: return "c > v ? c : v";
     case ACT_POW_C: return "d_pow(v, c)";
     default: return "d_pow(c, v)";
-  }
-}
-
-// Binary operation of OP_BINARY on operands x (left) and y (right).
-std::string binary_expr(int op) {
-  switch (op) {
-    case PONNI_BINARY_ADD: return "x + y";
-    case PONNI_BINARY_SUB: return "x - y";
-    case PONNI_BINARY_MUL: return "x * y";
-    case PONNI_BINARY_DIV: return "x / y";
-    case PONNI_BINARY_MIN: return "x < y ? x : y";
-    case PONNI_BINARY_MAX: return "x > y ? x : y";
-    default: return "powf(x, y)";
   }
 }
 
@@ -140,6 +157,25 @@ std::string act_expr(Step const& s, bool dbl = false) {
     case ACT_THRESHOLDED_RELU: return "act_thresholded_relu(v, " + lit(s.a) + ")";
     case ACT_ERF: return "d_erf(v)";
     case ACT_SELU_AG: return "act_selu_ag(v, " + lit(s.a) + ", " + lit(s.b) + ")";
+    case ACT_ACOS: return "d_acos(v)";
+    case ACT_ACOSH: return "d_acosh(v)";
+    case ACT_ASIN: return "d_asin(v)";
+    case ACT_ASINH: return "d_asinh(v)";
+    case ACT_ATAN: return "d_atan(v)";
+    case ACT_ATANH: return "d_atanh(v)";
+    case ACT_CEIL: return "d_ceil(v)";
+    case ACT_COS: return "d_cos(v)";
+    case ACT_COSH: return "d_cosh(v)";
+    case ACT_FLOOR: return "d_floor(v)";
+    case ACT_SIN: return "d_sin(v)";
+    case ACT_SINH: return "d_sinh(v)";
+    case ACT_TAN: return "d_tan(v)";
+    case ACT_ROUND: return "d_round(v)";
+    case ACT_SIGN: return "act_sign(v)";
+    case ACT_IS_NAN: return "act_is_nan(v)";
+    case ACT_IS_INF: return "act_is_inf(v, " + lit(s.a) + ", " + lit(s.b) + ")";
+    case ACT_NOT: return "act_not(v)";
+    case ACT_NONZERO: return "act_nonzero(v)";
     default: return "v";
   }
 }
@@ -311,6 +347,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         case OP_SAVE: slots[op.slot] = cur; break;
         case OP_LOAD: cur = tiles(op.n_out); need = cur * tr; break;
         case OP_BINARY: need = (cur + 2 * tiles(op.n_out)) * (half ? 16 : tr); cur = tiles(op.n_out); break;
+        case OP_SELECT: need = (cur + 4 * tiles(op.n_out)) * (half ? 16 : tr); cur = tiles(op.n_out); break;
         case OP_REDUCE: need = cur * (half ? 16 : tr); cur = 1; break;
         default: need = half ? cur * 16 : cur * tr; break;  // 16-bit states widen to fp32 for barriers
       }
@@ -564,7 +601,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         o << "    add_rows<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L);\n";
       } else if (act_has_param(st.act)) {
         o << "    map_const<" << tiles(n) << ">(" << v << ", " << vec(st.off, n) << ", L, [](" << F << " v, " << F << " c) { return "
-          << const_expr(st.act) << "; });\n";
+          << const_expr(st) << "; });\n";
         if (!zero_at_zero(st.act)) pad = true;
       } else {
         o << "    map<" << tiles(n) << ">(" << v << ", [](" << F << " v) { return " << act(st) << "; });\n";
@@ -625,7 +662,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             o << "      " << (m32 ? "t32_add_rows" : "tile_add_rows") << "(t, " << vec(st.off, n) << ", mo, L);\n";
           } else if (act_has_param(st.act)) {
             o << "      " << (m32 ? "t32_const" : "tile_const") << "(t, " << vec(st.off, n) << ", mo, L, [](" << F
-              << " v, " << F << " c) { return " << const_expr(st.act) << "; });\n";
+              << " v, " << F << " c) { return " << const_expr(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           } else {
             o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
@@ -649,7 +686,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
               o << "      t32_add_rows(t, " << vec(st.off, cur_n) << ", mo, L);\n";
             else if (act_has_param(st.act))
               o << "      t32_const(t, " << vec(st.off, cur_n) << ", mo, L, [](" << F << " v, " << F << " c) { return "
-                << const_expr(st.act) << "; });\n";
+                << const_expr(st) << "; });\n";
             else
               o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
           }
@@ -766,6 +803,34 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         cur_n = op.n_out;
         break;
       }
+      case OP_SELECT: {
+        // cond != 0 ? a : b; a constant operand is its vector broadcast over
+        // the tile's columns, a one-feature operand broadcasts over features.
+        std::string arg[3];
+        int consts = 0;
+        for (int k = 0; k < 3; k++) {
+          int const code = sel_src(op.aux, k);
+          if (code == 3) {
+            arg[k] = fresh();
+            o << "    auto " << arg[k] << " = bias_rows<" << tiles(op.n_out) << ", " << NT << ">("
+              << vec(consts++ == 0 ? op.woff : op.boff, op.n_out) << ", L);\n";
+            continue;
+          }
+          std::string const& e =
+              code == 0 ? cur : saved[code == 1 ? op.slot : static_cast<int>(op.f0)].first;
+          arg[k] = half ? "to_f32(" + e + ")" : e;
+        }
+        auto flag = [&](int bit) { return (op.aux & bit) ? std::string("true") : std::string("false"); };
+        std::string call = "select3<" + std::to_string(op.n_out) + ", " + flag(SEL_COND_SCALAR) + ", " +
+                           flag(SEL_A_SCALAR) + ", " + flag(SEL_B_SCALAR) + ">(" + arg[0] + ", " + arg[1] + ", " +
+                           arg[2] + ", L)";
+        if (half) call = "to_h<E>(" + call + ")";
+        std::string const nv = fresh();
+        o << "    auto " << nv << " = " << call << ";\n";
+        cur = nv;
+        cur_n = op.n_out;
+        break;
+      }
       case OP_REDUCE: {
         std::string const nv = fresh();
         std::string call = "reduce<" + std::to_string(op.aux) + ", " + std::to_string(cur_n) + ">(" +
@@ -845,7 +910,7 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
       Step const& st = p.steps[begin + k];
       if (act_has_param(st.act))
         o << "    with_vec" << tv(n) << "(" << a << ", P + " << st.off << ", [](real v, real c) { return "
-          << const_expr(st.act) << "; });\n";
+          << const_expr(st) << "; });\n";
       else
         o << "    map" << tv(n) << "(" << a << ", [](real v) { return " << (dbl ? act_expr(st, true) : act_fast_expr(st))
           << "; });\n";
@@ -877,6 +942,17 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         o << "    binary<" << V << ", " << op.n_out << ", " << W << ", " << op.aux << ">(s, sv" << op.slot << ");\n";
         o << finish(op.n_out) << "(s, s);\n";
         break;
+      case OP_SELECT: {
+        auto sv = [&](int code, int slot) {
+          for (int k = 0; k < 3; k++)
+            if (sel_src(op.aux, k) == code) return "sv" + std::to_string(slot);
+          return std::string("s");  // unused operand
+        };
+        o << "    select3<" << V << ", " << op.n_out << ", " << W << ", " << op.aux << ">(s, " << sv(1, op.slot) << ", "
+          << sv(2, static_cast<int>(op.f0)) << ", P + " << op.woff << ", P + " << op.boff << ");\n";
+        o << finish(op.n_out) << "(s, s);\n";
+        break;
+      }
       case OP_REDUCE:
         o << "    reduce<" << V << ", " << cur_n << ", " << W << ", " << op.aux << ">(s);\n";
         o << finish(1) << "(s, s);\n";

@@ -472,6 +472,32 @@ __device__ inline S<(N + 15) / 16, NT> binary(S<TA, NT> const& a, S<TB, NT> cons
   return out;
 }
 
+// out = cond != 0 ? a : b over N features (interpreter.py Where /
+// CompareSelect); an operand with one feature (SC / SA / SB) is broadcast.
+template <int N, bool SC, bool SA, bool SB, int TC, int TA, int TB, int NT>
+__device__ inline S<(N + 15) / 16, NT> select3(S<TC, NT> const& c, S<TA, NT> const& a, S<TB, NT> const& b,
+                                               Lane const& L) {
+  constexpr int T = (N + 15) / 16;
+  S<T, NT> out;
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    real const c0 = SC ? feature0(c, n, L) : real(0);
+    real const a0 = SA ? feature0(a, n, L) : real(0);
+    real const b0 = SB ? feature0(b, n, L) : real(0);
+#pragma unroll
+    for (int m = 0; m < T; m++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        real const x = SC ? c0 : c.v[SC ? 0 : m][n][e];
+        real const y = SA ? a0 : a.v[SA ? 0 : m][n][e];
+        real const z = SB ? b0 : b.v[SB ? 0 : m][n][e];
+        out.v[m][n][e] = apply_select<real>(x, y, z);
+      }
+  }
+  zero_pad<N, T, NT>(out, L);
+  return out;
+}
+
 __device__ inline real xprod(real v) {
   v *= __shfl_xor(v, 16);
   return v * __shfl_xor(v, 32);

@@ -193,6 +193,33 @@ __host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops,
         }
         break;
       }
+      case OP_SELECT: {  // interpreter.py:178-183 Where / CompareSelect: cond != 0 ? a : b
+        // Operand k comes from the state, a saved slot or a constant vector;
+        // a one-feature operand is read once, before an in-place write.
+        View2 const s1 = buf[BUF_SAVED + op.slot];
+        View2 const s2 = buf[BUF_SAVED + (op.f0 >= 0 ? static_cast<int>(op.f0) : op.slot)];
+        int const scalar_bits[3] = {SEL_COND_SCALAR, SEL_A_SCALAR, SEL_B_SCALAR};
+        int coff = op.woff;
+        C const* cvec[3] = {nullptr, nullptr, nullptr};
+        View2 src[3];
+        C first[3];
+        for (int k = 0; k < 3; k++) {
+          int const code = sel_src(op.aux, k);
+          src[k] = code == 0 ? in : code == 1 ? s1 : s2;
+          if (code == 3) {
+            cvec[k] = params + coff;
+            coff = op.boff;
+          }
+          first[k] = cvec[k] ? cvec[k][0] : load_as<S>(at<S>(src[k], 0, b));
+        }
+        for (int f = 0; f < op.n_out; f++) {
+          C v[3];
+          for (int k = 0; k < 3; k++)
+            v[k] = (op.aux & scalar_bits[k]) ? first[k] : cvec[k] ? cvec[k][f] : load_as<S>(at<S>(src[k], f, b));
+          store_as<S, C>(at<S>(out, f, b), apply_select<C>(v[0], v[1], v[2]));
+        }
+        break;
+      }
       case OP_REDUCE: {  // emitter.py:475-547
         int const n = op.n_in;
         C r;

@@ -278,6 +278,33 @@ __device__ inline void binary(C (&s)[W][V], C const (&sv)[W][V]) {
   }
 }
 
+// state = cond != 0 ? a : b (interpreter.py:178-183 Where / CompareSelect).  AUX
+// holds the operand sources of cond, a, b (2 bits each: 0 the state, 1 sv1,
+// 2 sv2, 3 a constant vector, c1 for the first constant operand and c2 for
+// a second) and the one-feature (broadcast) flags of program.h SelectAux.
+template <int V, int NOUT, int W, int AUX, class C>
+__device__ inline void select3(C (&s)[W][V], C const (&sv1)[W][V], C const (&sv2)[W][V], C const* __restrict__ c1,
+                               C const* __restrict__ c2) {
+  // The condition is never a constant, so b is the second constant exactly
+  // when a is a constant too.
+  auto operand = [&](int k, int f, int v) -> C {
+    int const code = sel_src(AUX, k);
+    bool const second_const = k == 2 && sel_src(AUX, 1) == 3;
+    return code == 0 ? s[f][v] : code == 1 ? sv1[f][v] : code == 2 ? sv2[f][v] : second_const ? c2[f] : c1[f];
+  };
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    C const k0 = operand(0, 0, v), k1 = operand(1, 0, v), k2 = operand(2, 0, v);
+#pragma unroll
+    for (int f = 0; f < NOUT; f++) {
+      C const c = (AUX & SEL_COND_SCALAR) ? k0 : operand(0, f, v);
+      C const a = (AUX & SEL_A_SCALAR) ? k1 : operand(1, f, v);
+      C const b = (AUX & SEL_B_SCALAR) ? k2 : operand(2, f, v);
+      s[f][v] = apply_select<C>(c, a, b);
+    }
+  }
+}
+
 // Reduction over the N features into feature 0 (emitter.py:475-547); OP is
 // a ponni_reduce_op value: 0 sum, 1 mean, 2 max, 3 min, 4 L1, 5 L2,
 // 6 sum of squares, 7 log-sum, 8 log-sum-exp, 9 product.

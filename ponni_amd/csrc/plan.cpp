@@ -41,10 +41,35 @@ bool is_dense(int kind) { return kind == PONNI_LAYER_MATVEC || kind == PONNI_LAY
 // Kinds that read a saved slot.
 bool reads_slot(int kind) {
   return kind == PONNI_LAYER_BINOP_ADD || kind == PONNI_LAYER_BINOP_CONCATENATE ||
-         kind == PONNI_LAYER_BINOP_PROJECTION_ADD || kind == PONNI_LAYER_LOAD_STATE || kind == PONNI_LAYER_BINARY;
+         kind == PONNI_LAYER_BINOP_PROJECTION_ADD || kind == PONNI_LAYER_LOAD_STATE || kind == PONNI_LAYER_BINARY ||
+         kind == PONNI_LAYER_SELECT;
 }
 
-bool is_graph_kind(int kind) { return kind >= PONNI_LAYER_DENSE && kind <= PONNI_LAYER_CONST_BINARY; }
+bool is_graph_kind(int kind) { return kind >= PONNI_LAYER_DENSE && kind <= PONNI_LAYER_SELECT; }
+
+// The operands of a PONNI_LAYER_SELECT (cond, a, b): where each comes from
+// (PONNI_SELECT_*), its slot when saved (the first saved operand is
+// d.slot, the second attr[1]), whether it is one feature, and the number
+// of constant operands.
+struct SelectOperands {
+  int src[3];
+  int slot[3];
+  bool scalar[3];
+  int num_slots = 0;
+  int num_const = 0;
+};
+SelectOperands select_operands(ponni_layer_desc const& d) {
+  SelectOperands o{};
+  int const scalar_bits[3] = {PONNI_SELECT_COND_SCALAR, PONNI_SELECT_A_SCALAR, PONNI_SELECT_B_SCALAR};
+  for (int k = 0; k < 3; k++) {
+    o.src[k] = (d.flags >> (2 * k)) & 3;
+    o.slot[k] = -1;
+    o.scalar[k] = (d.flags & scalar_bits[k]) != 0;
+    if (o.src[k] == PONNI_SELECT_SLOT) o.slot[k] = o.num_slots++ == 0 ? d.slot : static_cast<int>(d.attr[1]);
+    if (o.src[k] == PONNI_SELECT_CONST) o.num_const++;
+  }
+  return o;
+}
 
 bool is_save(int kind) { return kind == PONNI_LAYER_SAVE_STATE; }
 
@@ -97,6 +122,7 @@ char const* label_of(int kind) {
     case PONNI_LAYER_REDUCE: return "Reduce";
     case PONNI_LAYER_UNARY: return "Unary";
     case PONNI_LAYER_CONST_BINARY: return "Const_Binary";
+    case PONNI_LAYER_SELECT: return "Select";
     default: return "?";
   }
 }
@@ -109,6 +135,7 @@ int64_t param_count(ponni_layer_desc const& d) {
     case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(d.n_aux) * d.n_in + d.n_in;
     case PONNI_LAYER_DENSE: return int64_t(d.n_out) * d.n_in + ((d.flags & PONNI_FLAG_DENSE_BIAS) ? d.n_out : 0);
     case PONNI_LAYER_CONST_BINARY: return d.n_in;
+    case PONNI_LAYER_SELECT: return int64_t(select_operands(d).num_const) * d.n_out;
     default: return 0;
   }
 }
@@ -125,7 +152,8 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
     if (d.n_in <= 0 || d.n_out <= 0) return fail(PONNI_ERR_INVALID_MODEL, where + "num_inputs and num_outputs must be > 0");
     bool const same_width = !is_dense(d.kind) && d.kind != PONNI_LAYER_BINOP_CONCATENATE &&
                             d.kind != PONNI_LAYER_LOAD_STATE && d.kind != PONNI_LAYER_BINARY &&
-                            d.kind != PONNI_LAYER_REDUCE && d.kind != PONNI_LAYER_EXTERNAL;
+                            d.kind != PONNI_LAYER_REDUCE && d.kind != PONNI_LAYER_EXTERNAL &&
+                            d.kind != PONNI_LAYER_SELECT;
     if (same_width && d.n_in != d.n_out) return fail(PONNI_ERR_INVALID_MODEL, where + "input/output size mismatch");
     if (is_save(d.kind) || reads_slot(d.kind) || ext_saves(d) || ext_reads(d)) {
       if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
@@ -168,13 +196,42 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
           return fail(PONNI_ERR_INVALID_MODEL, where + "num outputs != the saved state's width");
         if (d.kind == PONNI_LAYER_BINARY) {
           int const op = static_cast<int>(d.attr[0]);
-          if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_POW)
+          if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_PRELU)
             return fail(PONNI_ERR_INVALID_MODEL, where + "unknown binary operation");
           if (d.n_aux != saved) return fail(PONNI_ERR_INVALID_MODEL, where + "n_aux != the saved state's width");
           if ((saved != 1 && saved != d.n_out) || (d.n_in != 1 && d.n_in != d.n_out) ||
               (d.n_out != std::max(d.n_in, saved)))
             return fail(PONNI_ERR_INVALID_MODEL, where + "unsupported broadcasting: operand sizes " + std::to_string(d.n_in) +
                                                      " and " + std::to_string(saved) + ", output size " +
+                                                     std::to_string(d.n_out));
+        }
+        break;
+      }
+      case PONNI_LAYER_SELECT: {
+        SelectOperands const o = select_operands(d);
+        int states = 0;
+        for (int k = 0; k < 3; k++) {
+          if (o.src[k] > PONNI_SELECT_CONST) return fail(PONNI_ERR_INVALID_MODEL, where + "unknown operand source");
+          states += o.src[k] == PONNI_SELECT_STATE;
+        }
+        if (states != 1) return fail(PONNI_ERR_INVALID_MODEL, where + "exactly one operand is the state");
+        if (o.src[0] == PONNI_SELECT_CONST) return fail(PONNI_ERR_INVALID_MODEL, where + "the condition is not a constant");
+        if (o.num_slots == 2 && (d.attr[1] != static_cast<int>(d.attr[1]) || d.attr[1] < 0 || d.attr[1] >= kMaxSlots))
+          return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
+        for (int k = 0; k < 3; k++) {
+          int width = d.n_out;
+          if (o.src[k] == PONNI_SELECT_STATE) width = d.n_in;
+          if (o.src[k] == PONNI_SELECT_SLOT) {
+            if (!saved_seen[o.slot[k]])
+              return fail(PONNI_ERR_INVALID_MODEL, where + "reads saved state " + std::to_string(o.slot[k]) +
+                                                       " before any Save_State wrote it");
+            width = saved_size[o.slot[k]];
+          }
+          if (o.src[k] == PONNI_SELECT_CONST && o.scalar[k])
+            return fail(PONNI_ERR_INVALID_MODEL, where + "a constant operand holds n_out values");
+          if ((width != 1 && width != d.n_out) || o.scalar[k] != (width == 1 && d.n_out > 1))
+            return fail(PONNI_ERR_INVALID_MODEL, where + "unsupported broadcasting: an operand of " +
+                                                     std::to_string(width) + " features, output size " +
                                                      std::to_string(d.n_out));
         }
         break;
@@ -188,14 +245,14 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
       }
       case PONNI_LAYER_UNARY: {
         int const op = static_cast<int>(d.attr[0]);
-        if (d.attr[0] != op || op < PONNI_UNARY_ABS || op > PONNI_UNARY_SELU)
+        if (d.attr[0] != op || op < PONNI_UNARY_ABS || op > PONNI_UNARY_NONZERO)
           return fail(PONNI_ERR_INVALID_MODEL, where + "unknown unary operation");
         if (op == PONNI_UNARY_CELU && !(d.attr[1] != 0)) return fail(PONNI_ERR_INVALID_MODEL, where + "Celu alpha must be nonzero");
         break;
       }
       case PONNI_LAYER_CONST_BINARY: {
         int const op = static_cast<int>(d.attr[0]);
-        if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_POW)
+        if (d.attr[0] != op || op < PONNI_BINARY_ADD || op > PONNI_BINARY_PRELU)
           return fail(PONNI_ERR_INVALID_MODEL, where + "unknown binary operation");
         break;
       }
@@ -252,7 +309,12 @@ Step make_step(ponni_layer_desc const& d) {
         case PONNI_BINARY_DIV: s.act = left ? ACT_RDIV_C : ACT_DIV_C; break;
         case PONNI_BINARY_MIN: s.act = left ? ACT_RMIN_C : ACT_MIN_C; break;
         case PONNI_BINARY_MAX: s.act = left ? ACT_RMAX_C : ACT_MAX_C; break;
-        default: s.act = left ? ACT_RPOW_C : ACT_POW_C; break;
+        case PONNI_BINARY_POW: s.act = left ? ACT_RPOW_C : ACT_POW_C; break;
+        default:
+          s.act = ACT_CBIN;
+          s.a = d.attr[0];
+          s.b = left ? 1 : 0;
+          break;
       }
       break;
     }
@@ -277,6 +339,7 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
         case PONNI_LAYER_BIAS: return W;
         case PONNI_LAYER_LAYER_NORM: return 2 * W;
         case PONNI_LAYER_BINOP_PROJECTION_ADD: return int64_t(W) * W + W;
+        case PONNI_LAYER_SELECT: return int64_t(select_operands(d).num_const) * W;
         default: return 0;
       }
     case PONNI_PATH_MFMA:
@@ -296,6 +359,7 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
           case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
           case PONNI_LAYER_BINOP_PROJECTION_ADD:
             return int64_t(steps(d.n_aux)) * tiles(d.n_in) * 256 + round_up(d.n_in, 16);
+          case PONNI_LAYER_SELECT: return int64_t(select_operands(d).num_const) * round_up(d.n_out, 16);
           default: return 0;
         }
       }
@@ -309,6 +373,7 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
         case PONNI_LAYER_LAYER_NORM: return 2 * round_up(d.n_in, 16);
         case PONNI_LAYER_BINOP_PROJECTION_ADD:
           return int64_t(tiles(d.n_aux)) * tiles(d.n_in) * 256 + round_up(d.n_in, 16);
+        case PONNI_LAYER_SELECT: return int64_t(select_operands(d).num_const) * round_up(d.n_out, 16);
         default: return 0;
       }
     }
@@ -440,6 +505,24 @@ void lower(ponni_plan_s& p) {
         op.code = OP_REDUCE;
         op.aux = static_cast<int>(d.attr[0]);
         break;
+      case PONNI_LAYER_SELECT: {
+        SelectOperands const o = select_operands(d);
+        op.code = OP_SELECT;
+        op.aux = (o.scalar[0] ? SEL_COND_SCALAR : 0) | (o.scalar[1] ? SEL_A_SCALAR : 0) |
+                 (o.scalar[2] ? SEL_B_SCALAR : 0);
+        int slots = 0;
+        for (int k = 0; k < 3; k++) {
+          int code = 0;
+          if (o.src[k] == PONNI_SELECT_SLOT) code = ++slots;  // first or second saved operand
+          if (o.src[k] == PONNI_SELECT_CONST) code = 3;
+          op.aux |= code << (SEL_SRC_BITS * k);
+        }
+        op.slot = d.slot;
+        op.f0 = o.num_slots == 2 ? d.attr[1] : -1.0;
+        // Constant operands are packed one after the other.
+        op.boff = static_cast<int32_t>(op.woff + (o.num_const == 2 ? vec_size(p, d.n_out) : 0));
+        break;
+      }
       default: {  // lone pointwise layer
         op.code = OP_POINTWISE;
         op.epi_begin = static_cast<int32_t>(p.steps.size());
@@ -646,6 +729,9 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
         dense(0, d.n_aux, d.n_in, false);
         vec(size - vec_size(p, d.n_in), int64_t(d.n_aux) * d.n_in, d.n_in);
         break;
+      case PONNI_LAYER_SELECT:
+        for (int c = 0; c < select_operands(d).num_const; c++) vec(c * vec_size(p, d.n_out), int64_t(c) * d.n_out, d.n_out);
+        break;
       default:
         break;
     }
@@ -730,6 +816,10 @@ bool segment_range(ponni_layer_desc const& d, int seg, int64_t& first, int64_t& 
     case PONNI_LAYER_DENSE:
       first = seg == 1 ? int64_t(d.n_out) * d.n_in : 0;
       count = seg == 0 ? int64_t(d.n_out) * d.n_in : (seg == 1 && (d.flags & PONNI_FLAG_DENSE_BIAS)) ? d.n_out : 0;
+      break;
+    case PONNI_LAYER_SELECT:  // one segment per constant operand, in operand order
+      first = int64_t(seg) * d.n_out;
+      count = seg >= 0 && seg < select_operands(d).num_const ? d.n_out : 0;
       break;
     default: break;
   }

@@ -100,6 +100,48 @@ template <class T> __host__ __device__ inline T act_selu_ag(T x, T alpha, T gamm
   return gamma * (x > T(0) ? x : alpha * (d_exp(x) - T(1)));
 }
 
+// Unary math and predicates of generated graphs (interpreter.py:15-117,
+// :171-181); a boolean is 1 / 0.
+__host__ __device__ inline float d_acos(float x) { return acosf(x); }
+__host__ __device__ inline double d_acos(double x) { return acos(x); }
+__host__ __device__ inline float d_acosh(float x) { return acoshf(x); }
+__host__ __device__ inline double d_acosh(double x) { return acosh(x); }
+__host__ __device__ inline float d_asin(float x) { return asinf(x); }
+__host__ __device__ inline double d_asin(double x) { return asin(x); }
+__host__ __device__ inline float d_asinh(float x) { return asinhf(x); }
+__host__ __device__ inline double d_asinh(double x) { return asinh(x); }
+__host__ __device__ inline float d_atan(float x) { return atanf(x); }
+__host__ __device__ inline double d_atan(double x) { return atan(x); }
+__host__ __device__ inline float d_atanh(float x) { return atanhf(x); }
+__host__ __device__ inline double d_atanh(double x) { return atanh(x); }
+__host__ __device__ inline float d_ceil(float x) { return ceilf(x); }
+__host__ __device__ inline double d_ceil(double x) { return ceil(x); }
+__host__ __device__ inline float d_cos(float x) { return cosf(x); }
+__host__ __device__ inline double d_cos(double x) { return cos(x); }
+__host__ __device__ inline float d_cosh(float x) { return coshf(x); }
+__host__ __device__ inline double d_cosh(double x) { return cosh(x); }
+__host__ __device__ inline float d_floor(float x) { return floorf(x); }
+__host__ __device__ inline double d_floor(double x) { return floor(x); }
+__host__ __device__ inline float d_sin(float x) { return sinf(x); }
+__host__ __device__ inline double d_sin(double x) { return sin(x); }
+__host__ __device__ inline float d_sinh(float x) { return sinhf(x); }
+__host__ __device__ inline double d_sinh(double x) { return sinh(x); }
+__host__ __device__ inline float d_tan(float x) { return tanf(x); }
+__host__ __device__ inline double d_tan(double x) { return tan(x); }
+__host__ __device__ inline float d_round(float x) { return rintf(x); }  // ties to even, numpy round
+__host__ __device__ inline double d_round(double x) { return rint(x); }
+template <class T> __host__ __device__ inline T act_sign(T x) {
+  return x > T(0) ? T(1) : x < T(0) ? T(-1) : x == T(0) ? T(0) : x;  // NaN stays NaN
+}
+template <class T> __host__ __device__ inline T act_is_nan(T x) { return x != x ? T(1) : T(0); }
+template <class T> __host__ __device__ inline T act_is_inf(T x, T detect_negative, T detect_positive) {
+  bool const neg = x == -__builtin_inff() && detect_negative != T(0);
+  bool const pos = x == __builtin_inff() && detect_positive != T(0);
+  return neg || pos ? T(1) : T(0);
+}
+template <class T> __host__ __device__ inline T act_not(T x) { return x == T(0) ? T(1) : T(0); }
+template <class T> __host__ __device__ inline T act_nonzero(T x) { return x != T(0) ? T(1) : T(0); }
+
 // Element-wise op of the state v with a constant c, emitter.py:261-275.
 template <class T> __host__ __device__ inline T act_const(int act, T v, T c) {
   switch (act) {
@@ -119,7 +161,8 @@ template <class T> __host__ __device__ inline T act_const(int act, T v, T c) {
   }
 }
 
-// Tensor-tensor binary operation of generated graphs, emitter.py:261-275.
+// Tensor-tensor binary operation of generated graphs (ponni_binary_op),
+// emitter.py:261-275; comparisons and logic (interpreter.py:132-162) give 1 / 0.
 template <class T> __host__ __device__ inline T apply_binary(int op, T l, T r) {
   switch (op) {
     case 0: return l + r;
@@ -128,9 +171,21 @@ template <class T> __host__ __device__ inline T apply_binary(int op, T l, T r) {
     case 3: return l / r;
     case 4: return l < r ? l : r;
     case 5: return l > r ? l : r;
+    case 7: return l == r ? T(1) : T(0);
+    case 8: return l > r ? T(1) : T(0);
+    case 9: return l >= r ? T(1) : T(0);
+    case 10: return l < r ? T(1) : T(0);
+    case 11: return l <= r ? T(1) : T(0);
+    case 12: return (l != T(0)) && (r != T(0)) ? T(1) : T(0);
+    case 13: return (l != T(0)) || (r != T(0)) ? T(1) : T(0);
+    case 14: return (l != T(0)) != (r != T(0)) ? T(1) : T(0);
+    case 15: return l >= T(0) ? l : l * r;  // PRelu
     default: return d_pow(l, r);
   }
 }
+
+// state = cond != 0 ? a : b
+template <class T> __host__ __device__ inline T apply_select(T cond, T a, T b) { return cond != T(0) ? a : b; }
 
 // Apply one parameter-free (or scalar-parameter) layer-template activation
 // to every element visited by `each` (the NARROW and MFMA families, which run
@@ -173,6 +228,27 @@ __host__ __device__ inline T apply_step(int act, T x, T bias, T a, T b) {
     case ACT_THRESHOLDED_RELU: return act_thresholded_relu(x, a);
     case ACT_ERF: return d_erf(x);
     case ACT_SELU_AG: return act_selu_ag(x, a, b);
+    case ACT_ACOS: return d_acos(x);
+    case ACT_ACOSH: return d_acosh(x);
+    case ACT_ASIN: return d_asin(x);
+    case ACT_ASINH: return d_asinh(x);
+    case ACT_ATAN: return d_atan(x);
+    case ACT_ATANH: return d_atanh(x);
+    case ACT_CEIL: return d_ceil(x);
+    case ACT_COS: return d_cos(x);
+    case ACT_COSH: return d_cosh(x);
+    case ACT_FLOOR: return d_floor(x);
+    case ACT_SIN: return d_sin(x);
+    case ACT_SINH: return d_sinh(x);
+    case ACT_TAN: return d_tan(x);
+    case ACT_ROUND: return d_round(x);
+    case ACT_SIGN: return act_sign(x);
+    case ACT_IS_NAN: return act_is_nan(x);
+    case ACT_IS_INF: return act_is_inf(x, a, b);
+    case ACT_NOT: return act_not(x);
+    case ACT_NONZERO: return act_nonzero(x);
+    case ACT_CBIN: return b != T(0) ? apply_binary<T>(static_cast<int>(a), bias, x)
+                                    : apply_binary<T>(static_cast<int>(a), x, bias);
     case ACT_RELU: return act_relu(x);
     case ACT_LEAKY_RELU: return act_leaky_relu(x, a);
     case ACT_ELU: return act_elu(x, a);

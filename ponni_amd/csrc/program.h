@@ -42,24 +42,45 @@ enum Act : int32_t {
   ACT_THRESHOLDED_RELU = 28,  // v > a ? v : 0
   ACT_ERF = 29,
   ACT_SELU_AG = 30,           // b * (v > 0 ? v : a*(exp(v)-1)), generated Selu(alpha, gamma)
+  // ACT_ABS + ponni_unary_op for the rest (interpreter.py:15-117):
+  ACT_ACOS = 31,
+  ACT_ACOSH = 32,
+  ACT_ASIN = 33,
+  ACT_ASINH = 34,
+  ACT_ATAN = 35,
+  ACT_ATANH = 36,
+  ACT_CEIL = 37,
+  ACT_COS = 38,
+  ACT_COSH = 39,
+  ACT_FLOOR = 40,
+  ACT_SIN = 41,
+  ACT_SINH = 42,
+  ACT_TAN = 43,
+  ACT_ROUND = 44,       // nearest, ties to even
+  ACT_SIGN = 45,        // -1 / 0 / 1, NaN kept
+  ACT_IS_NAN = 46,      // 1 / 0
+  ACT_IS_INF = 47,      // 1 / 0; a = detect_negative, b = detect_positive
+  ACT_NOT = 48,         // v == 0 ? 1 : 0
+  ACT_NONZERO = 49,     // v != 0 ? 1 : 0 (Cast to bool)
   // Element-wise op with a constant vector c = params[off + f] (generated
   // Add/Sub/Mul/Div/Min/Max/Pow with one constant operand, emitter.py:261-275).
   // ACT_BIAS doubles as v + c.
-  ACT_SUB_C = 40,   // v - c
-  ACT_RSUB_C = 41,  // c - v
-  ACT_MUL_C = 42,   // v * c
-  ACT_DIV_C = 43,   // v / c
-  ACT_RDIV_C = 44,  // c / v
-  ACT_MIN_C = 45,   // v < c ? v : c
-  ACT_RMIN_C = 46,  // c < v ? c : v
-  ACT_MAX_C = 47,   // v > c ? v : c
-  ACT_RMAX_C = 48,  // c > v ? c : v
-  ACT_POW_C = 49,   // pow(v, c)
-  ACT_RPOW_C = 50   // pow(c, v)
+  ACT_SUB_C = 60,   // v - c
+  ACT_RSUB_C = 61,  // c - v
+  ACT_MUL_C = 62,   // v * c
+  ACT_DIV_C = 63,   // v / c
+  ACT_RDIV_C = 64,  // c / v
+  ACT_MIN_C = 65,   // v < c ? v : c
+  ACT_RMIN_C = 66,  // c < v ? c : v
+  ACT_MAX_C = 67,   // v > c ? v : c
+  ACT_RMAX_C = 68,  // c > v ? c : v
+  ACT_POW_C = 69,   // pow(v, c)
+  ACT_RPOW_C = 70,  // pow(c, v)
+  ACT_CBIN = 71     // ponni_binary_op a (comparisons, logic, PRelu) of v and c; b != 0: c on the left
 };
 
 // Steps that read a per-feature parameter vector at Step::off.
-constexpr bool act_has_param(int act) { return act == ACT_BIAS || (act >= ACT_SUB_C && act <= ACT_RPOW_C); }
+constexpr bool act_has_param(int act) { return act == ACT_BIAS || (act >= ACT_SUB_C && act <= ACT_CBIN); }
 
 struct Step {
   int32_t act;   // Act
@@ -85,8 +106,23 @@ enum OpCode : int32_t {
   OP_REDUCE = 13,     // state[0] = reduce(state[0..n_in)); aux = ponni_reduce_op   emitter.py:475-547
   // A caller-implemented layer (PONNI_LAYER_EXTERNAL): aux = the caller's
   // index, boff = PONNI_FLAG_EXT_* bits | EXT_ALSO_TMP1.
-  OP_EXTERNAL = 14
+  OP_EXTERNAL = 14,
+  // state = cond != 0 ? a : b (interpreter.py:178-183 Where / CompareSelect); aux =
+  // SelectAux bits; slot = the first saved operand's slot, f0 = the second's;
+  // woff / boff = parameter offsets of the first / second constant operand.
+  OP_SELECT = 15
 };
+
+// OP_SELECT's aux: operand sources (2 bits each: 0 state, 1 first slot
+// operand, 2 second slot operand, 3 constant) of cond, a, b, then the
+// one-feature (broadcast) flags.
+enum SelectAux : int32_t {
+  SEL_SRC_BITS = 2,
+  SEL_COND_SCALAR = 1 << 6,
+  SEL_A_SCALAR = 1 << 7,
+  SEL_B_SCALAR = 1 << 8
+};
+constexpr int sel_src(int aux, int operand) { return (aux >> (2 * operand)) & 3; }
 
 // OP_EXTERNAL's boff: a leading saving layer also fills tmp1
 // (ponni_Inference.h:499-514).

@@ -166,6 +166,40 @@ def graph_fingerprint(graph: Graph) -> str:
     return f"fnv1a64:{fnv1a64(text.encode('utf-8')):016x}"
 
 
+def graph_from_dict(data: dict) -> Graph:
+    """A Graph from its to_dict() form, the canonical_ir.json the reference
+    compiler writes next to every generated header (kokkos_nn/compiler.py:316,
+    ir.py:137-148).  The JSON holds no constant values: every constant starts
+    at zero in its declared shape and is filled by load_weights."""
+    tensors: dict[int, TensorValue] = {}
+    for key, t in data["tensors"].items():
+        shape = tuple(Symbol(d) if isinstance(d, str) else int(d) for d in t["shape"])
+        tensors[int(key)] = TensorValue(int(t["id"]), t["name"], shape, DType(t["dtype"]), t.get("producer"),
+                                        list(t.get("consumers", [])), bool(t.get("is_input", False)),
+                                        bool(t.get("is_output", False)), bool(t.get("is_constant", False)),
+                                        t.get("constant_name"))
+    nodes = [Node(int(n["id"]), n["op"], [int(i) for i in n["inputs"]], [int(o) for o in n["outputs"]],
+                  dict(n.get("attributes", {})), n.get("source_name", "")) for n in data["nodes"]]
+    constants = {}
+    for name, c in data["constants"].items():
+        dtype = DType(c["dtype"])
+        npt = {DType.FLOAT32: np.float32, DType.FLOAT64: np.float64, DType.INT32: np.int32,
+               DType.INT64: np.int64, DType.BOOL: np.bool_}[dtype]
+        shape = tuple(int(d) for d in c["shape"])
+        constants[name] = ConstantTensor(c["name"], shape, dtype, np.zeros(shape, dtype=npt),
+                                         c.get("canonical_layout", "onnx"), bool(c.get("learned", False)))
+    g = Graph([int(i) for i in data["inputs"]], [int(o) for o in data["outputs"]], tensors, nodes, constants,
+              dict(data.get("metadata", {})))
+    g.rebuild_links()
+    return g
+
+
+def load_canonical_ir(path) -> Graph:
+    """Read a canonical_ir.json file (graph_from_dict)."""
+    with open(path, encoding="utf-8") as f:
+        return graph_from_dict(json.load(f))
+
+
 # ---- building graphs ------------------------------------------------------------
 
 class GraphBuilder:
@@ -198,9 +232,16 @@ class GraphBuilder:
                                         constant_name=name)
         return tid
 
-    def node(self, op: str, inputs: list, size: int, attributes: dict | None = None, name: str = "") -> int:
+    def node(self, op: str, inputs: list, size: int, attributes: dict | None = None, name: str = "",
+             dtype: DType | None = None) -> int:
+        """A node with one output of `size` features; the output is boolean
+        for comparisons, logic and predicates, else the graph's type."""
         nid = len(self.nodes)
         out = self._tensor(name or f"{op.lower()}_{nid}", size)
+        if dtype is None and op in _BOOL_OPS:
+            dtype = DType.BOOL
+        if dtype is not None:
+            self.tensors[out].dtype = DType(dtype)
         self.nodes.append(Node(nid, op, list(inputs), [out], dict(attributes or {}), name))
         return out
 
@@ -230,6 +271,36 @@ class GraphBuilder:
 
     def softmax(self, x: int, log: bool = False) -> int:
         return self.node("LogSoftmax" if log else "Softmax", [x], self.size(x), {"axis": -1})
+
+    def compare(self, op: str, a: int, b: int) -> int:
+        """Equal / Greater / GreaterOrEqual / Less / LessOrEqual (boolean output)."""
+        return self.node(op, [a, b], max(self.size(a), self.size(b)))
+
+    def where(self, cond: int, a: int, b: int) -> int:
+        return self.node("Where", [cond, a, b], max(self.size(cond), self.size(a), self.size(b)))
+
+    def nary(self, op: str, *xs: int) -> int:
+        """Mean or Sum of tensors of one or the same number of features."""
+        return self.node(op, list(xs), max(self.size(x) for x in xs))
+
+    def clip(self, x: int, lo: float | None = None, hi: float | None = None) -> int:
+        """Clip with attribute bounds (either may be absent)."""
+        attrs = {}
+        if lo is not None:
+            attrs["min"] = float(lo)
+        if hi is not None:
+            attrs["max"] = float(hi)
+        return self.node("Clip", [x], self.size(x), attrs)
+
+    def gather(self, x: int, indices) -> int:
+        idx = [int(i) for i in indices]
+        return self.node("Gather", [x], len(idx), {"axis": 1, "indices": idx})
+
+    def batch_norm(self, x: int, scale, bias, mean, var, epsilon: float = 1e-5, name: str = "") -> int:
+        name = name or f"batch_norm_{len(self.nodes)}"
+        ins = [x] + [self.constant(f"{name}.{k}", np.asarray(v).reshape(-1), "output", learned=k in ("scale", "bias"))
+                     for k, v in (("scale", scale), ("bias", bias), ("mean", mean), ("var", var))]
+        return self.node("BatchNormalization", ins, self.size(x), {"epsilon": float(epsilon)}, name)
 
     def layer_norm(self, x: int, scale, bias=None, epsilon: float = 1e-5, name: str = "") -> int:
         name = name or f"layer_norm_{len(self.nodes)}"
@@ -282,6 +353,9 @@ def _unary_layer(op: str, n: int, attrs: dict) -> Layer:
         return Layer(A.LAYER_HARD_SWISH, n, n, label="HardSwish")
     if op == "Mish":
         return Layer(A.LAYER_MISH, n, n, label="Mish")
+    if op == "IsInf":
+        return Layer(A.LAYER_UNARY, n, n, attr=(A.UNARY_OPS[op], float(int(attrs.get("detect_negative", 1))),
+                                               float(int(attrs.get("detect_positive", 1))), 0), label=op)
     if op in A.UNARY_OPS:
         alpha = float(attrs.get("alpha", 1.6732631921768188 if op == "Selu" else 1.0))
         gamma = float(attrs.get("gamma", 1.0507010221481323))
@@ -297,75 +371,310 @@ class _Param:
 
 class LoweredGraph:
     """A graph as a layer chain (`layers`) plus, per layer, the function that
-    rebuilds its parameters from a {constant name: array} mapping."""
+    rebuilds its parameters from a {constant name: array} mapping.  `derived`
+    holds the constants the expansion introduced (a Mean's divisor, a
+    BatchNormalization denominator ...) as functions of that mapping."""
 
-    def __init__(self, layers: list[Layer], params: list[_Param | None], notes: list[str]):
+    def __init__(self, layers: list[Layer], params: list[_Param | None], notes: list[str],
+                 derived: dict[str, Callable[[dict], np.ndarray]] | None = None):
         self.layers = layers
         self.params = params
         self.notes = notes
+        self.derived = derived or {}
 
     def layer_params(self, constants: dict) -> list[np.ndarray]:
-        return [p.build(constants) if p is not None else np.zeros(0) for p in self.params]
+        c = dict(constants)
+        for name, f in self.derived.items():
+            c[name] = f(c)
+        return [p.build(c) if p is not None else np.zeros(0) for p in self.params]
 
 
-def _expand(graph: Graph) -> tuple[list[Node], dict[int, int]]:
-    """Resolve aliases, split fused dense variants (interpreter.py:353-381) into
-    Dense + element-wise nodes, and return (nodes, alias map)."""
+# Operations the layer chain takes as they are after expansion.
+_ELEM_BINARY = set(A.BINARY_OPS)
+_ELEM_UNARY = _TEMPLATE_ACTIVATIONS | set(A.UNARY_OPS)
+_COMPARISONS = {"Equal", "Greater", "GreaterOrEqual", "Less", "LessOrEqual"}
+_BOOL_OPS = _COMPARISONS | {"And", "Or", "Xor", "Not", "IsNaN", "IsInf"}
+
+
+@dataclass
+class _Expanded:
+    nodes: list
+    alias: dict
+    tensors: dict
+    derived: dict
+
+
+def _expand(graph: Graph) -> _Expanded:
+    """Rewrite the graph into the operations the layer chain takes.
+
+    Aliases resolve away (and Cast, which keeps the value: interpreter.py:
+    157-159, a boolean being 1 / 0); the optimizer's compound forms split into
+    their elementary steps in evaluation order: the fused Dense variants
+    (interpreter.py:353-381), ResidualAddActivation, ElementwiseChain,
+    PointwiseRegion and the mapped reductions (interpreter.py:206-237, :389-
+    425), CompareSelect, Clip, PRelu, n-ary Mean / Sum, BatchNormalization,
+    LpNormalization (interpreter.py:136-193, :344-351).  A Dense input_map
+    becomes a Dense over the concatenation of the tensors it reads, its
+    weight columns summed per source element (and constant entries folded
+    into the bias); a lone Gather becomes a Dense with one-hot rows.  Both
+    read unselected elements with weight 0, so a non-finite unselected
+    element (0 * inf) spoils the output where the reference skips it.
+
+    The graph itself is not modified: new tensors go into a copy of its
+    tensor table."""
     alias: dict[int, int] = {}
+    tensors = dict(graph.tensors)
+    derived: dict[str, Callable[[dict], np.ndarray]] = {}
+    nodes: list[Node] = []
+    fdtype = graph.tensors[graph.inputs[0]].dtype
+    npt = np.float32 if fdtype == DType.FLOAT32 else np.float64
+    next_tensor = max(tensors) + 1
 
     def r(t: int) -> int:
         while t in alias:
             t = alias[t]
         return t
 
-    nodes: list[Node] = []
-    next_tensor = max(graph.tensors) + 1
-    tensors = graph.tensors
+    def size(t: int) -> int:
+        return tensors[t].sample_size
 
-    def new_tensor(like: int) -> int:
+    def new_tensor(n: int, name: str, dtype: DType | None = None) -> int:
         nonlocal next_tensor
         tid = next_tensor
         next_tensor += 1
-        src = tensors[like]
-        tensors[tid] = TensorValue(tid, f"{src.name}.pre", src.shape, src.dtype)
+        tensors[tid] = TensorValue(tid, name, (Symbol("batch"), int(n)), dtype or fdtype)
         return tid
+
+    def derived_constant(n: int, name: str, f: Callable[[dict], np.ndarray]) -> int:
+        """A constant tensor of n values computed from the graph constants."""
+        nonlocal next_tensor
+        tid = next_tensor
+        next_tensor += 1
+        cname = f"__ponni_derived_{tid}"
+        tensors[tid] = TensorValue(tid, name, (int(n),), fdtype, is_constant=True, constant_name=cname)
+        derived[cname] = f
+        return tid
+
+    def literal(values, name: str) -> int:
+        v = np.asarray(values, dtype=np.float64).reshape(-1)
+        return derived_constant(v.size, name, lambda c, v=v: v)
+
+    def cvalues(c: dict, t: int) -> np.ndarray:
+        return np.asarray(c[tensors[t].constant_name], dtype=np.float64).reshape(-1)
+
+    def add(op: str, ins: list, out: int, attrs: dict | None = None, src: Node | None = None) -> None:
+        nodes.append(Node(src.id if src else -1, op, list(ins), [out], dict(attrs or {}),
+                          src.source_name if src else ""))
+
+    def out_for(op: str, ins: list, out: int | None, label: str) -> int:
+        if out is not None:
+            return out
+        n = max(size(t) for t in ins)
+        return new_tensor(n, f"{label}.{op}", DType.BOOL if op in _BOOL_OPS else None)
+
+    def pointwise(op: str, ins: list, attrs: dict, out: int | None, label: str, src: Node | None) -> int:
+        """Emit one pointwise operation (interpreter.py _pointwise_step); returns its tensor."""
+        ins = [r(t) for t in ins]
+        if op == "Cast":
+            if out is None:
+                return ins[0]
+            alias[out] = ins[0]
+            return ins[0]
+        if op in _ELEM_BINARY and len(ins) == 2:
+            out = out_for(op, ins, out, label)
+            add(op, ins, out, {}, src)
+            return out
+        if op == "IsInf":
+            out = out_for(op, ins, out, label)
+            add(op, ins, out, {"detect_negative": int(attrs.get("detect_negative", 1)),
+                               "detect_positive": int(attrs.get("detect_positive", 1))}, src)
+            return out
+        if op in _ELEM_UNARY and len(ins) == 1:
+            out = out_for(op, ins, out, label)
+            add(op, ins, out, attrs, src)
+            return out
+        if op in ("Mean", "Sum"):
+            acc = ins[0]
+            for k, t in enumerate(ins[1:]):
+                last = op == "Sum" and k == len(ins) - 2
+                acc = pointwise("Add", [acc, t], {}, out if last else None, label, src)
+            if op == "Mean":
+                acc = pointwise("Div", [acc, literal([len(ins)], f"{label}.count")], {}, out, label, src)
+            elif len(ins) == 1 and out is not None:
+                alias[out] = acc
+            return acc
+        if op == "Where":
+            out = out_for(op, ins, out, label)
+            add("Where", ins, out, {}, src)
+            return out
+        if op == "CompareSelect":
+            cond = pointwise(str(attrs["comparison"]), ins[:2], {}, None, label, src)
+            return pointwise("Where", [cond, ins[2], ins[3]], {}, out, label, src)
+        if op == "Clip":
+            # value < lo ? lo : value, then value > hi ? hi : value: the
+            # constant on the left keeps a NaN (emitter.py:823-835, np.clip).
+            lo = ins[1] if len(ins) > 1 else (literal([attrs["min"]], f"{label}.min") if "min" in attrs else None)
+            hi = ins[2] if len(ins) > 2 else (literal([attrs["max"]], f"{label}.max") if "max" in attrs else None)
+            v = ins[0]
+            if lo is None and hi is None:
+                if out is not None:
+                    alias[out] = v
+                return v
+            if lo is not None:
+                v = pointwise("Max", [lo, v], {}, out if hi is None else None, label, src)
+            if hi is not None:
+                v = pointwise("Min", [hi, v], {}, out, label, src)
+            return v
+        if op == "BatchNormalization":
+            # (x - mean) / sqrt(var + eps) * scale + bias (emitter.py:890-900)
+            x, scale, bias, mean, var = ins
+            eps = float(attrs.get("epsilon", 1e-5))
+            if tensors[var].is_constant:
+                def denom(c, var=var, eps=eps):
+                    v = cvalues(c, var).astype(npt)
+                    return np.sqrt(v + npt(eps)).astype(np.float64)
+                den = derived_constant(size(var), f"{label}.denominator", denom)
+            else:
+                den = pointwise("Sqrt", [pointwise("Add", [var, literal([eps], f"{label}.eps")], {}, None, label,
+                                                   src)], {}, None, label, src)
+            v = pointwise("Sub", [x, mean], {}, None, label, src)
+            v = pointwise("Div", [v, den], {}, None, label, src)
+            v = pointwise("Mul", [v, scale], {}, None, label, src)
+            return pointwise("Add", [v, bias], {}, out, label, src)
+        if op == "ElementwiseChain":
+            return chain(attrs["steps"], None, out, label, src)
+        raise GraphError(f"no lowering for pointwise operation {op}")
+
+    def chain(steps: list, prev: int | None, out: int | None, label: str, src: Node | None,
+              local: dict | None = None) -> int:
+        """Ordered steps whose operand "prev" is the previous step's value;
+        `local` maps a region's own tensor ids to the emitted ones."""
+        local = local or {}
+        cur = prev
+        for k, st in enumerate(steps):
+            ins = [cur if v == "prev" else local.get(int(v), int(v)) for v in st["inputs"]]
+            cur = pointwise(st["op"], ins, dict(st.get("attributes", {})), out if k == len(steps) - 1 else None,
+                            label, src)
+        return cur
+
+    def region(steps: list, label: str, src: Node | None, final: int | None = None) -> dict:
+        """A PointwiseRegion's steps (each naming its output tensor); the
+        intermediate tensors of the region are made anew.  Returns the map
+        from the region's tensor ids to the ones emitted."""
+        local: dict[int, int] = {}
+        for st in steps:
+            ins = [local.get(int(v), int(v)) for v in st["inputs"]]
+            target = int(st["outputs"][0])
+            out = final if target == final else None
+            if st["op"] == "ElementwiseChain":
+                res = chain(st["attributes"]["steps"], None, out, label, src, local)
+            else:
+                res = pointwise(st["op"], ins, dict(st.get("attributes", {})), out, label, src)
+            local[target] = res
+        return local
+
+    def dense_input(n: Node, ins: list) -> tuple[int, dict]:
+        """The Dense's input tensor and the weight transformation its input_map needs."""
+        if "input_map" not in n.attributes:
+            return r(ins[0]), {}
+        entries = [(r(int(e["tensor"])), int(e["index"])) for e in n.attributes["input_map"]]
+        sources: list[int] = []
+        for t, _ in entries:
+            if not tensors[t].is_constant and t not in sources:
+                sources.append(t)
+        if not sources:
+            raise GraphError(f"Dense {n.source_name!r} reads constants only")
+        offset, width = {}, 0
+        for t in sources:
+            offset[t] = width
+            width += size(t)
+        columns: list[list[int]] = [[] for _ in range(width)]
+        const_columns: list[tuple[int, int, int]] = []
+        for k, (t, i) in enumerate(entries):
+            if tensors[t].is_constant:
+                const_columns.append((k, t, i))
+            else:
+                columns[offset[t] + i].append(k)
+        if len(sources) == 1:
+            x = sources[0]
+        else:
+            x = new_tensor(width, f"{n.source_name or 'dense'}.inputs")
+            add("Concat", sources, x, {"axis": 1}, n)
+        if len(entries) == width and not const_columns and all(c == [k] for k, c in enumerate(columns)):
+            return x, {}
+        return x, {"columns": columns, "const_columns": const_columns, "map_width": len(entries)}
 
     for n in graph.nodes:
         ins = [r(t) for t in n.inputs]
         out = n.outputs[0]
+        label = n.source_name or f"{n.op.lower()}_{n.id}"
         if n.op in _ALIASES or (n.op == "Concat" and len(ins) == 1):
             alias[out] = ins[0]
             continue
         if n.op in _DENSE_OPS:
-            if "input_map" in n.attributes:
-                raise GraphError("Dense input_map (a fused gather) is not supported; pass the canonical graph")
-            attrs = {"weight": n.attributes["weight"], "bias": n.attributes.get("bias")}
+            x, fold = dense_input(n, ins)
+            attrs = {"weight": n.attributes["weight"], "bias": n.attributes.get("bias"), **fold}
             if n.op == "Dense":
-                nodes.append(Node(n.id, "Dense", [ins[0]], [out], attrs, n.source_name))
+                add("Dense", [x], out, attrs, n)
                 continue
-            pre = new_tensor(out)
-            nodes.append(Node(n.id, "Dense", [ins[0]], [pre], attrs, n.source_name))
+            pre = new_tensor(size(out), f"{label}.dense")
+            add("Dense", [x], pre, attrs, n)
             if n.op == "DenseBiasActivation":
-                nodes.append(Node(n.id, n.attributes["activation"], [pre], [out],
-                                  dict(n.attributes.get("activation_attributes", {}))))
+                pointwise(n.attributes["activation"], [pre], dict(n.attributes.get("activation_attributes", {})),
+                          out, label, n)
             elif n.op == "DenseResidualActivation":
-                mid = new_tensor(out)
-                nodes.append(Node(n.id, "Add", [pre, r(int(n.attributes["residual"]))], [mid]))
-                nodes.append(Node(n.id, n.attributes["activation"], [mid], [out],
-                                  dict(n.attributes.get("activation_attributes", {}))))
+                mid = pointwise("Add", [pre, int(n.attributes["residual"])], {}, None, label, n)
+                pointwise(n.attributes["activation"], [mid], dict(n.attributes.get("activation_attributes", {})),
+                          out, label, n)
             else:
-                cur = pre
                 steps = n.attributes.get("epilogue_steps", [])
-                for k, st in enumerate(steps):
-                    dst = out if k == len(steps) - 1 else new_tensor(out)
-                    sins = [cur if v == "prev" else r(int(v)) for v in st["inputs"]]
-                    nodes.append(Node(n.id, st["op"], sins, [dst], dict(st.get("attributes", {}))))
-                    cur = dst
-                if not steps:
+                if steps:
+                    chain(steps, pre, out, label, n)
+                else:
                     alias[out] = pre
             continue
-        nodes.append(Node(n.id, n.op, ins, [out], dict(n.attributes), n.source_name))
-    return nodes, alias
+        if n.op == "ResidualAddActivation":
+            mid = pointwise("Add", ins[:2], {}, None, label, n)
+            pointwise(n.attributes["activation"], [mid], dict(n.attributes.get("activation_attributes", {})),
+                      out, label, n)
+            continue
+        if n.op == "PointwiseRegion":
+            region(n.attributes["steps"], label, n, final=out)
+            continue
+        if n.op == "Gather":
+            idx = [int(i) % size(ins[0]) for i in n.attributes["indices"]]
+            add("Dense", [ins[0]], out, {"weight": None, "bias": None, "onehot": idx}, n)
+            continue
+        if n.op == "LpNormalization":
+            # norm == 0 ? 0 : x / norm (emitter.py:903-919)
+            p = int(n.attributes.get("p", 2))
+            norm = new_tensor(1, f"{label}.norm")
+            add("ReduceL1" if p == 1 else "ReduceL2", [ins[0]], norm, {"keepdims": 1}, n)
+            zero = pointwise("Equal", [norm, literal([0.0], f"{label}.zero")], {}, None, label, n)
+            q = pointwise("Div", [ins[0], norm], {}, None, label, n)
+            pointwise("Where", [zero, literal(np.zeros(size(out)), f"{label}.zeros"), q], {}, out, label, n)
+            continue
+        if n.op.startswith("Reduce") and ("map_steps" in n.attributes or "map_region_steps" in n.attributes):
+            # The reduction reads the value of its fused map (passes.py:984-1020).
+            if "map_steps" in n.attributes:
+                m = chain(n.attributes["map_steps"], None, None, label, n)
+            else:
+                local = region(n.attributes["map_region_steps"], label, n)
+                m = local[int(n.attributes["map_output"])]
+            attrs = {k: v for k, v in n.attributes.items() if k not in ("map_steps", "map_region_steps",
+                                                                        "map_output", "map_size")}
+            add(n.op, [m], out, attrs, n)
+            continue
+        if n.op in ("Concat", "Softmax", "LogSoftmax", "LayerNormalization") or n.op.startswith("Reduce"):
+            add(n.op, ins, out, n.attributes, n)
+            continue
+        pointwise(n.op, ins, dict(n.attributes), out, label, n)
+    return _Expanded(nodes, alias, tensors, derived)
+
+
+def _weight_column(c: dict, wname: str, nout: int, nmap: int, k: int) -> np.ndarray:
+    """Column k of a Dense weight [nout, nmap]."""
+    return np.asarray(c[wname], dtype=np.float64).reshape(nout, nmap)[:, k]
 
 
 def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
@@ -379,8 +688,8 @@ def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
     """
     if len(graph.inputs) != 1 or len(graph.outputs) != 1:
         raise GraphError("generated models have one input and one output")
-    nodes, alias = _expand(graph)
-    T = graph.tensors
+    ex = _expand(graph)
+    nodes, alias, T = ex.nodes, ex.alias, ex.tensors
     output = graph.outputs[0]
     while output in alias:
         output = alias[output]
@@ -419,6 +728,7 @@ def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
             d = producer.get(n.inputs[k])
             other = n.inputs[1 - k]
             if (d is not None and d.op == "Dense" and id(d) not in skip and uses.get(d.outputs[0], 0) == 1
+                    and "columns" not in d.attributes and "onehot" not in d.attributes
                     and size(other) == size(n.outputs[0]) and size(d.outputs[0]) == size(other)):
                 # The Dense's use of X moves to the Add; its output disappears.
                 proj[id(n)] = d
@@ -516,21 +826,92 @@ def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
         if op == "Dense":
             x = n.inputs[0]
             make_state(x, 1)
+            nin = size(x)
+            if "onehot" in n.attributes:
+                # Gather: row f of W picks element idx[f] (emitter.py:931-934).
+                idx = list(n.attributes["onehot"])
+
+                def build(c, idx=idx, nin=nin):
+                    w = np.zeros((len(idx), nin))
+                    w[np.arange(len(idx)), idx] = 1.0
+                    return w.reshape(-1)
+                emit(Layer(A.LAYER_DENSE, nin, nout, label="Gather"), _Param(build))
+                consume(x)
+                state = out
+                continue
             wname = const_of(n.attributes["weight"])
             bid = n.attributes.get("bias")
             bname = const_of(bid) if bid is not None else None
-            nin = size(x)
-            if T[n.attributes["weight"]].sample_size != nin * nout:
-                raise GraphError(f"Dense {n.source_name!r}: weight size does not match {nout}x{nin}")
+            fold = n.attributes.get("columns")
+            nmap = int(n.attributes.get("map_width", nin))
+            if T[n.attributes["weight"]].sample_size != nmap * nout:
+                raise GraphError(f"Dense {n.source_name!r}: weight size does not match {nout}x{nmap}")
+            const_cols = [(k, const_of(t), i) for k, t, i in n.attributes.get("const_columns", [])]
+            has_bias = bname is not None or bool(const_cols)
 
-            def build(c, wname=wname, bname=bname, nin=nin, nout=nout):
-                w = np.asarray(c[wname], dtype=np.float64).reshape(-1)
-                if bname is None:
-                    return w
-                return np.concatenate([w, vec(bname, nout)(c)])
-            emit(Layer(A.LAYER_DENSE, nin, nout, flags=A.FLAG_DENSE_BIAS if bname else 0, label="Dense"),
+            def build(c, wname=wname, bname=bname, nin=nin, nout=nout, fold=fold, nmap=nmap, const_cols=const_cols):
+                w = np.asarray(c[wname], dtype=np.float64).reshape(nout, nmap)
+                if fold is not None:
+                    # input_map: column j of the folded weight is the sum of
+                    # the map columns that read source element j; constant
+                    # entries are folded into the bias.
+                    wf = np.zeros((nout, nin))
+                    for j, ks in enumerate(fold):
+                        for k in ks:
+                            wf[:, j] += w[:, k]
+                    w = wf
+                if bname is None and not const_cols:
+                    return w.reshape(-1)
+                b = vec(bname, nout)(c) if bname is not None else np.zeros(nout)
+                for k, cn, i in const_cols:
+                    b = b + _weight_column(c, wname, nout, nmap, k) * np.asarray(c[cn], dtype=np.float64).reshape(-1)[i]
+                return np.concatenate([w.reshape(-1), b])
+            emit(Layer(A.LAYER_DENSE, nin, nout, flags=A.FLAG_DENSE_BIAS if has_bias else 0, label="Dense"),
                  _Param(build))
             consume(x)
+            state = out
+            continue
+        if op == "Where":
+            # interpreter.py:181-185: cond != 0 ? a : b.  One tensor operand
+            # is the state, the others saved slots or constant vectors.
+            ops3 = list(n.inputs)
+            if is_const(ops3[0]):
+                raise GraphError("Where with a constant condition should be folded before lowering")
+            tens = [t for t in ops3 if not is_const(t)]
+            st = state if state in tens else tens[0]
+            count = ops3.count(st)
+            for t in tens:
+                if t != st and t not in slots:
+                    raise GraphError(f"Where: operand {T[t].name!r} is not saved")
+            make_state(st, count)
+            if count > 1:
+                save(st)
+            flags, slot_ids, const_names = 0, [], []
+            used_state = False
+            for k, t in enumerate(ops3):
+                if is_const(t):
+                    code = A.SELECT_CONST
+                    const_names.append(const_of(t))
+                elif t == st and not used_state:
+                    code = A.SELECT_STATE
+                    used_state = True
+                else:
+                    code = A.SELECT_SLOT
+                    slot_ids.append(slots[t])
+                flags |= code << (2 * k)
+                if not is_const(t):
+                    if size(t) not in (1, nout):
+                        raise GraphError(f"unsupported Where broadcasting: operand sizes "
+                                         f"{[size(u) for u in ops3]}, output size {nout}")
+                    if size(t) == 1 and nout > 1:
+                        flags |= (A.SELECT_COND_SCALAR, A.SELECT_A_SCALAR, A.SELECT_B_SCALAR)[k]
+
+            def build(c, names=tuple(const_names), nout=nout):
+                return np.concatenate([vec(cn, nout)(c) for cn in names]) if names else np.zeros(0)
+            emit(Layer(A.LAYER_SELECT, size(st), nout, slot=slot_ids[0] if slot_ids else 0, flags=flags,
+                       attr=(0, slot_ids[1] if len(slot_ids) > 1 else 0, 0, 0), label="Where"),
+                 _Param(build) if const_names else None)
+            consume(*ops3)
             state = out
             continue
         if op in A.BINARY_OPS:
@@ -644,7 +1025,7 @@ def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
         emit(Layer(A.LAYER_LOAD_STATE, size(state), size(output), slot=slots[output], label="Load_State"))
     if not layers:
         raise GraphError("an empty graph has no kernel")
-    return LoweredGraph(layers, params, notes)
+    return LoweredGraph(layers, params, notes, ex.derived)
 
 
 # ---- the generated model -----------------------------------------------------------

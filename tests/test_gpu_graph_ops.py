@@ -106,3 +106,47 @@ def test_domain_ops_on_gpu(cuda, op, path, dtype):
     else:
         xh = xg.astype(np.float16).astype(np.float64)
         check_half(got, oracle.forward(layers, xh, oracle.MODE_F16_OPERANDS))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("path", ["generic", "narrow", "fused"])
+@pytest.mark.parametrize("seed", range(6))
+def test_op_graphs_on_gpu(cuda, seed, path, dtype):
+    """Random graphs over Where / comparisons / logic / Clip / PRelu /
+    BatchNormalization / Mean / Sum / Gather / LpNormalization / IsNaN /
+    IsInf and the unary math (tests/graph_cases.py) on every kernel family.
+    fp16 runs and most fp32 runs use graphs continuous in their input; seeds
+    0 and 3 add the step functions in fp32."""
+    import torch
+
+    from tests import graph_cases as GC
+    from tests.test_gpu_parity import check_f32, check_half
+
+    smooth = dtype == "f16" or seed % 3 != 0
+    gr = GC.op_graph(seed, smooth=smooth, aligned=path == "fused", narrow=path == "narrow")
+    gm = G.GeneratedModel(gr, path=path)
+    try:
+        plan = gm.plan(dtype)
+    except P.PonniError as e:
+        if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+            pytest.skip(e.message)
+        raise
+    assert plan.path == path
+    B = [4099, 1000, 257][seed % 3]
+    x = GC.in_domain_input(gr.size(gr.inputs[0]), B, 50 + seed)
+    print(f"op graph seed={seed} smooth={smooth}: path={path} dtype={dtype} B={B} "
+          f"layers={len(gm.lowered.layers)}", flush=True)
+    xt = torch.from_numpy(x.astype(np.float32)).cuda()
+    y = torch.full((gm.num_outputs, B), float("nan"), dtype=torch.float32, device="cuda:0")
+    if dtype == "f16":
+        gm.infer_batch_half2(xt, y)
+    else:
+        gm.infer_batch(xt, y)
+    torch.cuda.synchronize()
+    got = y.double().cpu().numpy()
+    layers = lowered_with_params(gr)
+    if dtype == "f32":
+        check_f32(got, oracle.forward(layers, x))
+    else:
+        check_half(got, oracle.forward(layers, x, oracle.MODE_F16_OPERANDS))

@@ -414,3 +414,117 @@ def test_narrow_generated_graphs_take_the_narrow_path():
                         if op in text)
     assert {"binary<", "reduce<"} <= seen, seen
     assert G.GeneratedModel(C.c5_graph(False)).plan("f32").path == "fused"
+
+
+# ---- selection, logic, normalization and unary math -----------------------------
+
+def _one_node(op, ins_values, attrs=None, size=None, bool_out=False):
+    """y = op(x, constants...) on a 1-row input; returns the oracle's float64 answer per column."""
+    x = np.asarray(ins_values[0], dtype=np.float64)
+    n = x.shape[0]
+    g = G.GraphBuilder(n, dtype="float64")
+    args = [g.input] + [g.constant(f"c{k}", v) for k, v in enumerate(ins_values[1:])]
+    out = g.node(op, args, size or n, attrs or {})
+    gr = g.finish(out)
+    return run_oracle(gr, x.reshape(n, -1)), NG.run_graph(gr, x.reshape(n, -1))
+
+
+def test_new_ops_closed_forms():
+    nan, inf = float("nan"), float("inf")
+    x = np.array([[-2.5], [-0.5], [0.5], [1.5], [2.5], [0.0]])
+    # Round: ties to even (emitter.py:1659-1667); Sign keeps NaN
+    got, ref = _one_node("Round", [x])
+    assert got.ravel().tolist() == [-2.0, -0.0, 0.0, 2.0, 2.0, 0.0]
+    got, _ = _one_node("Sign", [np.array([[-3.0], [0.0], [2.0], [nan]])])
+    assert got.ravel()[:3].tolist() == [-1.0, 0.0, 1.0] and np.isnan(got.ravel()[3])
+    # IsInf with detect_negative = 0
+    v = np.array([[-inf], [inf], [1.0], [nan]])
+    got, _ = _one_node("IsInf", [v], {"detect_negative": 0, "detect_positive": 1})
+    assert got.ravel().tolist() == [0.0, 1.0, 0.0, 0.0]
+    got, _ = _one_node("IsInf", [v])
+    assert got.ravel().tolist() == [1.0, 1.0, 0.0, 0.0]
+    got, _ = _one_node("IsNaN", [v])
+    assert got.ravel().tolist() == [0.0, 0.0, 0.0, 1.0]
+    # PRelu: x >= 0 ? x : x * slope
+    got, _ = _one_node("PRelu", [np.array([[-2.0], [0.0], [3.0]]), [0.25]])
+    assert got.ravel().tolist() == [-0.5, 0.0, 3.0]
+    # Clip keeps a NaN (the constant bound on the left of the comparison)
+    got, _ = _one_node("Clip", [np.array([[-5.0], [0.3], [5.0], [nan]])], {"min": -1.0, "max": 2.0})
+    assert got.ravel()[:3].tolist() == [-1.0, 0.3, 2.0] and np.isnan(got.ravel()[3])
+    # comparisons and logic give 1 / 0; any nonzero is true
+    a = np.array([[1.0], [2.0], [3.0]])
+    for op, want in (("Equal", [0, 1, 0]), ("Greater", [0, 0, 1]), ("GreaterOrEqual", [0, 1, 1]),
+                     ("Less", [1, 0, 0]), ("LessOrEqual", [1, 1, 0])):
+        got, _ = _one_node(op, [a, [2.0]])
+        assert got.ravel().tolist() == want, op
+    b = np.array([[0.0], [0.5], [-2.0], [0.0]])
+    for op, want in (("And", [0, 1, 0, 0]), ("Or", [1, 1, 1, 0]), ("Xor", [1, 0, 1, 0])):
+        got, _ = _one_node(op, [b, [1.0, 1.0, 0.0, 0.0]])
+        assert got.ravel().tolist() == want, op
+    got, _ = _one_node("Not", [b])
+    assert got.ravel().tolist() == [1.0, 0.0, 0.0, 1.0]
+    # LpNormalization: a zero vector stays zero; p = 1 and p = 2
+    got, _ = _one_node("LpNormalization", [np.array([[0.0, 3.0], [0.0, -4.0]])], {"p": 2})
+    assert got.tolist() == [[0.0, 0.6], [0.0, -0.8]]
+    got, _ = _one_node("LpNormalization", [np.array([[3.0], [-1.0]])], {"p": 1})
+    assert got.ravel().tolist() == [0.75, -0.25]
+    # BatchNormalization: (x - mean) / sqrt(var + eps) * scale + bias
+    got, _ = _one_node("BatchNormalization", [np.array([[3.0], [1.0]]), [2.0, 1.0], [0.5, -1.0], [1.0, 1.0],
+                                              [4.0 - 1e-5, 0.25 - 1e-5]], {"epsilon": 1e-5})
+    assert np.allclose(got.ravel(), [2.5, -1.0], rtol=1e-12)
+    # n-ary Mean / Sum
+    g = G.GraphBuilder(2, dtype="float64")
+    u = g.unary("Neg", g.input)
+    m = g.nary("Mean", g.input, u, g.binary("Mul", g.input, g.constant("k", [4.0])))
+    got = run_oracle(g.finish(m), np.array([[3.0], [-6.0]]))
+    assert got.ravel().tolist() == [4.0, -8.0]
+    # Gather reorders and repeats
+    g = G.GraphBuilder(3, dtype="float64")
+    got = run_oracle(g.finish(g.gather(g.input, [2, 0, 0, -1])), np.array([[1.0], [2.0], [3.0]]))
+    assert got.ravel().tolist() == [3.0, 1.0, 1.0, 3.0]
+
+
+def test_unary_math_against_numpy():
+    x = np.linspace(-0.95, 0.95, 41).reshape(41, 1)
+    for op, f in (("Acos", np.arccos), ("Asin", np.arcsin), ("Atan", np.arctan), ("Atanh", np.arctanh),
+                  ("Asinh", np.arcsinh), ("Sin", np.sin), ("Cos", np.cos), ("Tan", np.tan), ("Sinh", np.sinh),
+                  ("Cosh", np.cosh), ("Floor", np.floor), ("Ceil", np.ceil)):
+        got, _ = _one_node(op, [x])
+        assert np.allclose(got, f(x), rtol=1e-15, atol=1e-15), op
+    got, _ = _one_node("Acosh", [1.0 + np.abs(x)])
+    assert np.allclose(got, np.arccosh(1.0 + np.abs(x)), rtol=1e-15)
+
+
+def test_where_operand_sources():
+    """Where takes the state, one or two saved slots and constants in every
+    position; a one-feature operand broadcasts."""
+    rng = np.random.default_rng(3)
+    g = G.GraphBuilder(4, dtype="float64")
+    a = g.dense(g.input, rng.standard_normal((6, 4)), None, name="a")
+    b = g.dense(g.input, rng.standard_normal((6, 4)), None, name="b")
+    c = g.compare("Greater", a, b)
+    s = g.reduce("ReduceSum", b)
+    w1 = g.where(c, a, b)                     # cond state, two slots
+    w2 = g.where(c, g.constant("k", rng.standard_normal(6)), w1)
+    w3 = g.where(g.compare("Less", s, g.constant("z", [0.0])), w2, g.constant("k2", [0.5]))  # scalar cond
+    w4 = g.where(c, s, w3)                    # scalar a from a slot
+    gr = g.finish(g.binary("Add", w4, a))
+    lw = G.lower_graph(gr)
+    assert sum(l.label == "Where" for l in lw.layers) == 4
+    x = rng.standard_normal((4, 50))
+    assert np.allclose(run_oracle(gr, x), NG.run_graph(gr, x), rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("smooth", [True, False])
+@pytest.mark.parametrize("seed", range(16))
+def test_op_graphs_oracle_vs_numpy(seed, smooth):
+    from tests import graph_cases as GC
+
+    gr = GC.op_graph(seed, smooth=smooth, aligned=seed % 2 == 0, dtype="float64" if seed % 4 == 3 else "float32")
+    x = GC.in_domain_input(gr.size(gr.inputs[0]), 48, seed)
+    with np.errstate(all="ignore"):
+        want = NG.run_graph(gr, x)
+    got = run_oracle(gr, x)
+    assert np.isfinite(want).all()
+    tol = 1e-12 * max(1.0, np.abs(want).max())
+    assert np.allclose(got, want, rtol=1e-11, atol=tol), np.abs(got - want).max()
