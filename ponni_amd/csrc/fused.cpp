@@ -298,30 +298,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::string const F = half ? "float" : "real", F4 = half ? "floatx4" : "realx4";
   int const es = dbl ? 8 : 4;  // packed parameter element bytes
   auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
-  // 16-column tiles per wave.  16-bit plans run two waves per SIMD (32
+  // 16-column tiles per wave: two.  16-bit plans run two waves per SIMD (32
   // columns each) with A fragments staged through LDS (fused_f16.h dense_hs).
-  int NT = 2;
-  int half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
-  if (half) {
-    if (char const* v = std::getenv("PONNI_HALF_NT")) {  // tuning override
-      int const t = std::atoi(v);
-      if (t == 1 || t == 2 || t == 4) NT = t;
-    }
-    if (p.mfma32) NT = 2;  // 32x32 tiles: one 32-column tile per wave
-    half_wps = NT == 1 ? 4 : 2;
-    if (char const* v = std::getenv("PONNI_HALF_WPS")) {  // tuning override
-      int const t = std::atoi(v);
-      if (t >= 1 && t <= 4) half_wps = t;
-    }
-  }
+  int const NT = 2;
+  int const half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
   int64_t const param_bytes = (p.packed_elements * es + 31) / 32 * 32;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
-  // The LDS tanh table is opt-in: its random 2-byte LDS reads contend with
-  // the A-fragment reads of the workgroup's waves (measured slower than the
-  // hardware transcendentals on c4).
-  cfg.lut_bytes = 0;
-  if (char const* v = std::getenv("PONNI_TANH_LUT"))  // tuning override: 1 = table lookup
-    if (std::strcmp(v, "1") == 0 && half && p.lut_tanh_off >= 0) cfg.lut_bytes = kLutWords * 4;
   cfg.waves = 4;
   // Register budget.  A live tile holds 8 registers per lane (fp32 with 2
   // column tiles, or 16-bit with 4); a dense op holds its input, its output
@@ -389,7 +371,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const target = 4 * cfg.waves_per_simd;  // waves per CU the registers allow
     int best = 0;
     for (int w = 4; w <= 16; w += 4) {
-      int const per_block_lds = cfg.lds_bytes + cfg.lut_bytes + w * saved_per_wave;
+      int const per_block_lds = cfg.lds_bytes + w * saved_per_wave;
       if (per_block_lds > 160 * 1024) break;
       int const by_lds = per_block_lds > 0 ? (160 * 1024) / per_block_lds : 1 << 20;
       int const blocks = std::min(by_lds, target / w);
@@ -446,10 +428,6 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v == 0 || v == 1) o << "#define PONNI_FULL_SLOT_CHUNKS " << v << "\n";
   }
-  if (char const* d = std::getenv("PONNI_CHUNK_DMA")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v == 0 || v == 1) o << "#define PONNI_CHUNK_DMA " << v << "\n";
-  }
   if (char const* d = std::getenv("PONNI_RING_DEPTH")) {  // tuning override
     int const v = std::atoi(d);
     if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
@@ -470,30 +448,20 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   } else {
     o << "  " << F << " const* __restrict__ P0 = gparams;\n";
   }
-  if (cfg.lut_bytes > 0) {
-    o << "  __shared__ unsigned short lut_tanh[" << cfg.lut_bytes / 2 << "];\n";
-    o << "  stage_bytes(lut_tanh, gparams + " << p.lut_tanh_off << ", " << cfg.lut_bytes << ");\n";
-    o << "  __syncthreads();\n";
-  }
   // 16-bit plans: dense layers in program order (weights, 32-feature steps);
   // the last one's successor is the first (the next tile of the loop).
   struct DenseRef {
     int woff, ts, to;
   };
   std::vector<DenseRef> dense_seq;
-  // (32x32 tiles: 16-feature steps and 32-feature output tiles)
-  bool const m32 = p.mfma32;
   for (Op const& op : p.ops)
-    if (op.code == OP_DENSE)
-      dense_seq.push_back(m32 ? DenseRef{op.woff, op.n_in / 16, op.n_out / 32}
-                              : DenseRef{op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
+    if (op.code == OP_DENSE) dense_seq.push_back(DenseRef{op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
   // (tuning override PONNI_HALF_STAGE=0: A fragments straight from L1/L2 per wave)
-  bool const half_staged =
-      m32 || !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
+  bool const half_staged = !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
   if (half && half_staged && !dense_seq.empty()) {
     o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
     o << "  Stage<E> st{a_slots, 0};\n";
-    o << "  " << (m32 ? "stage_first32<" : "stage_first<") << dense_seq[0].ts << ", " << dense_seq[0].to << ", "
+    o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", "
       << cfg.waves << ">(st, reinterpret_cast<E const*>(gparams + " << dense_seq[0].woff << "));\n";
     o << "  __syncthreads();\n";
   }
@@ -551,8 +519,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   if (in_dma) {
     o << "  __shared__ unsigned in_buf[" << cfg.waves << "][" << in_dma_bytes / 4 / cfg.waves << "];\n";
     o << "  L.col0 = (int64_t(blockIdx.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
-    if (m32) o << "  if (blockIdx.x < tiles) prefetch_rows_lds32<" << n_in0 << ">(x, ldx, L, in_buf[wave_id()]);\n";
-    else o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
+    o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
     // The LDS writes of these loads complete with vmcnt, which the compiler
     // does not track for reads of in_buf: each tile's rows are waited for
     // explicitly, here for the first tile and before the output stores for
@@ -569,15 +536,13 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::string cur = fresh();
   int cur_n = p.layers.front().n_in;
   if (in_dma) {
-    if (m32) o << "    auto " << cur << " = load_rows_lds32<" << cur_n << ", E>(in_buf[wave_id()], L);\n";
-    else o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
+    o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
     o << "    wait_lds();\n";
     o << "    if (tile + gridDim.x < tiles) {\n      Lane Ln = L;\n      Ln.col0 = ((tile + gridDim.x) * " << NW
       << " + wave_id()) * " << WCOLS << ";\n      "
-      << (m32 ? "prefetch_rows_lds32<" + std::to_string(cur_n) : "prefetch_rows_lds<" + std::to_string(cur_n) + ", " + std::to_string(NT))
+      << "prefetch_rows_lds<" + std::to_string(cur_n) + ", " + std::to_string(NT)
       << ">(x, ldx, Ln, in_buf[wave_id()]);\n    }\n";
-  } else if (m32) o << "    auto " << cur << " = load_rows_h32<" << cur_n << ">(x, ldx, L);\n";
-  else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
+  } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
   // The logistic family runs on the hardware transcendentals (pointwise.h),
@@ -623,18 +588,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         // 16-bit rounding, and the add then costs no VALU op).
         bool const lead_bias = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
         bool const seed = lead_bias && (half || (op.aux & DENSE_BIAS_FIRST));
-        // A 16-bit block ending in Tanh looks the activation up in the LDS table.
-        bool const lut_tanh = half && !m32 && cfg.lut_bytes > 0 && op.epi_count > (seed ? 1 : 0) &&
-                              p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH;
-        if (m32) {
-          std::string const init = seed ? "SeedRows32{" + vec(p.steps[op.epi_begin].off, n) + ", L.lane >> 5}" : "SeedZero32{}";
-          auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
-          dense_index++;
-          o << "    auto " << nv << " = dense_hs32<" << op.n_in / 32 << ", " << n / 32 << ", " << cfg.waves << ", "
-            << next.ts << ", " << next.to << ">(" << cur << ", reinterpret_cast<E const*>(P + " << op.woff
-            << "), reinterpret_cast<E const*>(P + " << next.woff << "), st, L, " << init
-            << ", [&](int mo, floatx4 (&t)[4], Vec<E>::x4 (&o)[4]) {\n";
-        } else if (half && !half_staged) {
+        if (half && !half_staged) {
           std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
           o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, " << init << ", [&](int mo, floatx4 (&t)["
@@ -655,13 +609,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
             << op.woff << ", " << init << ", L, [&](int mo, " << F4 << " (&t)[" << NT << "]) {\n";
         }
-        int const last = op.epi_count - (lut_tanh ? 1 : 0);
-        for (int s = seed ? 1 : 0; s < last; s++) {
+        for (int s = seed ? 1 : 0; s < op.epi_count; s++) {
           Step const& st = p.steps[op.epi_begin + s];
           if (st.act == ACT_BIAS) {
-            o << "      " << (m32 ? "t32_add_rows" : "tile_add_rows") << "(t, " << vec(st.off, n) << ", mo, L);\n";
+            o << "      tile_add_rows(t, " << vec(st.off, n) << ", mo, L);\n";
           } else if (act_has_param(st.act)) {
-            o << "      " << (m32 ? "t32_const" : "tile_const") << "(t, " << vec(st.off, n) << ", mo, L, [](" << F
+            o << "      tile_const(t, " << vec(st.off, n) << ", mo, L, [](" << F
               << " v, " << F << " c) { return " << const_expr(st) << "; });\n";
             if (!zero_at_zero(st.act)) pad = true;
           } else {
@@ -669,30 +622,14 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
-        if (pad && n % 16 && !m32) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
-        if (half) o << (lut_tanh ? "      tile_lut_odd<E>(t, o, lut_tanh);\n" : "      tile_round<E>(t, o);\n");
+        if (pad && n % 16) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
+        if (half) o << "      tile_round<E>(t, o);\n";
         o << "    });\n";
         cur = nv;
         cur_n = n;
         break;
       }
       case OP_POINTWISE: {
-        if (m32) {
-          // Widths are multiples of 32: no padding to restore.
-          o << "    for_tiles32(" << cur << ", [&](int mo, floatx4 (&t)[4]) {\n";
-          for (int s = 0; s < op.epi_count; s++) {
-            Step const& st = p.steps[op.epi_begin + s];
-            if (st.act == ACT_BIAS)
-              o << "      t32_add_rows(t, " << vec(st.off, cur_n) << ", mo, L);\n";
-            else if (act_has_param(st.act))
-              o << "      t32_const(t, " << vec(st.off, cur_n) << ", mo, L, [](" << F << " v, " << F << " c) { return "
-                << const_expr(st) << "; });\n";
-            else
-              o << "      tile_map(t, [](" << F << " v) { return " << act(st) << "; });\n";
-          }
-          o << "    });\n";
-          break;
-        }
         std::string const f = open32();
         epilogue(f, cur_n, op.epi_begin, op.epi_count);
         close32();
@@ -846,8 +783,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   if (half && in_dma) o << "    wait_vmem();\n";
-  if (m32) o << "    store_rows_h32<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
-  else if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";
   if (!vec_lds.empty()) {
@@ -1200,7 +1136,7 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   }
   p.fused_fn = it->second->fn;
   p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
-  p.fused_persistent = cfg.lds_bytes > 0 || cfg.lut_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers;
+  p.fused_persistent = cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers;
   p.fused_columns_per_block = cfg.columns_per_block;
   p.fused_waves = cfg.waves;
   return PONNI_OK;

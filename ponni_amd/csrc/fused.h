@@ -11,13 +11,9 @@ namespace ponni_hip {
 // Packed parameter blocks up to this size are staged in LDS by the kernel.
 constexpr int64_t kFusedLdsParamBytes = 64 * 1024;
 constexpr int kNTColumns = 32;
-// A 16-bit activation table: 32768 entries (non-negative bit patterns) in
-// 16384 32-bit words.
-constexpr int kLutWords = 16384;  // batch columns per wave (fused_f32.h kNT * 16)
 
 struct FusedConfig {
   int lds_bytes = 0;          // 0: parameters stream from L2
-  int lut_bytes = 0;          // LDS activation table of 16-bit plans (0: none)
   int vec_bytes = 0;          // LDS copy of the per-feature vectors (0: none)
   int waves = 4;              // waves per workgroup
   int waves_per_simd = 2;     // occupancy the kernel is compiled for

@@ -22,24 +22,17 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 template <class E> struct Vec;
 template <> struct Vec<_Float16> {
   using x4 = f16x4;
   using x8 = f16x8;
   __device__ static floatx4 mfma(x8 a, x8 b, floatx4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-  __device__ static floatx16 mfma32(x8 a, x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
 };
 template <> struct Vec<__bf16> {
   using x4 = bf16x4;
   using x8 = bf16x8;
   __device__ static floatx4 mfma(x8 a, x8 b, floatx4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-  __device__ static floatx16 mfma32(x8 a, x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
 };
 
 template <int T, int NT, class E>
@@ -55,41 +48,6 @@ __device__ inline typename Vec<E>::x4 round4(floatx4 v) {
 template <class E>
 __device__ inline floatx4 widen4(typename Vec<E>::x4 v) {
   return __builtin_convertvector(v, floatx4);
-}
-
-// Odd activation of a 16-bit value by table lookup.  `lut` holds f(|h|)
-// rounded to E for all 32768 non-negative bit patterns h (index = bits of
-// |h|); the sign is copied back, which is exact for an odd f (tanh).  Each
-// pair of elements costs one packed shift, two bit extractions, two LDS
-// reads and one and-or: no transcendental.  The value looked up is the
-// 16-bit rounding of the fp32 result, so f runs on a 16-bit operand, as the
-// reference's half arithmetic evaluates activations on a half value
-// (ponni_TwoHalf.h:138-153: fp32 per lane of a half input, rounded back).
-template <class E, int NT>
-__device__ inline void tile_lut_odd(floatx4 const (&t)[NT], typename Vec<E>::x4 (&o)[NT],
-                                    unsigned short const* __restrict__ lut) {
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-  char const* __restrict__ base = reinterpret_cast<char const*>(lut);
-#pragma unroll
-  for (int n = 0; n < NT; n++) {
-    u32x2 const bits = __builtin_bit_cast(u32x2, round4<E>(t[n]));
-    u32x2 r;
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      // Byte offsets 2|h| of both halves at once; the sign bits shift out.
-      // (The element is copied to a scalar first: a bit cast of a vector
-      // element lvalue reads element 0 with this compiler.)
-      unsigned const pk = bits[k];
-      unsigned const q = __builtin_bit_cast(unsigned, __builtin_bit_cast(u16x2, pk) << (unsigned short)1);
-      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      h2 v;
-      v[0] = *reinterpret_cast<_Float16 const*>(base + (q & 0xffffu));
-      v[1] = *reinterpret_cast<_Float16 const*>(base + (q >> 16));
-      r[k] = __builtin_bit_cast(unsigned, v) | (pk & 0x80008000u);
-    }
-    o[n] = __builtin_bit_cast(typename Vec<E>::x4, r);
-  }
 }
 
 #ifndef PONNI_RING_DEPTH
@@ -305,14 +263,9 @@ constexpr int kSlotFrags = 8 * kChunkTiles;  // fragments per slot (256 input fe
 #ifndef PONNI_TILE_GROUP
 #define PONNI_TILE_GROUP 2
 #endif
+
 #ifndef PONNI_DEFER_EPILOGUE
 #define PONNI_DEFER_EPILOGUE 1
-#endif
-// Chunks staged with 16-byte LDS-DMA loads (chunk_dma) instead of through
-// registers and LDS writes: frees the staging registers (c4: 244 -> 223
-// VGPRs) but measured slower on c4 (3.39 ms against 3.12 ms), so opt-in.
-#ifndef PONNI_CHUNK_DMA
-#define PONNI_CHUNK_DMA 0
 #endif
 
 template <class E>
@@ -348,26 +301,6 @@ __device__ inline void chunk_store(ChunkRegs<NF, WAVES, E> const& r, Stage<E> co
   for (int k = 0; k < r.K; k++) {
     int const f = wave + WAVES * k;
     if (NF >= WAVES * (k + 1) || f < NF) st.slots[(slot * kSlotFrags + f) * 64 + lane] = r.v[k];
-  }
-}
-
-// The NF fragments of a chunk requested straight into LDS slot `slot` with
-// 16-byte LDS-DMA loads (global_load_lds_dwordx4: lane l's 16 bytes land at
-// the fragment's base + 16 l, the fragment layout itself), no registers and
-// no LDS write instructions: this wave's fragments f = wave + WAVES k, those
-// below `count` (NF when the chunk is full).  They complete under vmcnt,
-// which the compiler does not track for LDS reads: the caller waits
-// (wait_vmem) before the barrier that publishes the slot.
-template <int NF, int WAVES, class E>
-__device__ inline void chunk_dma(E const* __restrict__ chunk, Stage<E> const& st, int slot, int wave, int lane,
-                                 int count = NF) {
-  constexpr int K = (NF + WAVES - 1) / WAVES;
-#pragma unroll
-  for (int k = 0; k < K; k++) {
-    int const f = wave + WAVES * k;
-    if (f < count)
-      __builtin_amdgcn_global_load_lds(static_cast<void const*>(chunk + f * 512 + lane * 8),
-                                       (lds_ptr)(st.slots + (slot * kSlotFrags + f) * 64), 16, 0, 0);
   }
 }
 
@@ -412,11 +345,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
     int const nt_next = last ? 0 : cmin(CT, TO - t0 - CT);
     constexpr int NFX = cmax(CT * TS, NFN);
     ChunkRegs<NFX, WAVES, E> nx;
-    if (PONNI_CHUNK_DMA) {
-      // Straight into the other slot (last read before the previous barrier).
-      if (!last) chunk_dma<CT * TS, WAVES>(w + (t0 + CT) * TS * 512, st, st.cur ^ 1, wave, L.lane, nt_next * TS);
-      else chunk_dma<NFN, WAVES>(w_next, st, st.cur ^ 1, wave, L.lane);
-    } else if (!last) {
+    if (!last) {
       E const* __restrict__ src = w + (t0 + CT) * TS * 512;
       if (nt_next == CT) {
         auto const r = chunk_load<CT * TS, WAVES>(src, wave, L.lane);
@@ -487,9 +416,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
       }
     }
     // Slot cur ^ 1 was last read before the previous barrier.
-    if (PONNI_CHUNK_DMA) {
-      wait_vmem();
-    } else if (!last) {
+    if (!last) {
       if (nt_next == CT) {
         ChunkRegs<CT * TS, WAVES, E> r;
 #pragma unroll
@@ -526,12 +453,7 @@ template <int TS, int TO, int WAVES, class E>
 __device__ inline void stage_first(Stage<E>& st, E const* __restrict__ w) {
   int const wave = wave_id(), lane = threadIdx.x & 63;
   constexpr int NF = cmin(ct16(TS), TO) * TS;
-  if (PONNI_CHUNK_DMA) {
-    chunk_dma<NF, WAVES>(w, st, 0, wave, lane);
-    wait_vmem();
-  } else {
-    chunk_store<NF, WAVES>(chunk_load<NF, WAVES>(w, wave, lane), st, 0, wave, lane);
-  }
+  chunk_store<NF, WAVES>(chunk_load<NF, WAVES>(w, wave, lane), st, 0, wave, lane);
   st.cur = 0;
 }
 
@@ -600,249 +522,6 @@ __device__ inline H<TA + TB, NT, E> concat_h(H<TA, NT, E> const& a, H<TB, NT, E>
 #pragma unroll
     for (int n = 0; n < NT; n++) s.v[TA + m][n] = b.v[m][n];
   return s;
-}
-
-// ---- 32x32 tiles: v_mfma_f32_32x32x16_{f16,bf16} -------------------------
-// Plans made only of dense layers and pointwise steps, every width a
-// multiple of 32, run on the 32x32x16 MFMA: one 1 KB A fragment serves all 32
-// columns of a wave in one instruction, which halves the A-fragment LDS reads
-// per FLOP of the 16x16x32 form at the same register footprint.
-//
-// Register tile H32<T,E>::v[m][b] (4 elements of E per lane): lane l = 32h + c,
-// element r <-> feature 32m + 8b + 4h + r, column col0 + c.  That is the D
-// layout of v_mfma_f32_32x32x16 (result element 4b + r of lane l is row
-// 8b + 4h + r, column c).  Step s = 2m + u of the next dense layer contracts
-// the 16 features of groups b = 2u, 2u + 1 of tile m: the B operand (lane l
-// holds column c at contraction indices 8h + j, j = 0..7) is the lane's own
-// v[m][2u] followed by v[m][2u + 1], so index 8h + j <-> feature
-// 32m + 8(2u + j/4) + 4h + j%4.  The host packs A (lane l holds row l%32 at
-// the same contraction indices) in that order: 1 KB per (output tile, step).
-template <int T, class E>
-struct H32 {
-  typename Vec<E>::x4 v[T > 0 ? T : 1][4];
-};
-
-// The lane's element pointer for row 4h, column col0 + c (as lane_ptr).
-template <class E>
-__device__ inline E* lane_ptr32(E* p, int64_t ld, Lane const& L) {
-  int64_t off = int64_t(4 * (L.lane >> 5)) * ld + L.col0 + (L.lane & 31);
-  asm volatile("" : "+v"(off));
-  return p + off;
-}
-
-template <int N, class E>
-__device__ inline H32<N / 32, E> load_rows_h32(E const* __restrict__ x, int64_t ld, Lane const& L) {
-  static_assert(N % 32 == 0, "32-feature tiles");
-  constexpr int T = N / 32;
-  H32<T, E> s;
-  E const* __restrict__ xl = lane_ptr32(x, ld, L);
-  bool const ok = L.col0 + 32 <= L.batch || L.col0 + (L.lane & 31) < L.batch;
-#pragma unroll
-  for (int m = 0; m < T; m++)
-#pragma unroll
-    for (int b = 0; b < 4; b++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) s.v[m][b][r] = ok ? xl[int64_t(32 * m + 8 * b + r) * ld] : E(0.0f);
-  return s;
-}
-
-// Input rows requested into LDS one tile ahead (as prefetch_rows_lds):
-// instruction i = (4m + b) 4 + r writes lane l's element to dword buf[i * 64 + l].
-template <int N, class E>
-__device__ inline void prefetch_rows_lds32(E const* __restrict__ x, int64_t ld, Lane const& L,
-                                           unsigned* __restrict__ buf) {
-  static_assert(N % 32 == 0, "32-feature tiles");
-  E const* __restrict__ xl = lane_ptr32(x, ld, L);
-  bool const ok = L.col0 + 32 <= L.batch || L.col0 + (L.lane & 31) < L.batch;
-#pragma unroll
-  for (int m = 0; m < N / 32; m++)
-#pragma unroll
-    for (int b = 0; b < 4; b++)
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if (ok)
-          __builtin_amdgcn_global_load_lds(static_cast<void const*>(xl + int64_t(32 * m + 8 * b + r) * ld),
-                                           (lds_ptr)(buf + ((m * 4 + b) * 4 + r) * 64), 2, 0, 0);
-}
-
-template <int N, class E>
-__device__ inline H32<N / 32, E> load_rows_lds32(unsigned const* __restrict__ buf, Lane const& L) {
-  constexpr int T = N / 32;
-  H32<T, E> s;
-  bool const ok = L.col0 + 32 <= L.batch || L.col0 + (L.lane & 31) < L.batch;
-#pragma unroll
-  for (int m = 0; m < T; m++)
-#pragma unroll
-    for (int b = 0; b < 4; b++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        unsigned short const bits = static_cast<unsigned short>(buf[((m * 4 + b) * 4 + r) * 64 + L.lane]);
-        s.v[m][b][r] = ok ? __builtin_bit_cast(E, bits) : E(0.0f);
-      }
-  return s;
-}
-
-template <int N, int T, class E>
-__device__ inline void store_rows_h32(H32<T, E> const& s, E* __restrict__ y, int64_t ld, Lane const& L) {
-  static_assert(N == 32 * T, "32-feature tiles");
-  E* __restrict__ yl = lane_ptr32(y, ld, L);
-  bool const ok = L.col0 + 32 <= L.batch || L.col0 + (L.lane & 31) < L.batch;
-  if (!ok) return;
-#pragma unroll
-  for (int m = 0; m < T; m++)
-#pragma unroll
-    for (int b = 0; b < 4; b++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) yl[int64_t(32 * m + 8 * b + r) * ld] = s.v[m][b][r];
-}
-
-// Epilogue helpers on the fp32 view t[b] of output tile mo (element r of t[b]
-// is feature 32 mo + 8b + 4h + r); vectors are padded to 16 features.
-__device__ inline void t32_add_rows(floatx4 (&t)[4], float const* __restrict__ v, int mo, Lane const& L) {
-#pragma unroll
-  for (int b = 0; b < 4; b++) t[b] += ld4(v + 32 * mo + 8 * b + 4 * (L.lane >> 5));
-}
-
-template <class F>
-__device__ inline void t32_const(floatx4 (&t)[4], float const* __restrict__ c, int mo, Lane const& L, F f) {
-#pragma unroll
-  for (int b = 0; b < 4; b++) {
-    floatx4 const cc = ld4(c + 32 * mo + 8 * b + 4 * (L.lane >> 5));
-#pragma unroll
-    for (int r = 0; r < 4; r++) t[b][r] = f(t[b][r], cc[r]);
-  }
-}
-
-// Pointwise steps on the whole state: f(mo, t) on the fp32 view of each tile,
-// rounded back once.
-template <int T, class E, class F>
-__device__ inline void for_tiles32(H32<T, E>& s, F f) {
-#pragma unroll
-  for (int m = 0; m < T; m++) {
-    floatx4 t[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) t[b] = widen4<E>(s.v[m][b]);
-    f(m, t);
-#pragma unroll
-    for (int b = 0; b < 4; b++) s.v[m][b] = round4<E>(t[b]);
-  }
-}
-
-// Accumulator seeds: zero, or the per-feature vector v in the D layout.
-struct SeedZero32 {
-  __device__ floatx16 operator()(int) const {
-    floatx16 z;
-#pragma unroll
-    for (int i = 0; i < 16; i++) z[i] = 0.0f;
-    return z;
-  }
-};
-struct SeedRows32 {
-  float const* __restrict__ v;
-  int h;
-  __device__ floatx16 operator()(int mo) const {
-    floatx16 s;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      floatx4 const q = ld4(v + 32 * mo + 8 * b + 4 * h);
-#pragma unroll
-      for (int r = 0; r < 4; r++) s[4 * b + r] = q[r];
-    }
-    return s;
-  }
-};
-
-// Epilogue of output tile mo from its accumulator: epi on the fp32 view.
-template <int TO, class E, class Epi>
-__device__ __attribute__((always_inline)) inline void finish32(int mo, floatx16 const& acc, H32<TO, E>& out, Epi& epi) {
-  floatx4 t[4];
-#pragma unroll
-  for (int i = 0; i < 16; i++) t[i / 4][i % 4] = acc[i];
-  epi(mo, t, out.v[mo]);
-}
-
-#ifndef PONNI_RING32
-#define PONNI_RING32 4
-#endif
-
-// Output tiles per LDS chunk for a layer of TS 16-feature steps: as many as
-// fit one slot, at most 4 (independent accumulation chains).
-constexpr int ct32(int ts) { return cmin(4, kSlotFrags / ts); }
-
-// Dense layer on the 32x32x16 MFMA with LDS-staged A fragments (the chunk
-// protocol of dense_hs: on entry slot st.cur holds this layer's first chunk,
-// on exit the first chunk of w_next, TSN steps and TON output tiles).
-// init(mo) seeds tile mo's accumulator; epi(mo, t, o) finishes it on the fp32
-// view t and writes the 16-bit result to o.
-template <int TI, int TO, int WAVES, int TSN, int TON, class E, class Init, class Epi>
-__device__ inline H32<TO, E> dense_hs32(H32<TI, E> const& in, E const* __restrict__ w,
-                                        E const* __restrict__ w_next, Stage<E>& st, Lane const& L, Init init,
-                                        Epi epi) {
-  using V8 = typename Vec<E>::x8;
-  constexpr int TS = 2 * TI;
-  constexpr int CT = ct32(TS);
-  constexpr int NCH = (TO + CT - 1) / CT;
-  constexpr int NFN = cmin(ct32(TSN), TON) * TSN;
-  static_assert(TS <= 16 && TSN <= 16 && CT >= 1, "at most 256 input features");
-  int const wave = wave_id();
-  H32<TO, E> out;
-  floatx16 prev;
-#pragma unroll
-  for (int ch = 0; ch < NCH; ch++) {
-    int const t0 = ch * CT;
-    bool const last = ch + 1 == NCH;
-    int const nt_next = last ? 0 : cmin(CT, TO - t0 - CT);
-    // The next chunk into the other slot (last read before the previous barrier).
-    if (!last) chunk_dma<CT * TS, WAVES>(w + (t0 + CT) * TS * 512, st, st.cur ^ 1, wave, L.lane, nt_next * TS);
-    else chunk_dma<NFN, WAVES>(w_next, st, st.cur ^ 1, wave, L.lane);
-    V8 const* __restrict__ sl = st.slots + st.cur * (kSlotFrags * 64) + L.lane;
-    // One output tile at a time; the previous tile's epilogue runs after this
-    // tile's MFMAs are issued (across chunk barriers too), so the SIMD's other
-    // wave's matrix work and this wave's VALU work interleave.  The chunk's
-    // A fragments stream through an R-deep register ring, each requested R
-    // MFMAs before its use.
-    int const nt_ch = cmin(CT, TO - t0);  // output tiles in this chunk (t0 < TO)
-    constexpr int R = PONNI_RING32;
-    V8 ring[R];
-#pragma unroll
-    for (int i = 0; i < R; i++)
-      if (i < nt_ch * TS) ring[i] = sl[i * 64];
-#pragma unroll
-    for (int q = 0; q < CT; q++) {
-      int const mo = t0 + q;
-      if (mo < TO) {
-        floatx16 acc = init(mo);
-        if (PONNI_SETPRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int s = 0; s < TS; s++) {
-          int const i = q * TS + s;
-          V8 const a = ring[i % R];
-          if (i + R < nt_ch * TS) ring[i % R] = sl[(i + R) * 64];
-          V8 const b = __builtin_shufflevector(in.v[s / 2][2 * (s % 2)], in.v[s / 2][2 * (s % 2) + 1], 0, 1, 2, 3,
-                                               4, 5, 6, 7);
-          acc = Vec<E>::mfma32(a, b, acc);
-        }
-        if (PONNI_SETPRIO) __builtin_amdgcn_s_setprio(0);
-        if (mo > 0) finish32(mo - 1, prev, out, epi);
-        prev = acc;
-      }
-    }
-    wait_vmem();
-    __syncthreads();
-    st.cur ^= 1;
-  }
-  finish32(TO - 1, prev, out, epi);
-  return out;
-}
-
-// Kernel prologue: the first dense layer's first chunk into slot 0.
-template <int TS, int TO, int WAVES, class E>
-__device__ inline void stage_first32(Stage<E>& st, E const* __restrict__ w) {
-  int const wave = wave_id(), lane = threadIdx.x & 63;
-  constexpr int NF = cmin(ct32(TS), TO) * TS;
-  chunk_dma<NF, WAVES>(w, st, 0, wave, lane);
-  wait_vmem();
-  st.cur = 0;
 }
 
 }  // namespace fused

@@ -578,42 +578,6 @@ void lower(ponni_plan_s& p) {
   }
   p.tmp_features[0] = tmp_max[0];
   p.tmp_features[1] = tmp_max[1];
-
-  // FUSED 16-bit plans evaluate a Tanh that ends a dense block by table
-  // lookup (fused_f16.h tile_lut_odd): 32768 16-bit entries after the packed
-  // parameters, 16-byte aligned.
-  p.lut_tanh_off = -1;
-  if (p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16)) {
-    for (Op const& op : p.ops)
-      if (op.code == OP_DENSE && op.epi_count > 0 && p.steps[op.epi_begin + op.epi_count - 1].act == ACT_TANH) {
-        p.lut_tanh_off = round_up(static_cast<int>(p.packed_elements), 4);
-        p.packed_elements = p.lut_tanh_off + kLutWords;
-        break;
-      }
-  }
-
-  // 32x32 tiles (opt-in, PONNI_MFMA32=1): a chain of dense layers and
-  // pointwise steps whose every width is a multiple of 32 (then the packed
-  // sizes equal those of the 16x16 layout: K * N / 2 words per dense block).
-  // Per KB of A fragments read from LDS both layouts do the same work (two
-  // 16x16x32 MFMAs over a wave's two column tiles, or one 32x32x16), and the
-  // 32x32 kernel measured slower on c4, so 16x16 stays the default.
-  p.mfma32 = false;
-  char const* m32 = std::getenv("PONNI_MFMA32");
-  if (m32 != nullptr && std::strcmp(m32, "1") == 0 && p.path == PONNI_PATH_FUSED &&
-      (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16)) {
-    bool ok = p.layers.front().n_in % 32 == 0;
-    bool any_dense = false;
-    for (Op const& op : p.ops) {
-      if (op.code == OP_DENSE) {
-        any_dense = true;
-        ok = ok && op.n_in % 32 == 0 && op.n_out % 32 == 0;
-      } else if (op.code != OP_POINTWISE) {
-        ok = false;
-      }
-    }
-    p.mfma32 = ok && any_dense;
-  }
 }
 
 bool mfma_supports(ponni_plan_s const& p) {
@@ -629,12 +593,12 @@ bool mfma_supports(ponni_plan_s const& p) {
 // Where each parameter lands in the packed buffer of the plan's path:
 // emit(slot, kind, layer, index) names every packed slot that holds
 // parameter `index` (master-copy order) of layer `layer`; the slots it never
-// names hold zero (padding) or, in 16-bit FUSED plans, the tanh table.
+// names hold zero (padding).
 //   SLOT_VALUE  element `slot` of the packed buffer (fp32, or fp64 for F64
 //               plans): the value rounded to the plan's type
 //   SLOT_HALF   16-bit element `slot` of a 16-bit FUSED buffer: the value's
-//               fp16 / bf16 bits (v_mfma_f32_16x16x32 / 32x32x16 A-fragment
-//               order, see fused_f16.h)
+//               fp16 / bf16 bits (v_mfma_f32_16x16x32 A-fragment order, see
+//               fused_f16.h)
 //   SLOT_WORD   32-bit word `slot` of a 16-bit FUSED buffer: the value
 //               rounded to the plan's 16-bit type, stored as fp32
 template <class Emit>
@@ -652,22 +616,6 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
       auto idx = [&](int k, int n) { return src0 + (transposed ? int64_t(n) * K + k : int64_t(k) * N + n); };
       if (half_fused) {
         int64_t const hb = 2 * base;  // 16-bit index of the layer's first word
-        if (p.mfma32) {
-          // v_mfma_f32_32x32x16 A fragment of output tile mo and 16-feature step
-          // s = 2m + u: lane l = 32hh + c, element j holds W[k][32 mo + c] with
-          // k = 32m + 8(2u + j/4) + 4hh + j%4 (fused_f16.h H32).  K, N are
-          // multiples of 32.
-          int const TN = N / 32, TS = K / 16;
-          for (int mo = 0; mo < TN; mo++)
-            for (int st = 0; st < TS; st++)
-              for (int l = 0; l < 64; l++)
-                for (int j = 0; j < 8; j++) {
-                  int const k = 32 * (st / 2) + 8 * (2 * (st % 2) + j / 4) + 4 * (l >> 5) + (j & 3);
-                  int const n = 32 * mo + (l & 31);
-                  emit(hb + ((int64_t(mo) * TS + st) * 64 + l) * 8 + j, SLOT_HALF, i, idx(k, n));
-                }
-          return;
-        }
         // v_mfma_f32_16x16x32 A fragment of output tile mo and 32-feature
         // step t: lane l, element j holds W[16(2t + j/4) + 4(l/16) + j%4][16 mo + l%16].
         int const TK = (K + 15) / 16, TN = (N + 15) / 16, TS = (TK + 1) / 2;
@@ -754,15 +702,6 @@ void pack_words_half(ponni_plan_s const& p, std::vector<uint32_t>& out) {
     float const f = static_cast<float>(v);
     return p.dtype == PONNI_F16 ? float_to_half_bits(f) : float_to_bf16_bits(f);
   };
-  if (p.lut_tanh_off >= 0) {
-    // tanh of every non-negative 16-bit value, evaluated in double and rounded to the type.
-    auto* h = reinterpret_cast<uint16_t*>(out.data() + p.lut_tanh_off);
-    for (uint32_t b = 0; b < 2 * kLutWords; b++) {
-      double const x = p.dtype == PONNI_F16 ? half_bits_to_float(static_cast<uint16_t>(b))
-                                            : bf16_bits_to_float(static_cast<uint16_t>(b));
-      h[b] = bits16(std::tanh(x));
-    }
-  }
   auto* h = reinterpret_cast<uint16_t*>(out.data());
   visit_param_slots(p, [&](int64_t slot, int kind, int layer, int64_t idx) {
     double const v = p.params[layer][idx];
@@ -1456,7 +1395,7 @@ int ponni_plan_kernel_config(ponni_plan plan, int32_t* threads, int32_t* columns
   (void)fused_source(*plan, cfg);
   *threads = 64 * cfg.waves;
   *columns_per_block = cfg.columns_per_block;
-  *persistent = (cfg.lds_bytes > 0 || cfg.lut_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers) ? 1 : 0;
+  *persistent = (cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers) ? 1 : 0;
   return PONNI_OK;
 }
 

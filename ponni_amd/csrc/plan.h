@@ -130,12 +130,6 @@ struct ponni_plan_s {
   std::vector<ponni_hip::Step> steps;
   std::vector<int64_t> layer_param_offset;  // per layer, in packed elements
   int64_t packed_elements = 0;
-  // FUSED 16-bit plans: offset (in 32-bit words) of the tanh table appended
-  // to the packed parameters, -1 when no dense block ends in Tanh.
-  int64_t lut_tanh_off = -1;
-  // FUSED 16-bit plans of dense layers and pointwise steps only, every width
-  // a multiple of 32: 32x32x16 MFMA tiles (dense weights packed for them).
-  bool mfma32 = false;
 
   // Device state.
   bool device_dirty = true;
