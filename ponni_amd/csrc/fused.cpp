@@ -261,16 +261,7 @@ bool compile(std::string const& source, bool contract, std::vector<char>& code, 
 }  // namespace
 
 // Can the FUSED generator express this chain?
-bool fused_supports(ponni_plan_s const& p) {
-  if (p.max_width > 256) return false;
-  for (auto const& d : p.layers) {
-    if (d.kind == PONNI_LAYER_BINOP_CONCATENATE) {
-      int const lead = (d.flags & PONNI_FLAG_CONCAT_AFTER) ? d.n_in : d.n_out - d.n_in;
-      if (lead % 16 != 0) return false;
-    }
-  }
-  return true;
-}
+bool fused_supports(ponni_plan_s const& p) { return p.max_width <= 256; }
 
 // Generate the HIP source of the plan's kernel.  Offsets are those of the
 // MFMA packing (plan.cpp, pack_params).
@@ -685,13 +676,20 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
       case OP_CONCAT: {
         auto const& sv = saved[op.slot];
         std::string const nv = fresh();
-        std::string const fn = half ? "concat_h" : "concat";
-        if (op.aux)
-          o << "    auto " << nv << " = " << fn << "<" << tiles(cur_n) << ", " << tiles(sv.second) << ">(" << cur
-            << ", " << sv.first << ");\n";
-        else
-          o << "    auto " << nv << " = " << fn << "<" << tiles(sv.second) << ", " << tiles(cur_n) << ">("
-            << sv.first << ", " << cur << ");\n";
+        // after: [state; saved], else [saved; state] (ponni_Binop_Concatenate.h:63-86)
+        std::string const first = op.aux ? cur : sv.first, second = op.aux ? sv.first : cur;
+        int const n1 = op.aux ? cur_n : sv.second, n2 = op.aux ? sv.second : cur_n;
+        if (n1 % 16 == 0) {
+          o << "    auto " << nv << " = " << (half ? "concat_h<" : "concat<") << tiles(n1) << ", " << tiles(n2)
+            << ">(" << first << ", " << second << ");\n";
+        } else if (half) {
+          // (16-bit values are exact in fp32: the moves round nothing)
+          o << "    auto " << nv << " = to_h<E>(concat_any<" << n1 << ", " << n2 << ">(to_f32(" << first
+            << "), to_f32(" << second << "), L));\n";
+        } else {
+          o << "    auto " << nv << " = concat_any<" << n1 << ", " << n2 << ">(" << first << ", " << second
+            << ", L);\n";
+        }
         cur = nv;
         cur_n = op.n_out;
         break;

@@ -382,6 +382,46 @@ __device__ inline S<TA + TB, NT> concat(S<TA, NT> const& a, S<TB, NT> const& b) 
   return s;
 }
 
+// [a; b] when a's N1 features do not fill whole tiles (N1 % 16 != 0): b's
+// feature j moves to output feature N1 + j.  Output element e of tile m in
+// lane group g holds feature f = 16 m + 4 g + e; with N1 = 16 Q + R and
+// e - R = 4 dq + je (0 <= je < 4), the b feature f - N1 sits in element je of
+// lane group (g + dq) mod 4, column c, of tile m - Q (or m - Q - 1 when
+// g + dq < 0), so every output element is one of two shuffles from the same
+// source lane.  Rows >= N1 + N2 stay zero.
+template <int N1, int N2, int TA, int TB, int NT>
+__device__ inline S<(N1 + N2 + 15) / 16, NT> concat_any(S<TA, NT> const& a, S<TB, NT> const& b, Lane const& L) {
+  constexpr int T = (N1 + N2 + 15) / 16;
+  constexpr int Q = N1 / 16, R = N1 % 16;
+  S<T, NT> out;
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      int const d = e - R;
+      int const dq = d >= 0 ? 0 : -((3 - d) / 4);
+      int const je = d - 4 * dq;
+      int const G = L.g + dq;
+      int const src = ((G & 3) << 4) | L.c;
+      int const f = 16 * m + 4 * L.g + e;
+      int const mb = m - Q;
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        real const va = m < TA ? a.v[m < TA ? m : 0][n][e] : real(0);
+        if (16 * m + 16 <= N1) {  // the whole tile from a
+          out.v[m][n][e] = va;
+          continue;
+        }
+        real const v0 = (mb >= 0 && mb < TB) ? __shfl(b.v[(mb >= 0 && mb < TB) ? mb : 0][n][je], src) : real(0);
+        real const v1 =
+            (mb - 1 >= 0 && mb - 1 < TB) ? __shfl(b.v[(mb - 1 >= 0 && mb - 1 < TB) ? mb - 1 : 0][n][je], src) : real(0);
+        real const vb = G < 0 ? v1 : v0;
+        out.v[m][n][e] = f < N1 ? va : (f < N1 + N2 ? vb : real(0));
+      }
+    }
+  return out;
+}
+
 // Saved residual states may live in LDS instead of registers (one region per
 // wave, lane-contiguous 16-byte chunks, so accesses are bank-conflict free).
 template <int T, int NT>

@@ -1061,7 +1061,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {
       delete p;
-      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs F32/F16/BF16, width <= 256 and 16-aligned concatenation");
+      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs width <= 256");
     }
   } else if (chosen == PONNI_PATH_MFMA) {
     if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {

@@ -420,3 +420,32 @@ def test_narrow_vector_rows(cuda, dtype, B):
             check_f32(got, oracle.forward(layers, xg))
         else:
             check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "f64"])
+@pytest.mark.parametrize("after", [True, False])
+def test_concatenation_any_lead_width_fused(cuda, after, dtype):
+    """Binop_Concatenate whose leading block is not a whole number of 16-row
+    tiles (the FUSED tile library moves the other block by lane-group
+    shuffles): lead widths 1..40, mid-chain, so the result feeds a dense layer,
+    on FUSED against the oracle."""
+    rng = np.random.default_rng(5)
+    for lead in (1, 3, 4, 5, 8, 12, 13, 16, 17, 20, 28, 40):
+        other = int(rng.choice([3, 7, 16, 24]))
+        n_state, n_saved = (lead, other) if after else (other, lead)
+        layers = [P.Save_State(0, 6), P.Matvec(rng.uniform(-0.5, 0.5, (6, n_saved))), P.Tanh(n_saved),
+                  P.Save_State(1, n_saved), P.Matvec(rng.uniform(-0.5, 0.5, (n_saved, n_state))), P.Relu(n_state),
+                  P.Binop_Concatenate(1, n_state, n_state + n_saved, after),
+                  P.Matvec(rng.uniform(-0.5, 0.5, (n_state + n_saved, 5))), P.Sigmoid(5)]
+        # (slot 0 is never read: it checks that an unused save changes nothing)
+        x = rng.standard_normal((6, 1000))
+        print(f"concat lead={lead} other={other} after={after} dtype={dtype}", flush=True)
+        got, xg, m = gpu_run(layers, x, dtype, "fused")
+        assert m.path == "fused"
+        if dtype == "f64":
+            want = oracle.forward(layers, xg, oracle.MODE_F64)
+            assert np.allclose(got, want, rtol=1e-12, atol=1e-12), np.abs(got - want).max()
+        elif dtype == "f16":
+            check_half(got, oracle.forward(layers, xg, oracle.MODE_F16_OPERANDS))
+        else:
+            check_f32(got, oracle.forward(layers, xg))

@@ -330,3 +330,35 @@ def test_fp16_modes_are_close_to_fp64():
     # fp16-operand results are exactly representable in binary16
     got = run(layers, x, oracle.MODE_F16_OPERANDS)
     assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+
+
+def reference_mid_chain_concat_before(state, saved):
+    """What the reference executor returns for a mid-chain
+    Binop_Concatenate(after=false): the barrier is in place
+    (overwrite_input = true, src/layers/ponni_Binop_Concatenate.h:17), so
+    compute_all_outputs gets the same tmp buffer as input and output
+    (src/ponni_Inference.h:515-541) and writes it row by row
+    (ponni_Binop_Concatenate.h:76-81): out[i] = i < n2 ? saved[i] : in[i - n2],
+    where in[i - n2] has already been overwritten."""
+    n1, n2 = len(state), len(saved)
+    buf = list(state) + [0.0] * n2  # the tmp buffer (capacity-wide)
+    for irow in range(n1 + n2):
+        buf[irow] = saved[irow] if irow < n2 else buf[irow - n2]
+    return buf
+
+
+def test_mid_chain_concatenation_before_records_the_reference_defect():
+    """The reference's in-place [saved; current] loses the current rows: every
+    row repeats the saved state with period n2.  This build (every kernel
+    family and the oracle) returns the layer's documented [saved; current]."""
+    state, saved = [1.0, 2.0, 3.0], [10.0, 20.0]
+    assert reference_mid_chain_concat_before(state, saved) == [10.0, 20.0, 10.0, 20.0, 10.0]
+    assert reference_mid_chain_concat_before([1.0], [10.0, 20.0, 30.0]) == [10.0, 20.0, 30.0, 10.0]
+    # The oracle on a chain where the concatenation is mid-chain (the state
+    # lives in tmp1 and is not the last layer): Save(x) ; Relu ; Concat(before) ; Matvec(I).
+    x = np.array([[-1.0, 4.0], [2.0, -3.0]])
+    layers = [P.Save_State(0, 2), P.Relu(2), P.Binop_Concatenate(0, 2, 4, False), P.Matvec(np.eye(4))]
+    got = oracle.forward(layers, x, oracle.MODE_F64)
+    assert got.tolist() == [[-1.0, 4.0], [2.0, -3.0], [0.0, 4.0], [2.0, 0.0]]
+    ref = [reference_mid_chain_concat_before([max(v, 0.0) for v in x[:, b]], list(x[:, b])) for b in range(2)]
+    assert np.array(ref).T.tolist() == [[-1.0, 4.0], [2.0, -3.0], [-1.0, 4.0], [2.0, -3.0]]
