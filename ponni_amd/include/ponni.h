@@ -60,6 +60,7 @@
 #include <vector>
 
 #include "ponni/device.h"
+#include "ponni/two_half.h"
 #include "ponni/ponni_file.h"
 #include "ponni_hip.h"
 

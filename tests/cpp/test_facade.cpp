@@ -546,6 +546,73 @@ __global__ void in_kernel_sarray(typename Model::Params p, float* result) {
   result[0] = out(0);
 }
 
+// unit/core/test_core_unit.cpp:1019-1069: TwoHalf / TwoMask lanes.  The 16
+// results of the reference test, computed where `two_half_lanes` runs.
+__host__ __device__ inline void two_half_lanes(float* r) {
+  using ponni::TwoHalf;
+  using ponni::TwoMask;
+  TwoHalf const left = TwoHalf::from_floats(2.0f, -3.0f);
+  TwoHalf const right = TwoHalf::from_floats(4.0f, 5.0f);
+  TwoHalf const added = left + right;
+  TwoHalf const fused = TwoHalf::fma(left, right, TwoHalf::from_floats(1.0f, 2.0f));
+  TwoHalf const rounded_even = TwoHalf::round(TwoHalf::from_floats(2.5f, -3.5f));
+  TwoHalf const rounded_odd = TwoHalf::round(TwoHalf::from_floats(1.5f, -2.5f));
+  TwoHalf const signs = TwoHalf::sign(TwoHalf::from_floats(__builtin_nanf(""), -0.0f));
+  TwoMask const greater = TwoHalf::greater(left, right);
+  TwoMask const either = TwoMask::logical_or(greater, TwoMask::from_bools(true, false));
+  TwoMask const inverted = TwoMask::logical_not(either);
+  TwoHalf const selected = TwoHalf::select(inverted, left, right);
+  float const v[16] = {added.low(),        added.high(),       fused.low(),       fused.high(),
+                       rounded_even.low(), rounded_even.high(), rounded_odd.low(), rounded_odd.high(),
+                       signs.low(),        signs.high(),       greater.low() ? 1.0f : 0.0f, greater.high() ? 1.0f : 0.0f,
+                       inverted.low() ? 1.0f : 0.0f, inverted.high() ? 1.0f : 0.0f, selected.low(), selected.high()};
+  for (int i = 0; i < 16; i++) r[i] = v[i];
+}
+
+__global__ void two_half_kernel(float* r) { two_half_lanes(r); }
+
+void check_two_half_lanes(float const* r) {
+  CHECK(r[0] == 6.0f && r[1] == 2.0f && r[2] == 9.0f && r[3] == -13.0f);
+  CHECK(r[4] == 2.0f && r[5] == -4.0f && r[6] == 2.0f && r[7] == -2.0f);  // ties to even
+  CHECK(std::isnan(r[8]) && r[9] == 0.0f && !std::signbit(r[9]));          // sign(NaN), sign(-0) = +0
+  CHECK(r[10] == 0.0f && r[11] == 0.0f && r[12] == 0.0f && r[13] == 1.0f);
+  CHECK(r[14] == 4.0f && r[15] == -3.0f);
+}
+
+void test_two_half_cpu() {
+  float r[16];
+  two_half_lanes(r);
+  check_two_half_lanes(r);
+  using ponni::TwoHalf;
+  // one rounding per lane: 2^-11 * (1 + 2^-10) * (1 - 2^-10) + (1 + 2^-10) is
+  // exactly (1 + 2^-10) + 2^-11 - 2^-31, just below the midpoint, so it
+  // rounds down to 1 + 2^-10 (two roundings would tie to 1 + 2^-9).
+  TwoHalf const a = TwoHalf::splat(static_cast<_Float16>(std::ldexp(1.0f + std::ldexp(1.0f, -10), -11)));
+  TwoHalf const b = TwoHalf::splat(static_cast<_Float16>(1.0f - std::ldexp(1.0f, -10)));
+  TwoHalf const c = TwoHalf::splat(static_cast<_Float16>(1.0f + std::ldexp(1.0f, -10)));
+  CHECK(TwoHalf::fma(a, b, c).low() == 1.0f + std::ldexp(1.0f, -10));
+  // activations in fp32 per lane, rounded once; predicates
+  TwoHalf const x = TwoHalf::from_floats(0.5f, -1.25f);
+  CHECK(TwoHalf::tanh(x).low() == static_cast<float>(static_cast<_Float16>(std::tanh(0.5f))));
+  CHECK(TwoHalf::relu(x).high() == 0.0f && TwoHalf::leaky_relu(x, 0.5f).high() == -0.625f);
+  CHECK(TwoHalf::maximum(x, TwoHalf::zero()).low() == 0.5f && TwoHalf::minimum(x, TwoHalf::zero()).high() == -1.25f);
+  TwoHalf const inf = TwoHalf::from_floats(-INFINITY, INFINITY);
+  CHECK(!TwoHalf::is_inf(inf, false, true).low() && TwoHalf::is_inf(inf, false, true).high());
+  CHECK(TwoHalf::is_nan(TwoHalf::from_floats(__builtin_nanf(""), 1.0f)).low());
+  CHECK(ponni::TwoMask::equal(ponni::TwoMask::splat(true), ponni::TwoMask::from_bools(true, false)).low());
+  CHECK(sizeof(TwoHalf) == sizeof(__half2) && sizeof(ponni::TwoMask) == 1);
+}
+
+void test_two_half_gpu() {
+  float* d = nullptr;
+  CHECK(hipMalloc(&d, 16 * sizeof(float)) == hipSuccess);
+  hipLaunchKernelGGL(two_half_kernel, dim3(1), dim3(1), 0, 0, d);
+  float r[16];
+  CHECK(hipMemcpy(r, d, sizeof r, hipMemcpyDeviceToHost) == hipSuccess);
+  check_two_half_lanes(r);
+  CHECK(hipFree(d) == hipSuccess);
+}
+
 void test_in_kernel_gpu() {
   using namespace ponni;
   {  // unit/core/test_core_unit.cpp:280-322: the four-block model, batch and in-kernel agree
@@ -924,6 +991,7 @@ int main(int argc, char** argv) {
   test_weights_files<ponni::HostSpace>();
   test_sixteen_bit_types();
   test_initializers_cpu();
+  test_two_half_cpu();
   test_rebinding_cpu();
   test_user_layers_cpu();
   test_host_models_cpu();
@@ -936,6 +1004,7 @@ int main(int argc, char** argv) {
     test_known_answers_gpu();
     test_views_streams_capacity_gpu();
     test_in_kernel_gpu();
+    test_two_half_gpu();
   }
   std::printf("%s: %d checks, %d failures\n", cpu_only ? "cpu" : "cpu+gpu", g_checks, g_failures);
   return g_failures == 0 ? 0 : 1;
