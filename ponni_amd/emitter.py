@@ -207,9 +207,17 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w('    ponni::abort("GeneratedModel learned parameter index is out of range");')
     w("  }")
     w("")
-    w(f"  explicit {class_name}(hipStream_t stream = nullptr) : stream_(stream), storage_(storage_parameter_elements, 0.0) {{")
-    w("    scalar_ = make_plan(" + ("PONNI_F64" if scalar == "double" else "PONNI_F32") + ");")
-    w("    half_ = make_plan(PONNI_F16);")
+    w("  // Copies share the weights, plans and buffers (the reference's generated model")
+    w("  // holds Kokkos Views, which copy shallowly): a copy taken before load_weights or")
+    w("  // set_parameters sees them, and a copy may be captured by value in a kernel.")
+    w(f"  explicit {class_name}(hipStream_t stream = nullptr) : state_(std::make_shared<State>()) {{")
+    w("    state_->stream = stream;")
+    w("    state_->storage.assign(static_cast<std::size_t>(storage_parameter_elements), 0.0);")
+    w("    state_->loaded = storage_parameter_elements == 0;")
+    w("    state_->scalar = make_plan(" + ("PONNI_F64" if scalar == "double" else "PONNI_F32") + ");")
+    w("    state_->half = make_plan(PONNI_F16);")
+    w("    push(state_->scalar.get());")
+    w("    push(state_->half.get());")
     w("  }")
     w("")
     w("  static constexpr int get_num_parameters() { return static_cast<int>(learned_parameter_elements); }")
@@ -224,20 +232,20 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("      if (error) *error = ponni_last_error();")
     w("      return false;")
     w("    }")
-    w("    storage_ = std::move(st);")
-    w("    loaded_ = true;")
-    w("    push(scalar_.get());")
-    w("    push(half_.get());")
+    w("    state_->storage = std::move(st);")
+    w("    state_->loaded = true;")
+    w("    push(state_->scalar.get());")
+    w("    push(state_->half.get());")
     w("    return true;")
     w("  }")
     w("  bool save_parameters(std::string const& path, std::string* error = nullptr) const {")
-    w("    if (!loaded_) {")
+    w("    if (!state_->loaded) {")
     w('      if (error) *error = "generated model parameters are not loaded";')
     w("      return false;")
     w("    }")
     w("    std::vector<ponni_tensor_spec> specs = cspecs();")
     w("    int const rc = ponni_file_write_tensors(path.c_str(), model_fingerprint().c_str(), specs.data(),")
-    w("                                            static_cast<int>(specs.size()), storage_.data(), stored_scalar_bytes,")
+    w("                                            static_cast<int>(specs.size()), state_->storage.data(), stored_scalar_bytes,")
     w('                                            "ponni", "generated");')
     w("    if (rc != PONNI_OK) {")
     w("      if (error) *error = ponni_last_error();")
@@ -245,16 +253,16 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    }")
     w("    return true;")
     w("  }")
-    w("  bool weights_loaded() const { return loaded_; }")
+    w("  bool weights_loaded() const { return state_->loaded; }")
     w("")
     w("  // ---- parameters (emitter.py:1768-1895): learned order, host vectors or device views ----")
     w("  template <class T>")
     w("  void get_parameters(std::vector<T>& destination) const {")
-    w('    if (!loaded_) ponni::abort("GeneratedModel::get_parameters called before load_weights");')
+    w('    if (!state_->loaded) ponni::abort("GeneratedModel::get_parameters called before load_weights");')
     w("    if (static_cast<std::int64_t>(destination.size()) != learned_parameter_elements)")
     w('      ponni::abort("GeneratedModel::get_parameters destination extent is incorrect");')
     w("    for (std::int64_t i = 0; i < learned_parameter_elements; i++)")
-    w("      destination[i] = static_cast<T>(static_cast<Scalar>(storage_[parameter_storage_index(i)]));")
+    w("      destination[i] = static_cast<T>(static_cast<Scalar>(state_->storage[parameter_storage_index(i)]));")
     w("  }")
     w("  // Device views: any [1, n] or [n, 1] ponni::View holding the n learned parameters.")
     w("  template <class T>")
@@ -265,13 +273,13 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("  }")
     w("  template <class T>")
     w("  void set_parameters(std::vector<T> const& source) {")
-    w('    if (!loaded_) ponni::abort("GeneratedModel::set_parameters called before load_weights");')
+    w('    if (!state_->loaded) ponni::abort("GeneratedModel::set_parameters called before load_weights");')
     w("    if (static_cast<std::int64_t>(source.size()) != learned_parameter_elements)")
     w('      ponni::abort("GeneratedModel::set_parameters source extent is incorrect");')
     w("    for (std::int64_t i = 0; i < learned_parameter_elements; i++)")
-    w("      storage_[parameter_storage_index(i)] = static_cast<Scalar>(source[i]);")
-    w("    push(scalar_.get());")
-    w("    push(half_.get());")
+    w("      state_->storage[parameter_storage_index(i)] = static_cast<Scalar>(source[i]);")
+    w("    push(state_->scalar.get());")
+    w("    push(state_->half.get());")
     w("  }")
     w("  template <class T>")
     w("  void set_parameters(ponni::View<T> const& source) {")
@@ -279,16 +287,16 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("  }")
     w("  // The fp16 copy follows every parameter change already; kept for the API.")
     w("  void refresh_half_parameters() {")
-    w('    if (!loaded_) ponni::abort("GeneratedModel::refresh_half_parameters called before load_weights");')
-    w("    push(half_.get());")
+    w('    if (!state_->loaded) ponni::abort("GeneratedModel::refresh_half_parameters called before load_weights");')
+    w("    push(state_->half.get());")
     w("  }")
     w("  bool parameters_are_finite() const {")
-    w("    if (!loaded_) return false;")
+    w("    if (!state_->loaded) return false;")
     w("    for (std::int64_t i = 0; i < learned_parameter_elements; i++)")
-    w("      if (!std::isfinite(static_cast<Scalar>(storage_[parameter_storage_index(i)]))) return false;")
+    w("      if (!std::isfinite(static_cast<Scalar>(state_->storage[parameter_storage_index(i)]))) return false;")
     w("    return true;")
     w("  }")
-    w("  bool parameters_synchronized() const { return loaded_; }")
+    w("  bool parameters_synchronized() const { return state_->loaded; }")
     w("")
     w("  // ---- inference ----")
     w("  // x [num_inputs, B], y [num_outputs, B]: LayoutRight device views of Scalar.")
@@ -299,9 +307,9 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     if gm.scalar in kernels:
         k = kernels[gm.scalar]
         w(f"    launch({class_name}_kernels::k_{gm.scalar}::{k['name']}, {k['threads']}, {k['cols']}, "
-          f"{'true' if k['persistent'] else 'false'}, scalar_.get(), x.data(), x.stride(0), y.data(), y.stride(0), batch);")
+          f"{'true' if k['persistent'] else 'false'}, state_->scalar.get(), x.data(), x.stride(0), y.data(), y.stride(0), batch);")
     else:
-        w("    ponni::check(ponni_forward(scalar_.get(), x.data(), x.stride(0), y.data(), y.stride(0), batch, stream_),")
+        w("    ponni::check(ponni_forward(state_->scalar.get(), x.data(), x.stride(0), y.data(), y.stride(0), batch, state_->stream),")
         w('                 "infer_batch");')
     w("  }")
     w("")
@@ -312,22 +320,32 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    std::int64_t const batch = checked_batch(x, y);")
     w("    half_buffers(batch);")
     w("    unsigned const blocks_in = static_cast<unsigned>((num_inputs * batch + 255) / 256);")
-    w("    hipLaunchKernelGGL((convert_rows<Scalar, _Float16>), dim3(blocks_in), dim3(256), 0, stream_, x.data(),")
-    w("                       static_cast<std::int64_t>(x.stride(0)), hx_, batch, num_inputs * batch, batch);")
+    w("    hipLaunchKernelGGL((convert_rows<Scalar, _Float16>), dim3(blocks_in), dim3(256), 0, state_->stream, x.data(),")
+    w("                       static_cast<std::int64_t>(x.stride(0)), state_->hx, batch, num_inputs * batch, batch);")
     if "f16" in kernels:
         k = kernels["f16"]
         w(f"    launch({class_name}_kernels::k_f16::{k['name']}, {k['threads']}, {k['cols']}, "
-          f"{'true' if k['persistent'] else 'false'}, half_.get(), hx_, batch, hy_, batch, batch);")
+          f"{'true' if k['persistent'] else 'false'}, state_->half.get(), state_->hx, batch, state_->hy, batch, batch);")
     else:
-        w("    ponni::check(ponni_forward(half_.get(), hx_, batch, hy_, batch, batch, stream_), \"infer_batch_half2\");")
+        w("    ponni::check(ponni_forward(state_->half.get(), state_->hx, batch, state_->hy, batch, batch, state_->stream), \"infer_batch_half2\");")
     w("    unsigned const blocks_out = static_cast<unsigned>((num_outputs * batch + 255) / 256);")
-    w("    hipLaunchKernelGGL((convert_rows<_Float16, Scalar>), dim3(blocks_out), dim3(256), 0, stream_, hy_, batch,")
+    w("    hipLaunchKernelGGL((convert_rows<_Float16, Scalar>), dim3(blocks_out), dim3(256), 0, state_->stream, state_->hy, batch,")
     w("                       y.data(), static_cast<std::int64_t>(y.stride(0)), num_outputs * batch, batch);")
     w("  }")
     w("")
-    w("  // One sample inside an application kernel (emitter.py:1897-1901): the model object")
-    w("  // holds host state, so kernels take the trivially copyable handle device() returns")
-    w("  // and call its infer_one.")
+    w("  // One sample inside an application kernel (emitter.py:1897-1901): capture a copy")
+    w("  // of the model by value and call infer_one.  Device code reads the plan's device")
+    w("  // description, which the model carries by value and whose buffers stay in place")
+    w("  // across parameter changes; host code reads the host description the copies share.")
+    w("  __host__ __device__ void infer_one(ponni::SArray<Scalar, num_inputs> const& in,")
+    w("                                    ponni::SArray<Scalar, num_outputs>& out) const {")
+    w("#if defined(__HIP_DEVICE_COMPILE__)")
+    w("    ponni::forward_one<Scalar>(device_model_, in.data(), 1, out.data(), 1);")
+    w("#else")
+    w("    ponni::forward_one<Scalar>(state_->host_model, in.data(), 1, out.data(), 1);")
+    w("#endif")
+    w("  }")
+    w("  // A trivially copyable handle for kernels that take plain arguments.")
     w("  struct Device {")
     w("    ponni_device_model model;")
     w("    __device__ void infer_one(ponni::SArray<Scalar, num_inputs> const& in,")
@@ -336,13 +354,6 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    }")
     w("  };")
     w("  Device device() const { return Device{device_model_}; }")
-    w("")
-    w("  ~" + class_name + "() {")
-    w("    if (hx_) (void)hipFree(hx_);")
-    w("    if (hy_) (void)hipFree(hy_);")
-    w("  }")
-    w(f"  {class_name}({class_name} const&) = delete;")
-    w(f"  {class_name}& operator=({class_name} const&) = delete;")
     w("")
     w(" private:")
     w(f"  static constexpr int num_layers = {len(layers)};")
@@ -388,13 +399,20 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("      std::vector<Scalar> v(static_cast<std::size_t>(n));")
     w("      for (std::int64_t j = 0; j < n; j++) {")
     w("        std::int64_t const g = gather()[begin()[l] + j];")
-    w("        v[j] = static_cast<Scalar>(g >= 0 ? storage_[g] : literal(-g - 1));")
+    w("        v[j] = static_cast<Scalar>(g >= 0 ? state_->storage[g] : literal(-g - 1));")
     w("      }")
     w('      ponni::check(ponni_plan_set_layer_params(plan, l, v.data(), n), "GeneratedModel parameters");')
     w("    }")
+    w("    if (plan != state_->scalar.get()) return;")
+    w('    ponni::check(ponni_plan_host_model(plan, &state_->host_model), "GeneratedModel host model");')
     w("    int devices = 0;")
-    w("    if (plan == scalar_.get() && hipGetDeviceCount(&devices) == hipSuccess && devices > 0)")
-    w('      ponni::check(ponni_plan_device_model(plan, &device_model_), "GeneratedModel device model");')
+    w("    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) return;")
+    w("    ponni_device_model m{};")
+    w('    ponni::check(ponni_plan_device_model(plan, &m), "GeneratedModel device model");')
+    w("    // Copies hold device_model_ by value: its buffers must not move once set.")
+    w("    if (device_model_.ops != nullptr && (m.ops != device_model_.ops || m.params != device_model_.params))")
+    w('      ponni::abort("GeneratedModel device description moved");')
+    w("    device_model_ = m;")
     w("  }")
     w("  std::vector<ponni_tensor_spec> cspecs() const {")
     w("    std::vector<ponni_tensor_spec> out;")
@@ -429,7 +447,7 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    std::int64_t grid = tiles;")
     w("    if (persistent) {")
     w("      // Resident workgroups of this kernel on the device, found once per kernel.")
-    w("      std::int64_t& resident = plan == scalar_.get() ? resident_[0] : resident_[1];")
+    w("      std::int64_t& resident = plan == state_->scalar.get() ? state_->resident[0] : state_->resident[1];")
     w("      if (resident == 0) {")
     w("        int dev = 0, cus = 0, per = 0;")
     w("        (void)hipGetDevice(&dev);")
@@ -439,7 +457,7 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("      }")
     w("      grid = std::min<std::int64_t>(tiles, resident);")
     w("    }")
-    w("    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(threads), 0, stream_,")
+    w("    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(threads), 0, state_->stream,")
     w("                       static_cast<PT const*>(params), x, ldx, y, ldy, batch);")
     w("    hipError_t const e = hipGetLastError();")
     w('    if (e != hipSuccess) ponni::abort(std::string("GeneratedModel kernel launch: ") + hipGetErrorString(e));')
@@ -454,23 +472,35 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    dst[r * ldd + c] = static_cast<To>(static_cast<float>(src[r * lds + c]));")
     w("  }")
     w("  void half_buffers(std::int64_t batch) const {")
-    w("    if (batch <= half_capacity_) return;")
-    w("    if (hx_) (void)hipFree(hx_);")
-    w("    if (hy_) (void)hipFree(hy_);")
-    w('    if (hipMalloc(&hx_, sizeof(_Float16) * num_inputs * batch) != hipSuccess) ponni::abort("hipMalloc");')
-    w('    if (hipMalloc(&hy_, sizeof(_Float16) * num_outputs * batch) != hipSuccess) ponni::abort("hipMalloc");')
-    w("    half_capacity_ = batch;")
+    w("    if (batch <= state_->half_capacity) return;")
+    w("    if (state_->hx) (void)hipFree(state_->hx);")
+    w("    if (state_->hy) (void)hipFree(state_->hy);")
+    w('    if (hipMalloc(&state_->hx, sizeof(_Float16) * num_inputs * batch) != hipSuccess) ponni::abort("hipMalloc");')
+    w('    if (hipMalloc(&state_->hy, sizeof(_Float16) * num_outputs * batch) != hipSuccess) ponni::abort("hipMalloc");')
+    w("    state_->half_capacity = batch;")
     w("  }")
     w("")
-    w("  hipStream_t stream_ = nullptr;")
-    w("  std::vector<double> storage_;")
-    w("  bool loaded_ = storage_parameter_elements == 0;")
-    w("  std::shared_ptr<ponni_plan_s> scalar_, half_;")
+    w("  struct State {")
+    w("    hipStream_t stream = nullptr;")
+    w("    std::vector<double> storage;")
+    w("    bool loaded = false;")
+    w("    std::shared_ptr<ponni_plan_s> scalar, half;")
+    w("    ponni_device_model host_model{};")
+    w("    _Float16* hx = nullptr;")
+    w("    _Float16* hy = nullptr;")
+    w("    std::int64_t half_capacity = 0;")
+    w("    std::int64_t resident[2] = {0, 0};")
+    w("    State() = default;")
+    w("    State(State const&) = delete;")
+    w("    State& operator=(State const&) = delete;")
+    w("    ~State() {")
+    w("      if (hx) (void)hipFree(hx);")
+    w("      if (hy) (void)hipFree(hy);")
+    w("    }")
+    w("  };")
+    w("  // First member: device code reads it at the same offset host code wrote it.")
     w("  ponni_device_model device_model_{};")
-    w("  mutable _Float16* hx_ = nullptr;")
-    w("  mutable _Float16* hy_ = nullptr;")
-    w("  mutable std::int64_t half_capacity_ = 0;")
-    w("  mutable std::int64_t resident_[2] = {0, 0};")
+    w("  std::shared_ptr<State> state_;")
     w("};")
     w("")
     w(ns_close)

@@ -91,7 +91,9 @@ def test_emitted_header_text(tmp_path):
 def test_generated_header_on_gpu(cuda, tmp_path, model):
     """tests/cpp/test_generated.cpp over an emitted header: infer_batch
     (the ahead-of-time kernel), infer_batch_half2 and infer_one (an
-    application kernel over device()) against the CPU oracle, on a weights
+    application kernel over device(), a kernel lambda holding a copy of the
+    model taken before its weights were loaded -- bit-identical to the
+    device() kernel -- and the host) against the CPU oracle, on a weights
     file saved by the Python model (c5, f64) or written by the reference
     generator (tiny, tests/golden/tiny_generated.ponni); then the parameter
     API (get, set from a device view, save) against the Python model.  fp32
@@ -149,6 +151,9 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
     want = oracle.forward(oracle_layers(ref), x.astype(np.float64), mode)
     check(out("y_batch.bin"), want)
     check(out("y_one.bin"), want)
+    # The model captured by value runs the device() handle's code on the same description.
+    np.testing.assert_array_equal(out("y_copy.bin"), out("y_one.bin"))
+    check(out("y_host.bin"), want)
     if model != "f64":  # (the random F64 graph's Exp / Div leave the fp16 range)
         xh = x.astype(np.float16).astype(np.float64)
         check_half(out("y_half.bin"), oracle.forward(oracle_layers(ref), xh, oracle.MODE_F16_OPERANDS))
@@ -159,6 +164,8 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
     want = oracle.forward(oracle_layers(ref), x.astype(np.float64), mode)
     check(out("y_batch_scaled.bin"), want)
     check(out("y_one_scaled.bin"), want)
+    np.testing.assert_array_equal(out("y_copy_scaled.bin"), out("y_one_scaled.bin"))
+    check(out("y_host_scaled.bin"), want)
     saved = G.GeneratedModel(make_graph())
     saved.load_weights(str(tmp_path / "saved.ponni"))
     np.testing.assert_array_equal(saved.storage, ref.storage)
