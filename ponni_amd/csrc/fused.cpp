@@ -497,24 +497,52 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o << "  Lane L;\n  L.lane = threadIdx.x & 63;\n  L.g = L.lane >> 4;\n  L.c = L.lane & 15;\n  L.batch = batch;\n";
   o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
   // 16-bit plans request each tile's input rows into LDS one tile ahead
-  // (fused_f16.h prefetch_rows_lds) when the buffer fits next to the staged
+  // (fused_f16.h prefetch_rows_lds16) when the buffer fits next to the staged
   // A fragments (2 slots x 8 fragments x PONNI_CHUNK_TILES KB) and vectors.
   int const n_in0 = p.layers.front().n_in;
-  int const in_dma_bytes = cfg.waves * tiles(n_in0) * NT * 4 * 64 * 4;
+  int const in_rows_elems = tiles(n_in0) * 16 * 16 * NT;  // per wave, row-major 16-bit
+  int const in_dma_bytes = cfg.waves * in_rows_elems * 2;
   int chunk_tiles = 4;
   if (char const* d = std::getenv("PONNI_CHUNK_TILES")) chunk_tiles = std::max(1, std::min(8, std::atoi(d)));
   bool in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + 2 * 8 * 1024 * chunk_tiles + 16 * 1024 <= 160 * 1024;
   if (char const* v = std::getenv("PONNI_INPUT_DMA"))  // tuning override
     in_dma = in_dma && std::strcmp(v, "0") != 0;
   std::string const WCOLS = std::to_string(16 * NT), NW = std::to_string(cfg.waves);
+  // The next tile's rows are requested inside the second dense layer, right
+  // after its first chunk's weight loads (fused_f16.h dense_hs hook): waits
+  // for weight chunks (vmcnt counts in issue order) then never wait for
+  // them, the next one a chunk later.  With one dense layer: after this
+  // tile's rows are read.
+  int const hook_dense = half && half_staged && in_dma && dense_seq.size() >= 2 ? 1 : -1;
+  std::string const prefetch_next = "if (pre_next) prefetch_rows_lds16<" + std::to_string(n_in0) + ", " +
+                                    std::to_string(NT) + ">(x, ldx, Ln, in_buf[wave_id()]);";
+  // The last op, a dense layer whose epilogue is its bias (the seed) and
+  // activations without parameters, runs transposed and writes 8-byte runs
+  // of output rows (fused_f16.h store_rows_ht).
+  bool out_transposed = false;
+  if (half && half_staged && !p.ops.empty() && p.ops.back().code == OP_DENSE) {
+    Op const& op = p.ops.back();
+    bool const lead = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
+    out_transposed = true;
+    for (int s = lead ? 1 : 0; s < op.epi_count; s++) {
+      int const a = p.steps[op.epi_begin + s].act;
+      if (a == ACT_BIAS || act_has_param(a)) out_transposed = false;
+    }
+  }
+  if (out_transposed)
+    o << "  bool const yvec = ((reinterpret_cast<uint64_t>(y) | uint64_t(ldy) * 2) & 7) == 0;\n";
   if (in_dma) {
-    o << "  __shared__ unsigned in_buf[" << cfg.waves << "][" << in_dma_bytes / 4 / cfg.waves << "];\n";
+    o << "  __shared__ unsigned short in_buf[" << cfg.waves << "][" << in_rows_elems << "];\n";
+    // Whole tiles of a 16-byte aligned x with a row stride of a multiple of
+    // 8 elements go through LDS; others (the batch's last tile) load directly.
+    o << "  bool const xvec = ((reinterpret_cast<uint64_t>(x) | uint64_t(ldx) * 2) & 15) == 0;\n";
     o << "  L.col0 = (int64_t(blockIdx.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
-    o << "  if (blockIdx.x < tiles) prefetch_rows_lds<" << n_in0 << ", " << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
+    o << "  if (blockIdx.x < tiles && xvec && L.col0 + " << WCOLS << " <= batch) prefetch_rows_lds16<" << n_in0 << ", "
+      << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
     // The LDS writes of these loads complete with vmcnt, which the compiler
     // does not track for reads of in_buf: each tile's rows are waited for
     // explicitly, here for the first tile and before the output stores for
-    // the next one (requested at the top of the tile, so long landed).
+    // the next one (requested during the tile, so long landed).
     o << "  wait_vmem();\n";
   }
   o << "  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {\n";
@@ -527,12 +555,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::string cur = fresh();
   int cur_n = p.layers.front().n_in;
   if (in_dma) {
-    o << "    auto " << cur << " = load_rows_lds<" << cur_n << ", " << NT << ", E>(in_buf[wave_id()], L);\n";
+    o << "    auto " << cur << " = xvec && L.col0 + " << WCOLS << " <= batch ? load_rows_lds16<" << cur_n << ", " << NT
+      << ", E>(in_buf[wave_id()], L) : load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
     o << "    wait_lds();\n";
-    o << "    if (tile + gridDim.x < tiles) {\n      Lane Ln = L;\n      Ln.col0 = ((tile + gridDim.x) * " << NW
-      << " + wave_id()) * " << WCOLS << ";\n      "
-      << "prefetch_rows_lds<" + std::to_string(cur_n) + ", " + std::to_string(NT)
-      << ">(x, ldx, Ln, in_buf[wave_id()]);\n    }\n";
+    o << "    Lane Ln = L;\n    Ln.col0 = ((tile + gridDim.x) * " << NW << " + wave_id()) * " << WCOLS << ";\n";
+    o << "    bool const pre_next = tile + gridDim.x < tiles && xvec && Ln.col0 + " << WCOLS << " <= batch;\n";
+    if (hook_dense < 0) o << "    " << prefetch_next << "\n";
   } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
   else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
@@ -566,6 +594,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
     if (pad && n % 16) o << "    zero_pad<" << n << ", " << tiles(n) << ">(" << v << ", L);\n";
   };
+  std::string dense_hook;  // closes a dense_hs call that takes the prefetch hook
+  bool pad_ok = true;      // false for a transposed tile
   for (Op const& op : p.ops) {
     o << "    // op code " << op.code << "\n";
     switch (op.code) {
@@ -585,13 +615,20 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, " << init << ", [&](int mo, floatx4 (&t)["
             << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
         } else if (half) {
-          std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
+          bool const tr = out_transposed && &op == &p.ops.back();
+          bool const hook = static_cast<int>(dense_index) == hook_dense;
+          std::string const init = !seed ? "SeedZero{}"
+                                   : tr  ? "SeedRowsT{" + vec(p.steps[op.epi_begin].off, n) + ", L.c}"
+                                         : "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}";
           auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
           dense_index++;
           o << "    auto " << nv << " = dense_hs<" << tiles(op.n_in) << ", " << tiles(n) << ", " << NT << ", "
-            << cfg.waves << ", " << next.ts << ", " << next.to << ">(" << cur << ", reinterpret_cast<E const*>(P + "
+            << cfg.waves << ", " << next.ts << ", " << next.to << (tr || hook ? tr ? ", true" : ", false" : "")
+            << (hook ? ", 0" : "") << ">(" << cur << ", reinterpret_cast<E const*>(P + "
             << op.woff << "), reinterpret_cast<E const*>(P + " << next.woff << "), st, L, " << init
             << ", [&](int mo, floatx4 (&t)[" << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
+          if (hook) dense_hook = "    }, [&] { " + prefetch_next + " });\n";
+          if (tr) pad_ok = false;
         } else {
           std::string const init = seed ? "bias_rows<" + std::to_string(tiles(n)) + ">(" + vec(p.steps[op.epi_begin].off, n) + ", L)"
                                         : "zeros<" + std::to_string(tiles(n)) + ">()";
@@ -613,9 +650,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
-        if (pad && n % 16) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
+        // (a transposed tile's padding rows are never read nor stored)
+        if (pad && n % 16 && pad_ok) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
         if (half) o << "      tile_round<E>(t, o);\n";
-        o << "    });\n";
+        o << (dense_hook.empty() ? "    });\n" : dense_hook);
+        dense_hook.clear();
+        pad_ok = true;
         cur = nv;
         cur_n = n;
         break;
@@ -781,7 +821,8 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     }
   }
   if (half && in_dma) o << "    wait_vmem();\n";
-  if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
+  if (out_transposed) o << "    store_rows_ht<" << cur_n << ">(" << cur << ", y, ldy, L, yvec);\n";
+  else if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   o << "  }\n}\n";
   if (!vec_lds.empty()) {

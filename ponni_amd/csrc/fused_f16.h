@@ -98,52 +98,46 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
 }
 
 // ---- input rows prefetched into LDS one tile ahead ----------------------
-// Each lane's input elements (row 16m + 4g + e, column col0 + 16n + c) are
-// requested with global_load_lds_ushort: instruction i = (m NT + n) 4 + e
-// writes lane l's element, zero-extended, to the dword buf[i * 64 + l] (the
-// DMA's per-lane stride is 4 bytes).  The next tile's rows are requested as
-// soon as this tile's are read, so their HBM latency hides behind a whole
-// tile of work.  Lanes outside the rows or the batch issue nothing and read 0.
+// A wave's input tile (rows 0..16T-1, columns col0 .. col0 + 16 NT - 1) is
+// requested with global_load_lds_dwordx4: piece p = 64 i + l of instruction
+// i is row p / (2 NT), columns 8 (p % (2 NT)) .. +7, and lands at buf + 8 p,
+// so buf holds the tile row-major ([row][16 NT columns]).  Only whole tiles
+// of a 16-byte aligned x with a row stride of a multiple of 8 elements are
+// requested this way (the caller checks); rows >= N issue nothing.  The
+// loads are asynchronous: the caller waits (vmcnt) before reading buf.
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int N, int NT, class E>
-__device__ inline void prefetch_rows_lds(E const* __restrict__ x, int64_t ld, Lane const& L,
-                                         unsigned* __restrict__ buf) {
+__device__ inline void prefetch_rows_lds16(E const* __restrict__ x, int64_t ld, Lane const& L,
+                                           unsigned short* __restrict__ buf) {
   constexpr int T = (N + 15) / 16;
-  E const* __restrict__ xl = lane_ptr(x, ld, L);
-  bool const full = L.col0 + 16 * NT <= L.batch;
+  constexpr int PR = 2 * NT;  // 16-byte pieces per row
+  static_assert(16 * PR % 64 == 0, "whole instructions per tile");
 #pragma unroll
-  for (int m = 0; m < T; m++)
-#pragma unroll
-    for (int n = 0; n < NT; n++) {
-      bool const col_ok = full || L.col0 + 16 * n + L.c < L.batch;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        int const f = 16 * m + 4 * L.g + e;
-        if ((N % 16 == 0 || f < N) && col_ok)
-          __builtin_amdgcn_global_load_lds(static_cast<void const*>(xl + int64_t(16 * m + e) * ld + 16 * n),
-                                           (lds_ptr)(buf + ((m * NT + n) * 4 + e) * 64), 2, 0, 0);
-      }
-    }
+  for (int i = 0; i < T * 16 * PR / 64; i++) {
+    int const piece = 64 * i + L.lane;
+    int const r = piece / PR, k = piece % PR;
+    if (N % 16 == 0 || r < N)
+      __builtin_amdgcn_global_load_lds(static_cast<void const*>(x + int64_t(r) * ld + L.col0 + 8 * k),
+                                       (lds_ptr)(buf + 64 * 8 * i), 16, 0, 0);
+  }
 }
 
+// The lane's tile elements from a prefetched buf; rows >= N read 0.
 template <int N, int NT, class E>
-__device__ inline H<(N + 15) / 16, NT, E> load_rows_lds(unsigned const* __restrict__ buf, Lane const& L) {
+__device__ inline H<(N + 15) / 16, NT, E> load_rows_lds16(unsigned short const* __restrict__ buf, Lane const& L) {
   constexpr int T = (N + 15) / 16;
   H<T, NT, E> s;
-  bool const full = L.col0 + 16 * NT <= L.batch;
 #pragma unroll
   for (int m = 0; m < T; m++)
 #pragma unroll
-    for (int n = 0; n < NT; n++) {
-      bool const col_ok = full || L.col0 + 16 * n + L.c < L.batch;
+    for (int n = 0; n < NT; n++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         int const f = 16 * m + 4 * L.g + e;
-        unsigned short const bits = static_cast<unsigned short>(buf[((m * NT + n) * 4 + e) * 64 + L.lane]);
-        s.v[m][n][e] = ((N % 16 == 0 || f < N) && col_ok) ? __builtin_bit_cast(E, bits) : E(0.0f);
+        unsigned short const bits = buf[f * (16 * NT) + 16 * n + L.c];
+        s.v[m][n][e] = (N % 16 == 0 || f < N) ? __builtin_bit_cast(E, bits) : E(0.0f);
       }
-    }
   return s;
 }
 
@@ -167,6 +161,34 @@ __device__ inline void store_rows_h(H<T, NT, E> const& s, E* __restrict__ y, int
         if ((N % 16 == 0 || f < N) && col_ok) yl[int64_t(16 * m + e) * ld + 16 * n] = s.v[m][n][e];
       }
     }
+}
+
+// Transposed tile (a dense layer run with its MFMA operands swapped, fused
+// dense_hs<..., TR = true>): lane l, element e <-> feature 16m + c, column
+// col0 + 16n + 4g + e, so each lane's 4 elements are consecutive columns of
+// one output row.  Whole tiles of an 8-byte aligned y with a row stride of a
+// multiple of 4 elements (vec_ok) store them as one 8-byte write; otherwise
+// element by element inside the batch.  Rows >= N are not written.
+template <int N, int T, int NT, class E>
+__device__ inline void store_rows_ht(H<T, NT, E> const& s, E* __restrict__ y, int64_t ld, Lane const& L,
+                                     bool vec_ok) {
+  bool const full = vec_ok && L.col0 + 16 * NT <= L.batch;
+#pragma unroll
+  for (int m = 0; m < T; m++) {
+    int const f = 16 * m + L.c;
+    if (N % 16 != 0 && f >= N) continue;
+    E* __restrict__ yr = y + int64_t(f) * ld + L.col0 + 4 * L.g;
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+      if (full) {
+        *reinterpret_cast<typename Vec<E>::x4*>(yr + 16 * n) = s.v[m][n];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (L.col0 + 16 * n + 4 * L.g + e < L.batch) yr[16 * n + e] = s.v[m][n][e];
+      }
+    }
+  }
 }
 
 template <int T, int NT, class E>
@@ -315,14 +337,25 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 #endif
 constexpr int ct16(int ts) { return PONNI_FULL_SLOT_CHUNKS ? kSlotFrags / ts : kChunkTiles; }
 
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
 // Dense layer with LDS-staged A fragments.  On entry slot st.cur holds this
 // layer's first chunk; on exit it holds the first chunk of `w_next`, the next
 // dense layer (TSN fragments per tile, TON output tiles).  init / epi as in
-// dense_h.
-template <int TI, int TO, int NT, int WAVES, int TSN, int TON, class E, class Init, class Epi>
+// dense_h.  TR runs the MFMAs with their operands swapped (the transposed
+// product, same fragments): the output tile is then transposed (feature
+// 16m + c, column 16n + 4g + e; store_rows_ht), which only a layer whose
+// output goes straight to memory can use, seeded with SeedRowsT.  hook()
+// runs once, in chunk HOOK_CH right after that chunk's global loads are
+// issued, so memory requests it makes queue behind them: a later wait for
+// the chunk's loads (vmcnt counts in issue order) does not wait for them.
+template <int TI, int TO, int NT, int WAVES, int TSN, int TON, bool TR = false, int HOOK_CH = -1, class E,
+          class Init, class Epi, class Hook = NoHook>
 __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restrict__ w,
                                         E const* __restrict__ w_next, Stage<E>& st, Lane const& L, Init init,
-                                        Epi epi) {
+                                        Epi epi, Hook hook = Hook()) {
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
   constexpr int TS = (TI + 1) / 2;
@@ -364,6 +397,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
 #pragma unroll
       for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
     }
+    if (ch == HOOK_CH) hook();
     V8 const* __restrict__ sl = st.slots + st.cur * (kSlotFrags * 64) + L.lane;
     // GT output tiles at a time: GT * NT independent accumulation chains.
 #pragma unroll
@@ -395,7 +429,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
             V8 const b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int q = 0; q < GT; q++)
-              if (mo0 + q < TO) acc[q][n] = Vec<E>::mfma(a[q], b, acc[q][n]);
+              if (mo0 + q < TO) acc[q][n] = TR ? Vec<E>::mfma(b, a[q], acc[q][n]) : Vec<E>::mfma(a[q], b, acc[q][n]);
           }
         }
         if (PONNI_SETPRIO) __builtin_amdgcn_s_setprio(0);
@@ -465,6 +499,15 @@ struct SeedRows {
   float const* __restrict__ b;
   int g;
   __device__ floatx4 operator()(int mo) const { return ld4(b + 16 * mo + 4 * g); }
+};
+// Seeds of a transposed tile: feature 16 mo + c in every element.
+struct SeedRowsT {
+  float const* __restrict__ b;
+  int c;
+  __device__ floatx4 operator()(int mo) const {
+    float const v = b[16 * mo + c];
+    return floatx4{v, v, v, v};
+  }
 };
 
 // Final rounding of an epilogue tile to the 16-bit state.

@@ -360,6 +360,46 @@ def test_half_fused_chain_without_dense_layers(cuda, dtype):
             check_half(got, want, 2e-3)
 
 
+HALF_IO_CHAINS = {
+    # one dense layer: next tile's rows requested at the top of the tile;
+    # transposed output of 24 features (a partial feature tile)
+    "one_dense": lambda r: [P.Matvec(r.uniform(-0.3, 0.3, (40, 24))), P.Bias(r.uniform(-0.1, 0.1, 24)),
+                            P.Sigmoid(24)],
+    # two dense layers: the request rides on the last (transposed) layer's chunk
+    "two_dense": lambda r: [P.Matvec(r.uniform(-0.2, 0.2, (64, 48))), P.Bias(r.uniform(-0.1, 0.1, 48)),
+                            P.Tanh(48), P.Matvec(r.uniform(-0.2, 0.2, (48, 10))), P.Bias(r.uniform(-0.1, 0.1, 10))],
+    # three dense layers, c4's shape at small widths
+    "three_dense": lambda r: [P.Matvec(r.uniform(-0.2, 0.2, (32, 64))), P.Bias(r.uniform(-0.1, 0.1, 64)),
+                              P.Tanh(64), P.Matvec(r.uniform(-0.15, 0.15, (64, 64))),
+                              P.Bias(r.uniform(-0.1, 0.1, 64)), P.Tanh(64),
+                              P.Matvec(r.uniform(-0.15, 0.15, (64, 16))), P.Bias(r.uniform(-0.1, 0.1, 16))],
+    # last op not a dense layer: the untransposed store
+    "dense_then_norm": lambda r: [P.Matvec(r.uniform(-0.2, 0.2, (24, 40))), P.Bias(r.uniform(-0.1, 0.1, 40)),
+                                  P.Tanh(40), P.Matvec(r.uniform(-0.2, 0.2, (40, 40))), P.LayerNorm(40)],
+}
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("chain", sorted(HALF_IO_CHAINS))
+def test_half_fused_input_output_paths(cuda, chain, dtype):
+    """16-bit FUSED input and output paths: whole tiles of an aligned x
+    (row stride a multiple of 8) stream through LDS with 16-byte requests,
+    the last tile and misaligned strides load directly; a last dense layer
+    runs transposed and writes 8-byte runs of output rows when y's stride
+    allows, element by element otherwise.  Batches with a partial last tile,
+    aligned and misaligned strides; nothing is written past the batch."""
+    rng = np.random.default_rng(77)
+    layers = HALF_IO_CHAINS[chain](rng)
+    n_in = layers[0].n_in
+    for B in (4099, 20013):
+        x = rng.standard_normal((n_in, B))
+        for pad in ((-B) % 8 + 8, (-B) % 8 + 3):
+            print(f"half io: chain={chain} dtype={dtype} B={B} ld={B + pad}", flush=True)
+            got, xg, m = gpu_run(layers, x, dtype=dtype, path="fused", pad=pad)
+            assert m.path == "fused"
+            check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
