@@ -376,6 +376,18 @@ int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y,
  * -1 for a non-FUSED plan. */
 int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len);
 
+/* C++ text of an F32 / F64 plan's per-sample program: the op list of its
+ * GENERIC lowering, which ponni_plan_device_model / ponni_plan_host_model
+ * describe, as static constexpr members (dtype, num_ops, ops, steps,
+ * tmp_features, saved_features, saved_total) for a struct that
+ * ponni::forward_one_program (ponni_amd/include/ponni/device.h) runs with
+ * each op expanded at compile time.  Generated model headers embed it for
+ * infer_one, the reference emitter's per-model body with planned local
+ * storage (kokkos_nn/emitter.py:1897-1901).  Returns the length including
+ * the terminating NUL (copying it when buf holds at least that many bytes),
+ * or -1 (other dtypes). */
+int64_t ponni_plan_program_source(ponni_plan plan, char* buf, int64_t len);
+
 /* Compile a FUSED plan's kernel with hipRTC now (no device needed; the result
  * is cached in-process and under $PONNI_JIT_CACHE or ~/.cache/ponni_hip) so the
  * first ponni_forward does not pay for it.  A no-op for the other paths.

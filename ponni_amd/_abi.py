@@ -166,6 +166,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_forward_timed.argtypes = [vp, vp, i64, vp, i64, i64, vp, vp, vp]
     L.ponni_plan_kernel_source.restype = i64
     L.ponni_plan_kernel_source.argtypes = [vp, ctypes.c_char_p, i64]
+    L.ponni_plan_program_source.restype = i64
+    L.ponni_plan_program_source.argtypes = [vp, ctypes.c_char_p, i64]
     L.ponni_plan_compile.restype = ctypes.c_int
     L.ponni_plan_compile.argtypes = [vp]
     L.ponni_plan_kernel_config.restype = ctypes.c_int

@@ -7,6 +7,8 @@
 // Each case follows the reference layer it cites.
 #pragma once
 
+#include <utility>
+
 #include "../../include/ponni_hip.h"
 #include "pointwise.h"
 #include "program.h"
@@ -41,13 +43,15 @@ struct NoExternal {
   __host__ __device__ void operator()(int, int, View2 const&, View2 const&, View2 const&, int, int, int64_t) const {}
 };
 
+// One op of a plan's program for sample b.  Inlined into its caller, so a
+// caller that passes an op known at compile time (run_program) gets the op's
+// branch alone, with its sizes and offsets as constants.
 template <class S, class Ext = NoExternal>
-__host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
-                               typename Compute<S>::type const* __restrict__ params,
-                               View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext = Ext()) {
+__host__ __device__ __attribute__((always_inline)) inline void run_op(
+    Op const op, Step const* __restrict__ steps, typename Compute<S>::type const* __restrict__ params,
+    View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext) {
   using C = typename Compute<S>::type;
-  for (int o = 0; o < num_ops; o++) {
-    Op const op = ops[o];
+  {
     View2 const in = buf[op.src];
     View2 const out = buf[op.dst];
     switch (op.code) {
@@ -258,6 +262,31 @@ __host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops,
         break;
     }
   }
+}
+
+// The ops of a plan's program in order, for sample b.
+template <class S, class Ext = NoExternal>
+__host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
+                                        typename Compute<S>::type const* __restrict__ params,
+                                        View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext = Ext()) {
+  for (int o = 0; o < num_ops; o++) run_op<S, Ext>(ops[o], steps, params, buf, b, ext);
+}
+
+// The same for a program known at compile time: Program::ops / ::steps are
+// constexpr arrays (ponni_plan_program_source), each op expanded in place
+// (the op is a constant expression, so its switch and sizes fold).
+template <class S, class Program, int I, class Ext>
+__host__ __device__ __attribute__((always_inline)) inline void run_program_op(
+    typename Compute<S>::type const* __restrict__ params, View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b,
+    Ext const& ext) {
+  constexpr Op op = Program::ops[I];
+  run_op<S, Ext>(op, Program::steps, params, buf, b, ext);
+}
+template <class S, class Program, class Ext, int... I>
+__host__ __device__ inline void run_program(typename Compute<S>::type const* __restrict__ params,
+                                            View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext,
+                                            std::integer_sequence<int, I...>) {
+  (run_program_op<S, Program, I, Ext>(params, buf, b, ext), ...);
 }
 
 }  // namespace ponni_hip

@@ -15,6 +15,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <sstream>
 #include <string>
 
 #include "fused.h"
@@ -966,6 +967,21 @@ namespace ponni_hip {
 int set_error(int status, std::string const& message) { return fail(status, message); }
 }  // namespace ponni_hip
 
+namespace {
+
+// A double as C++ source that reads back to the same value.
+std::string double_literal(double v) {
+  if (std::isnan(v)) return "__builtin_nan(\"\")";
+  if (std::isinf(v)) return v > 0 ? "__builtin_inf()" : "-__builtin_inf()";
+  char b[40];
+  std::snprintf(b, sizeof b, "%.17g", v);
+  std::string t = b;
+  if (t.find_first_of(".eE") == std::string::npos) t += ".0";
+  return t;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* ponni_last_error(void) { return g_last_error.c_str(); }
@@ -1366,6 +1382,57 @@ int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {
   if (buf != nullptr) {
     if (len < need) {
       fail(PONNI_ERR_INVALID_ARGUMENT, "buffer too small for the kernel source");
+      return -1;
+    }
+    std::memcpy(buf, src.c_str(), static_cast<size_t>(need));
+  }
+  return need;
+}
+
+int64_t ponni_plan_program_source(ponni_plan plan, char* buf, int64_t len) {
+  if (plan == nullptr) {
+    fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
+    return -1;
+  }
+  if (plan->dtype != PONNI_F32 && plan->dtype != PONNI_F64) {
+    fail(PONNI_ERR_UNSUPPORTED, "per-sample programs run F32 and F64 plans");
+    return -1;
+  }
+  ponni_plan_s const* t = generic_twin(*plan);
+  if (t == nullptr) {
+    fail(PONNI_ERR_INVALID_ARGUMENT, "out of host memory");
+    return -1;
+  }
+  std::ostringstream o;
+  o << "  static constexpr int dtype = " << t->dtype << ";\n";
+  o << "  static constexpr int num_ops = " << t->ops.size() << ";\n";
+  o << "  static constexpr ponni_hip::Op ops[" << std::max<size_t>(t->ops.size(), 1) << "] = {\n";
+  for (Op const& op : t->ops)
+    o << "      {" << op.code << ", " << op.n_in << ", " << op.n_out << ", " << op.slot << ", " << op.aux << ", "
+      << op.woff << ", " << op.boff << ", " << op.epi_begin << ", " << op.epi_count << ", " << op.src << ", "
+      << op.dst << ", " << double_literal(op.f0) << ", " << double_literal(op.f1) << ", " << double_literal(op.f2)
+      << "},\n";
+  if (t->ops.empty()) o << "      {},\n";
+  o << "  };\n";
+  o << "  static constexpr ponni_hip::Step steps[" << std::max<size_t>(t->steps.size(), 1) << "] = {\n";
+  for (Step const& st : t->steps)
+    o << "      {" << st.act << ", " << st.off << ", " << double_literal(st.a) << ", " << double_literal(st.b) << "},\n";
+  if (t->steps.empty()) o << "      {},\n";
+  o << "  };\n";
+  o << "  static constexpr int tmp_features[2] = {" << t->tmp_features[0] << ", " << t->tmp_features[1] << "};\n";
+  int total = 0;
+  o << "  static constexpr int saved_features[" << kMaxSlots << "] = {";
+  for (int sl = 0; sl < kMaxSlots; sl++) {
+    o << (sl ? ", " : "") << t->saved_features[sl];
+    total += t->saved_features[sl];
+  }
+  o << "};\n";
+  o << "  static constexpr int saved_total = " << total << ";\n";
+  std::string const src = o.str();
+  int64_t const need = static_cast<int64_t>(src.size()) + 1;
+  if (buf != nullptr) {
+    if (len < need) {
+      fail(PONNI_ERR_INVALID_ARGUMENT, "buffer too small for the program source");
       return -1;
     }
     std::memcpy(buf, src.c_str(), static_cast<size_t>(need));

@@ -113,6 +113,7 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
             src = plan.kernel_source()
             kernels[dt] = dict(src=_kernel_text(src), name=_kernel_name(src), threads=threads, cols=cols,
                                persistent=persistent, path=plan.path)
+    program = gm.plan(gm.scalar).program_source()
     includes = set()
     for k in kernels.values():
         includes.add("narrow_jit.h" if k["path"] == "narrow" else None)
@@ -333,16 +334,25 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("                       y.data(), static_cast<std::int64_t>(y.stride(0)), num_outputs * batch, batch);")
     w("  }")
     w("")
+    w("  // The model's per-sample program (the library's GENERIC lowering of it), fixed at")
+    w("  // compile time: infer_one expands every op in place, with thread-private states")
+    w("  // sized to the model (the reference's planned local storage).")
+    w("  struct program {")
+    for line in program.rstrip("\n").split("\n"):
+        w("  " + line)
+    w("  };")
+    w("")
     w("  // One sample inside an application kernel (emitter.py:1897-1901): capture a copy")
-    w("  // of the model by value and call infer_one.  Device code reads the plan's device")
-    w("  // description, which the model carries by value and whose buffers stay in place")
-    w("  // across parameter changes; host code reads the host description the copies share.")
+    w("  // of the model by value and call infer_one.  Device code reads the parameters of")
+    w("  // the plan's device description, which the model carries by value and whose")
+    w("  // buffers stay in place across parameter changes; host code those of the host")
+    w("  // description the copies share.")
     w("  __host__ __device__ void infer_one(ponni::SArray<Scalar, num_inputs> const& in,")
     w("                                    ponni::SArray<Scalar, num_outputs>& out) const {")
     w("#if defined(__HIP_DEVICE_COMPILE__)")
-    w("    ponni::forward_one<Scalar>(device_model_, in.data(), 1, out.data(), 1);")
+    w("    ponni::forward_one_program<Scalar, program>(device_model_.params, in.data(), 1, out.data(), 1);")
     w("#else")
-    w("    ponni::forward_one<Scalar>(state_->host_model, in.data(), 1, out.data(), 1);")
+    w("    ponni::forward_one_program<Scalar, program>(state_->host_model.params, in.data(), 1, out.data(), 1);")
     w("#endif")
     w("  }")
     w("  // A trivially copyable handle for kernels that take plain arguments.")
@@ -350,7 +360,7 @@ def emit_cpp_header(graph: Graph, path: str, namespace: str = "ponni::generated"
     w("    ponni_device_model model;")
     w("    __device__ void infer_one(ponni::SArray<Scalar, num_inputs> const& in,")
     w("                              ponni::SArray<Scalar, num_outputs>& out) const {")
-    w("      ponni::forward_one<Scalar>(model, in.data(), 1, out.data(), 1);")
+    w("      ponni::forward_one_program<Scalar, program>(model.params, in.data(), 1, out.data(), 1);")
     w("    }")
     w("  };")
     w("  Device device() const { return Device{device_model_}; }")

@@ -68,4 +68,35 @@ __host__ __device__ inline void forward_one(ponni_device_model const& m, real co
                            0, ext);
 }
 
+// One sample through a program fixed at compile time: Program holds the
+// plan's GENERIC op list as constexpr members (the text
+// ponni_plan_program_source writes, which generated model headers embed),
+// so every op is expanded in place with its sizes and offsets as constants
+// and the thread-private states are sized to the plan (the reference
+// emitter's per-model infer_one body with planned local storage,
+// kokkos_nn/emitter.py:1897-1901).  params: the parameters of the same
+// plan's ponni_plan_device_model (device code) or ponni_plan_host_model
+// (host code) description; Program::dtype must match `real`.
+template <class real, class Program, class Ext = ponni_hip::NoExternal>
+__host__ __device__ inline void forward_one_program(void const* params, real const* in, int64_t in_ld, real* out,
+                                                    int64_t out_ld, Ext const& ext = Ext()) {
+  static_assert(Program::dtype == (sizeof(real) == 8 ? PONNI_F64 : PONNI_F32), "program dtype and real differ");
+  constexpr int t1 = Program::tmp_features[0] > 0 ? Program::tmp_features[0] : 1;
+  constexpr int t2 = Program::tmp_features[1] > 0 ? Program::tmp_features[1] : 1;
+  constexpr int sv = Program::saved_total > 0 ? Program::saved_total : 1;
+  real tmp1[t1], tmp2[t2], saved[sv];
+  ponni_hip::View2 buf[ponni_hip::BUF_SAVED + ponni_hip::kMaxSlots];
+  buf[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
+  buf[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
+  buf[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp1), 1};
+  buf[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp2), 1};
+  int off = 0;
+  for (int s = 0; s < ponni_hip::kMaxSlots; s++) {
+    buf[ponni_hip::BUF_SAVED + s] = {reinterpret_cast<char*>(saved + off), 1};
+    off += Program::saved_features[s];
+  }
+  ponni_hip::run_program<real, Program, Ext>(static_cast<real const*>(params), buf, 0, ext,
+                                             std::make_integer_sequence<int, Program::num_ops>());
+}
+
 }  // namespace ponni

@@ -236,6 +236,16 @@ class Inference:
         A.lib().ponni_plan_kernel_source(self._plan, buf, n)
         return buf.value.decode()
 
+    def program_source(self) -> str:
+        """constexpr C++ members of the plan's per-sample program (F32 / F64 plans),
+        for ponni::forward_one_program (ponni_plan_program_source)."""
+        n = A.lib().ponni_plan_program_source(self._plan, None, 0)
+        if n < 0:
+            A.check(A.PONNI_ERR_UNSUPPORTED)
+        buf = ctypes.create_string_buffer(n)
+        A.lib().ponni_plan_program_source(self._plan, buf, n)
+        return buf.value.decode()
+
     def kernel_config(self) -> tuple[int, int, bool]:
         """(threads per workgroup, batch columns per workgroup, persistent grid) of the
         generated kernel (FUSED or generated NARROW plans)."""

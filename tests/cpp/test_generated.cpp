@@ -6,9 +6,11 @@
 // the model taken before load_weights, as the reference's test does; and on
 // the host); then read the learned parameters, halve them through a device
 // view, run infer_batch and every infer_one again and save the parameters.
-// tests/test_cpp.py compares every output.
+// tests/test_cpp.py compares every output.  With --host (no GPU needed) only
+// the host infer_one runs: y_host.bin, then y_host_scaled.bin after halving
+// the parameters through set_parameters.
 // Arrays on disk are raw Model::Scalar values (float, or double for F64Model).
-//   test_generated <c5|tiny|f64> <weights.ponni> <x.bin [num_inputs, B]> <B> <out_dir>
+//   test_generated <c5|tiny|f64> <weights.ponni> <x.bin [num_inputs, B]> <B> <out_dir> [--host]
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -51,6 +53,43 @@ static void write_raw(std::string const& path, std::vector<T> const& v) {
   FILE* f = std::fopen(path.c_str(), "wb");
   if (!f || std::fwrite(v.data(), sizeof(T), v.size(), f) != v.size()) ponni::abort("cannot write " + path);
   std::fclose(f);
+}
+
+// infer_one on the host, sample by sample, for x [num_inputs, B] (row stride B).
+template <class Model>
+std::vector<typename Model::Scalar> host_outputs(Model const& m, std::vector<typename Model::Scalar> const& x,
+                                                 int B) {
+  using T = typename Model::Scalar;
+  std::vector<T> out(std::size_t(Model::num_outputs) * B);
+  for (int b = 0; b < B; b++) {
+    ponni::SArray<T, Model::num_inputs> in;
+    ponni::SArray<T, Model::num_outputs> o;
+    for (int f = 0; f < Model::num_inputs; f++) in(f) = x[std::size_t(f) * B + b];
+    m.infer_one(in, o);
+    for (int f = 0; f < Model::num_outputs; f++) out[std::size_t(f) * B + b] = o(f);
+  }
+  return out;
+}
+
+template <class Model>
+int run_host(char const* weights, char const* xpath, int B, std::string const& dir) {
+  using T = typename Model::Scalar;
+  Model m;
+  Model const early = m;  // sees the weights loaded below
+  std::string err;
+  if (!m.load_weights(weights, &err)) {
+    std::fprintf(stderr, "load_weights: %s\n", err.c_str());
+    return 1;
+  }
+  std::vector<T> const xh = read_raw<T>(xpath, std::size_t(Model::num_inputs) * B);
+  write_raw(dir + "/y_host.bin", host_outputs(early, xh, B));
+  std::vector<T> p(Model::get_num_parameters());
+  m.get_parameters(p);
+  for (T& v : p) v *= T(0.5);
+  m.set_parameters(p);
+  write_raw(dir + "/y_host_scaled.bin", host_outputs(early, xh, B));
+  std::printf("test_generated --host: wrote %d samples (%s)\n", B, Model::model_fingerprint().c_str());
+  return 0;
 }
 
 template <class Model>
@@ -99,18 +138,7 @@ int run(char const* weights, char const* xpath, int B, std::string const& dir) {
     hipLaunchKernelGGL(for_each_sample<decltype(body)>, dim3((B + 127) / 128), dim3(128), 0, 0, B, body);
     return hipDeviceSynchronize() == hipSuccess;
   };
-  // infer_one on the host, sample by sample.
-  auto host = [&] {
-    std::vector<T> out(std::size_t(Model::num_outputs) * B);
-    for (int b = 0; b < B; b++) {
-      ponni::SArray<T, Model::num_inputs> in;
-      ponni::SArray<T, Model::num_outputs> o;
-      for (int f = 0; f < Model::num_inputs; f++) in(f) = xh[std::size_t(f) * B + b];
-      early.infer_one(in, o);
-      for (int f = 0; f < Model::num_outputs; f++) out[std::size_t(f) * B + b] = o(f);
-    }
-    return out;
-  };
+  auto host = [&] { return host_outputs(early, xh, B); };
   m.infer_batch(x, y);
   m.infer_batch_half2(x, yh);
   if (!one() || !captured()) return 1;
@@ -143,14 +171,19 @@ int run(char const* weights, char const* xpath, int B, std::string const& dir) {
 }
 
 int main(int argc, char** argv) {
-  if (argc != 6) {
-    std::fprintf(stderr, "usage: %s c5|tiny|f64 weights.ponni x.bin batch out_dir\n", argv[0]);
+  bool const host = argc == 7 && std::strcmp(argv[6], "--host") == 0;
+  if (argc != 6 && !host) {
+    std::fprintf(stderr, "usage: %s c5|tiny|f64 weights.ponni x.bin batch out_dir [--host]\n", argv[0]);
     return 2;
   }
   int const B = std::atoi(argv[4]);
-  if (std::strcmp(argv[1], "c5") == 0) return run<ponni::generated::C5Model>(argv[2], argv[3], B, argv[5]);
-  if (std::strcmp(argv[1], "tiny") == 0) return run<ponni::generated::TinyModel>(argv[2], argv[3], B, argv[5]);
-  if (std::strcmp(argv[1], "f64") == 0) return run<ponni::generated::F64Model>(argv[2], argv[3], B, argv[5]);
+  using namespace ponni::generated;
+  if (std::strcmp(argv[1], "c5") == 0)
+    return host ? run_host<C5Model>(argv[2], argv[3], B, argv[5]) : run<C5Model>(argv[2], argv[3], B, argv[5]);
+  if (std::strcmp(argv[1], "tiny") == 0)
+    return host ? run_host<TinyModel>(argv[2], argv[3], B, argv[5]) : run<TinyModel>(argv[2], argv[3], B, argv[5]);
+  if (std::strcmp(argv[1], "f64") == 0)
+    return host ? run_host<F64Model>(argv[2], argv[3], B, argv[5]) : run<F64Model>(argv[2], argv[3], B, argv[5]);
   std::fprintf(stderr, "unknown model %s\n", argv[1]);
   return 2;
 }

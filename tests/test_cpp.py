@@ -86,19 +86,10 @@ def test_emitted_header_text(tmp_path):
     assert "#include" not in text.split("namespace M5_kernels")[1]
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("model", ["c5", "tiny", "f64"])
-def test_generated_header_on_gpu(cuda, tmp_path, model):
-    """tests/cpp/test_generated.cpp over an emitted header: infer_batch
-    (the ahead-of-time kernel), infer_batch_half2 and infer_one (an
-    application kernel over device(), a kernel lambda holding a copy of the
-    model taken before its weights were loaded -- bit-identical to the
-    device() kernel -- and the host) against the CPU oracle, on a weights
-    file saved by the Python model (c5, f64) or written by the reference
-    generator (tiny, tests/golden/tiny_generated.ponni); then the parameter
-    API (get, set from a device view, save) against the Python model.  fp32
-    bar: relative L2 <= 1e-5 and max-abs <= 1e-4; fp64: 1e-11; fp16: relative
-    L2 <= 2e-3 against fp16 operands."""
+def _generated_case(tmp_path, model):
+    """(graph factory, weights file, x, batch, output reader, oracle layer builder,
+    oracle mode, check) of one emitted-header case: c5 and f64 on weights the
+    Python model saved, tiny on the file the reference generator wrote."""
     import numpy as np
 
     import oracle
@@ -106,7 +97,7 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
     from ponni_amd import graph as G
     from tests.cpp.gen_headers import f64_graph
     from tests.golden.make_generated_fixtures import tiny_graph
-    from tests.test_gpu_parity import check_f32, check_half
+    from tests.test_gpu_parity import check_f32
 
     if not os.path.exists(GEN_BIN):
         pytest.fail(f"{GEN_BIN} is missing: build with `python -c 'import __graft_entry__ as g; g.build()'`")
@@ -126,10 +117,6 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
     B = 4099
     x = np.random.default_rng(12).standard_normal((n_in, B)).astype(dt)
     x.tofile(tmp_path / "x.bin")
-    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.bin"), str(B), str(tmp_path)],
-                       capture_output=True, text=True, timeout=300)
-    print(r.stdout, r.stderr)
-    assert r.returncode == 0, r.stdout + r.stderr
 
     def out(name):
         return np.fromfile(tmp_path / name, dtype=dt).reshape(n_out, B).astype(np.float64)
@@ -148,6 +135,79 @@ def test_generated_header_on_gpu(cuda, tmp_path, model):
             check_f32(got, want, scale_tol=False)
 
     mode = oracle.MODE_F64 if dt == np.float64 else oracle.MODE_F32
+    return make_graph, weights, ref, x, B, dt, out, oracle_layers, mode, check
+
+
+@pytest.mark.parametrize("model", ["c5", "tiny", "f64"])
+def test_generated_header_infer_one_on_host(tmp_path, model):
+    """The emitted header's infer_one on the host (no GPU): the model's
+    per-sample program compiled into the header (ponni_plan_program_source,
+    ponni::forward_one_program), run by a copy of the model taken before its
+    weights were loaded, against the CPU oracle; again after halving the
+    parameters.  fp32: relative L2 <= 1e-5, max-abs <= 1e-4; fp64: 1e-11."""
+    import oracle
+
+    _, weights, ref, x, B, dt, out, oracle_layers, mode, check = _generated_case(tmp_path, model)
+    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.bin"), str(B), str(tmp_path), "--host"],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    check(out("y_host.bin"), oracle.forward(oracle_layers(ref), x.astype("float64"), mode))
+    ref.set_parameters(ref.get_parameters() * 0.5)
+    check(out("y_host_scaled.bin"), oracle.forward(oracle_layers(ref), x.astype("float64"), mode))
+
+
+def test_program_source_is_the_generic_lowering():
+    """ponni_plan_program_source is the plan's GENERIC lowering whatever path
+    the plan runs on (same text, the plan's scratch widths), keeps doubles
+    exact, and refuses 16-bit plans."""
+    import numpy as np
+
+    import ponni_amd as P
+    from ponni_amd import configs as C
+
+    for layers in (C.c2_layers(True), C.c3_layers(True)):
+        m = P.create_inference_model(*layers, dtype="f32")
+        g = P.create_inference_model(*layers, dtype="f32", path="generic")
+        src = m.program_source()
+        assert src == g.program_source()
+        body = src.split("ops[")[1].split("};")[0]
+        n_ops = int(src.split("num_ops = ")[1].split(";")[0])
+        assert n_ops >= len(layers) // 3 and body.count("\n      {") == n_ops
+        inf = g.info()
+        assert f"tmp_features[2] = {{{inf.tmp1_features}, {inf.tmp2_features}}};" in src
+        assert "static constexpr int dtype = 1;" in src
+    ln = P.create_inference_model(P.LayerNorm(np.ones(3), np.zeros(3), 1.0 / 3.0), dtype="f64")
+    assert repr(1.0 / 3.0) in ln.program_source() or "0.33333333333333331" in ln.program_source()
+    with pytest.raises(P.PonniError):
+        P.create_inference_model(*C.c4_layers(), dtype="f16").program_source()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model", ["c5", "tiny", "f64"])
+def test_generated_header_on_gpu(cuda, tmp_path, model):
+    """tests/cpp/test_generated.cpp over an emitted header: infer_batch
+    (the ahead-of-time kernel), infer_batch_half2 and infer_one (an
+    application kernel over device(), a kernel lambda holding a copy of the
+    model taken before its weights were loaded -- bit-identical to the
+    device() kernel -- and the host) against the CPU oracle, on a weights
+    file saved by the Python model (c5, f64) or written by the reference
+    generator (tiny, tests/golden/tiny_generated.ponni); then the parameter
+    API (get, set from a device view, save) against the Python model.  fp32
+    bar: relative L2 <= 1e-5 and max-abs <= 1e-4; fp64: 1e-11; fp16: relative
+    L2 <= 2e-3 against fp16 operands."""
+    import numpy as np
+
+    import oracle
+    from ponni_amd import graph as G
+    from tests.test_gpu_parity import check_half
+
+    make_graph, weights, ref, x, B, dt, out, oracle_layers, mode, check = _generated_case(tmp_path, model)
+    r = subprocess.run([GEN_BIN, model, str(weights), str(tmp_path / "x.bin"), str(B), str(tmp_path)],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+
     want = oracle.forward(oracle_layers(ref), x.astype(np.float64), mode)
     check(out("y_batch.bin"), want)
     check(out("y_one.bin"), want)
