@@ -476,7 +476,9 @@ def test_half_fused_input_output_paths(cuda, chain, dtype):
     rng = np.random.default_rng(77)
     layers = HALF_IO_CHAINS[chain](rng)
     n_in = layers[0].n_in
-    for B in (4099, 20013):
+    # 200,003 columns: every workgroup of the persistent grid loops over
+    # several tiles, so the next tile's rows are requested during this one.
+    for B in (4099, 20013, 200_003):
         x = rng.standard_normal((n_in, B))
         for pad in ((-B) % 8 + 8, (-B) % 8 + 3):
             print(f"half io: chain={chain} dtype={dtype} B={B} ld={B + pad}", flush=True)
@@ -524,8 +526,9 @@ def test_random_chains_reduced_precision_fused(cuda, dtype, seed):
     width = [24, 40, 64, 96][seed]
     layers = K.random_chain(rng, width, 2 + seed % 3)
     x = rng.standard_normal((width, 777))
-    got, xg, _ = gpu_run(layers, x, dtype=dtype, path="fused", pad=2)
-    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
+    for pad in (2, 7):  # row strides 779 (direct input loads) and 784 (input through LDS)
+        got, xg, _ = gpu_run(layers, x, dtype=dtype, path="fused", pad=pad)
+        check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
