@@ -419,11 +419,6 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v == 0 || v == 1) o << "#define PONNI_FULL_SLOT_CHUNKS " << v << "\n";
   }
-  if (char const* d = std::getenv("PONNI_RING_DEPTH")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v >= 1 && v <= 32) o << "#define PONNI_RING_DEPTH " << v << "\n";
-  }
-  if (half && std::getenv("PONNI_HALF_TILE_BARRIER")) o << "#define PONNI_TILE_BARRIER 1\n";  // tuning override
   if (dbl) o << "#define PONNI_REAL double\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
@@ -447,9 +442,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   std::vector<DenseRef> dense_seq;
   for (Op const& op : p.ops)
     if (op.code == OP_DENSE) dense_seq.push_back(DenseRef{op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
-  // (tuning override PONNI_HALF_STAGE=0: A fragments straight from L1/L2 per wave)
-  bool const half_staged = !(std::getenv("PONNI_HALF_STAGE") && std::strcmp(std::getenv("PONNI_HALF_STAGE"), "0") == 0);
-  if (half && half_staged && !dense_seq.empty()) {
+  if (half && !dense_seq.empty()) {
     o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
     o << "  Stage<E> st{a_slots, 0};\n";
     o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", "
@@ -513,14 +506,14 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   // for weight chunks (vmcnt counts in issue order) then never wait for
   // them, the next one a chunk later.  With one dense layer: after this
   // tile's rows are read.
-  int const hook_dense = half && half_staged && in_dma && dense_seq.size() >= 2 ? 1 : -1;
+  int const hook_dense = half && in_dma && dense_seq.size() >= 2 ? 1 : -1;
   std::string const prefetch_next = "if (pre_next) prefetch_rows_lds16<" + std::to_string(n_in0) + ", " +
                                     std::to_string(NT) + ">(x, ldx, Ln, in_buf[wave_id()]);";
   // The last op, a dense layer whose epilogue is its bias (the seed) and
   // activations without parameters, runs transposed and writes 8-byte runs
   // of output rows (fused_f16.h store_rows_ht).
   bool out_transposed = false;
-  if (half && half_staged && !p.ops.empty() && p.ops.back().code == OP_DENSE) {
+  if (half && !p.ops.empty() && p.ops.back().code == OP_DENSE) {
     Op const& op = p.ops.back();
     bool const lead = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
     out_transposed = true;
@@ -609,12 +602,7 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         // 16-bit rounding, and the add then costs no VALU op).
         bool const lead_bias = op.epi_count > 0 && p.steps[op.epi_begin].act == ACT_BIAS;
         bool const seed = lead_bias && (half || (op.aux & DENSE_BIAS_FIRST));
-        if (half && !half_staged) {
-          std::string const init = seed ? "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}" : "SeedZero{}";
-          o << "    auto " << nv << " = dense_h<" << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur
-            << ", reinterpret_cast<E const*>(P + " << op.woff << "), L, " << init << ", [&](int mo, floatx4 (&t)["
-            << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
-        } else if (half) {
+        if (half) {
           bool const tr = out_transposed && &op == &p.ops.back();
           bool const hook = static_cast<int>(dense_index) == hook_dense;
           std::string const init = !seed ? "SeedZero{}"

@@ -50,10 +50,6 @@ __device__ inline floatx4 widen4(typename Vec<E>::x4 v) {
   return __builtin_convertvector(v, floatx4);
 }
 
-#ifndef PONNI_RING_DEPTH
-#define PONNI_RING_DEPTH 4
-#endif
-
 // The lane's element pointer for row 4g, column col0 + c, opaque to the
 // compiler so that every row is one 64-bit add of a uniform (SGPR) offset.
 template <class E>
@@ -211,56 +207,6 @@ __device__ inline H<T, NT, E> to_h(S<T, NT> const& s) {
   return h;
 }
 
-// Dense layer on fp16/bf16 MFMA; returns the 16-bit output state.
-// init(mo) seeds output tile mo's fp32 accumulator (zero, or a bias that
-// then costs no VALU add); epi(mo, t, o) finishes tile mo: its remaining
-// epilogue steps in fp32 on t, then the 16-bit result into o.  The epilogue
-// of tile mo-1 runs after the MFMAs of tile mo; A fragments stream through an
-// R-deep ring (1 KB per fragment: 16 B per lane).
-template <int TI, int TO, int NT, class E, class Init, class Epi, int D = PONNI_RING_DEPTH>
-__device__ inline H<TO, NT, E> dense_h(H<TI, NT, E> const& in, E const* __restrict__ w, Lane const& L, Init init,
-                                       Epi epi) {
-  using V8 = typename Vec<E>::x8;
-  using V4 = typename Vec<E>::x4;
-  constexpr int TS = (TI + 1) / 2;
-  constexpr int NF = TS * TO;
-  constexpr int R = D < NF ? D : NF;
-  H<TO, NT, E> out;
-  V8 ring[R];
-#pragma unroll
-  for (int i = 0; i < R; i++) ring[i] = *reinterpret_cast<V8 const*>(w + i * 512 + L.lane * 8);
-  floatx4 prev[NT];
-#pragma unroll
-  for (int mo = 0; mo < TO; mo++) {
-#ifdef PONNI_TILE_BARRIER
-    // Keep the workgroup's waves on the same output tile so their identical
-    // A-fragment reads hit in L1 after the first wave's miss.
-    __syncthreads();
-#endif
-    floatx4 acc[NT];
-    floatx4 const seed = init(mo);
-#pragma unroll
-    for (int n = 0; n < NT; n++) acc[n] = seed;
-#pragma unroll
-    for (int t = 0; t < TS; t++) {
-      int const i = mo * TS + t;
-      V8 const a = ring[i % R];
-      if (i + R < NF) ring[i % R] = *reinterpret_cast<V8 const*>(w + (i + R) * 512 + L.lane * 8);
-#pragma unroll
-      for (int n = 0; n < NT; n++) {
-        V4 const lo = in.v[2 * t][n];
-        V4 const hi = (2 * t + 1 < TI) ? in.v[(2 * t + 1 < TI) ? 2 * t + 1 : 2 * t][n] : V4{E(0.0f), E(0.0f), E(0.0f), E(0.0f)};
-        V8 const b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[n] = Vec<E>::mfma(a, b, acc[n]);
-      }
-    }
-    if (mo > 0) epi(mo - 1, prev, out.v[mo - 1]);
-#pragma unroll
-    for (int n = 0; n < NT; n++) prev[n] = acc[n];
-  }
-  epi(TO - 1, prev, out.v[TO - 1]);
-  return out;
-}
 
 // ---- A fragments staged through LDS -------------------------------------
 // The workgroup's waves share the A fragments of CT consecutive output tiles
@@ -341,10 +287,13 @@ struct NoHook {
   __device__ void operator()() const {}
 };
 
-// Dense layer with LDS-staged A fragments.  On entry slot st.cur holds this
-// layer's first chunk; on exit it holds the first chunk of `w_next`, the next
-// dense layer (TSN fragments per tile, TON output tiles).  init / epi as in
-// dense_h.  TR runs the MFMAs with their operands swapped (the transposed
+// Dense layer on fp16/bf16 MFMA with LDS-staged A fragments; returns the
+// 16-bit output state.  init(mo) seeds output tile mo's fp32 accumulator
+// (zero, or a bias that then costs no VALU add); epi(mo, t, o) finishes tile
+// mo: its remaining epilogue steps in fp32 on t, then the 16-bit result into
+// o.  On entry slot st.cur holds this layer's first chunk; on exit it holds
+// the first chunk of `w_next`, the next dense layer (TSN fragments per tile,
+// TON output tiles).  TR runs the MFMAs with their operands swapped (the transposed
 // product, same fragments): the output tile is then transposed (feature
 // 16m + c, column 16n + 4g + e; store_rows_ht), which only a layer whose
 // output goes straight to memory can use, seeded with SeedRowsT.  hook()
@@ -491,7 +440,7 @@ __device__ inline void stage_first(Stage<E>& st, E const* __restrict__ w) {
   st.cur = 0;
 }
 
-// Accumulator seeds for dense_h: zero, or the per-feature vector b.
+// Accumulator seeds for dense_hs: zero, or the per-feature vector b.
 struct SeedZero {
   __device__ floatx4 operator()(int) const { return floatx4{0.0f, 0.0f, 0.0f, 0.0f}; }
 };
