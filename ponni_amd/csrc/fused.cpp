@@ -279,7 +279,22 @@ std::string fused_kernel_name(ponni_plan_s const& p) {
 
 std::string narrow_source_of(ponni_plan_s const& p, FusedConfig& cfg);
 
+namespace {
+std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allow_vec_staging);
+}  // namespace
+
+// A staged 16-bit plan whose per-feature vectors would not fit next to the
+// staging slots and input rows keeps them in global memory (L2).
 std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
+  FusedConfig first = cfg;
+  std::string src = fused_source_once(p, first, true);
+  if (first.lds_total > kFusedLdsBytes && first.vec_bytes > 0) return fused_source_once(p, cfg, false);
+  cfg = first;
+  return src;
+}
+
+namespace {
+std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allow_vec_staging) {
   if (p.path == PONNI_PATH_NARROW) return narrow_source_of(p, cfg);
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
   bool const dbl = p.dtype == PONNI_F64;  // fp64 tiles (v_mfma_f64_16x16x4f64)
@@ -396,14 +411,6 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     int const v = std::atoi(d);
     if (v == 0 || v == 1) o << "#define PONNI_DEFER_EPILOGUE " << v << "\n";
   }
-  if (char const* d = std::getenv("PONNI_LDS_RING")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v >= 1 && v <= 8) o << "#define PONNI_LDS_RING " << v << "\n";
-  }
-  if (char const* d = std::getenv("PONNI_CHUNK_TILES")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v >= 1 && v <= 8) o << "#define PONNI_CHUNK_TILES " << v << "\n";
-  }
   // fp32 plans whose parameters sit in LDS or registers keep each dense
   // tile's epilogue among the next tile's MFMAs (fused_f32.h dense_ep; c2
   // and c5 2.8 / 3.5 % faster).  Plans streaming parameters from L2 keep the
@@ -415,10 +422,6 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     if (v >= 0 && v <= 16) epi_interleave = v;
   }
 
-  if (char const* d = std::getenv("PONNI_FULL_SLOT_CHUNKS")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v == 0 || v == 1) o << "#define PONNI_FULL_SLOT_CHUNKS " << v << "\n";
-  }
   if (dbl) o << "#define PONNI_REAL double\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
@@ -434,20 +437,29 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   } else {
     o << "  " << F << " const* __restrict__ P0 = gparams;\n";
   }
-  // 16-bit plans: dense layers in program order (weights, 32-feature steps);
-  // the last one's successor is the first (the next tile of the loop).
+  // 16-bit plans: dense layers in program order, and the chunks their A
+  // fragments are staged in (fused_f16.h Stage): per layer, as many output
+  // tiles per chunk as fill a 32-fragment slot, the last chunk partial.
   struct DenseRef {
     int woff, ts, to;
   };
   std::vector<DenseRef> dense_seq;
   for (Op const& op : p.ops)
     if (op.code == OP_DENSE) dense_seq.push_back(DenseRef{op.woff, (tiles(op.n_in) + 1) / 2, tiles(op.n_out)});
+  int const slot_frags = 32, slots = 3;
   if (half && !dense_seq.empty()) {
-    o << "  __shared__ Vec<E>::x8 a_slots[2 * kSlotFrags * 64];\n";
-    o << "  Stage<E> st{a_slots, 0};\n";
-    o << "  stage_first<" << dense_seq[0].ts << ", " << dense_seq[0].to << ", "
-      << cfg.waves << ">(st, reinterpret_cast<E const*>(gparams + " << dense_seq[0].woff << "));\n";
-    o << "  __syncthreads();\n";
+    std::ostringstream tab;
+    int chunks = 0;
+    for (DenseRef const& d : dense_seq) {
+      int const ct = slot_frags / d.ts;
+      for (int t0 = 0; t0 < d.to; t0 += ct, chunks++)
+        tab << (chunks ? ", " : "") << d.woff + t0 * d.ts * 256 << ", " << std::min(ct, d.to - t0) * d.ts;
+    }
+    o << "  __shared__ Vec<E>::x8 a_slots[kSlots * kSlotFrags * 64];\n";
+    o << "  static constexpr int chunk_tab[" << 2 * chunks << "] = {" << tab.str() << "};\n";
+    o << "  Stage<E> st{a_slots, reinterpret_cast<E const*>(gparams), chunk_tab, " << chunks << ", 0};\n";
+    o << "  stage_begin<" << cfg.waves << ">(st);\n";
+    cfg.persistent_loop = true;
   }
   size_t dense_index = 0;
   std::map<int, int> slot_off;  // slot -> 4-vector offset in the wave's LDS region
@@ -467,9 +479,9 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   // fragments (a late global load would wait behind them: vmcnt is in order).
   // (Measured: c4 unchanged, c3 slower as a persistent fp32 kernel, so only
   // 16-bit plans, which are persistent anyway, stage them by default.)
-  bool stage_vecs = half && cfg.lds_bytes == 0 && !cfg.params_in_registers;
+  bool stage_vecs = allow_vec_staging && half && cfg.lds_bytes == 0 && !cfg.params_in_registers;
   if (char const* v = std::getenv("PONNI_STAGE_VECS"))  // tuning override
-    stage_vecs = std::strcmp(v, "1") == 0 && cfg.lds_bytes == 0 && !cfg.params_in_registers;
+    stage_vecs = allow_vec_staging && std::strcmp(v, "1") == 0 && cfg.lds_bytes == 0 && !cfg.params_in_registers;
   std::map<int, std::pair<int, int>> vec_lds;  // packed offset -> (LDS offset, length)
   int vec_total = 0;
   auto vec = [&](int off, int n) -> std::string {
@@ -491,13 +503,12 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
   o << "  int64_t const tiles = (batch + " << cfg.columns_per_block - 1 << ") / " << cfg.columns_per_block << ";\n";
   // 16-bit plans request each tile's input rows into LDS one tile ahead
   // (fused_f16.h prefetch_rows_lds16) when the buffer fits next to the staged
-  // A fragments (2 slots x 8 fragments x PONNI_CHUNK_TILES KB) and vectors.
+  // A fragments (3 slots of 32 KB) and vectors.
   int const n_in0 = p.layers.front().n_in;
   int const in_rows_elems = tiles(n_in0) * 16 * 16 * NT;  // per wave, row-major 16-bit
   int const in_dma_bytes = cfg.waves * in_rows_elems * 2;
-  int chunk_tiles = 4;
-  if (char const* d = std::getenv("PONNI_CHUNK_TILES")) chunk_tiles = std::max(1, std::min(8, std::atoi(d)));
-  bool in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + 2 * 8 * 1024 * chunk_tiles + 16 * 1024 <= 160 * 1024;
+  int const stage_bytes = half && !dense_seq.empty() ? slots * slot_frags * 1024 : 0;
+  bool in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + stage_bytes + 16 * 1024 <= kFusedLdsBytes;
   if (char const* v = std::getenv("PONNI_INPUT_DMA"))  // tuning override
     in_dma = in_dma && std::strcmp(v, "0") != 0;
   std::string const WCOLS = std::to_string(16 * NT), NW = std::to_string(cfg.waves);
@@ -608,13 +619,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
           std::string const init = !seed ? "SeedZero{}"
                                    : tr  ? "SeedRowsT{" + vec(p.steps[op.epi_begin].off, n) + ", L.c}"
                                          : "SeedRows{" + vec(p.steps[op.epi_begin].off, n) + ", L.g}";
-          auto const& next = dense_seq[(dense_index + 1) % dense_seq.size()];
           dense_index++;
           o << "    auto " << nv << " = dense_hs<" << tiles(op.n_in) << ", " << tiles(n) << ", " << NT << ", "
-            << cfg.waves << ", " << next.ts << ", " << next.to << (tr || hook ? tr ? ", true" : ", false" : "")
-            << (hook ? ", 0" : "") << ">(" << cur << ", reinterpret_cast<E const*>(P + "
-            << op.woff << "), reinterpret_cast<E const*>(P + " << next.woff << "), st, L, " << init
-            << ", [&](int mo, floatx4 (&t)[" << NT << "], Vec<E>::x4 (&o)[" << NT << "]) {\n";
+            << cfg.waves << (tr || hook ? tr ? ", true" : ", false" : "") << (hook ? ", 0" : "") << ">(" << cur
+            << ", st, L, " << init << ", [&](int mo, floatx4 (&t)[" << NT << "], Vec<E>::x4 (&o)[" << NT
+            << "]) {\n";
           if (hook) dense_hook = "    }, [&] { " + prefetch_next + " });\n";
           if (tr) pad_ok = false;
         } else {
@@ -808,7 +817,11 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
         break;
     }
   }
-  if (half && in_dma) o << "    wait_vmem();\n";
+  // Before the output stores: the input rows requested for the next tile
+  // have landed (with staging, every request but the last chunk's is done,
+  // and the rows were requested before it).
+  if (half && in_dma)
+    o << (stage_bytes > 0 ? "    wait_vmem_n<chunk_requests<" + NW + ">()>();\n" : std::string("    wait_vmem();\n"));
   if (out_transposed) o << "    store_rows_ht<" << cur_n << ">(" << cur << ", y, ldy, L, yvec);\n";
   else if (half) o << "    store_rows_h<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
   else o << "    store_rows<" << cur_n << ">(" << cur << ", y, ldy, L);\n";
@@ -822,8 +835,10 @@ std::string fused_source(ponni_plan_s const& p, FusedConfig& cfg) {
     head << "  float const* __restrict__ VP = reinterpret_cast<float const*>(lds_vec);\n";
   }
   cfg.vec_bytes = vec_total * 4;
+  cfg.lds_total = stage_bytes + (in_dma ? in_dma_bytes : 0) + cfg.vec_bytes + static_cast<int>(cfg.lds_bytes);
   return head.str() + o.str();
 }
+}  // namespace
 
 // ---- generated NARROW kernels ---------------------------------------------
 // A narrow chain (every width <= 16) as straight-line code over
@@ -1163,7 +1178,7 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   }
   p.fused_fn = it->second->fn;
   p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
-  p.fused_persistent = cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers;
+  p.fused_persistent = cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers || cfg.persistent_loop;
   p.fused_columns_per_block = cfg.columns_per_block;
   p.fused_waves = cfg.waves;
   return PONNI_OK;

@@ -11,6 +11,8 @@ namespace ponni_hip {
 // Packed parameter blocks up to this size are staged in LDS by the kernel.
 constexpr int64_t kFusedLdsParamBytes = 64 * 1024;
 constexpr int kNTColumns = 32;
+// LDS of one workgroup on gfx950.
+constexpr int kFusedLdsBytes = 160 * 1024;
 
 struct FusedConfig {
   int lds_bytes = 0;          // 0: parameters stream from L2
@@ -19,7 +21,9 @@ struct FusedConfig {
   int waves_per_simd = 2;     // occupancy the kernel is compiled for
   bool params_in_registers = false;  // parameters loaded once per wave, kept in VGPRs
   bool saved_in_lds = false;         // Save_State slots kept in LDS, not registers
+  bool persistent_loop = false;      // staged 16-bit plans: one workgroup per CU loops over tiles
   int columns_per_block = 128;
+  int lds_total = 0;                 // bytes of LDS the kernel declares
 };
 
 bool fused_supports(ponni_plan_s const& p);

@@ -209,79 +209,81 @@ __device__ inline H<T, NT, E> to_h(S<T, NT> const& s) {
 
 
 // ---- A fragments staged through LDS -------------------------------------
-// The workgroup's waves share the A fragments of CT consecutive output tiles
-// (a "chunk": CT * TS 1 KB fragments, contiguous in the packed parameters, as
-// many tiles as fill a slot) in one of two LDS slots.  While a chunk is computed from slot
-// `cur`, every wave loads its share of the next chunk (the next CT tiles of
-// the layer, or the first chunk of the next dense layer) into registers and
-// writes it to the other slot; a workgroup barrier ends the chunk.  Each
-// fragment is read once from L2 per workgroup instead of once per wave, and
-// the next chunk's load has a whole chunk of MFMA work to arrive in.
-#ifndef PONNI_CHUNK_TILES
-#define PONNI_CHUNK_TILES 4
-#endif
-constexpr int kChunkTiles = PONNI_CHUNK_TILES;
-constexpr int kSlotFrags = 8 * kChunkTiles;  // fragments per slot (256 input features)
-#ifndef PONNI_LDS_RING
-#define PONNI_LDS_RING 2
-#endif
+// The workgroup's waves share the A fragments of as many consecutive output
+// tiles of a dense layer as fill a 32 KB slot (a "chunk"; 4 tiles of a
+// 256-input layer, 16 of a 64-input one).  A plan's chunks, in the order
+// its dense layers run them, form a cyclic table (chunk_tab: the chunk's
+// parameter offset in floats and its fragment count); chunk k is computed
+// from slot k % 3 while chunks k + 1 and k + 2 are in flight to the other
+// two: at the start of chunk k every wave requests its share of chunk k + 2
+// with global_load_lds_dwordx4 (16 B per lane straight into LDS, no
+// registers), and at its end waits until only those requests are
+// outstanding (vmcnt counts in issue order, so chunk k + 1, requested a
+// chunk earlier, has landed), then a workgroup barrier.  Each fragment is
+// read from L2 once per workgroup instead of once per wave, and a request
+// has two chunks of work to arrive in.
+constexpr int kSlotFrags = 32;  // 1 KB fragments per slot
+constexpr int kSlots = 3;
+
+template <class E>
+struct Stage {
+  typename Vec<E>::x8* __restrict__ slots;  // LDS: kSlots x kSlotFrags x 64 lanes
+  E const* __restrict__ params;
+  int const* __restrict__ tab;  // chunk c: tab[2c] float offset, tab[2c + 1] fragments
+  int n;                        // chunks per tile
+  int k;                        // chunk being computed
+};
+
+// Requests per wave and chunk: the same for every chunk (partial chunks
+// repeat their last fragment), so a constant vmcnt covers exactly one chunk.
+template <int WAVES>
+constexpr int chunk_requests() {
+  return (kSlotFrags + WAVES - 1) / WAVES;
+}
+
+template <int WAVES, class E>
+__device__ inline void request_chunk(Stage<E> const& st, int kk, int wave, int lane) {
+  static_assert(kSlotFrags % WAVES == 0, "every wave makes the same number of requests");
+  int const c = kk % st.n;
+  E const* __restrict__ src = st.params + 2 * st.tab[2 * c];
+  int const nf = st.tab[2 * c + 1];
+  int const slot = kk % kSlots;
+#pragma unroll
+  for (int r = 0; r < chunk_requests<WAVES>(); r++) {
+    int const f = wave + WAVES * r;
+    int const fs = f < nf ? f : nf - 1;  // (a repeat lands in an unused fragment of the slot)
+    __builtin_amdgcn_global_load_lds(static_cast<void const*>(src + fs * 512 + lane * 8),
+                                     (lds_ptr)(st.slots + (slot * kSlotFrags + f) * 64), 16, 0, 0);
+  }
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ inline void wait_vmem_n() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// Kernel prologue: chunks 0 and 1 requested, landed, visible.
+template <int WAVES, class E>
+__device__ inline void stage_begin(Stage<E>& st) {
+  int const wave = wave_id(), lane = threadIdx.x & 63;
+  st.k = 0;
+  request_chunk<WAVES>(st, 0, wave, lane);
+  request_chunk<WAVES>(st, 1, wave, lane);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+}
+
 #ifndef PONNI_SETPRIO
 #define PONNI_SETPRIO 1
 #endif
 #ifndef PONNI_TILE_GROUP
 #define PONNI_TILE_GROUP 2
 #endif
-
 #ifndef PONNI_DEFER_EPILOGUE
 #define PONNI_DEFER_EPILOGUE 1
 #endif
-
-template <class E>
-struct Stage {
-  typename Vec<E>::x8* __restrict__ slots;  // LDS: 2 x kSlotFrags x 64 lanes
-  int cur;
-};
-
-// The NF fragments of a chunk this wave loads: f = wave + WAVES k.
-template <int NF, int WAVES, class E>
-struct ChunkRegs {
-  static constexpr int K = (NF + WAVES - 1) / WAVES;
-  typename Vec<E>::x8 v[K > 0 ? K : 1];
-};
-
-template <int NF, int WAVES, class E>
-__device__ inline ChunkRegs<NF, WAVES, E> chunk_load(E const* __restrict__ chunk, int wave, int lane) {
-  ChunkRegs<NF, WAVES, E> r;
-#pragma unroll
-  for (int k = 0; k < r.K; k++) {
-    int const f = wave + WAVES * k;
-    // (compile-time true when every wave has a k-th fragment: no branch)
-    if (NF >= WAVES * (k + 1) || f < NF)
-      r.v[k] = *reinterpret_cast<typename Vec<E>::x8 const*>(chunk + f * 512 + lane * 8);
-  }
-  return r;
-}
-
-template <int NF, int WAVES, class E>
-__device__ inline void chunk_store(ChunkRegs<NF, WAVES, E> const& r, Stage<E> const& st, int slot, int wave,
-                                   int lane) {
-#pragma unroll
-  for (int k = 0; k < r.K; k++) {
-    int const f = wave + WAVES * k;
-    if (NF >= WAVES * (k + 1) || f < NF) st.slots[(slot * kSlotFrags + f) * 64 + lane] = r.v[k];
-  }
-}
-
-constexpr int cmin(int a, int b) { return a < b ? a : b; }
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
-
-// Output tiles per chunk for a layer of TS 32-feature steps: a full slot
-// (a layer of 64 input features takes 16 tiles per chunk, so 4x fewer
-// barriers than 256), or kChunkTiles with PONNI_FULL_SLOT_CHUNKS=0.
-#ifndef PONNI_FULL_SLOT_CHUNKS
-#define PONNI_FULL_SLOT_CHUNKS 1
-#endif
-constexpr int ct16(int ts) { return PONNI_FULL_SLOT_CHUNKS ? kSlotFrags / ts : kChunkTiles; }
 
 struct NoHook {
   __device__ void operator()() const {}
@@ -291,27 +293,24 @@ struct NoHook {
 // 16-bit output state.  init(mo) seeds output tile mo's fp32 accumulator
 // (zero, or a bias that then costs no VALU add); epi(mo, t, o) finishes tile
 // mo: its remaining epilogue steps in fp32 on t, then the 16-bit result into
-// o.  On entry slot st.cur holds this layer's first chunk; on exit it holds
-// the first chunk of `w_next`, the next dense layer (TSN fragments per tile,
-// TON output tiles).  TR runs the MFMAs with their operands swapped (the transposed
-// product, same fragments): the output tile is then transposed (feature
-// 16m + c, column 16n + 4g + e; store_rows_ht), which only a layer whose
-// output goes straight to memory can use, seeded with SeedRowsT.  hook()
-// runs once, in chunk HOOK_CH right after that chunk's global loads are
-// issued, so memory requests it makes queue behind them: a later wait for
-// the chunk's loads (vmcnt counts in issue order) does not wait for them.
-template <int TI, int TO, int NT, int WAVES, int TSN, int TON, bool TR = false, int HOOK_CH = -1, class E,
-          class Init, class Epi, class Hook = NoHook>
-__device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restrict__ w,
-                                        E const* __restrict__ w_next, Stage<E>& st, Lane const& L, Init init,
-                                        Epi epi, Hook hook = Hook()) {
+// o.  The layer's chunks are st.k, st.k + 1, ... (the chunk table lists them
+// in this order).  TR runs the MFMAs with their operands swapped (the
+// transposed product, same fragments): the output tile is then transposed
+// (feature 16m + c, column 16n + 4g + e; store_rows_ht), which only a layer
+// whose output goes straight to memory can use, seeded with SeedRowsT.
+// hook() runs once, at the start of chunk HOOK_CH before the chunk's
+// request, so the memory requests it makes have landed when that chunk
+// ends.
+template <int TI, int TO, int NT, int WAVES, bool TR = false, int HOOK_CH = -1, class E, class Init, class Epi,
+          class Hook = NoHook>
+__device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, Stage<E>& st, Lane const& L, Init init, Epi epi,
+                                        Hook hook = Hook()) {
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
   constexpr int TS = (TI + 1) / 2;
-  constexpr int CT = ct16(TS);
+  static_assert(TS <= 8, "at most 256 input features");
+  constexpr int CT = kSlotFrags / TS;  // output tiles per chunk
   constexpr int NCH = (TO + CT - 1) / CT;
-  constexpr int NFN = cmin(ct16(TSN), TON) * TSN;  // fragments of the next layer's first chunk
-  static_assert(TS <= 8 && TSN <= 8, "at most 256 input features");
   // Tiles per group: GT must divide CT and TO (else one at a time); DEFER
   // runs a group's epilogue after the next group's MFMAs.
   constexpr int GT = (CT % PONNI_TILE_GROUP == 0 && TO % PONNI_TILE_GROUP == 0) ? PONNI_TILE_GROUP : 1;
@@ -322,32 +321,9 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
 #pragma unroll
   for (int ch = 0; ch < NCH; ch++) {
     int const t0 = ch * CT;
-    bool const last = ch + 1 == NCH;
-    // Next chunk: the next CT tiles of this layer, or the next layer's first chunk.
-    int const nt_next = last ? 0 : cmin(CT, TO - t0 - CT);
-    constexpr int NFX = cmax(CT * TS, NFN);
-    ChunkRegs<NFX, WAVES, E> nx;
-    if (!last) {
-      E const* __restrict__ src = w + (t0 + CT) * TS * 512;
-      if (nt_next == CT) {
-        auto const r = chunk_load<CT * TS, WAVES>(src, wave, L.lane);
-#pragma unroll
-        for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
-      } else {
-        // Partial chunk (the layer's last): only its own fragments.
-#pragma unroll
-        for (int k = 0; k < ChunkRegs<CT * TS, WAVES, E>::K; k++) {
-          int const f = wave + WAVES * k;
-          if (f < nt_next * TS) nx.v[k] = *reinterpret_cast<V8 const*>(src + f * 512 + L.lane * 8);
-        }
-      }
-    } else {
-      auto const r = chunk_load<NFN, WAVES>(w_next, wave, L.lane);
-#pragma unroll
-      for (int k = 0; k < r.K; k++) nx.v[k] = r.v[k];
-    }
     if (ch == HOOK_CH) hook();
-    V8 const* __restrict__ sl = st.slots + st.cur * (kSlotFrags * 64) + L.lane;
+    request_chunk<WAVES>(st, st.k + 2, wave, L.lane);
+    V8 const* __restrict__ sl = st.slots + (st.k % kSlots) * (kSlotFrags * 64) + L.lane;
     // GT output tiles at a time: GT * NT independent accumulation chains.
 #pragma unroll
     for (int tt = 0; tt < CT; tt += GT) {
@@ -398,46 +374,17 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, E const* __restr
         }
       }
     }
-    // Slot cur ^ 1 was last read before the previous barrier.
-    if (!last) {
-      if (nt_next == CT) {
-        ChunkRegs<CT * TS, WAVES, E> r;
-#pragma unroll
-        for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
-        chunk_store<CT * TS, WAVES>(r, st, st.cur ^ 1, wave, L.lane);
-      } else {
-        // Partial chunk: store only its fragments (compile-time count after unrolling).
-        ChunkRegs<CT * TS, WAVES, E> r;
-#pragma unroll
-        for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
-#pragma unroll
-        for (int k = 0; k < r.K; k++) {
-          int const f = wave + WAVES * k;
-          if (f < nt_next * TS) st.slots[((st.cur ^ 1) * kSlotFrags + f) * 64 + L.lane] = r.v[k];
-        }
-      }
-    } else {
-      ChunkRegs<NFN, WAVES, E> r;
-#pragma unroll
-      for (int k = 0; k < r.K; k++) r.v[k] = nx.v[k];
-      chunk_store<NFN, WAVES>(r, st, st.cur ^ 1, wave, L.lane);
-    }
+    // Chunk k + 1 has landed in every wave once only this chunk's requests
+    // are outstanding; the barrier also ends every wave's reads of slot k,
+    // which chunk k + 3's requests (made after it) overwrite.
+    wait_vmem_n<chunk_requests<WAVES>()>();
     __syncthreads();
-    st.cur ^= 1;
+    st.k++;
   }
   if (DEFER)
 #pragma unroll
     for (int q = 0; q < GT; q++) epi(TO - GT + q, prev[q], out.v[TO - GT + q]);
   return out;
-}
-
-// Kernel prologue: the first dense layer's first chunk into slot 0.
-template <int TS, int TO, int WAVES, class E>
-__device__ inline void stage_first(Stage<E>& st, E const* __restrict__ w) {
-  int const wave = wave_id(), lane = threadIdx.x & 63;
-  constexpr int NF = cmin(ct16(TS), TO) * TS;
-  chunk_store<NF, WAVES>(chunk_load<NF, WAVES>(w, wave, lane), st, 0, wave, lane);
-  st.cur = 0;
 }
 
 // Accumulator seeds for dense_hs: zero, or the per-feature vector b.

@@ -1462,7 +1462,7 @@ int ponni_plan_kernel_config(ponni_plan plan, int32_t* threads, int32_t* columns
   (void)fused_source(*plan, cfg);
   *threads = 64 * cfg.waves;
   *columns_per_block = cfg.columns_per_block;
-  *persistent = (cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers) ? 1 : 0;
+  *persistent = (cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers || cfg.persistent_loop) ? 1 : 0;
   return PONNI_OK;
 }
 

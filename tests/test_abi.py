@@ -268,6 +268,39 @@ def test_fused_kernels_compile_on_the_host(seed, tmp_path, monkeypatch):
     assert any(f.suffix == ".co" for f in tmp_path.iterdir())
 
 
+def deep_half_chain(norms=8, seed=61):
+    """16-bit chain whose per-feature vectors (17 KB) outgrow the LDS left
+    next to the A-fragment staging and the input rows (96 + 48 KB): 96 -> 256
+    dense layer, 8 x [LayerNorm (gamma / beta: 2 KB), Tanh], 256 -> 32 dense
+    layer."""
+    rng = np.random.default_rng(seed)
+    layers = [P.Matvec(rng.uniform(-0.15, 0.15, (96, 256))), P.Bias(rng.uniform(-0.1, 0.1, 256)), P.Tanh(256)]
+    for _ in range(norms):
+        layers += [P.LayerNorm(rng.uniform(0.5, 1.5, 256), rng.uniform(-0.2, 0.2, 256)), P.Tanh(256)]
+    return layers + [P.Matvec(rng.uniform(-0.1, 0.1, (256, 32))), P.Bias(rng.uniform(-0.1, 0.1, 32))]
+
+
+def test_half_fused_staging_and_lds_budget(tmp_path, monkeypatch):
+    """16-bit FUSED kernels stage each dense layer's A fragments in 32-fragment
+    chunks (a cyclic table, partial last chunks) through three LDS slots; a
+    plan whose per-feature vectors would not fit next to them reads the
+    vectors from global memory instead, and still compiles."""
+    monkeypatch.setenv("PONNI_JIT_CACHE", str(tmp_path))
+    m = create(P.configs.CONFIGS["c4"].layers(False), dtype="f16", path="fused")
+    src = m.kernel_source()
+    assert "a_slots[kSlots * kSlotFrags * 64]" in src and "lds_vec" in src
+    tab = src.split("chunk_tab[20] = {")[1].split("}")[0]
+    assert [int(v) for v in tab.split(",")][1::2] == [32] * 10  # every c4 chunk is a full slot
+    partial = create([P.Matvec(np.ones((40, 48))), P.Tanh(48), P.Matvec(np.ones((48, 80)))], dtype="f16",
+                     path="fused").kernel_source()
+    tab = partial.split("chunk_tab[")[1].split("{")[1].split("}")[0]
+    assert [int(v) for v in tab.split(",")][1::2] == [6, 10]  # 3 tiles x 2 steps; 5 tiles x 2 steps
+    deep = create(deep_half_chain(), dtype="f16", path="fused")
+    src = deep.kernel_source()
+    assert "lds_vec" not in src and "SeedRows{P + " in src
+    deep.compile()
+
+
 def test_fused_config_sources():
     # c2's parameters sit in LDS: its dense epilogues are pinned among the
     # MFMAs (dense_ep_il); c3 streams its parameters from L2 and keeps dense_ep.

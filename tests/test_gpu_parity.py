@@ -487,6 +487,20 @@ def test_half_fused_input_output_paths(cuda, chain, dtype):
             check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_half_fused_vectors_in_global_memory(cuda, dtype):
+    """A 16-bit FUSED plan whose per-feature vectors do not fit in LDS next
+    to the A-fragment staging and the input rows reads them from global
+    memory (tests/test_abi.py deep_half_chain)."""
+    from tests.test_abi import deep_half_chain
+
+    layers = deep_half_chain()
+    x = np.random.default_rng(62).standard_normal((96, 2049))
+    got, xg, m = gpu_run(layers, x, dtype=dtype, path="fused", pad=7)
+    assert m.path == "fused"
+    check_half(got, oracle.forward(layers, xg, ORACLE_MODE[dtype]), 2e-3)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
