@@ -496,6 +496,13 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
     }
     return "VP + " + std::to_string(it->second.first);
   };
+  // Contractions over the input state in contraction order (plan.cpp
+  // input_contractions): ", KS" with the steps that hold input features.
+  std::vector<int32_t> const in_k = half ? std::vector<int32_t>() : input_contractions(p);
+  auto k_steps = [&](int32_t woff, int n_in) -> std::string {
+    if (std::find(in_k.begin(), in_k.end(), woff) == in_k.end()) return "";
+    return ", " + std::to_string((n_in + 3) / 4);
+  };
   std::ostringstream head;
   head << o.str();
   o.str("");
@@ -566,7 +573,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
     o << "    bool const pre_next = tile + gridDim.x < tiles && xvec && Ln.col0 + " << WCOLS << " <= batch;\n";
     if (hook_dense < 0) o << "    " << prefetch_next << "\n";
   } else if (half) o << "    auto " << cur << " = load_rows_h<" << cur_n << ", " << NT << ">(x, ldx, L);\n";
-  else o << "    auto " << cur << " = load_rows<" << cur_n << ">(x, ldx, L);\n";
+  else o << "    auto " << cur << " = " << (in_k.empty() ? "load_rows<" : "load_rows_k<") << cur_n << ">(x, ldx, L);\n";
   std::map<int, std::pair<std::string, int>> saved;  // slot -> (expression, width)
   // The logistic family runs on the hardware transcendentals (pointwise.h),
   // except in F64 plans, which keep the libm forms.
@@ -631,7 +638,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
                                         : "zeros<" + std::to_string(tiles(n)) + ">()";
           o << "    auto " << nv << " = "
             << (epi_interleave > 0 ? "dense_ep_il<" + std::to_string(epi_interleave) + ", " : std::string("dense_ep<"))
-            << tiles(op.n_in) << ", " << tiles(n) << ">(" << cur << ", P + "
+            << tiles(op.n_in) << ", " << tiles(n) << k_steps(op.woff, op.n_in) << ">(" << cur << ", P + "
             << op.woff << ", " << init << ", L, [&](int mo, " << F4 << " (&t)[" << NT << "]) {\n";
         }
         for (int s = seed ? 1 : 0; s < op.epi_count; s++) {
@@ -741,7 +748,8 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
           std::string const b = fresh(), nv = fresh();
           o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
           o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", " << vec(op.boff, cur_n) << ", L);\n";
-          o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << sv.first
+          o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n)
+            << k_steps(op.woff, sv.second) << ">(" << sv.first
             << ", P + " << op.woff << ", " << b << ", L, [](int, " << F4 << " (&)[" << NT << "]) {});\n";
           o << "    add(" << cur << ", " << nv << ");\n";
         }

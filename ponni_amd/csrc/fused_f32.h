@@ -118,6 +118,30 @@ __device__ inline S<(N + 15) / 16, NT> load_rows(real const* __restrict__ x, int
   return s;
 }
 
+// The same in contraction order (input states read only by dense
+// contractions, plan.cpp input_contractions): lane group g, element e of
+// tile m holds feature 4(4m + e) + g, so the padding rows fill whole
+// contraction steps at the end.
+template <int N, int NT = kNT>
+__device__ inline S<(N + 15) / 16, NT> load_rows_k(real const* __restrict__ x, int64_t ld, Lane const& L) {
+  constexpr int T = (N + 15) / 16;
+  S<T, NT> s;
+  // Row 16m + 4e of the lane's row g: a uniform offset from one per-lane pointer.
+  real const* __restrict__ xl = x + int64_t(fresh(L.g)) * ld + fresh(L.c) + L.col0;
+#pragma unroll
+  for (int m = 0; m < T; m++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+      bool const col_ok = L.col0 + 16 * n + L.c < L.batch;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        int const f = 4 * (4 * m + e) + L.g;
+        s.v[m][n][e] = (f < N && col_ok) ? xl[int64_t(16 * m + 4 * e) * ld + 16 * n] : 0.0f;
+      }
+    }
+  return s;
+}
+
 template <int N, int T, int NT>
 __device__ inline void store_rows(S<T, NT> const& s, real* __restrict__ y, int64_t ld, Lane const& L) {
   real* __restrict__ yl = y + lane_offset(L, ld) + L.col0;
@@ -150,10 +174,13 @@ __device__ inline S<T, NT> zeros() {
 // R-deep register ring: fragment i + R is requested while fragment i is
 // consumed.  epi(mo, tile) finishes one output tile in place.  IL > 0 pins
 // each epilogue among the next tile's MFMAs, IL VALU (and as many
-// transcendentals) per input tile of MFMAs.
-template <int IL, int TI, int TO, int NT, class Epi, int D = 4>
+// transcendentals) per input tile of MFMAs.  Contraction step 4m + e runs
+// for 4m + e < KS only (an input state in contraction order, load_rows_k,
+// ends in all-padding steps).
+template <int IL, int TI, int TO, int KS = 4 * TI, int NT, class Epi, int D = 4>
 __device__ inline S<TO, NT> dense_ep_il(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
                                         Lane const& L, Epi epi) {
+  static_assert(KS > 4 * (TI - 1) && KS <= 4 * TI, "every input tile holds a step");
   constexpr int NF = TI * TO;
   constexpr int R = D < NF ? D : NF;
   realx4 ring[R];
@@ -170,9 +197,10 @@ __device__ inline S<TO, NT> dense_ep_il(S<TI, NT> const& in, real const* __restr
       if (i + R < NF) ring[i % R] = ld4(w + (i + R) * 256 + L.lane * 4);
 #pragma unroll
       for (int e = 0; e < 4; e++)
+        if (4 * m + e < KS)
 #pragma unroll
-        for (int n = 0; n < NT; n++)
-          acc.v[mo][n] = mfma4(a[e], in.v[m][n][e], acc.v[mo][n]);
+          for (int n = 0; n < NT; n++)
+            acc.v[mo][n] = mfma4(a[e], in.v[m][n][e], acc.v[mo][n]);
     }
     if (mo > 0) {
       epi(mo - 1, acc.v[mo - 1]);
@@ -186,23 +214,28 @@ __device__ inline S<TO, NT> dense_ep_il(S<TI, NT> const& in, real const* __restr
       // above orders the results within this tile's scheduling region (a
       // sched_barrier at the top of each tile); per input tile (4 NT MFMAs)
       // up to IL VALU and as many transcendentals follow.
-      if (IL > 0)
+      if (IL > 0) {
 #pragma unroll
-        for (int k = 0; k < TI; k++) {
+        for (int k = 0; k + 1 < TI; k++) {
           __builtin_amdgcn_sched_group_barrier(0x008, 4 * NT, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, IL, 0);
           __builtin_amdgcn_sched_group_barrier(0x400, IL, 0);
         }
+        // (the last input tile holds KS - 4 (TI - 1) steps)
+        __builtin_amdgcn_sched_group_barrier(0x008, (KS - 4 * (TI - 1)) * NT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, IL, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, IL, 0);
+      }
     }
   }
   epi(TO - 1, acc.v[TO - 1]);
   return acc;
 }
 
-template <int TI, int TO, int NT, class Epi, int D = 4>
+template <int TI, int TO, int KS = 4 * TI, int NT, class Epi, int D = 4>
 __device__ inline S<TO, NT> dense_ep(S<TI, NT> const& in, real const* __restrict__ w, S<TO, NT> acc,
                                      Lane const& L, Epi epi) {
-  return dense_ep_il<0, TI, TO, NT, Epi, D>(in, w, acc, L, epi);
+  return dense_ep_il<0, TI, TO, KS, NT, Epi, D>(in, w, acc, L, epi);
 }
 
 // Per-tile epilogue helpers (tile = one 16-feature row block, NT columns).

@@ -326,6 +326,41 @@ Step make_step(ponni_layer_desc const& d) {
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
+std::vector<int32_t> contractions_over_input(ponni_plan_s const& p) {
+  bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
+  if (p.path != PONNI_PATH_FUSED || half || p.layers.empty() || p.layers.front().n_in % 16 == 0) return {};
+  bool cur = true;                 // the state holds the input
+  bool saved[kMaxSlots] = {};      // slot s holds the input
+  std::vector<int32_t> woffs;
+  for (Op const& op : p.ops) {
+    switch (op.code) {
+      case OP_DENSE:
+        if (cur) woffs.push_back(op.woff);
+        cur = false;
+        break;
+      case OP_SAVE: saved[op.slot] = cur; break;
+      case OP_LOAD: cur = saved[op.slot]; break;
+      case OP_PROJ_ADD:
+        if (cur) return {};
+        if (saved[op.slot]) woffs.push_back(op.woff);
+        break;
+      case OP_ADD:
+      case OP_CONCAT:
+      case OP_BINARY:
+      case OP_SELECT:
+      case OP_EXTERNAL:
+        if (cur || saved[op.slot] || (op.code == OP_SELECT && op.f0 >= 0 && saved[static_cast<int>(op.f0)]))
+          return {};
+        break;
+      default:
+        if (cur) return {};
+        break;
+    }
+  }
+  if (cur) return {};
+  return woffs;
+}
+
 // Per-path packed size and layout of one layer's parameters.
 // GENERIC: reference layout.  NARROW: padded to the width class W.
 // MFMA: dense weights in A-fragment order, vectors padded to 16.
@@ -608,9 +643,12 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
   int const vec_kind = half_fused ? SLOT_WORD : SLOT_VALUE;
   int const L = static_cast<int>(p.layers.size());
   int const W = p.width_class;
+  std::vector<int32_t> const in_k = contractions_over_input(p);
   for (int i = 0; i < L; i++) {
     ponni_layer_desc const& d = p.layers[i];
     int64_t const base = p.layer_param_offset[i];
+    // (this layer's weights are read by a contraction over the input state)
+    bool const k_in = std::find(in_k.begin(), in_k.end(), static_cast<int32_t>(base)) != in_k.end();
     // Dense weights W [K, N] (row k, column n) starting at parameter src0; a
     // transposed source holds W^T [N, K] (generated Dense, "output_input").
     auto dense = [&](int64_t src0, int K, int N, bool transposed) {
@@ -636,7 +674,9 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
           for (int n = 0; n < N; n++) emit(base + int64_t(k) * W + n, SLOT_VALUE, i, idx(k, n));
       } else {
         // A fragment of v_mfma_f32_16x16x4f32 for output tile mo and input
-        // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16].
+        // tile m: lane l, element v holds W[16m + 4(l/16) + v][16mo + l%16]
+        // (a contraction over the input state in contraction order, see
+        // input_contractions: W[4(4m + v) + l/16][...]).
         // v_mfma_f64_16x16x4f64 returns result row 4e + g in element e of
         // lane group g (fp32: row 4g + e), so fp64 tiles take their A rows in
         // that transposed order and the result lands in the fp32 tile layout.
@@ -646,7 +686,7 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
           for (int m = 0; m < TK; m++)
             for (int l = 0; l < 64; l++)
               for (int v = 0; v < 4; v++) {
-                int const k = 16 * m + 4 * (l >> 4) + v;
+                int const k = k_in ? 4 * (4 * m + v) + (l >> 4) : 16 * m + 4 * (l >> 4) + v;
                 int const r = l & 15;
                 int const n = 16 * mo + (rows_t ? (r & 3) * 4 + (r >> 2) : r);
                 if (k < K && n < N) emit(base + ((int64_t(mo) * TK + m) * 64 + l) * 4 + v, SLOT_VALUE, i, idx(k, n));
@@ -965,6 +1005,7 @@ int reallocate_scratch(ponni_plan_s& p, int64_t batch) {
 
 namespace ponni_hip {
 int set_error(int status, std::string const& message) { return fail(status, message); }
+std::vector<int32_t> input_contractions(ponni_plan_s const& p) { return contractions_over_input(p); }
 }  // namespace ponni_hip
 
 namespace {

@@ -101,6 +101,15 @@ ponni_plan_s* generic_twin(ponni_plan_s& plan);
 int set_error(int status, std::string const& message);  // ponni_last_error(); returns status
 int host_twin(ponni_plan_s& plan, ponni_plan_s*& twin);
 
+// FUSED fp32 / fp64 plans whose input width is not a multiple of 16 and
+// whose input state is only ever read by dense contractions (Matvec, Dense,
+// the projection of Binop_Projection_Add; through saves and loads): the
+// packed-parameter offsets of those contractions.  Their input tile then
+// holds feature 4s + g in lane group g, element e of input tile m, s = 4m +
+// e (contraction order), so the all-padding steps of those contractions are
+// skipped; the weight packing and the kernel agree on it.  Empty otherwise.
+std::vector<int32_t> input_contractions(ponni_plan_s const& p);
+
 // Width classes each register path is instantiated for.
 int narrow_width_class(int max_width);      // 0 if too wide
 int mfma_width_class(int dtype, int max_width);  // tiles of 16 features; 0 if too wide

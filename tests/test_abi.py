@@ -301,6 +301,26 @@ def test_half_fused_staging_and_lds_budget(tmp_path, monkeypatch):
     deep.compile()
 
 
+def test_input_in_contraction_order_only_for_contractions():
+    """FUSED fp32 / fp64 plans whose input width is not a multiple of 16 load
+    the input in contraction order, and skip the all-padding contraction
+    steps, only when every read of the input state is a dense contraction
+    (c5: two Dense layers and the projection skip)."""
+    def src(layers, dtype="f32"):
+        return create(layers, dtype=dtype, path="fused").kernel_source()
+
+    c5 = src(P.configs.CONFIGS["c5"].layers(False))
+    assert "load_rows_k<24>" in c5 and c5.count(", 6>(") == 3  # 24 inputs: 6 of 8 steps
+    rng = np.random.default_rng(3)
+    w = lambda a, b: rng.uniform(-0.3, 0.3, (a, b))  # noqa: E731
+    assert "load_rows_k<24>" in src([P.Matvec(w(24, 32)), P.Relu(32)], "f64")
+    assert "load_rows_k" not in src([P.Matvec(w(32, 32)), P.Relu(32)])  # no padding
+    assert "load_rows_k" not in src([P.Relu(24), P.Matvec(w(24, 8))])  # pointwise on the input
+    assert "load_rows_k" not in src([P.Save_State(0, 24), P.Matvec(w(24, 24)), P.Binop_Add(0, 24)])
+    assert "load_rows_k" not in src([P.Save_State(0, 24), P.Matvec(w(24, 24)),
+                                     P.Binop_Concatenate(0, 24, 48)])
+
+
 def test_fused_config_sources():
     # c2's parameters sit in LDS: its dense epilogues are pinned among the
     # MFMAs (dense_ep_il); c3 streams its parameters from L2 and keeps dense_ep.
