@@ -21,6 +21,8 @@ work on ms_per_step.  `roofline.traffic` = HBM bytes per launch from the
 committed rocprofv3 PMC runs (profiles/traffic.json).  `cpu_baseline` times the
 CPU restatement of the reference (oracle/, OpenMP over samples as Kokkos'
 OpenMP RangePolicy) on a bounded sample of each configuration on this host.
+`measured_peaks` reports a device copy's and register-only MFMA loops' rates
+measured on the same GPU, beside the published peaks `frac` is priced on.
 """
 from __future__ import annotations
 
@@ -137,6 +139,31 @@ def make_inputs(cfg, torch, P, C):
         xs.append(x)
         ys.append(torch.empty((cfg.n_out, cfg.batch), dtype=tdt, device="cuda:0"))
     return xs, ys
+
+
+def measured_peaks(roofline, cfg):
+    """Copy and MFMA rates measured on this device (ponni_measure_peaks), and the
+    headline kernel's rate as a fraction of the one that bounds it.  Reported
+    beside the published peaks; `roofline.frac` stays priced on the published one."""
+    from ponni_amd import _abi as A
+
+    pk = A.Peaks()
+    A.check(A.lib().ponni_measure_peaks(ctypes.byref(pk), None))
+    out = {
+        "hbm_copy_GBps": round(pk.hbm_copy_gbps, 1),
+        "mfma_f16_TFLOPs": round(pk.mfma_f16_tflops, 1),
+        "mfma_f32_TFLOPs": round(pk.mfma_f32_tflops, 1),
+        "method": ("1 GiB device copy, the faster of two launch shapes (bytes read + written); "
+                   "register-only loops of "
+                   "v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32, one 512-thread workgroup "
+                   "per CU; medians of 3-5 launches"),
+    }
+    bound = {"hbm": pk.hbm_copy_gbps,
+             "mfma": {"f16": pk.mfma_f16_tflops, "bf16": pk.mfma_f16_tflops,
+                      "f32": pk.mfma_f32_tflops}.get(cfg.dtype)}[roofline["bound"]]
+    if bound:
+        out["frac_of_measured"] = round(roofline["achieved"] / bound, 4)
+    return out
 
 
 def time_config(cfg, steps, warmup, torch, P, C, ev):
@@ -280,6 +307,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU budget of the headline configuration")
     ap.add_argument("--cpu-seconds-others", type=float, default=6.0, help="CPU budget of each other configuration")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured copy and MFMA peaks")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a device copy of 256 MiB (reference for PMC byte counters)")
     ap.add_argument("--trace-summary", metavar="CSV", help="summarize a rocprofv3 kernel trace and exit")
@@ -335,6 +363,7 @@ def main() -> int:
             }
             del r
             torch.cuda.empty_cache()
+    peaks = None if args.no_peaks else measured_peaks(head["roofline"], cfg)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, args.cpu_seconds)
@@ -364,6 +393,7 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": head["roofline"],
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "configs": others,
     }

@@ -471,6 +471,19 @@ int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed,
 #define PONNI_DIST_UNIFORM 0
 #define PONNI_DIST_NORMAL 1
 
+/* Measured peaks of the current device, reported by bench.py beside the
+ * published ones (no counterpart in the reference): the rate of a 1 GiB
+ * device copy (bytes read + written per second) and of register-only loops
+ * of v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32 with one 512-thread
+ * workgroup per CU (the 16-bit FUSED kernels' occupancy); medians of a few
+ * launches.  Allocates 2 GiB of device memory for the call; synchronous. */
+typedef struct ponni_peaks {
+  double hbm_copy_gbps;
+  double mfma_f16_tflops;
+  double mfma_f32_tflops;
+} ponni_peaks;
+int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream);
+
 /* --- .ponni weight files (host only) ------------------------------------- */
 
 /* FNV-1a-64 of a byte string, utils/ponni_safetensors.h:25-32. */

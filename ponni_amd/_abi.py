@@ -91,6 +91,11 @@ class TensorSpec(ctypes.Structure):
     ]
 
 
+class Peaks(ctypes.Structure):
+    _fields_ = [("hbm_copy_gbps", ctypes.c_double), ("mfma_f16_tflops", ctypes.c_double),
+                ("mfma_f32_tflops", ctypes.c_double)]
+
+
 class PlanInfo(ctypes.Structure):
     _fields_ = [
         ("path", ctypes.c_int32),
@@ -182,6 +187,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_forward_host.argtypes = [vp, vp, i64, vp, i64, i64, ctypes.c_int32]
     L.ponni_fill_synthetic.restype = ctypes.c_int
     L.ponni_fill_synthetic.argtypes = [vp, i32, i64, u64, u64, i32, ctypes.c_double, ctypes.c_double, vp]
+    L.ponni_measure_peaks.restype = ctypes.c_int
+    L.ponni_measure_peaks.argtypes = [ctypes.POINTER(Peaks), vp]
     L.ponni_fnv1a64.restype = u64
     L.ponni_fnv1a64.argtypes = [vp, sz]
     L.ponni_template_fingerprint.restype = ctypes.c_int

@@ -43,3 +43,26 @@ def test_timed_forward_rejects_null_events():
     with pytest.raises(P.PonniError) as e:
         m.forward_raw_timed(0, 1, 0, 1, 1, 0, 0, 0)
     assert e.value.status == P._abi.PONNI_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.gpu
+def test_measured_peaks_are_plausible(cuda):
+    """ponni_measure_peaks: every rate positive and under MI355X's published
+    peak (8 TB/s HBM, 2.5 PFLOP/s fp16 and 157.3 TFLOP/s fp32 dense MFMA) with
+    a margin for clocks above the nominal one."""
+    import ctypes
+
+    from ponni_amd import _abi as A
+
+    pk = A.Peaks()
+    print("measure peaks", flush=True)
+    A.check(A.lib().ponni_measure_peaks(ctypes.byref(pk), None))
+    assert 1000.0 < pk.hbm_copy_gbps < 1.2 * 8000.0, pk.hbm_copy_gbps
+    assert 500.0 < pk.mfma_f16_tflops < 1.2 * 2500.0, pk.mfma_f16_tflops
+    assert 30.0 < pk.mfma_f32_tflops < 1.2 * 157.3, pk.mfma_f32_tflops
+
+
+def test_measured_peaks_rejects_null_output():
+    from ponni_amd import _abi as A
+
+    assert A.lib().ponni_measure_peaks(None, None) == A.PONNI_ERR_INVALID_ARGUMENT
