@@ -141,28 +141,39 @@ def make_inputs(cfg, torch, P, C):
     return xs, ys
 
 
-def measured_peaks(roofline, cfg):
+def frac_of_measured(pk, roofline, dtype):
+    """A kernel's achieved rate over the measured rate of the unit that bounds it
+    (HBM: the faster of the copy and the read-only pass; None where no matching
+    rate is measured, e.g. fp64 MFMA)."""
+    bound = {"hbm": max(pk.hbm_copy_gbps, pk.hbm_read_gbps),
+             "mfma": {"f16": pk.mfma_f16_tflops, "bf16": pk.mfma_f16_tflops,
+                      "f32": pk.mfma_f32_tflops}.get(dtype)}[roofline["bound"]]
+    return round(roofline["achieved"] / bound, 4) if bound else None
+
+
+def measured_peaks(roofline, cfg, others):
     """Copy and MFMA rates measured on this device (ponni_measure_peaks), and the
-    headline kernel's rate as a fraction of the one that bounds it.  Reported
-    beside the published peaks; `roofline.frac` stays priced on the published one."""
+    headline kernel's rate as a fraction of the one that bounds it; each other
+    configuration's roofline gets the same `frac_of_measured`.  Reported beside
+    the published peaks; `roofline.frac` stays priced on the published one."""
     from ponni_amd import _abi as A
 
     pk = A.Peaks()
     A.check(A.lib().ponni_measure_peaks(ctypes.byref(pk), None))
+    for o in others.values():
+        o["roofline"]["frac_of_measured"] = frac_of_measured(pk, o["roofline"], o["dtype"])
     out = {
         "hbm_copy_GBps": round(pk.hbm_copy_gbps, 1),
+        "hbm_read_GBps": round(pk.hbm_read_gbps, 1),
         "mfma_f16_TFLOPs": round(pk.mfma_f16_tflops, 1),
         "mfma_f32_TFLOPs": round(pk.mfma_f32_tflops, 1),
         "method": ("1 GiB device copy, the faster of two launch shapes (bytes read + written); "
+                   "read-only pass over 1 GiB; HBM-bound kernels priced on the faster of the two; "
                    "register-only loops of "
                    "v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32, one 512-thread workgroup "
                    "per CU; medians of 3-5 launches"),
     }
-    bound = {"hbm": pk.hbm_copy_gbps,
-             "mfma": {"f16": pk.mfma_f16_tflops, "bf16": pk.mfma_f16_tflops,
-                      "f32": pk.mfma_f32_tflops}.get(cfg.dtype)}[roofline["bound"]]
-    if bound:
-        out["frac_of_measured"] = round(roofline["achieved"] / bound, 4)
+    out["frac_of_measured"] = frac_of_measured(pk, roofline, cfg.dtype)
     return out
 
 
@@ -363,7 +374,7 @@ def main() -> int:
             }
             del r
             torch.cuda.empty_cache()
-    peaks = None if args.no_peaks else measured_peaks(head["roofline"], cfg)
+    peaks = None if args.no_peaks else measured_peaks(head["roofline"], cfg, others)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, args.cpu_seconds)

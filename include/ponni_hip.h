@@ -472,8 +472,9 @@ int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed,
 #define PONNI_DIST_NORMAL 1
 
 /* Measured peaks of the current device, reported by bench.py beside the
- * published ones (no counterpart in the reference): the rate of a 1 GiB
- * device copy (bytes read + written per second) and of register-only loops
+ * published ones (no counterpart in the reference): the rates of a 1 GiB
+ * device copy (bytes read + written per second), of a read-only pass over
+ * the same 1 GiB, and of register-only loops
  * of v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32 with one 512-thread
  * workgroup per CU (the 16-bit FUSED kernels' occupancy); medians of a few
  * launches.  Allocates 2 GiB of device memory for the call; synchronous. */
@@ -481,6 +482,7 @@ typedef struct ponni_peaks {
   double hbm_copy_gbps;
   double mfma_f16_tflops;
   double mfma_f32_tflops;
+  double hbm_read_gbps;
 } ponni_peaks;
 int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream);
 

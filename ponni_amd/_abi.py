@@ -93,7 +93,7 @@ class TensorSpec(ctypes.Structure):
 
 class Peaks(ctypes.Structure):
     _fields_ = [("hbm_copy_gbps", ctypes.c_double), ("mfma_f16_tflops", ctypes.c_double),
-                ("mfma_f32_tflops", ctypes.c_double)]
+                ("mfma_f32_tflops", ctypes.c_double), ("hbm_read_gbps", ctypes.c_double)]
 
 
 class PlanInfo(ctypes.Structure):

@@ -1,5 +1,6 @@
 // Measured peaks of the device the library runs on, reported by bench.py
-// beside the published ones: a streaming device copy (HBM) and register-only
+// beside the published ones: a streaming device copy and a read-only stream
+// (HBM) and register-only
 // loops of the matrix instructions the kernels use, at the occupancy of the
 // 16-bit FUSED kernels (one 512-thread workgroup per CU, two waves per SIMD).
 #include <hip/hip_runtime.h>
@@ -35,6 +36,20 @@ __global__ __launch_bounds__(256) void copy_unrolled(f4 const* __restrict__ src,
     if (base + u * 256 < n) dst[base + u * 256] = v[u];
 }
 
+// Read-only stream: each workgroup reads 256 x U consecutive 16-byte elements
+// and writes nothing unless the sum takes a value zero-filled input never gives.
+template <int U>
+__global__ __launch_bounds__(256) void read_unrolled(f4 const* __restrict__ src, float* __restrict__ sink, int64_t n) {
+  int64_t const base = int64_t(blockIdx.x) * 256 * U + threadIdx.x;
+  f4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) v[u] = base + u * 256 < n ? src[base + u * 256] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float s = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; u++) s += v[u][0] + v[u][1] + v[u][2] + v[u][3];
+  if (s == 1.0f) sink[threadIdx.x] = s;
+}
+
 // Eight independent accumulators per lane; `iters` rounds of 8 MFMAs.
 __global__ __launch_bounds__(512) void mfma_f16_loop(float* __restrict__ out, int iters, float seed) {
   f4 acc[8];
@@ -67,8 +82,11 @@ __global__ __launch_bounds__(512) void mfma_f32_loop(float* __restrict__ out, in
 // Median of `reps` timed launches (after one warm-up), in ms.
 template <class Launch>
 float median_ms(Launch launch, hipStream_t stream, int reps) {
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0f;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    if (e0 != nullptr) (void)hipEventDestroy(e0);
+    return -1.0f;
+  }
   launch();
   std::vector<float> t;
   for (int r = 0; r < reps; r++) {
@@ -105,7 +123,12 @@ extern "C" int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream) {
     (void)hipFree(dst);
     return set_error(PONNI_ERR_DEVICE, "out of device memory");
   }
-  (void)hipMemsetAsync(src, 0, bytes, stream);
+  if (hipMemsetAsync(src, 0, bytes, stream) != hipSuccess) {
+    (void)hipFree(src);
+    (void)hipFree(dst);
+    (void)hipFree(sink);
+    return set_error(PONNI_ERR_DEVICE, "peak measurement: memset failed");
+  }
   int64_t const n4 = bytes / 16;
   // The faster of a grid-stride loop over 32 workgroups per CU and a one-pass
   // grid of 4 elements per thread.
@@ -122,6 +145,12 @@ extern "C" int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream) {
       },
       stream, 5);
   float const copy_ms = std::min(stride_ms > 0.0f ? stride_ms : pass_ms, pass_ms > 0.0f ? pass_ms : stride_ms);
+  float const read_ms = median_ms(
+      [&] {
+        hipLaunchKernelGGL(read_unrolled<4>, dim3(unsigned((n4 + 1023) / 1024)), dim3(256), 0, stream,
+                           static_cast<f4 const*>(src), sink, n4);
+      },
+      stream, 5);
   // Matrix pipes: one 512-thread workgroup per CU.
   int const iters = 4096;
   float const f16_ms = median_ms(
@@ -132,10 +161,11 @@ extern "C" int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream) {
   (void)hipFree(src);
   (void)hipFree(dst);
   (void)hipFree(sink);
-  if (err != hipSuccess || copy_ms <= 0.0f || f16_ms <= 0.0f || f32_ms <= 0.0f)
+  if (err != hipSuccess || copy_ms <= 0.0f || read_ms <= 0.0f || f16_ms <= 0.0f || f32_ms <= 0.0f)
     return set_error(PONNI_ERR_DEVICE, std::string("peak measurement failed: ") + hipGetErrorString(err));
   double const mfmas = double(cus) * 8 * iters * 8;  // waves x rounds x MFMAs per round
   out->hbm_copy_gbps = 2.0 * double(bytes) / (copy_ms * 1e-3) / 1e9;
+  out->hbm_read_gbps = double(bytes) / (read_ms * 1e-3) / 1e9;
   out->mfma_f16_tflops = mfmas * 16384.0 / (f16_ms * 1e-3) / 1e12;  // 16x16x32: 2*16*16*32 FLOP
   out->mfma_f32_tflops = mfmas * 2048.0 / (f32_ms * 1e-3) / 1e12;   // 16x16x4: 2*16*16*4 FLOP
   return PONNI_OK;

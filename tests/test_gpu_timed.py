@@ -58,6 +58,7 @@ def test_measured_peaks_are_plausible(cuda):
     print("measure peaks", flush=True)
     A.check(A.lib().ponni_measure_peaks(ctypes.byref(pk), None))
     assert 1000.0 < pk.hbm_copy_gbps < 1.2 * 8000.0, pk.hbm_copy_gbps
+    assert 1000.0 < pk.hbm_read_gbps < 1.2 * 8000.0, pk.hbm_read_gbps
     assert 500.0 < pk.mfma_f16_tflops < 1.2 * 2500.0, pk.mfma_f16_tflops
     assert 30.0 < pk.mfma_f32_tflops < 1.2 * 157.3, pk.mfma_f32_tflops
 
