@@ -745,12 +745,13 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
           o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << cur << ", " << sv.first
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), " << vec(op.boff, cur_n) << ", L);\n";
         } else {
-          std::string const b = fresh(), nv = fresh();
-          o << "    auto " << b << " = zeros<" << tiles(cur_n) << ">();\n";
-          o << "    add_rows<" << tiles(cur_n) << ">(" << b << ", " << vec(op.boff, cur_n) << ", L);\n";
-          o << "    auto " << nv << " = dense_ep<" << tiles(sv.second) << ", " << tiles(cur_n)
-            << k_steps(op.woff, sv.second) << ">(" << sv.first
-            << ", P + " << op.woff << ", " << b << ", L, [](int, " << F4 << " (&)[" << NT << "]) {});\n";
+          // The bias seeds the accumulators (no zero fill and add).
+          std::string const nv = fresh();
+          o << "    auto " << nv << " = "
+            << (epi_interleave > 0 ? "dense_ep_il<" + std::to_string(epi_interleave) + ", " : std::string("dense_ep<"))
+            << tiles(sv.second) << ", " << tiles(cur_n) << k_steps(op.woff, sv.second) << ">(" << sv.first
+            << ", P + " << op.woff << ", bias_rows<" << tiles(cur_n) << ">(" << vec(op.boff, cur_n)
+            << ", L), L, [](int, " << F4 << " (&)[" << NT << "]) {});\n";
           o << "    add(" << cur << ", " << nv << ");\n";
         }
         break;

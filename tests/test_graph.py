@@ -357,9 +357,10 @@ def test_c5_plan_is_fused_and_compiles():
     plan = gm.plan()
     assert plan.path == "fused"
     src = plan.kernel_source()
-    # four Dense ops with epilogues pinned among their MFMAs, the projection
-    # skip's plain contraction
-    assert src.count("dense_ep_il<16, ") == 4 and src.count("dense_ep<") == 1
+    # four Dense ops and the projection skip, epilogues pinned among their
+    # MFMAs; the skip's bias seeds its accumulators
+    assert src.count("dense_ep_il<16, ") == 5 and src.count("dense_ep<") == 0
+    assert "bias_rows<6>(P + 12480, L)" in src and "add_rows<" not in src
     assert "reduce<1, 96>" in src and "binary<96, false, true>" in src
     assert "concat<3, 3>" in src and "softmax<10, false>" in src
     plan.compile()
