@@ -745,14 +745,15 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
           o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << cur << ", " << sv.first
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), " << vec(op.boff, cur_n) << ", L);\n";
         } else {
-          // The bias seeds the accumulators (no zero fill and add).
+          // The bias seeds the accumulators; each finished tile adds the
+          // state's tile (proj + in, the same sum as in + proj).
           std::string const nv = fresh();
           o << "    auto " << nv << " = "
             << (epi_interleave > 0 ? "dense_ep_il<" + std::to_string(epi_interleave) + ", " : std::string("dense_ep<"))
             << tiles(sv.second) << ", " << tiles(cur_n) << k_steps(op.woff, sv.second) << ">(" << sv.first
             << ", P + " << op.woff << ", bias_rows<" << tiles(cur_n) << ">(" << vec(op.boff, cur_n)
-            << ", L), L, [](int, " << F4 << " (&)[" << NT << "]) {});\n";
-          o << "    add(" << cur << ", " << nv << ");\n";
+            << ", L), L, [&](int mo, " << F4 << " (&t)[" << NT << "]) { tile_add_state(t, " << cur << ", mo); });\n";
+          cur = nv;
         }
         break;
       }

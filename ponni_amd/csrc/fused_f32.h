@@ -306,6 +306,14 @@ __device__ inline void add(S<T, NT>& s, S<T, NT> const& o) {
     for (int n = 0; n < NT; n++) s.v[m][n] += o.v[m][n];
 }
 
+// Output tile mo of a contraction plus tile mo of state s (an element-wise
+// Add fused into the contraction's epilogue; mo is unrolled there).
+template <int T, int NT>
+__device__ inline void tile_add_state(realx4 (&t)[NT], S<T, NT> const& s, int mo) {
+#pragma unroll
+  for (int n = 0; n < NT; n++) t[n] += s.v[mo][n];
+}
+
 // Two-pass LayerNorm over N features, ponni_LayerNorm.h:82-98.
 template <int N, int T, int NT>
 __device__ inline void layer_norm(S<T, NT>& s, real const* __restrict__ gamma, real const* __restrict__ beta,
