@@ -171,7 +171,7 @@ def measured_peaks(roofline, cfg, others):
                    "read-only pass over 1 GiB; HBM-bound kernels priced on the faster of the two; "
                    "register-only loops of "
                    "v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32, one 512-thread workgroup "
-                   "per CU; medians of 3-5 launches"),
+                   "per CU; medians of 3-5 samples of 2-4 back-to-back launches"),
     }
     out["frac_of_measured"] = frac_of_measured(pk, roofline, cfg.dtype)
     return out

@@ -79,9 +79,11 @@ __global__ __launch_bounds__(512) void mfma_f32_loop(float* __restrict__ out, in
   out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Median of `reps` timed launches (after one warm-up), in ms.
+// Median over `reps` samples (after one warm-up launch) of the time per
+// launch, in ms; each sample times `per` launches back to back between two
+// events, so event overhead is spread over them.
 template <class Launch>
-float median_ms(Launch launch, hipStream_t stream, int reps) {
+float median_ms(Launch launch, hipStream_t stream, int reps, int per) {
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
     if (e0 != nullptr) (void)hipEventDestroy(e0);
@@ -92,10 +94,10 @@ float median_ms(Launch launch, hipStream_t stream, int reps) {
   for (int r = 0; r < reps; r++) {
     float ms = 0.0f;
     (void)hipEventRecord(e0, stream);
-    launch();
+    for (int i = 0; i < per; i++) launch();
     (void)hipEventRecord(e1, stream);
     if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) ms = -1.0f;
-    t.push_back(ms);
+    t.push_back(ms / per);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
@@ -137,26 +139,26 @@ extern "C" int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream) {
         hipLaunchKernelGGL(copy_kernel, dim3(cus * 32), dim3(256), 0, stream, static_cast<f4 const*>(src),
                            static_cast<f4*>(dst), n4);
       },
-      stream, 5);
+      stream, 5, 4);
   float const pass_ms = median_ms(
       [&] {
         hipLaunchKernelGGL(copy_unrolled<4>, dim3(unsigned((n4 + 1023) / 1024)), dim3(256), 0, stream,
                            static_cast<f4 const*>(src), static_cast<f4*>(dst), n4);
       },
-      stream, 5);
+      stream, 5, 4);
   float const copy_ms = std::min(stride_ms > 0.0f ? stride_ms : pass_ms, pass_ms > 0.0f ? pass_ms : stride_ms);
   float const read_ms = median_ms(
       [&] {
         hipLaunchKernelGGL(read_unrolled<4>, dim3(unsigned((n4 + 1023) / 1024)), dim3(256), 0, stream,
                            static_cast<f4 const*>(src), sink, n4);
       },
-      stream, 5);
+      stream, 5, 4);
   // Matrix pipes: one 512-thread workgroup per CU.
   int const iters = 4096;
   float const f16_ms = median_ms(
-      [&] { hipLaunchKernelGGL(mfma_f16_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3);
+      [&] { hipLaunchKernelGGL(mfma_f16_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3, 2);
   float const f32_ms = median_ms(
-      [&] { hipLaunchKernelGGL(mfma_f32_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3);
+      [&] { hipLaunchKernelGGL(mfma_f32_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3, 2);
   hipError_t const err = hipGetLastError();
   (void)hipFree(src);
   (void)hipFree(dst);
