@@ -246,7 +246,8 @@ typedef struct ponni_plan_info {
   int32_t num_saved_states;  /* get_num_saved_states()                            */
   int32_t tmp1_features;     /* get_planned_temporary_size<0>()                   */
   int32_t tmp2_features;     /* get_planned_temporary_size<1>()                   */
-  int32_t saved_features[8]; /* get_saved_state_size<i>() for slots 0..7          */
+  int32_t saved_features[8]; /* get_saved_state_size<i>() for slots 0..7 (any
+                              slot: ponni_plan_saved_state_size)              */
   int64_t num_parameters;    /* all layer parameters, trainable or not           */
   int64_t internal_state_capacity; /* internal_state_capacity()                   */
   int32_t max_width;         /* widest state anywhere in the chain                */
@@ -281,6 +282,12 @@ int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info);
  * Projection_Add NSAVE*n_in + n_in (W then bias), Dense n_out*n_in (+ n_out
  * with a bias), Const_Binary n_in, others 0. */
 int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer);
+
+/* get_saved_state_size<slot>() (ponni_Inference.h:204-223) for any slot
+ * index: the widest state any Save_State<slot> stores, 0 for an unused slot
+ * below get_num_saved_states(); -1 with an error for a negative slot or one
+ * at or beyond get_num_saved_states(). */
+int32_t ponni_plan_saved_state_size(ponni_plan plan, int32_t slot);
 
 /* Copy one layer's parameters from host memory, in the layer's own order
  * (Matvec W [n_in, n_out] row-major; LayerNorm gamma then beta;
@@ -349,6 +356,11 @@ int ponni_forward(ponni_plan plan, const void* x, int64_t ld_in, void* y,
  *   - The plan must already be on this device: one ponni_forward or
  *     ponni_plan_device_params call (which may allocate) puts it there, and
  *     a parameter change takes it off again; else PONNI_ERR_INVALID_ARGUMENT.
+ *     That includes a change found in a host array shared with the plan
+ *     (ponni_plan_share_layer_params with on_device = 0), reported with its
+ *     own message.  A captured graph of this call keeps reading the device
+ *     copy it was captured with: device-shared arrays are re-gathered by
+ *     every replay, host-shared ones need a ponni_forward and a re-capture.
  *   - A batch whose GENERIC state buffers exceed the array gives
  *     PONNI_ERR_SHAPE (ponni_forward has no such limit).
  *   - All calls on one GPU share its array: calls that overlap in time on
@@ -433,7 +445,10 @@ typedef struct ponni_device_model {
   int32_t num_outputs;
   int32_t max_width;  /* widest state of the chain */
   int32_t tmp_features[2];
-  int32_t saved_features[8];
+  int32_t num_slots;   /* saved-state slots (get_num_saved_states()) */
+  int32_t saved_total; /* features of all saved slots together */
+  const int32_t* slot_rows; /* max(num_slots, 1) entries: slot s starts at
+                               feature slot_rows[s] of the saved-state area */
 } ponni_device_model;
 
 /* Fill *out for `plan` (uploading its GENERIC form on first use and after

@@ -37,8 +37,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_forward.restype = ctypes.c_int
         L.oracle_forward.argtypes = [vp, ctypes.c_int32, vp, ctypes.c_int32, vp, ctypes.c_int64, vp,
                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]
-        L.oracle_plan_widths.restype = None
-        L.oracle_plan_widths.argtypes = [vp, ctypes.c_int32, vp, vp]
+        L.oracle_plan_widths.restype = ctypes.c_int32
+        L.oracle_plan_widths.argtypes = [vp, ctypes.c_int32, vp, vp, ctypes.c_int32]
         L.oracle_round_half.restype = ctypes.c_float
         L.oracle_round_half.argtypes = [ctypes.c_float]
         L.oracle_round_bf16.restype = ctypes.c_float
@@ -71,13 +71,15 @@ def forward(layers, x: np.ndarray, mode: int = MODE_F32, threads: int = 0) -> np
 
 
 def plan_widths(layers):
+    """([tmp1, tmp2] widths, [saved width of each slot 0 .. num_saved_states - 1])."""
     from ponni_amd.model import descs
 
     d = descs(layers)
     tmp = (ctypes.c_int32 * 2)()
-    saved = (ctypes.c_int32 * 8)()
-    lib().oracle_plan_widths(ctypes.addressof(d), len(layers), ctypes.addressof(tmp), ctypes.addressof(saved))
-    return list(tmp), list(saved)
+    cap = max([L.slot + 1 for L in layers if hasattr(L, "slot")] + [1])
+    saved = (ctypes.c_int32 * cap)()
+    n = lib().oracle_plan_widths(ctypes.addressof(d), len(layers), ctypes.addressof(tmp), ctypes.addressof(saved), cap)
+    return list(tmp), list(saved)[:n]
 
 
 def round_half(v: float) -> float:

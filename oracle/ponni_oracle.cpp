@@ -557,15 +557,19 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
 }
 
 // Scratch widths, get_planned_temporary_size<0/1>() and get_saved_state_size<s>().
-void plan_widths(std::vector<ponni_layer_desc> const& layers, int* tmp, int* saved) {
+// saved gets one entry per slot up to the highest Save_State index.
+void plan_widths(std::vector<ponni_layer_desc> const& layers, int* tmp, std::vector<int>& saved) {
   int const L = static_cast<int>(layers.size());
   tmp[0] = tmp[1] = 0;
-  for (int s = 0; s < 8; s++) saved[s] = 0;
+  saved.clear();
   bool in_tmp1 = false;
   int i = 0;
   while (i < L) {
     ponni_layer_desc const& d = layers[i];
-    if (d.kind == PONNI_LAYER_SAVE_STATE && d.slot >= 0 && d.slot < 8) saved[d.slot] = std::max(saved[d.slot], d.n_out);
+    if (d.kind == PONNI_LAYER_SAVE_STATE && d.slot >= 0) {
+      if (static_cast<int>(saved.size()) <= d.slot) saved.resize(d.slot + 1, 0);
+      saved[d.slot] = std::max(saved[d.slot], d.n_out);
+    }
     if (is_dense(d.kind)) {
       int end = i + 1;
       while (end < L && is_pointwise(layers[end].kind)) end++;
@@ -593,16 +597,20 @@ int forward(std::vector<ponni_layer_desc> const& layers, std::vector<double cons
   c.layers = layers;
   c.params = params;
   c.mode = mode;
-  int tmpw[2], savedw[8];
+  int tmpw[2];
+  std::vector<int> savedw;
   plan_widths(layers, tmpw, savedw);
+  int const num_slots = std::max<int>(static_cast<int>(savedw.size()), 1);
+  savedw.resize(num_slots, 0);
   int const n_in = layers.front().n_in;
   int const n_out = layers.back().n_out;
   // Inputs and outputs are converted to T at the boundary; scratch is T.
   std::vector<T> xs(size_t(n_in) * size_t(batch)), ys(size_t(n_out) * size_t(batch));
   std::vector<T> t1(size_t(tmpw[0]) * size_t(batch)), t2(size_t(tmpw[1]) * size_t(batch));
-  std::vector<std::vector<T>> sv(8);
-  Buf<T> saved[8];
-  for (int s = 0; s < 8; s++) {
+  std::vector<std::vector<T>> sv(num_slots);
+  std::vector<Buf<T>> saved_v(num_slots);
+  Buf<T>* saved = saved_v.data();
+  for (int s = 0; s < num_slots; s++) {
     sv[s].resize(size_t(savedw[s]) * size_t(batch));
     saved[s] = Buf<T>{sv[s].data(), batch};
   }
@@ -675,14 +683,18 @@ int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double co
   }
 }
 
-// Scratch planning of the reference: tmp1, tmp2, saved slot widths.
-void oracle_plan_widths(ponni_layer_desc const* layers, int32_t num_layers, int32_t* tmp, int32_t* saved) {
+// Scratch planning of the reference: tmp1, tmp2, saved slot widths (the
+// first max_saved slots); returns get_num_saved_states().
+int32_t oracle_plan_widths(ponni_layer_desc const* layers, int32_t num_layers, int32_t* tmp, int32_t* saved,
+                           int32_t max_saved) {
   std::vector<ponni_layer_desc> ls(layers, layers + num_layers);
-  int t[2], s[8];
+  int t[2];
+  std::vector<int> s;
   plan_widths(ls, t, s);
   tmp[0] = t[0];
   tmp[1] = t[1];
-  for (int i = 0; i < 8; i++) saved[i] = s[i];
+  for (int i = 0; i < max_saved; i++) saved[i] = i < static_cast<int>(s.size()) ? s[i] : 0;
+  return static_cast<int32_t>(s.size());
 }
 
 float oracle_round_half(float v) { return round_half(v); }

@@ -96,6 +96,10 @@ class Peaks(ctypes.Structure):
                 ("mfma_f32_tflops", ctypes.c_double), ("hbm_read_gbps", ctypes.c_double)]
 
 
+# Saved-state slot indices a plan may use: 0 .. MAX_SLOTS - 1 (program.h kMaxSlots).
+MAX_SLOTS = 4096
+
+
 class PlanInfo(ctypes.Structure):
     _fields_ = [
         ("path", ctypes.c_int32),
@@ -130,7 +134,8 @@ class DeviceModel(ctypes.Structure):
     _fields_ = [("ops", ctypes.c_void_p), ("steps", ctypes.c_void_p), ("params", ctypes.c_void_p),
                 ("num_ops", ctypes.c_int32), ("dtype", ctypes.c_int32), ("num_inputs", ctypes.c_int32),
                 ("num_outputs", ctypes.c_int32), ("max_width", ctypes.c_int32),
-                ("tmp_features", ctypes.c_int32 * 2), ("saved_features", ctypes.c_int32 * 8)]
+                ("tmp_features", ctypes.c_int32 * 2), ("num_slots", ctypes.c_int32), ("saved_total", ctypes.c_int32),
+                ("slot_rows", ctypes.c_void_p)]
 
 
 def lib() -> ctypes.CDLL:
@@ -155,6 +160,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_plan_get_info.argtypes = [vp, ctypes.POINTER(PlanInfo)]
     L.ponni_plan_layer_param_count.restype = i64
     L.ponni_plan_layer_param_count.argtypes = [vp, i32]
+    L.ponni_plan_saved_state_size.restype = i32
+    L.ponni_plan_saved_state_size.argtypes = [vp, i32]
     L.ponni_plan_set_layer_params.restype = ctypes.c_int
     L.ponni_plan_set_layer_params.argtypes = [vp, i32, vp, i64]
     L.ponni_plan_share_layer_params.restype = ctypes.c_int

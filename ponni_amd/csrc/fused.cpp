@@ -351,7 +351,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   // per SIMD (so one wave's VALU epilogue overlaps another's MFMAs).
   if (!half) {
     int saved_tiles = 0;
-    for (int s = 0; s < kMaxSlots; s++) saved_tiles += tiles(p.saved_features[s]);
+    for (int s = 0; s < p.num_slots; s++) saved_tiles += tiles(p.saved_features[s]);
     int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 4 * es * 4;  // per workgroup (4 waves)
     if (regs + 32 > 256 && worst_saved_regs > 0 && regs - worst_saved_regs <= 224 &&
         cfg.lds_bytes + saved_bytes <= 80 * 1024) {
@@ -362,10 +362,6 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   cfg.waves_per_simd = regs <= 128 ? 4 : regs <= 168 ? 3 : regs <= 256 ? 2 : 1;
   if (half) cfg.waves_per_simd = half_wps;
   if (p.fused_wps > 0) cfg.waves_per_simd = p.fused_wps;  // measured by fused_compile
-  if (char const* w = std::getenv("PONNI_FUSED_WAVES_PER_SIMD")) {  // tuning override
-    int const v = std::atoi(w);
-    if (v >= 1 && v <= 8) cfg.waves_per_simd = v;
-  }
 
   // Waves per workgroup: LDS-staged parameters are copied once per
   // workgroup, so when copies would cap the resident workgroups below the
@@ -373,7 +369,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   {
     int saved_per_wave = 0;  // bytes of LDS-resident saved states per wave
     if (cfg.saved_in_lds)
-      for (int s = 0; s < kMaxSlots; s++) saved_per_wave += tiles(p.saved_features[s]) * NT * 64 * 4 * es;
+      for (int s = 0; s < p.num_slots; s++) saved_per_wave += tiles(p.saved_features[s]) * NT * 64 * 4 * es;
     int const target = 4 * cfg.waves_per_simd;  // waves per CU the registers allow
     int best = 0;
     for (int w = 4; w <= 16; w += 4) {
@@ -387,10 +383,6 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
       }
     }
   }
-  if (char const* w = std::getenv("PONNI_FUSED_WAVES")) {  // tuning override
-    int const v = std::atoi(w);
-    if (v == 4 || v == 8 || v == 12 || v == 16) cfg.waves = v;
-  }
   // A workgroup of 16-bit plans is one wave per SIMD per occupancy level: its
   // waves share the staged A fragments and the activation table.
   if (half) cfg.waves = 4 * std::min(cfg.waves_per_simd, half_wps);
@@ -399,28 +391,12 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   std::ostringstream o;
   std::string const IO = half ? E : dbl ? std::string("double") : std::string("float");
   o << "// generated by libponni_hip for one plan\n";
-  if (char const* d = std::getenv("PONNI_SETPRIO")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v == 0 || v == 1) o << "#define PONNI_SETPRIO " << v << "\n";
-  }
-  if (char const* d = std::getenv("PONNI_TILE_GROUP")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v >= 1 && v <= 4) o << "#define PONNI_TILE_GROUP " << v << "\n";
-  }
-  if (char const* d = std::getenv("PONNI_DEFER_EPILOGUE")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v == 0 || v == 1) o << "#define PONNI_DEFER_EPILOGUE " << v << "\n";
-  }
   // fp32 plans whose parameters sit in LDS or registers keep each dense
   // tile's epilogue among the next tile's MFMAs (fused_f32.h dense_ep; c2
   // and c5 2.8 / 3.5 % faster).  Plans streaming parameters from L2 keep the
   // compiler's order: measured neutral at their occupancy (c3), and the
   // registers it frees would move c3 to two waves per SIMD, 8 % slower.
-  int epi_interleave = (!half && !dbl && (cfg.lds_bytes > 0 || cfg.params_in_registers)) ? 16 : 0;
-  if (char const* d = std::getenv("PONNI_EPI_INTERLEAVE")) {  // tuning override
-    int const v = std::atoi(d);
-    if (v >= 0 && v <= 16) epi_interleave = v;
-  }
+  int const epi_interleave = (!half && !dbl && (cfg.lds_bytes > 0 || cfg.params_in_registers)) ? 16 : 0;
 
   if (dbl) o << "#define PONNI_REAL double\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
@@ -465,7 +441,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   std::map<int, int> slot_off;  // slot -> 4-vector offset in the wave's LDS region
   if (cfg.saved_in_lds) {
     int off = 0;
-    for (int sl = 0; sl < kMaxSlots; sl++)
+    for (int sl = 0; sl < p.num_slots; sl++)
       if (p.saved_features[sl] > 0) {
         slot_off[sl] = off;
         off += tiles(p.saved_features[sl]) * NT * 64;
@@ -479,9 +455,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   // fragments (a late global load would wait behind them: vmcnt is in order).
   // (Measured: c4 unchanged, c3 slower as a persistent fp32 kernel, so only
   // 16-bit plans, which are persistent anyway, stage them by default.)
-  bool stage_vecs = allow_vec_staging && half && cfg.lds_bytes == 0 && !cfg.params_in_registers;
-  if (char const* v = std::getenv("PONNI_STAGE_VECS"))  // tuning override
-    stage_vecs = allow_vec_staging && std::strcmp(v, "1") == 0 && cfg.lds_bytes == 0 && !cfg.params_in_registers;
+  bool const stage_vecs = allow_vec_staging && half && cfg.lds_bytes == 0 && !cfg.params_in_registers;
   std::map<int, std::pair<int, int>> vec_lds;  // packed offset -> (LDS offset, length)
   int vec_total = 0;
   auto vec = [&](int off, int n) -> std::string {
@@ -515,9 +489,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   int const in_rows_elems = tiles(n_in0) * 16 * 16 * NT;  // per wave, row-major 16-bit
   int const in_dma_bytes = cfg.waves * in_rows_elems * 2;
   int const stage_bytes = half && !dense_seq.empty() ? slots * slot_frags * 1024 : 0;
-  bool in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + stage_bytes + 16 * 1024 <= kFusedLdsBytes;
-  if (char const* v = std::getenv("PONNI_INPUT_DMA"))  // tuning override
-    in_dma = in_dma && std::strcmp(v, "0") != 0;
+  bool const in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + stage_bytes + 16 * 1024 <= kFusedLdsBytes;
   std::string const WCOLS = std::to_string(16 * NT), NW = std::to_string(cfg.waves);
   // The next tile's rows are requested inside the second dense layer, right
   // after its first chunk's weight loads (fused_f16.h dense_hs hook): waits
@@ -872,11 +844,7 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
   auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
   // U groups of V samples per lane, 256 * V samples apart, so that all of a
   // lane's input rows are in flight before its first FMA.
-  int U = 1;
-  if (char const* e = std::getenv("PONNI_NARROW_UNROLL")) {  // tuning override
-    int const v = std::atoi(e);
-    if (v >= 1 && v <= 8) U = v;
-  }
+  int const U = 1;
   cfg = FusedConfig{};
   cfg.waves = 4;
   cfg.waves_per_simd = 4;
@@ -1086,7 +1054,7 @@ int compile_cached(ponni_plan_s const& p, std::string& key, std::vector<char>& c
 // wave fewer, and when it fits the next occupancy's register budget (512 /
 // waves, a multiple of 8) without spills it moves up one.
 int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, std::string& error) {
-  if (p.path == PONNI_PATH_FUSED && p.fused_wps == 0 && std::getenv("PONNI_FUSED_WAVES_PER_SIMD") == nullptr) {
+  if (p.path == PONNI_PATH_FUSED && p.fused_wps == 0) {
     FusedConfig est;
     (void)fused_source(p, est);
     int wps = est.waves_per_simd;
@@ -1210,13 +1178,21 @@ hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t 
   void* y = a.y;
   int64_t ldx = a.ld_x, ldy = a.ld_y, batch = a.batch;
   void* args[] = {&params, &x, &ldx, &y, &ldy, &batch};
-  if (a.ev_start != nullptr || a.ev_stop != nullptr) {
-    unsigned const threads = 64u * unsigned(p.fused_waves);
-    return hipExtModuleLaunchKernel(p.fused_fn, static_cast<uint32_t>(grid) * threads, 1, 1, threads, 1, 1, 0, stream,
-                                    args, nullptr, a.ev_start, a.ev_stop, 0);
+  unsigned const threads = 64u * unsigned(p.fused_waves);
+  bool const timed = a.ev_start != nullptr || a.ev_stop != nullptr;
+  // The extended launch takes the global work size in 32 bits; a grid
+  // beyond that is timed by events recorded around an ordinary launch.
+  if (timed && uint64_t(grid) * threads <= UINT32_MAX)
+    return hipExtModuleLaunchKernel(p.fused_fn, static_cast<uint32_t>(uint64_t(grid) * threads), 1, 1, threads, 1, 1,
+                                    0, stream, args, nullptr, a.ev_start, a.ev_stop, 0);
+  if (timed && a.ev_start != nullptr) {
+    hipError_t const e = hipEventRecord(a.ev_start, stream);
+    if (e != hipSuccess) return e;
   }
-  return hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, 64 * p.fused_waves, 1, 1, 0, stream, args,
-                               nullptr);
+  hipError_t const e =
+      hipModuleLaunchKernel(p.fused_fn, static_cast<unsigned>(grid), 1, 1, threads, 1, 1, 0, stream, args, nullptr);
+  if (e != hipSuccess || !timed || a.ev_stop == nullptr) return e;
+  return hipEventRecord(a.ev_stop, stream);
 }
 
 }  // namespace ponni_hip

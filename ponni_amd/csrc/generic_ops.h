@@ -36,6 +36,28 @@ __host__ __device__ inline S* at(View2 const& v, int f, int64_t b) {
   return reinterpret_cast<S*>(v.base) + (int64_t(f) * v.ld + b);
 }
 
+// The state handles of one sample's pass: input, output, tmp1 and tmp2
+// (fixed[Buffer]), and the saved slots, which share one area of the same
+// row stride -- slot s holds rows slot_row[s] .. slot_row[s] +
+// get_saved_state_size<s>() - 1 of `saved` -- so a plan may use any number
+// of slots.  slot_row has at least one entry (0 for a plan with no slot).
+struct Bufs {
+  View2 fixed[BUF_SAVED];
+  View2 saved;
+  int32_t const* slot_row;
+};
+
+template <class S>
+__host__ __device__ inline View2 slot_view(Bufs const& B, int s) {
+  return View2{reinterpret_cast<char*>(reinterpret_cast<S*>(B.saved.base) + int64_t(B.slot_row[s]) * B.saved.ld),
+               B.saved.ld};
+}
+
+template <class S>
+__host__ __device__ inline View2 buf_view(Bufs const& B, int id) {
+  return id < BUF_SAVED ? B.fixed[id] : slot_view<S>(B, id - BUF_SAVED);
+}
+
 // Caller-implemented layers (OP_EXTERNAL) are evaluated by `ext`:
 // ext(index, flags, in, out, saved, n_in, n_out, b) with the state handles of
 // the op; the library's own kernels never see such an op.
@@ -49,11 +71,11 @@ struct NoExternal {
 template <class S, class Ext = NoExternal>
 __host__ __device__ __attribute__((always_inline)) inline void run_op(
     Op const op, Step const* __restrict__ steps, typename Compute<S>::type const* __restrict__ params,
-    View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext) {
+    Bufs const& buf, int64_t b, Ext const& ext) {
   using C = typename Compute<S>::type;
   {
-    View2 const in = buf[op.src];
-    View2 const out = buf[op.dst];
+    View2 const in = buf_view<S>(buf, op.src);
+    View2 const out = buf_view<S>(buf, op.dst);
     switch (op.code) {
       case OP_DENSE: {
         // ponni_Inference.h:431-444 with Matvec::compute_output (ponni_Matvec.h:70-79).
@@ -135,18 +157,18 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
         for (int f = 0; f < op.n_out; f++) {
           S const v = *at<S>(in, f, b);
           *at<S>(out, f, b) = v;
-          if (op.aux) *at<S>(buf[BUF_TMP1], f, b) = v;
+          if (op.aux) *at<S>(buf.fixed[BUF_TMP1], f, b) = v;
         }
         break;
       }
       case OP_ADD: {  // ponni_Binop_Add.h:57-68
-        View2 const sv = buf[BUF_SAVED + op.slot];
+        View2 const sv = slot_view<S>(buf, op.slot);
         for (int f = 0; f < op.n_out; f++)
           store_as<S, C>(at<S>(out, f, b), load_as<S>(at<S>(in, f, b)) + load_as<S>(at<S>(sv, f, b)));
         break;
       }
       case OP_CONCAT: {  // ponni_Binop_Concatenate.h:63-86
-        View2 const sv = buf[BUF_SAVED + op.slot];
+        View2 const sv = slot_view<S>(buf, op.slot);
         int const n1 = op.n_in;
         int const n2 = op.n_out - op.n_in;
         if (op.aux) {
@@ -163,7 +185,7 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
         break;
       }
       case OP_PROJ_ADD: {  // ponni_Binop_Projection_Add.h:81-95
-        View2 const sv = buf[BUF_SAVED + op.slot];
+        View2 const sv = slot_view<S>(buf, op.slot);
         int const nsave = op.aux;
         int const n = op.n_out;
         C const* w = params + op.woff;
@@ -175,9 +197,9 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
         break;
       }
       case OP_EXTERNAL: {
-        View2 const sv = buf[BUF_SAVED + op.slot];
+        View2 const sv = slot_view<S>(buf, op.slot);
         ext(op.aux, op.boff, in, out, sv, op.n_in, op.n_out, b);
-        if (op.boff & EXT_ALSO_TMP1) ext(op.aux, op.boff, in, buf[BUF_TMP1], sv, op.n_in, op.n_out, b);
+        if (op.boff & EXT_ALSO_TMP1) ext(op.aux, op.boff, in, buf.fixed[BUF_TMP1], sv, op.n_in, op.n_out, b);
         break;
       }
       case OP_LOAD: {  // the state becomes a saved one
@@ -185,7 +207,7 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
         break;
       }
       case OP_BINARY: {  // emitter.py:735-741 with scalar-or-exact broadcasting
-        View2 const sv = buf[BUF_SAVED + op.slot];
+        View2 const sv = slot_view<S>(buf, op.slot);
         int const bop = op.aux & 0xff;
         bool const saved_left = op.aux & BIN_SAVED_LEFT;
         C const s0 = load_as<S>(at<S>(in, 0, b));
@@ -200,8 +222,8 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
       case OP_SELECT: {  // interpreter.py:178-183 Where / CompareSelect: cond != 0 ? a : b
         // Operand k comes from the state, a saved slot or a constant vector;
         // a one-feature operand is read once, before an in-place write.
-        View2 const s1 = buf[BUF_SAVED + op.slot];
-        View2 const s2 = buf[BUF_SAVED + (op.f0 >= 0 ? static_cast<int>(op.f0) : op.slot)];
+        View2 const s1 = slot_view<S>(buf, op.slot);
+        View2 const s2 = slot_view<S>(buf, op.f0 >= 0 ? static_cast<int>(op.f0) : op.slot);
         int const scalar_bits[3] = {SEL_COND_SCALAR, SEL_A_SCALAR, SEL_B_SCALAR};
         int coff = op.woff;
         C const* cvec[3] = {nullptr, nullptr, nullptr};
@@ -268,7 +290,7 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
 template <class S, class Ext = NoExternal>
 __host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops, Step const* __restrict__ steps,
                                         typename Compute<S>::type const* __restrict__ params,
-                                        View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext = Ext()) {
+                                        Bufs const& buf, int64_t b, Ext const& ext = Ext()) {
   for (int o = 0; o < num_ops; o++) run_op<S, Ext>(ops[o], steps, params, buf, b, ext);
 }
 
@@ -277,14 +299,14 @@ __host__ __device__ inline void run_ops(Op const* __restrict__ ops, int num_ops,
 // (the op is a constant expression, so its switch and sizes fold).
 template <class S, class Program, int I, class Ext>
 __host__ __device__ __attribute__((always_inline)) inline void run_program_op(
-    typename Compute<S>::type const* __restrict__ params, View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b,
+    typename Compute<S>::type const* __restrict__ params, Bufs const& buf, int64_t b,
     Ext const& ext) {
   constexpr Op op = Program::ops[I];
   run_op<S, Ext>(op, Program::steps, params, buf, b, ext);
 }
 template <class S, class Program, class Ext, int... I>
 __host__ __device__ inline void run_program(typename Compute<S>::type const* __restrict__ params,
-                                            View2 const (&buf)[BUF_SAVED + kMaxSlots], int64_t b, Ext const& ext,
+                                            Bufs const& buf, int64_t b, Ext const& ext,
                                             std::integer_sequence<int, I...>) {
   (run_program_op<S, Program, I, Ext>(params, buf, b, ext), ...);
 }

@@ -24,21 +24,16 @@ template <class real>
 void run_range(ponni_plan_s const& t, real const* params, real const* x, int64_t ldx, real* y, int64_t ldy,
                int64_t b0, int64_t b1) {
   int const width = std::max({t.max_width, t.tmp_features[0], t.tmp_features[1], 1});
-  int saved_total = 0;
-  for (int s = 0; s < kMaxSlots; s++) saved_total += t.saved_features[s];
-  std::vector<real> tmp1(width), tmp2(width), saved(std::max(saved_total, 1));
-  View2 buf[BUF_SAVED + kMaxSlots];
-  buf[BUF_TMP1] = {reinterpret_cast<char*>(tmp1.data()), 1};
-  buf[BUF_TMP2] = {reinterpret_cast<char*>(tmp2.data()), 1};
-  int off = 0;
-  for (int s = 0; s < kMaxSlots; s++) {
-    buf[BUF_SAVED + s] = {reinterpret_cast<char*>(saved.data() + off), 1};
-    off += t.saved_features[s];
-  }
+  std::vector<real> tmp1(width), tmp2(width), saved(std::max(t.saved_total, 1));
+  Bufs buf;
+  buf.fixed[BUF_TMP1] = {reinterpret_cast<char*>(tmp1.data()), 1};
+  buf.fixed[BUF_TMP2] = {reinterpret_cast<char*>(tmp2.data()), 1};
+  buf.saved = {reinterpret_cast<char*>(saved.data()), 1};
+  buf.slot_row = t.slot_rows.data();
   int const num_ops = static_cast<int>(t.ops.size());
   for (int64_t b = b0; b < b1; b++) {
-    buf[BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(x + b)), ldx};
-    buf[BUF_OUTPUT] = {reinterpret_cast<char*>(y + b), ldy};
+    buf.fixed[BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(x + b)), ldx};
+    buf.fixed[BUF_OUTPUT] = {reinterpret_cast<char*>(y + b), ldy};
     run_ops<real>(t.ops.data(), num_ops, t.steps.data(), params, buf, 0);
   }
 }
@@ -100,7 +95,9 @@ int ponni_plan_host_model(ponni_plan plan, ponni_device_model* out) {
   out->max_width = t->max_width;
   out->tmp_features[0] = t->tmp_features[0];
   out->tmp_features[1] = t->tmp_features[1];
-  for (int s = 0; s < kMaxSlots; s++) out->saved_features[s] = t->saved_features[s];
+  out->num_slots = t->num_slots;
+  out->saved_total = t->saved_total;
+  out->slot_rows = t->slot_rows.data();
   return PONNI_OK;
 }
 

@@ -26,12 +26,11 @@ __global__ __launch_bounds__(256) void generic_forward(LaunchArgs args) {
   using C = typename Compute<S>::type;
   int64_t const b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= args.batch) return;
-  View2 buf[BUF_SAVED + kMaxSlots];
+  Bufs buf;
 #pragma unroll
-  for (int i = 0; i < BUF_SAVED + kMaxSlots; i++) {
-    buf[i].base = static_cast<char*>(args.buffers[i]);
-    buf[i].ld = args.buffer_ld[i];
-  }
+  for (int i = 0; i < BUF_SAVED; i++) buf.fixed[i] = View2{static_cast<char*>(args.buffers[i]), args.buffer_ld[i]};
+  buf.saved = View2{static_cast<char*>(args.buffers[BUF_SAVED]), args.buffer_ld[BUF_SAVED]};
+  buf.slot_row = args.slot_rows;
   run_ops<S>(args.ops, args.num_ops, args.steps, static_cast<C const*>(args.params), buf, b);
 }
 

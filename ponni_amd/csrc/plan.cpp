@@ -144,8 +144,8 @@ int64_t param_count(ponni_layer_desc const& d) {
 // Each layer's own validate() plus the chain check of Inference::validate.
 int validate_chain(ponni_layer_desc const* layers, int n) {
   std::string where;
-  int saved_size[kMaxSlots];
-  bool saved_seen[kMaxSlots] = {};
+  std::vector<int> saved_size(kMaxSlots, 0);
+  std::vector<char> saved_seen(kMaxSlots, 0);
   for (int i = 0; i < n; i++) {
     ponni_layer_desc const& d = layers[i];
     where = "layer " + std::to_string(i) + " (" + label_of(d.kind) + "): ";
@@ -157,7 +157,7 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
                             d.kind != PONNI_LAYER_SELECT;
     if (same_width && d.n_in != d.n_out) return fail(PONNI_ERR_INVALID_MODEL, where + "input/output size mismatch");
     if (is_save(d.kind) || reads_slot(d.kind) || ext_saves(d) || ext_reads(d)) {
-      if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
+      if (d.slot < 0 || d.slot >= kMaxSlots) return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0," + std::to_string(kMaxSlots) + ")");
     }
     if (ext_saves(d)) {
       saved_size[d.slot] = d.n_out;
@@ -218,7 +218,7 @@ int validate_chain(ponni_layer_desc const* layers, int n) {
         if (states != 1) return fail(PONNI_ERR_INVALID_MODEL, where + "exactly one operand is the state");
         if (o.src[0] == PONNI_SELECT_CONST) return fail(PONNI_ERR_INVALID_MODEL, where + "the condition is not a constant");
         if (o.num_slots == 2 && (d.attr[1] != static_cast<int>(d.attr[1]) || d.attr[1] < 0 || d.attr[1] >= kMaxSlots))
-          return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0,8)");
+          return fail(PONNI_ERR_INVALID_MODEL, where + "saved-state index out of range [0," + std::to_string(kMaxSlots) + ")");
         for (int k = 0; k < 3; k++) {
           int width = d.n_out;
           if (o.src[k] == PONNI_SELECT_STATE) width = d.n_in;
@@ -326,11 +326,24 @@ Step make_step(ponni_layer_desc const& d) {
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
+// Rows of the saved-slot area (generic_ops.h Bufs): slot s after slots
+// 0 .. s-1, each get_saved_state_size<s>() rows high.
+void set_slot_rows(ponni_plan_s& p) {
+  p.saved_features.resize(p.num_slots, 0);
+  p.slot_rows.assign(std::max(p.num_slots, 1), 0);
+  int32_t row = 0;
+  for (int s = 0; s < p.num_slots; s++) {
+    p.slot_rows[s] = row;
+    row += p.saved_features[s];
+  }
+  p.saved_total = row;
+}
+
 std::vector<int32_t> contractions_over_input(ponni_plan_s const& p) {
   bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
   if (p.path != PONNI_PATH_FUSED || half || p.layers.empty() || p.layers.front().n_in % 16 == 0) return {};
   bool cur = true;                 // the state holds the input
-  bool saved[kMaxSlots] = {};      // slot s holds the input
+  std::vector<char> saved(std::max(p.num_slots, 1), 0);  // slot s holds the input
   std::vector<int32_t> woffs;
   for (Op const& op : p.ops) {
     switch (op.code) {
@@ -609,6 +622,12 @@ void lower(ponni_plan_s& p) {
     // A load replaces the state with a saved one: it reads the slot and
     // writes where the state lives (or the output).
     if (d.kind == PONNI_LAYER_LOAD_STATE) op.src = BUF_SAVED + d.slot;
+    // An op that reads or writes no slot names slot 0, a valid row of the
+    // slot table whatever the layer's own (unchecked) slot field holds.
+    bool uses_slot = is_save(d.kind) || ext_saves(d) || ext_reads(d) ||
+                     (reads_slot(d.kind) && d.kind != PONNI_LAYER_SELECT);
+    if (d.kind == PONNI_LAYER_SELECT) uses_slot = select_operands(d).num_slots > 0;
+    if (!uses_slot) op.slot = 0;
     p.ops.push_back(op);
     i++;
   }
@@ -935,13 +954,25 @@ int upload(ponni_plan_s& p) {
   // Parameters may be read by a launch still in flight; the reference's
   // deep_copy fences as well.
   HIP_TRY(hipDeviceSynchronize());
-  if (p.d_ops == nullptr) {
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_ops), sizeof(Op) * kMaxOps));
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_steps), sizeof(Step) * kMaxSteps));
+  // The op list, its steps and the slot rows, each sized to the plan.
+  if (p.d_ops_count < std::max<size_t>(p.ops.size(), 1)) {
+    if (p.d_ops) HIP_TRY(hipFree(p.d_ops));
+    p.d_ops = nullptr;
+    p.d_ops_count = std::max<size_t>(p.ops.size(), 1);
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_ops), sizeof(Op) * p.d_ops_count));
   }
+  if (p.d_steps_count < std::max<size_t>(p.steps.size(), 1)) {
+    if (p.d_steps) HIP_TRY(hipFree(p.d_steps));
+    p.d_steps = nullptr;
+    p.d_steps_count = std::max<size_t>(p.steps.size(), 1);
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_steps), sizeof(Step) * p.d_steps_count));
+  }
+  if (p.d_slot_rows == nullptr)
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p.d_slot_rows), sizeof(int32_t) * p.slot_rows.size()));
   HIP_TRY(hipMemcpy(p.d_ops, p.ops.data(), sizeof(Op) * p.ops.size(), hipMemcpyHostToDevice));
   if (!p.steps.empty())
     HIP_TRY(hipMemcpy(p.d_steps, p.steps.data(), sizeof(Step) * p.steps.size(), hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(p.d_slot_rows, p.slot_rows.data(), sizeof(int32_t) * p.slot_rows.size(), hipMemcpyHostToDevice));
   std::vector<double> packed;
   std::vector<uint32_t> words;
   bool const half_fused = p.path == PONNI_PATH_FUSED && (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16);
@@ -973,6 +1004,14 @@ int upload(ponni_plan_s& p) {
   }
   int const st = build_gather(p);
   if (st != PONNI_OK) return st;
+  // A GENERIC plan's allocation-free forward carves its state buffers from
+  // the fixed per-device scratch; its address is looked up here, where
+  // loading the code object that holds it may allocate, so that
+  // ponni_forward_no_alloc never does that lookup first.
+  if (p.path == PONNI_PATH_GENERIC) {
+    void* base = nullptr;
+    HIP_TRY(static_scratch(dev, &base));
+  }
   p.device_dirty = false;
   return PONNI_OK;
 }
@@ -994,10 +1033,7 @@ int reallocate_scratch(ponni_plan_s& p, int64_t batch) {
     if (p.tmp_features[b] > 0)
       HIP_TRY(hipMalloc(&p.d_scratch[b], es * size_t(p.tmp_features[b]) * size_t(batch)));
   }
-  for (int s = 0; s < p.num_slots; s++) {
-    if (p.saved_features[s] > 0)
-      HIP_TRY(hipMalloc(&p.d_scratch[2 + s], es * size_t(p.saved_features[s]) * size_t(batch)));
-  }
+  if (p.saved_total > 0) HIP_TRY(hipMalloc(&p.d_scratch[2], es * size_t(p.saved_total) * size_t(batch)));
   return PONNI_OK;
 }
 
@@ -1035,7 +1071,6 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   if (out_plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "out_plan is null");
   *out_plan = nullptr;
   if (layers == nullptr || num_layers <= 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "a model needs at least one layer");
-  if (num_layers > kMaxOps) return fail(PONNI_ERR_INVALID_ARGUMENT, "too many layers (limit 256)");
   if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
   if (path < PONNI_PATH_AUTO || path > PONNI_PATH_FUSED) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
   int const st = validate_chain(layers, num_layers);
@@ -1055,11 +1090,13 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
                           d.kind == PONNI_LAYER_BINOP_PROJECTION_ADD || d.kind == PONNI_LAYER_BINARY ? d.n_aux : 0});
     if (is_save(d.kind) || ext_saves(d)) {
       p->num_slots = std::max(p->num_slots, d.slot + 1);
+      if (static_cast<int>(p->saved_features.size()) <= d.slot) p->saved_features.resize(d.slot + 1, 0);
       p->saved_features[d.slot] = std::max(p->saved_features[d.slot], d.n_out);
     }
     if (d.kind == PONNI_LAYER_EXTERNAL) p->external = true;
   }
   p->max_width = max_width;
+  set_slot_rows(*p);
   // LayerNorm defaults are gamma = 1, beta = 0 (ponni_LayerNorm.h:39-45).
   for (int i = 0; i < num_layers; i++)
     if (layers[i].kind == PONNI_LAYER_LAYER_NORM)
@@ -1131,6 +1168,10 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   p->path = chosen;
   p->width_class = chosen == PONNI_PATH_NARROW ? narrow_w : chosen == PONNI_PATH_MFMA ? mfma : 0;
   lower(*p);
+  if (p->packed_elements > INT32_MAX) {
+    delete p;
+    return fail(PONNI_ERR_UNSUPPORTED, "the model's parameters exceed 2^31 elements");
+  }
   p->narrow_jit = chosen == PONNI_PATH_NARROW && jit_enabled && narrow_jit_supports(*p);
   *out_plan = p;
   return PONNI_OK;
@@ -1146,6 +1187,7 @@ void ponni_plan_destroy(ponni_plan plan) {
     release_scratch(*plan);
     if (plan->d_ops) (void)hipFree(plan->d_ops);
     if (plan->d_steps) (void)hipFree(plan->d_steps);
+    if (plan->d_slot_rows) (void)hipFree(plan->d_slot_rows);
     if (plan->d_params) (void)hipFree(plan->d_params);
     if (plan->d_gather) (void)hipFree(plan->d_gather);
     if (plan->d_gather_src) (void)hipFree(plan->d_gather_src);
@@ -1166,7 +1208,7 @@ int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info) {
   info->num_saved_states = plan->num_slots;
   info->tmp1_features = plan->tmp_features[0];
   info->tmp2_features = plan->tmp_features[1];
-  for (int s = 0; s < kMaxSlots; s++) info->saved_features[s] = plan->saved_features[s];
+  for (int s = 0; s < 8 && s < plan->num_slots; s++) info->saved_features[s] = plan->saved_features[s];
   int64_t total = 0;
   for (auto const& v : plan->params) total += static_cast<int64_t>(v.size());
   info->num_parameters = total;
@@ -1174,6 +1216,15 @@ int ponni_plan_get_info(ponni_plan plan, ponni_plan_info* info) {
   info->max_width = plan->max_width;
   info->width_class = plan->width_class;
   return PONNI_OK;
+}
+
+int32_t ponni_plan_saved_state_size(ponni_plan plan, int32_t slot) {
+  if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null"), -1;
+  if (slot < 0 || slot >= plan->num_slots)
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "saved-state slot " + std::to_string(slot) + " out of range [0," +
+                                                std::to_string(plan->num_slots) + ")"),
+           -1;
+  return plan->saved_features[slot];
 }
 
 int64_t ponni_plan_layer_param_count(ponni_plan plan, int32_t layer) {
@@ -1283,11 +1334,11 @@ namespace {
 // Bytes of GENERIC state buffers (tmp1, tmp2, saved slots) for `batch`
 // columns when carved from one array, each buffer 256-byte aligned; fills
 // the byte offset of each (-1: not used).
-size_t carved_scratch_bytes(ponni_plan_s const& p, int64_t batch, int64_t (&offset)[2 + kMaxSlots]) {
+size_t carved_scratch_bytes(ponni_plan_s const& p, int64_t batch, int64_t (&offset)[3]) {
   size_t const es = element_size(p.dtype);
   size_t total = 0;
-  for (int b = 0; b < 2 + kMaxSlots; b++) {
-    int const features = b < 2 ? p.tmp_features[b] : (b - 2 < p.num_slots ? p.saved_features[b - 2] : 0);
+  for (int b = 0; b < 3; b++) {
+    int const features = b < 2 ? p.tmp_features[b] : p.saved_total;
     offset[b] = -1;
     if (features <= 0) continue;
     offset[b] = static_cast<int64_t>(total);
@@ -1306,11 +1357,17 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   if (x == nullptr || y == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "input or output pointer is null");
   if (ld_in < batch || ld_out < batch)
     return fail(PONNI_ERR_SHAPE, "Error: Provided output dimensions do not match the model and input batch");
+  bool const was_dirty = plan->device_dirty;
   if (plan->num_shared_host > 0) {
     int const st = pull_shared(*plan, false);
     if (st != PONNI_OK) return st;
   }
   if (plan->device_dirty) {
+    if (no_alloc && !was_dirty)
+      return fail(PONNI_ERR_INVALID_ARGUMENT,
+                  "ponni_forward_no_alloc: a host array shared with the plan (ponni_plan_share_layer_params, "
+                  "on_device = 0) changed since the plan was last put on the device; one ponni_forward call, "
+                  "which may allocate, uploads the new values (share device arrays to refresh them without one)");
     if (no_alloc)
       return fail(PONNI_ERR_INVALID_ARGUMENT,
                   "ponni_forward_no_alloc: the plan is not on the device yet (its parameters changed or it never "
@@ -1322,11 +1379,11 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(PONNI_ERR_DEVICE, "plan was first used on another device");
   }
-  void* scratch[2 + kMaxSlots] = {};
+  void* scratch[3] = {};  // tmp1, tmp2, the saved-slot area
   int64_t scratch_ld = 0;
   if (no_alloc) {
     if (plan->path == PONNI_PATH_GENERIC) {
-      int64_t offset[2 + kMaxSlots];
+      int64_t offset[3];
       size_t const need = carved_scratch_bytes(*plan, batch, offset);
       if (need > kStaticScratchBytes)
         return fail(PONNI_ERR_SHAPE, "ponni_forward_no_alloc: batch " + std::to_string(batch) + " needs " +
@@ -1334,7 +1391,7 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
                                          std::to_string(kStaticScratchBytes) + " bytes (use ponni_forward)");
       void* base = nullptr;
       if (need > 0) HIP_TRY(static_scratch(plan->device, &base));
-      for (int b = 0; b < 2 + kMaxSlots; b++)
+      for (int b = 0; b < 3; b++)
         if (offset[b] >= 0) scratch[b] = static_cast<char*>(base) + offset[b];
       scratch_ld = batch;
     }
@@ -1345,7 +1402,7 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
     } else if (batch > plan->capacity) {
       plan->capacity = batch;  // register paths keep no batch scratch
     }
-    for (int b = 0; b < 2 + kMaxSlots; b++) scratch[b] = plan->d_scratch[b];
+    for (int b = 0; b < 3; b++) scratch[b] = plan->d_scratch[b];
     scratch_ld = plan->capacity;
   }
   LaunchArgs a{};
@@ -1365,10 +1422,11 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   a.buffer_ld[BUF_INPUT] = ld_in;
   a.buffers[BUF_OUTPUT] = y;
   a.buffer_ld[BUF_OUTPUT] = ld_out;
-  for (int b = 0; b < 2 + kMaxSlots; b++) {
+  for (int b = 0; b < 3; b++) {
     a.buffers[BUF_TMP1 + b] = scratch[b];
     a.buffer_ld[BUF_TMP1 + b] = scratch_ld;
   }
+  a.slot_rows = plan->d_slot_rows;
   a.ev_start = ev_start;
   a.ev_stop = ev_stop;
   hipError_t err = hipSuccess;
@@ -1461,14 +1519,11 @@ int64_t ponni_plan_program_source(ponni_plan plan, char* buf, int64_t len) {
   if (t->steps.empty()) o << "      {},\n";
   o << "  };\n";
   o << "  static constexpr int tmp_features[2] = {" << t->tmp_features[0] << ", " << t->tmp_features[1] << "};\n";
-  int total = 0;
-  o << "  static constexpr int saved_features[" << kMaxSlots << "] = {";
-  for (int sl = 0; sl < kMaxSlots; sl++) {
-    o << (sl ? ", " : "") << t->saved_features[sl];
-    total += t->saved_features[sl];
-  }
+  o << "  static constexpr int num_slots = " << t->num_slots << ";\n";
+  o << "  static constexpr int32_t slot_rows[" << t->slot_rows.size() << "] = {";
+  for (size_t sl = 0; sl < t->slot_rows.size(); sl++) o << (sl ? ", " : "") << t->slot_rows[sl];
   o << "};\n";
-  o << "  static constexpr int saved_total = " << total << ";\n";
+  o << "  static constexpr int saved_total = " << t->saved_total << ";\n";
   std::string const src = o.str();
   int64_t const need = static_cast<int64_t>(src.size()) + 1;
   if (buf != nullptr) {
@@ -1530,7 +1585,9 @@ ponni_plan_s* generic_twin(ponni_plan_s& plan) {
     t->num_slots = plan.num_slots;
     t->external = plan.external;
     t->max_width = plan.max_width;
-    for (int s = 0; s < kMaxSlots; s++) t->saved_features[s] = plan.saved_features[s];
+    t->saved_features = plan.saved_features;
+    t->slot_rows = plan.slot_rows;
+    t->saved_total = plan.saved_total;
     t->path = PONNI_PATH_GENERIC;
     t->width_class = 0;
     lower(*t);
@@ -1583,7 +1640,9 @@ int ponni_plan_device_model(ponni_plan plan, ponni_device_model* out) {
   out->max_width = t.max_width;
   out->tmp_features[0] = t.tmp_features[0];
   out->tmp_features[1] = t.tmp_features[1];
-  for (int s = 0; s < kMaxSlots; s++) out->saved_features[s] = t.saved_features[s];
+  out->num_slots = t.num_slots;
+  out->saved_total = t.saved_total;
+  out->slot_rows = t.d_slot_rows;
   return PONNI_OK;
 }
 

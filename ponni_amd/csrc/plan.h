@@ -30,9 +30,11 @@ struct LaunchArgs {
   int64_t batch;
   int32_t num_inputs;
   int32_t num_outputs;
-  // generic path scratch (unused elsewhere)
-  void* buffers[BUF_SAVED + kMaxSlots];
-  int64_t buffer_ld[BUF_SAVED + kMaxSlots];
+  // generic path: input, output, tmp1, tmp2, then the saved-slot area
+  // (unused elsewhere), and the slot row table of that area (generic_ops.h Bufs)
+  void* buffers[BUF_SAVED + 1];
+  int64_t buffer_ld[BUF_SAVED + 1];
+  const int32_t* slot_rows;
   // Host side only (kernels ignore them): events the runtime stamps with the
   // start and end of the kernel's own dispatch (ponni_forward_timed), or null.
   hipEvent_t ev_start;
@@ -129,7 +131,11 @@ struct ponni_plan_s {
   bool external = false;           // holds PONNI_LAYER_EXTERNAL layers
   int32_t num_fused_blocks = 0;
   int32_t tmp_features[2] = {0, 0};
-  int32_t saved_features[ponni_hip::kMaxSlots] = {};
+  std::vector<int32_t> saved_features;  // per slot, num_slots entries
+  // Row of each slot in the saved-state area (max(num_slots, 1) entries)
+  // and the area's height, the sum of the slots' widths.
+  std::vector<int32_t> slot_rows;
+  int32_t saved_total = 0;
 
   // Host master copy of every layer's parameters (exact in double).
   std::vector<std::vector<double>> params;
@@ -145,9 +151,11 @@ struct ponni_plan_s {
   int device = -1;
   ponni_hip::Op* d_ops = nullptr;
   ponni_hip::Step* d_steps = nullptr;
+  int32_t* d_slot_rows = nullptr;
+  size_t d_ops_count = 0, d_steps_count = 0;  // capacities of d_ops / d_steps
   void* d_params = nullptr;
   size_t d_params_bytes = 0;
-  void* d_scratch[2 + ponni_hip::kMaxSlots] = {};  // tmp1, tmp2, saved slots
+  void* d_scratch[3] = {};  // tmp1, tmp2, the saved-slot area
   int64_t capacity = 0;
 
   // GENERIC twin of this plan for ponni_plan_device_model (created on first

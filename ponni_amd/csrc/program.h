@@ -165,8 +165,9 @@ struct Op {
   double f0, f1, f2;  // scalar attributes (epsilon, out_min, out_max), exact for F64 plans
 };
 
-constexpr int kMaxSlots = 8;  // saved-state slots a plan may use
-constexpr int kMaxOps = 256;
-constexpr int kMaxSteps = 512;
+// Saved-state slot indices a plan may use: 0 .. kMaxSlots - 1.  Slots are
+// sized from the plan (one area, Bufs in generic_ops.h); the bound only
+// keeps the per-slot table small for a stray index.
+constexpr int kMaxSlots = 4096;
 
 }  // namespace ponni_hip

@@ -677,7 +677,7 @@ def _weight_column(c: dict, wname: str, nout: int, nmap: int, k: int) -> np.ndar
     return np.asarray(c[wname], dtype=np.float64).reshape(nout, nmap)[:, k]
 
 
-def lower_graph(graph: Graph, max_slots: int = 8) -> LoweredGraph:
+def lower_graph(graph: Graph, max_slots: int = A.MAX_SLOTS) -> LoweredGraph:
     """Linearize `graph` into a layer chain over one state and saved slots.
 
     Each node's operands must be in the state or in a slot; a tensor that is

@@ -23,16 +23,15 @@
 namespace ponni {
 
 // Thread-private state limits of forward_one: the widest state of the chain
-// (MAXW features) and all saved slots together (MAXSAVED features).
+// (MAXW features) and all saved slots together (MAXSAVED features, any
+// number of slots).
 constexpr int kInKernelMaxWidth = 256;
 constexpr int kInKernelMaxSaved = 512;
 
 // Can forward_one<real, MAXW, MAXSAVED> evaluate this model?
 template <int MAXW = kInKernelMaxWidth, int MAXSAVED = kInKernelMaxSaved>
 __host__ __device__ inline bool fits_in_kernel(ponni_device_model const& m) {
-  int saved = 0;
-  for (int s = 0; s < 8; s++) saved += m.saved_features[s];
-  return m.max_width <= MAXW && m.tmp_features[0] <= MAXW && m.tmp_features[1] <= MAXW && saved <= MAXSAVED;
+  return m.max_width <= MAXW && m.tmp_features[0] <= MAXW && m.tmp_features[1] <= MAXW && m.saved_total <= MAXSAVED;
 }
 
 // One sample: out[f * out_ld] = model(in[k * in_ld]) for f < num_outputs.
@@ -53,16 +52,13 @@ __host__ __device__ inline void forward_one(ponni_device_model const& m, real co
   }
   real tmp[2][MAXW];
   real saved[MAXSAVED];
-  ponni_hip::View2 buf[ponni_hip::BUF_SAVED + ponni_hip::kMaxSlots];
-  buf[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
-  buf[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
-  buf[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp[0]), 1};
-  buf[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp[1]), 1};
-  int off = 0;
-  for (int s = 0; s < ponni_hip::kMaxSlots; s++) {
-    buf[ponni_hip::BUF_SAVED + s] = {reinterpret_cast<char*>(saved + off), 1};
-    off += m.saved_features[s];
-  }
+  ponni_hip::Bufs buf;
+  buf.fixed[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
+  buf.fixed[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
+  buf.fixed[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp[0]), 1};
+  buf.fixed[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp[1]), 1};
+  buf.saved = {reinterpret_cast<char*>(saved), 1};
+  buf.slot_row = m.slot_rows;
   ponni_hip::run_ops<real>(static_cast<ponni_hip::Op const*>(m.ops), m.num_ops,
                            static_cast<ponni_hip::Step const*>(m.steps), static_cast<real const*>(m.params), buf,
                            0, ext);
@@ -85,16 +81,13 @@ __host__ __device__ inline void forward_one_program(void const* params, real con
   constexpr int t2 = Program::tmp_features[1] > 0 ? Program::tmp_features[1] : 1;
   constexpr int sv = Program::saved_total > 0 ? Program::saved_total : 1;
   real tmp1[t1], tmp2[t2], saved[sv];
-  ponni_hip::View2 buf[ponni_hip::BUF_SAVED + ponni_hip::kMaxSlots];
-  buf[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
-  buf[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
-  buf[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp1), 1};
-  buf[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp2), 1};
-  int off = 0;
-  for (int s = 0; s < ponni_hip::kMaxSlots; s++) {
-    buf[ponni_hip::BUF_SAVED + s] = {reinterpret_cast<char*>(saved + off), 1};
-    off += Program::saved_features[s];
-  }
+  ponni_hip::Bufs buf;
+  buf.fixed[ponni_hip::BUF_INPUT] = {reinterpret_cast<char*>(const_cast<real*>(in)), in_ld};
+  buf.fixed[ponni_hip::BUF_OUTPUT] = {reinterpret_cast<char*>(out), out_ld};
+  buf.fixed[ponni_hip::BUF_TMP1] = {reinterpret_cast<char*>(tmp1), 1};
+  buf.fixed[ponni_hip::BUF_TMP2] = {reinterpret_cast<char*>(tmp2), 1};
+  buf.saved = {reinterpret_cast<char*>(saved), 1};
+  buf.slot_row = Program::slot_rows;
   ponni_hip::run_program<real, Program, Ext>(static_cast<real const*>(params), buf, 0, ext,
                                              std::make_integer_sequence<int, Program::num_ops>());
 }

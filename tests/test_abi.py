@@ -58,7 +58,8 @@ def test_validation_errors():
     expect_error([P.Elu(2, 0.0)], A.PONNI_ERR_INVALID_MODEL, "ELU alpha")
     expect_error([P.LayerNorm(np.ones(2), np.zeros(2), 0.0)], A.PONNI_ERR_INVALID_MODEL, "epsilon")
     expect_error([P.MinMaxNorm(2, 1.0, 1.0)], A.PONNI_ERR_INVALID_MODEL, "out_max > out_min")
-    expect_error([P.Save_State(9, 2)], A.PONNI_ERR_INVALID_MODEL, "index out of range")
+    expect_error([P.Save_State(4096, 2)], A.PONNI_ERR_INVALID_MODEL, "index out of range")
+    expect_error([P.Save_State(-1, 2)], A.PONNI_ERR_INVALID_MODEL, "index out of range")
     expect_error([P.Matvec(np.ones((40, 40)))], A.PONNI_ERR_UNSUPPORTED, "NARROW", path="narrow")
     expect_error([P.Matvec(np.ones((2, 2)))], A.PONNI_ERR_UNSUPPORTED, "MFMA", path="mfma", dtype="f64")
 
@@ -82,9 +83,12 @@ def test_scratch_planning_matches_reference_rules(seed):
     rng = np.random.default_rng(seed)
     layers = random_chain(rng, [3, 8, 20, 33][seed % 4], 2 + seed % 4)
     inf = create(layers, path="generic").info()
+    m = create(layers, path="generic")
     tmp, saved = oracle.plan_widths(layers)
     assert [inf.tmp1_features, inf.tmp2_features] == tmp
-    assert list(inf.saved_features) == saved
+    assert inf.num_saved_states == len(saved)
+    assert list(inf.saved_features)[:len(saved)] == saved[:8]
+    assert [A.lib().ponni_plan_saved_state_size(m._plan, s) for s in range(len(saved))] == saved
 
 
 def test_reference_scratch_answers():

@@ -15,6 +15,7 @@ import pytest
 
 import oracle
 import ponni_amd as P
+from ponni_amd import _abi as A
 from ponni_amd import configs as C
 from ponni_amd import graph as G
 from tests import numpy_graph as NG
@@ -231,14 +232,18 @@ def test_random_graphs_oracle_vs_numpy(seed):
 
 
 def test_slot_reuse_and_limit():
-    # 9 tensors live at once overflow the 8 saved-state slots.
+    # 9 tensors live at once take at least eight saved slots: fine by
+    # default, too many for a linearization capped below what it uses.
     g = G.GraphBuilder(4)
     xs = [g.unary("Relu", g.dense(g.input, np.eye(4), None, name=f"b{i}")) for i in range(9)]
     acc = xs[0]
     for t in xs[1:]:
         acc = g.binary("Add", acc, t)
+    gr = g.finish(acc)
+    used = len({l.slot for l in G.lower_graph(gr).layers if l.kind == A.LAYER_SAVE_STATE})
+    assert used >= 8
     with pytest.raises(G.GraphError, match="live saved tensors"):
-        G.lower_graph(g.finish(acc))
+        G.lower_graph(gr, max_slots=used - 1)
     # A chain reuses slot 0 after each tensor's last use.
     g = G.GraphBuilder(4)
     t = g.input

@@ -109,7 +109,8 @@ def test_host_model_description():
     d = A.DeviceModel()
     A.check(A.lib().ponni_plan_host_model(m._plan, ctypes.byref(d)))
     assert d.num_inputs == 4 and d.num_outputs == 10 and d.dtype == A.F64 and d.num_ops > 0
-    assert d.saved_features[0] == 4 and d.ops and d.params
+    assert d.num_slots == 1 and d.saved_total == 4 and d.ops and d.params
+    assert ctypes.cast(d.slot_rows, ctypes.POINTER(ctypes.c_int32))[0] == 0
     # The host parameters are readable host memory: the Matvec's 24 ones.
     vals = np.ctypeslib.as_array(ctypes.cast(d.params, ctypes.POINTER(ctypes.c_double)), shape=(24,))
     assert np.array_equal(vals, np.ones(24))

@@ -1,0 +1,135 @@
+"""Plans with many saved-state slots.
+
+The reference takes any Save_State<ISAVE> index and sizes each slot from
+the chain (src/layers/ponni_Save_State.h:7-83; get_saved_state_size,
+src/ponni_Inference.h:204-223).  These tests hold chains whose slot count
+no fixed table covers:
+
+- a 42-block residual chain that keeps 12 states live at once (U-shaped:
+  12 saves, then 12 adds in reverse order), then reuses three slots;
+- a chain whose only slot index is 100 (101 slots, 100 of them unused);
+- a generated graph with 12 branches all live at the same time.
+
+CPU: the scratch planning against the reference rules (the oracle's
+plan_widths), the per-slot size query, and host execution (the plan's
+GENERIC op list on host threads) against the oracle.  GPU: every kernel
+family that takes the plan, against the oracle at the fp32 bars."""
+import numpy as np
+import pytest
+
+import oracle
+import ponni_amd as P
+from ponni_amd import _abi as A
+from ponni_amd import graph as G
+from tests.test_graph import lowered_with_params
+import tests.numpy_graph as NG
+
+
+def u_shaped(width=32, live=12, tail=16, seed=0):
+    rng = np.random.default_rng(seed)
+
+    def W(a, b):
+        return rng.standard_normal((a, b)) * (0.5 / np.sqrt(a))
+
+    def b(n):
+        return rng.uniform(-0.1, 0.1, n)
+
+    L = [P.Matvec(W(8, width)), P.Bias(b(width)), P.Tanh(width)]
+    for k in range(live):
+        L += [P.Save_State(k, width), P.Matvec(W(width, width)), P.Bias(b(width)), P.Gelu(width, True)]
+    for k in reversed(range(live)):
+        L += [P.Binop_Add(k, width), P.LayerNorm(width), P.Matvec(W(width, width)), P.Tanh(width)]
+    for j in range(tail):
+        s = j % 3
+        L += [P.Save_State(s, width), P.Matvec(W(width, width)), P.Bias(b(width)), P.Relu(width), P.Binop_Add(s, width)]
+    L += [P.Matvec(W(width, 4))]
+    return L
+
+
+def sparse_slot(width=24, seed=1):
+    rng = np.random.default_rng(seed)
+    return [P.Matvec(rng.standard_normal((6, width)) * 0.4), P.Tanh(width), P.Save_State(100, width),
+            P.Matvec(rng.standard_normal((width, width)) * 0.2), P.Sigmoid(width), P.Binop_Add(100, width),
+            P.Binop_Concatenate(100, width, 2 * width, False), P.Matvec(rng.standard_normal((2 * width, 3)) * 0.3)]
+
+
+def branches_graph(n_branch=12, n_in=10, width=20, seed=2):
+    """n_branch Dense + Tanh branches of the input, all computed before the
+    first of the Adds that sum them, then a Dense output."""
+    rng = np.random.default_rng(seed)
+    g = G.GraphBuilder(n_in)
+    br = [g.unary("Tanh", g.dense(g.input, rng.standard_normal((width, n_in)) * 0.4, rng.uniform(-0.1, 0.1, width),
+                                  name=f"branch{k}")) for k in range(n_branch)]
+    acc = br[0]
+    for t in br[1:]:
+        acc = g.binary("Add", acc, t)
+    return g.finish(g.dense(acc, rng.standard_normal((5, width)) * 0.2, name="head"))
+
+
+def check(got, want):
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    err = np.abs(got - want).max()
+    assert np.isfinite(got).all()
+    assert rel <= 1e-5 and err <= 1e-4 * max(1.0, np.abs(want).max()), f"relL2={rel:.3e} maxabs={err:.3e}"
+
+
+@pytest.mark.parametrize("make", [u_shaped, sparse_slot])
+def test_planning_and_host_execution(make):
+    layers = make()
+    m = P.create_inference_model(*layers, path="generic")
+    inf = m.info()
+    tmp, saved = oracle.plan_widths(layers)
+    assert inf.num_saved_states == len(saved) and len(saved) in (12, 101)
+    assert [inf.tmp1_features, inf.tmp2_features] == tmp
+    assert [A.lib().ponni_plan_saved_state_size(m._plan, s) for s in range(len(saved))] == saved
+    assert A.lib().ponni_plan_saved_state_size(m._plan, len(saved)) == -1
+    x = np.random.default_rng(3).standard_normal((layers[0].n_in, 777)).astype(np.float32)
+    check(m.forward_host(x), oracle.forward(layers, x))
+    # The default path takes the plan too (FUSED keeps the slots on chip).
+    assert P.create_inference_model(*layers).path in ("fused", "generic")
+
+
+def test_graph_with_twelve_live_branches_lowers():
+    gr = branches_graph()
+    gm = G.GeneratedModel(gr)
+    saves = [L for L in gm.lowered.layers if L.kind == A.LAYER_SAVE_STATE]
+    assert len({L.slot for L in saves}) >= 11
+    x = np.random.default_rng(4).standard_normal((10, 300))
+    want = NG.run_graph(gr, x)
+    got = oracle.forward(lowered_with_params(gr), x, oracle.MODE_F64)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["generic", "fused"])
+@pytest.mark.parametrize("make", [u_shaped, sparse_slot])
+def test_many_slots_on_gpu(cuda, make, path):
+    import torch
+
+    layers = make()
+    m = P.create_inference_model(*layers, path=path)
+    assert m.path == path
+    B = 20_011
+    print(f"many slots: {make.__name__} path={path} B={B} slots={m.info().num_saved_states}", flush=True)
+    x = torch.from_numpy(np.random.default_rng(5).standard_normal((layers[0].n_in, B)).astype(np.float32)).cuda()
+    y = m.forward_batch_parallel(x)
+    torch.cuda.synchronize()
+    check(y.cpu().numpy().astype(np.float64), oracle.forward(layers, x.cpu().numpy()).astype(np.float64))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["generic", "fused"])
+def test_graph_with_twelve_live_branches_on_gpu(cuda, path):
+    import torch
+
+    gr = branches_graph()
+    gm = G.GeneratedModel(gr, path=path)
+    assert gm.plan("f32").path == path
+    B = 4_099
+    print(f"twelve-branch graph: path={path} B={B}", flush=True)
+    x = np.random.default_rng(6).standard_normal((10, B))
+    xt = torch.from_numpy(x.astype(np.float32)).cuda()
+    y = torch.full((gm.num_outputs, B), float("nan"), dtype=torch.float32, device="cuda:0")
+    gm.infer_batch(xt, y)
+    torch.cuda.synchronize()
+    check(y.double().cpu().numpy(), oracle.forward(lowered_with_params(gr), xt.double().cpu().numpy()))
