@@ -230,8 +230,8 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
             "frac_per_step": round(work * B / (ms_per_step * 1e-3) / cfg.peak, 4),
             # (PMC traffic is measured for the configurations' own precision and batch only)
             "traffic": (pmc_traffic(cfg.name)
-                        if cfg.dtype == C.CONFIGS[cfg.name].dtype and cfg.batch == C.CONFIGS[cfg.name].batch
-                        else None),
+                        if cfg.name in C.CONFIGS and cfg.dtype == C.CONFIGS[cfg.name].dtype
+                        and cfg.batch == C.CONFIGS[cfg.name].batch else None),
         },
         "path": model.path,
     }
@@ -347,7 +347,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    cfg = with_dtype(C.CONFIGS[args.config], args.dtype, C)
+    cfg = with_dtype({**C.CONFIGS, **C.SUPPLEMENTARY}[args.config], args.dtype, C)
     if args.batch:
         cfg = dataclasses.replace(cfg, batch=args.batch)
     head = time_config(cfg, args.steps, args.warmup, torch, P, C, ev)
@@ -358,6 +358,7 @@ def main() -> int:
         runs.append(("c1_large", dataclasses.replace(
             C.CONFIGS["c1"], batch=C1_LARGE_BATCH,
             description=C.CONFIGS["c1"].description + ", supplementary batch of 67,108,864 (not a BASELINE config)")))
+        runs += list(C.SUPPLEMENTARY.items())
         for name, c in runs:
             r = time_config(c, max(10, args.steps // 2), args.warmup, torch, P, C, ev)
             others[name] = {

@@ -18,6 +18,9 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libponni_oracle.so"
 
 MODE_F32, MODE_F64, MODE_F16_OPERANDS, MODE_BF16_OPERANDS, MODE_F16_CHAIN, MODE_F16_HALF2 = 0, 1, 2, 3, 4, 5
+# Modes 2 / 3 with every dense dot product summed in 32-feature blocks: a
+# second fp32 order, for measuring a chain's sensitivity to summation order.
+MODE_F16_OPERANDS_BLOCKED, MODE_BF16_OPERANDS_BLOCKED = 6, 7
 
 _lib = None
 

@@ -26,7 +26,12 @@
 // template half model (half_t: v += W * x rounds the product and the sum),
 // 5 fp16 chain of the generated half2 model (each dot-product step one
 // rounded fma, ponni_TwoHalf.h:97-105; activations in fp32 of the half value,
-// rounded, :138-153).
+// rounded, :138-153), 6 / 7 as 2 / 3 with every dense dot product summed in
+// 32-feature blocks (each block's products summed exactly, then added to the
+// fp32 running sum with one rounding: the k-blocking of a 32-deep matrix
+// instruction).  Modes 6 and 7 are not a restatement of the reference: they
+// are a second legitimate fp32 order, which tests use to measure how far a
+// chain's result moves under a change of summation order.
 //
 // Pinning: tests/test_oracle.py checks every function here against the
 // reference's known-answer tests (unit/core/*.cpp, unit/performance_benchmark)
@@ -321,8 +326,8 @@ struct Ctx {
   int mode = 0;
   T store(T v) const {
     if constexpr (std::is_same_v<T, float>) {
-      if (mode == 2) return round_half(v);
-      if (mode == 3) return round_bf16(v);
+      if (mode == 2 || mode == 6) return round_half(v);
+      if (mode == 3 || mode == 7) return round_bf16(v);
     }
     return v;
   }
@@ -526,11 +531,18 @@ void run_sample(Ctx<T> const& c, Buf<T> x, Buf<T> y, Buf<T> tmp1, Buf<T> tmp2, B
       bool const bias = generated && (d.flags & PONNI_FLAG_DENSE_BIAS);
       for (int f = 0; f < d.n_out; f++) {  // compute_fused_dense_block, ponni_Inference.h:431-444
         T v = T(0);
-        if (generated) {  // emitter.py:701-710: sum = bias; sum += W[f][k] x[k]
-          if (bias) v = T(w[int64_t(d.n_out) * d.n_in + f]);
-          for (int k = 0; k < d.n_in; k++) v = dense_step(c, v, T(w[int64_t(f) * d.n_in + k]), in(k, b));
+        if (generated && bias) v = T(w[int64_t(d.n_out) * d.n_in + f]);  // emitter.py:701-710: sum = bias
+        auto weight = [&](int k) {  // W[f][k] of a generated Dense, W(k, f) of a Matvec
+          return T(generated ? w[int64_t(f) * d.n_in + k] : w[int64_t(k) * d.n_out + f]);
+        };
+        if (c.mode == 6 || c.mode == 7) {
+          for (int k0 = 0; k0 < d.n_in; k0 += 32) {
+            double blk = 0.0;
+            for (int k = k0; k < std::min(k0 + 32, d.n_in); k++) blk += double(weight(k)) * double(in(k, b));
+            v = T(double(v) + blk);
+          }
         } else {
-          for (int k = 0; k < d.n_in; k++) v = dense_step(c, v, T(w[int64_t(k) * d.n_out + f]), in(k, b));
+          for (int k = 0; k < d.n_in; k++) v = dense_step(c, v, weight(k), in(k, b));
         }
         for (int e = i + 1; e < end; e++) v = pointwise<T>(c.layers[e], c.params[e], v, f);
         out(f, b) = c.store(v);
@@ -660,15 +672,17 @@ int oracle_forward(ponni_layer_desc const* layers, int32_t num_layers, double co
   }
   // fp16 / bf16 operand modes see every parameter at the operand precision.
   std::vector<double> rounded;
-  if (mode == 2 || mode == 3) {
+  if (mode == 2 || mode == 3 || mode == 6 || mode == 7) {
     rounded.assign(params, params + off);
-    for (double& v : rounded) v = mode == 2 ? round_half(float(v)) : round_bf16(float(v));
+    for (double& v : rounded) v = (mode == 2 || mode == 6) ? round_half(float(v)) : round_bf16(float(v));
     for (int i = 0; i < num_layers; i++) ps[i] = rounded.data() + (ps[i] - params);
   }
   switch (mode) {
     case 0:
     case 2:
     case 3:
+    case 6:
+    case 7:
       return forward<float, float>(ls, ps, mode, static_cast<float const*>(x), ld_x, static_cast<float*>(y), ld_y,
                                    batch, threads);
     case 1:

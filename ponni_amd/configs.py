@@ -183,3 +183,22 @@ CONFIGS = {
     "c5": Config("c5", "Generated branched fp32 graph 24->[96->48 | 48]->concat 96 + proj skip, centre, ->10 softmax",
                  4_194_304, 24, 10, "f32", c5_layers, ("normal", 0.0, 1.0), 4, "mfma", 136, 22_656, FP32_PEAK),
 }
+
+
+def wide512_layers(nonzero_bias: bool = False) -> List[M.Layer]:
+    """Supplementary wide chain: fp16 MLP 64->512->512->64 with tanh, weights
+    Glorot-uniform, biases zero unless nonzero_bias."""
+    s, widths, out = 5, [64, 512, 512], []
+    for i in range(2):
+        out += [M.Matvec(glorot_uniform(widths[i], widths[i + 1], s, 1 + 2 * i)),
+                M.Bias(_bias(widths[i + 1], s, 2 + 2 * i, nonzero_bias)), M.Tanh(widths[i + 1])]
+    out += [M.Matvec(glorot_uniform(512, 64, s, 5)), M.Bias(_bias(64, s, 6, nonzero_bias))]
+    return out
+
+
+# Workloads measured beside the BASELINE configurations (not part of BASELINE.json).
+SUPPLEMENTARY = {
+    "wide512": Config("wide512", "fp16 MLP 64->512->512->64, tanh, fp32 accumulate (supplementary, wider than "
+                      "256 features; not a BASELINE config)", 4_194_304, 64, 64, "f16", wide512_layers,
+                      ("normal", 0.0, 1.0), 5, "mfma", 256, 655_360, FP16_PEAK),
+}

@@ -261,7 +261,17 @@ bool compile(std::string const& source, bool contract, std::vector<char>& code, 
 }  // namespace
 
 // Can the FUSED generator express this chain?
-bool fused_supports(ponni_plan_s const& p) { return p.max_width <= 256; }
+// Widest state a FUSED kernel keeps in registers: 16-bit states up to 1024
+// features, fp32 up to 512 and fp64 up to 256 (one 16-column tile per wave
+// beyond 256 features).
+int fused_max_width(int dtype) {
+  return dtype == PONNI_F64 ? 256 : (dtype == PONNI_F16 || dtype == PONNI_BF16) ? 1024 : 512;
+}
+
+bool fused_supports(ponni_plan_s const& p) { return p.max_width <= fused_max_width(p.dtype); }
+
+// 16-column tiles per wave: two, one for plans wider than 256 features.
+int fused_nt(ponni_plan_s const& p) { return p.max_width > 256 ? 1 : 2; }
 
 // Generate the HIP source of the plan's kernel.  Offsets are those of the
 // MFMA packing (plan.cpp, pack_params).
@@ -304,10 +314,19 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   std::string const F = half ? "float" : "real", F4 = half ? "floatx4" : "realx4";
   int const es = dbl ? 8 : 4;  // packed parameter element bytes
   auto lit = [&](double v) { return dbl ? dlit(v) : flit(static_cast<float>(v)); };
-  // 16-column tiles per wave: two.  16-bit plans run two waves per SIMD (32
-  // columns each) with A fragments staged through LDS (fused_f16.h dense_hs).
-  int const NT = 2;
-  int const half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
+  // 16-column tiles per wave: two (one beyond 256 features).  16-bit plans
+  // run two waves per SIMD with A fragments staged through LDS (fused_f16.h
+  // dense_hs), or one when the widest layer's two states do not fit in
+  // half the registers.
+  int const NT = fused_nt(p);
+  int half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
+  if (half) {
+    int widest = 0;  // 16-bit input and output tiles of the widest dense op
+    for (Op const& op : p.ops)
+      if (op.code == OP_DENSE) widest = std::max(widest, tiles(op.n_in) + tiles(op.n_out));
+    // 2 NT registers per 16-bit tile; accumulators, fragments, addresses.
+    if (widest * 2 * NT + 2 * 2 * NT * 4 + 2 * 4 + 48 > 256) half_wps = 1;
+  }
   int64_t const param_bytes = (p.packed_elements * es + 31) / 32 * 32;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   cfg.waves = 4;
@@ -316,7 +335,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   // and its A-fragment ring.  Parameters small enough to live in registers
   // next to that state are loaded once per wave and reused for every tile.
   int worst = 0, worst_saved_regs = 0;
-  int const tr = dbl ? 16 : 8;  // registers per lane of one fp32 / fp64 tile (2 column tiles)
+  int const tr = (dbl ? 8 : 4) * NT;  // registers per lane of one fp32 / fp64 tile
   {
     int cur = tiles(p.layers.front().n_in);
     std::map<int, int> slots;
@@ -352,7 +371,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   if (!half) {
     int saved_tiles = 0;
     for (int s = 0; s < p.num_slots; s++) saved_tiles += tiles(p.saved_features[s]);
-    int const saved_bytes = saved_tiles * kNTColumns / 16 * 64 * 4 * es * 4;  // per workgroup (4 waves)
+    int const saved_bytes = saved_tiles * NT * 64 * 4 * es * 4;  // per workgroup (4 waves)
     if (regs + 32 > 256 && worst_saved_regs > 0 && regs - worst_saved_regs <= 224 &&
         cfg.lds_bytes + saved_bytes <= 80 * 1024) {
       cfg.saved_in_lds = true;
@@ -399,6 +418,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   int const epi_interleave = (!half && !dbl && (cfg.lds_bytes > 0 || cfg.params_in_registers)) ? 16 : 0;
 
   if (dbl) o << "#define PONNI_REAL double\n";
+  if (NT != 2) o << "#define PONNI_NT " << NT << "\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
@@ -489,7 +509,8 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   int const in_rows_elems = tiles(n_in0) * 16 * 16 * NT;  // per wave, row-major 16-bit
   int const in_dma_bytes = cfg.waves * in_rows_elems * 2;
   int const stage_bytes = half && !dense_seq.empty() ? slots * slot_frags * 1024 : 0;
-  bool const in_dma = half && in_dma_bytes <= 64 * 1024 && in_dma_bytes + stage_bytes + 16 * 1024 <= kFusedLdsBytes;
+  bool const in_dma = half && NT % 2 == 0 && in_dma_bytes <= 64 * 1024 &&
+                      in_dma_bytes + stage_bytes + 16 * 1024 <= kFusedLdsBytes;
   std::string const WCOLS = std::to_string(16 * NT), NW = std::to_string(cfg.waves);
   // The next tile's rows are requested inside the second dense layer, right
   // after its first chunk's weight loads (fused_f16.h dense_hs hook): waits

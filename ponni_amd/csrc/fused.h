@@ -10,7 +10,6 @@ namespace ponni_hip {
 
 // Packed parameter blocks up to this size are staged in LDS by the kernel.
 constexpr int64_t kFusedLdsParamBytes = 64 * 1024;
-constexpr int kNTColumns = 32;
 // LDS of one workgroup on gfx950.
 constexpr int kFusedLdsBytes = 160 * 1024;
 
@@ -26,6 +25,8 @@ struct FusedConfig {
   int lds_total = 0;                 // bytes of LDS the kernel declares
 };
 
+// Widest state a FUSED kernel of this dtype keeps on chip.
+int fused_max_width(int dtype);
 bool fused_supports(ponni_plan_s const& p);
 // Can the NARROW plan run as a generated kernel (narrow_jit.h)?
 bool narrow_jit_supports(ponni_plan_s const& p);

@@ -305,7 +305,7 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, Stage<E>& st, La
   using V8 = typename Vec<E>::x8;
   using V4 = typename Vec<E>::x4;
   constexpr int TS = (TI + 1) / 2;
-  static_assert(TS <= 8, "at most 256 input features");
+  static_assert(TS <= kSlotFrags, "at most 1024 input features (one output tile per chunk)");
   constexpr int CT = kSlotFrags / TS;  // output tiles per chunk
   constexpr int NCH = (TO + CT - 1) / CT;
   // Tiles per group: GT must divide CT and TO (else one at a time); DEFER

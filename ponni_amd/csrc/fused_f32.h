@@ -44,7 +44,12 @@ __device__ inline double d_max(double a, double b) { return fmax(a, b); }
 __device__ inline float d_min(float a, float b) { return fminf(a, b); }
 __device__ inline double d_min(double a, double b) { return fmin(a, b); }
 
-constexpr int kNT = 2;  // default 16-column tiles per wave (fp32 path)
+// 16-column tiles per wave: 2, or 1 for plans wider than 256 features (the
+// generated source then defines PONNI_NT before including this header).
+#ifndef PONNI_NT
+#define PONNI_NT 2
+#endif
+constexpr int kNT = PONNI_NT;  // default column tiles of the tile routines
 
 template <int T, int NT = kNT>
 struct S {

@@ -1155,7 +1155,8 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   } else if (chosen == PONNI_PATH_FUSED) {
     if (!fused_supports(*p)) {
       delete p;
-      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs width <= 256");
+      return fail(PONNI_ERR_UNSUPPORTED, "FUSED path needs width <= " + std::to_string(fused_max_width(dtype)) +
+                                             " (fp16 / bf16 1024, fp32 512, fp64 256)");
     }
   } else if (chosen == PONNI_PATH_MFMA) {
     if (dtype == PONNI_F64 || mfma == 0 || p->num_slots > kMfmaMaxSlots || !mfma_supports(*p)) {

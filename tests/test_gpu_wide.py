@@ -1,0 +1,73 @@
+"""Chains wider than 256 features.
+
+The reference runs any width through the same forward_batch_parallel: the
+widths come from the layers' View extents (src/layers/ponni_Matvec.h:62-65)
+and one launch covers the chain (src/ponni_Inference.h:384-388).  Here FUSED
+keeps the states of 16-bit chains up to 1024 features and of fp32 chains up
+to 512 in registers (one 16-column tile per wave beyond 256 features; the
+contraction runs over 32-feature steps of any count); wider fp32 and fp64
+chains take GENERIC.
+
+CPU: the path each width takes, and that every FUSED kernel compiles
+(hipRTC, no device).  GPU: chains of 320, 512 and 1024 features with a
+residual and a LayerNorm at full width, on the default path and on GENERIC,
+against the oracle at the fixed bars."""
+import numpy as np
+import pytest
+
+import oracle
+import ponni_amd as P
+from ponni_amd import _abi as A
+
+
+def wide_chain(width, n_in=40, n_out=24, seed=0):
+    rng = np.random.default_rng(seed + width)
+
+    def W(a, b):
+        return rng.uniform(-1, 1, (a, b)) * np.sqrt(3.0 / a)
+
+    return [P.Matvec(W(n_in, width)), P.Bias(rng.uniform(-0.1, 0.1, width)), P.Tanh(width),
+            P.Save_State(0, width), P.Matvec(W(width, width)), P.Bias(rng.uniform(-0.1, 0.1, width)),
+            P.Gelu(width, True), P.LayerNorm(rng.uniform(0.5, 1.5, width), rng.uniform(-0.2, 0.2, width)),
+            P.Binop_Add(0, width), P.Matvec(W(width, width)), P.Bias(rng.uniform(-0.1, 0.1, width)), P.Relu(width),
+            P.Matvec(W(width, n_out)), P.Bias(rng.uniform(-0.1, 0.1, n_out))]
+
+
+EXPECTED = {("f32", 320): "fused", ("f32", 512): "fused", ("f32", 1024): "generic",
+            ("f16", 320): "fused", ("f16", 512): "fused", ("f16", 1024): "fused",
+            ("bf16", 512): "fused", ("f64", 320): "generic"}
+
+
+@pytest.mark.parametrize("dtype,width", sorted(EXPECTED))
+def test_wide_path_choice_and_compile(dtype, width, tmp_path, monkeypatch):
+    monkeypatch.setenv("PONNI_JIT_CACHE", str(tmp_path))
+    m = P.create_inference_model(*wide_chain(width), dtype=dtype)
+    assert m.path == EXPECTED[(dtype, width)]
+    if m.path == "fused":
+        m.compile()
+        src = m.kernel_source()
+        assert "#define PONNI_NT 1" in src
+    else:
+        with pytest.raises(P.PonniError) as e:
+            P.create_inference_model(*wide_chain(width), dtype=dtype, path="fused")
+        assert e.value.status == A.PONNI_ERR_UNSUPPORTED
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("dtype,width", sorted(EXPECTED))
+def test_wide_chain_on_gpu(cuda, dtype, width, path):
+    from tests.test_gpu_parity import ORACLE_MODE, check_f32, check_half, gpu_run
+
+    layers = wide_chain(width)
+    x = np.random.default_rng(width).standard_normal((40, 3001))
+    print(f"wide chain: width={width} dtype={dtype} path={path} B=3001", flush=True)
+    got, xg, m = gpu_run(layers, x, dtype=dtype, path=path, pad=5)
+    assert m.path == (EXPECTED[(dtype, width)] if path == "auto" else path)
+    want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
+    if dtype == "f64":
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    elif dtype == "f32":
+        check_f32(got, want)
+    else:
+        check_half(got, want)
