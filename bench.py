@@ -141,11 +141,17 @@ def make_inputs(cfg, torch, P, C):
     return xs, ys
 
 
-def frac_of_measured(pk, roofline, dtype):
+SMALL_LAUNCH_BYTES = 64 << 20  # HBM-bound launches up to this size are priced on the 12 MB copy
+
+
+def frac_of_measured(pk, roofline, dtype, launch_bytes=None):
     """A kernel's achieved rate over the measured rate of the unit that bounds it
-    (HBM: the faster of the copy and the read-only pass; None where no matching
-    rate is measured, e.g. fp64 MFMA)."""
-    bound = {"hbm": max(pk.hbm_copy_gbps, pk.hbm_read_gbps),
+    (HBM: the faster of the 1 GiB copy and the read-only pass, or for a launch
+    of at most SMALL_LAUNCH_BYTES the c1-shaped 12 MB copy, whose time is
+    mostly launch and DRAM latency; None where no matching rate is measured,
+    e.g. fp64 MFMA)."""
+    small = launch_bytes is not None and launch_bytes <= SMALL_LAUNCH_BYTES
+    bound = {"hbm": pk.hbm_copy_12mb_gbps if small else max(pk.hbm_copy_gbps, pk.hbm_read_gbps),
              "mfma": {"f16": pk.mfma_f16_tflops, "bf16": pk.mfma_f16_tflops,
                       "f32": pk.mfma_f32_tflops}.get(dtype)}[roofline["bound"]]
     return round(roofline["achieved"] / bound, 4) if bound else None
@@ -161,19 +167,23 @@ def measured_peaks(roofline, cfg, others):
     pk = A.Peaks()
     A.check(A.lib().ponni_measure_peaks(ctypes.byref(pk), None))
     for o in others.values():
-        o["roofline"]["frac_of_measured"] = frac_of_measured(pk, o["roofline"], o["dtype"])
+        o["roofline"]["frac_of_measured"] = frac_of_measured(pk, o["roofline"], o["dtype"], o.get("launch_bytes"))
     out = {
         "hbm_copy_GBps": round(pk.hbm_copy_gbps, 1),
         "hbm_read_GBps": round(pk.hbm_read_gbps, 1),
+        "hbm_copy_12MB_GBps": round(pk.hbm_copy_12mb_gbps, 1),
+        "copy_12MB_us": round(pk.copy_12mb_us, 3),
         "mfma_f16_TFLOPs": round(pk.mfma_f16_tflops, 1),
         "mfma_f32_TFLOPs": round(pk.mfma_f32_tflops, 1),
         "method": ("1 GiB device copy, the faster of two launch shapes (bytes read + written); "
                    "read-only pass over 1 GiB; HBM-bound kernels priced on the faster of the two; "
-                   "register-only loops of "
+                   "a copy of c1's traffic at c1's launch shape (1,000,000 columns, 8 MB read from two rows, "
+                   "4 MB written, 16-byte lanes, 48 sets in rotation, mean of the dispatches' own durations), "
+                   "which prices HBM-bound launches of at most 64 MiB; register-only loops of "
                    "v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32, one 512-thread workgroup "
                    "per CU; medians of 3-5 samples of 2-4 back-to-back launches"),
     }
-    out["frac_of_measured"] = frac_of_measured(pk, roofline, cfg.dtype)
+    out["frac_of_measured"] = frac_of_measured(pk, roofline, cfg.dtype, cfg.bytes_per_sample * cfg.batch)
     return out
 
 
@@ -209,6 +219,16 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
             ev.destroy(e)
     ms_per_step = total_ms / steps
     kernel_ms = sum(per) / len(per)
+    # The same number of launches over the same buffer rotation, issued by the
+    # library's own host code (ponni_forward_steps): the per-step time of the C
+    # ABI path, without the Python call in between.
+    from ponni_amd import _abi as A
+
+    xp = (ctypes.c_void_p * len(xs))(*[x.data_ptr() for x in xs])
+    yp = (ctypes.c_void_p * len(ys))(*[y.data_ptr() for y in ys])
+    cabi = ctypes.c_double()
+    A.check(A.lib().ponni_forward_steps(model._plan, xp, xs[0].stride(0), yp, ys[0].stride(0), B, len(xs), steps,
+                                        stream, ctypes.byref(cabi)))
     work = cfg.flops_per_sample if cfg.bound == "mfma" else cfg.bytes_per_sample
     unit = "TFLOP/s" if cfg.bound == "mfma" else "GB/s"
     scale = 1e12 if cfg.bound == "mfma" else 1e9
@@ -218,6 +238,7 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
         "layers": layers,
         "samples_per_s": B / (ms_per_step * 1e-3),
         "ms_per_step": ms_per_step,
+        "ms_per_step_c_abi": cabi.value,
         "kernel_ms_mean": kernel_ms,
         "kernel_ms_min": per_sorted[0],
         "kernel_ms_median": statistics.median(per_sorted),
@@ -368,6 +389,8 @@ def main() -> int:
                 "path": r["path"],
                 "samples_per_s": round(r["samples_per_s"], 1),
                 "ms_per_step": round(r["ms_per_step"], 5),
+                "ms_per_step_c_abi": round(r["ms_per_step_c_abi"], 5),
+                "launch_bytes": c.bytes_per_sample * c.batch,
                 "kernel_ms_mean": round(r["kernel_ms_mean"], 5),
                 "kernel_ms_min": round(r["kernel_ms_min"], 5),
                 "kernel_ms_median": round(r["kernel_ms_median"], 5),
@@ -399,6 +422,7 @@ def main() -> int:
             "workload": f"{cfg.name}: {cfg.description}",
             "global_batch": cfg.batch,
             "path": head["path"],
+            "ms_per_step_c_abi": round(head["ms_per_step_c_abi"], 5),
             "kernel_ms_mean": round(head["kernel_ms_mean"], 5),
             "kernel_ms_min": round(head["kernel_ms_min"], 5),
             "kernel_ms_median": round(head["kernel_ms_median"], 5),

@@ -380,6 +380,16 @@ int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y,
                         int64_t ld_out, int64_t batch, hipStream_t stream,
                         hipEvent_t start, hipEvent_t stop);
 
+/* `steps` ponni_forward calls issued back to back from the library's host
+ * code on `stream` (input and output pairs x[i % sets], y[i % sets]) between
+ * two events; *ms_per_step = the elapsed time / steps.  A measurement aid
+ * with no counterpart in the reference: the per-step time of the C ABI path
+ * (host submission included) without an interpreter in between.
+ * Synchronizes `stream`. */
+int ponni_forward_steps(ponni_plan plan, const void* const* x, int64_t ld_in, void* const* y,
+                        int64_t ld_out, int64_t batch, int32_t sets, int32_t steps,
+                        hipStream_t stream, double* ms_per_step);
+
 /* Source text of the kernel generated for a FUSED plan -- the counterpart of
  * the per-model executor the reference instantiates at compile time
  * (ponni_Inference.h:453-555) and of the emitted infer_batch body
@@ -492,12 +502,18 @@ int ponni_fill_synthetic(void* x, int32_t dtype, int64_t n, uint64_t seed,
  * the same 1 GiB, and of register-only loops
  * of v_mfma_f32_16x16x32_f16 and v_mfma_f32_16x16x4f32 with one 512-thread
  * workgroup per CU (the 16-bit FUSED kernels' occupancy); medians of a few
- * launches.  Allocates 2 GiB of device memory for the call; synchronous. */
+ * launches.  Also a copy of c1's traffic at c1's launch shape: 1,000,000
+ * columns, 8 MB read from two rows and 4 MB written to one, 256-thread
+ * workgroups with 16-byte accesses, 48 buffer sets in rotation, the mean of
+ * the dispatches' own durations.  Allocates 2 GiB of device memory for the
+ * call; synchronous. */
 typedef struct ponni_peaks {
   double hbm_copy_gbps;
   double mfma_f16_tflops;
   double mfma_f32_tflops;
   double hbm_read_gbps;
+  double hbm_copy_12mb_gbps; /* bytes read + written per second, c1-shaped copy */
+  double copy_12mb_us;       /* its mean kernel duration */
 } ponni_peaks;
 int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream);
 

@@ -93,7 +93,8 @@ class TensorSpec(ctypes.Structure):
 
 class Peaks(ctypes.Structure):
     _fields_ = [("hbm_copy_gbps", ctypes.c_double), ("mfma_f16_tflops", ctypes.c_double),
-                ("mfma_f32_tflops", ctypes.c_double), ("hbm_read_gbps", ctypes.c_double)]
+                ("mfma_f32_tflops", ctypes.c_double), ("hbm_read_gbps", ctypes.c_double),
+                ("hbm_copy_12mb_gbps", ctypes.c_double), ("copy_12mb_us", ctypes.c_double)]
 
 
 # Saved-state slot indices a plan may use: 0 .. MAX_SLOTS - 1 (program.h kMaxSlots).
@@ -176,6 +177,8 @@ def lib() -> ctypes.CDLL:
     L.ponni_forward_no_alloc.argtypes = [vp, vp, i64, vp, i64, i64, vp]
     L.ponni_forward_timed.restype = ctypes.c_int
     L.ponni_forward_timed.argtypes = [vp, vp, i64, vp, i64, i64, vp, vp, vp]
+    L.ponni_forward_steps.restype = ctypes.c_int
+    L.ponni_forward_steps.argtypes = [vp, vp, i64, vp, i64, i64, i32, i32, vp, ctypes.POINTER(ctypes.c_double)]
     L.ponni_plan_kernel_source.restype = i64
     L.ponni_plan_kernel_source.argtypes = [vp, ctypes.c_char_p, i64]
     L.ponni_plan_program_source.restype = i64

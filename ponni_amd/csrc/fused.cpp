@@ -270,7 +270,9 @@ int fused_max_width(int dtype) {
 
 bool fused_supports(ponni_plan_s const& p) { return p.max_width <= fused_max_width(p.dtype); }
 
-// 16-column tiles per wave: two, one for plans wider than 256 features.
+// 16-column tiles per wave: two, one for plans wider than 256 features
+// (a 16-bit 512-feature chain with two spills 72 registers at one wave per
+// SIMD; with one it runs spill-free).
 int fused_nt(ponni_plan_s const& p) { return p.max_width > 256 ? 1 : 2; }
 
 // Generate the HIP source of the plan's kernel.  Offsets are those of the
@@ -1177,6 +1179,12 @@ int fused_prepare(ponni_plan_s& p, std::string& error) {
   }
   p.fused_fn = it->second->fn;
   p.fused_blocks_per_cu = it->second->blocks_per_cu > 0 ? it->second->blocks_per_cu : 1;
+  // The persistent grid's size, looked up once rather than at every launch.
+  if (hipDeviceGetAttribute(&p.fused_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      p.fused_cus <= 0) {
+    error = "no compute units";
+    return PONNI_ERR_DEVICE;
+  }
   p.fused_persistent = cfg.lds_bytes > 0 || cfg.vec_bytes > 0 || cfg.params_in_registers || cfg.persistent_loop;
   p.fused_columns_per_block = cfg.columns_per_block;
   p.fused_waves = cfg.waves;
@@ -1187,11 +1195,7 @@ hipError_t fused_launch(ponni_plan_s const& p, LaunchArgs const& a, hipStream_t 
   int64_t const blocks = (a.batch + p.fused_columns_per_block - 1) / p.fused_columns_per_block;
   int64_t grid = blocks;
   if (p.fused_persistent) {
-    int dev = 0, cus = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    int64_t const resident = int64_t(cus) * p.fused_blocks_per_cu;
+    int64_t const resident = int64_t(p.fused_cus) * p.fused_blocks_per_cu;
     grid = blocks < resident ? blocks : resident;
   }
   void const* params = a.params;

@@ -50,6 +50,53 @@ __global__ __launch_bounds__(256) void read_unrolled(f4 const* __restrict__ src,
   if (s == 1.0f) sink[threadIdx.x] = s;
 }
 
+// A copy shaped like c1's NARROW kernel: 256-thread workgroups, each lane 4
+// consecutive columns of two input rows (two 16-byte loads) and of one output
+// row (one 16-byte store), i.e. 8 bytes read and 4 written per column.
+__global__ __launch_bounds__(256) void rows2to1(f4 const* __restrict__ x, f4* __restrict__ y, int64_t n4) {
+  int64_t const i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n4) y[i] = x[i] + x[n4 + i];
+}
+
+// Mean kernel duration (ms) of rows2to1 over `columns` columns, from events
+// each dispatch stamps itself (hipExtLaunchKernel, as ponni_forward_timed
+// times the forward kernels), over `sets` input / output pairs in rotation so
+// that no launch finds its data in the MALL; -1 on failure.
+float small_copy_ms(int64_t columns, int sets, hipStream_t stream) {
+  int64_t const n4 = columns / 4;
+  size_t const set_bytes = size_t(n4) * 16 * 3;
+  char* buf = nullptr;
+  if (hipMalloc(&buf, set_bytes * sets) != hipSuccess) return -1.0f;
+  float result = -1.0f;
+  std::vector<hipEvent_t> ev(2 * size_t(sets), nullptr);
+  bool ok = hipMemsetAsync(buf, 0, set_bytes * sets, stream) == hipSuccess;
+  for (auto& e : ev) ok = ok && hipEventCreate(&e) == hipSuccess;
+  dim3 const grid(unsigned((n4 + 255) / 256)), block(256);
+  double sum = 0.0;
+  for (int pass = 0; ok && pass < 2; pass++) {  // the first pass warms up
+    for (int i = 0; ok && i < sets; i++) {
+      f4 const* x = reinterpret_cast<f4 const*>(buf + set_bytes * i);
+      f4* y = reinterpret_cast<f4*>(buf + set_bytes * i + size_t(n4) * 32);
+      int64_t n = n4;
+      void* args[] = {&x, &y, &n};
+      ok = hipExtLaunchKernel(reinterpret_cast<void const*>(rows2to1), grid, block, args, 0, stream, ev[2 * i],
+                              ev[2 * i + 1], 0) == hipSuccess;
+    }
+    ok = ok && hipStreamSynchronize(stream) == hipSuccess;
+    sum = 0.0;
+    for (int i = 0; ok && i < sets; i++) {
+      float ms = 0.0f;
+      ok = hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) == hipSuccess;
+      sum += ms;
+    }
+  }
+  if (ok) result = static_cast<float>(sum / sets);
+  for (auto& e : ev)
+    if (e != nullptr) (void)hipEventDestroy(e);
+  (void)hipFree(buf);
+  return result;
+}
+
 // Eight independent accumulators per lane; `iters` rounds of 8 MFMAs.
 __global__ __launch_bounds__(512) void mfma_f16_loop(float* __restrict__ out, int iters, float seed) {
   f4 acc[8];
@@ -159,16 +206,23 @@ extern "C" int ponni_measure_peaks(ponni_peaks* out, hipStream_t stream) {
       [&] { hipLaunchKernelGGL(mfma_f16_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3, 2);
   float const f32_ms = median_ms(
       [&] { hipLaunchKernelGGL(mfma_f32_loop, dim3(cus), dim3(512), 0, stream, sink, iters, 1.0f); }, stream, 3, 2);
-  hipError_t const err = hipGetLastError();
+  hipError_t err = hipGetLastError();
   (void)hipFree(src);
   (void)hipFree(dst);
   (void)hipFree(sink);
-  if (err != hipSuccess || copy_ms <= 0.0f || read_ms <= 0.0f || f16_ms <= 0.0f || f32_ms <= 0.0f)
+  // c1's traffic at c1's launch shape: 1,000,000 columns, 12 MB per launch,
+  // 48 sets (576 MB) in rotation.
+  int64_t const small_columns = 1000000;
+  float const small_ms = err == hipSuccess ? small_copy_ms(small_columns, 48, stream) : -1.0f;
+  if (err == hipSuccess) err = hipGetLastError();
+  if (err != hipSuccess || copy_ms <= 0.0f || read_ms <= 0.0f || f16_ms <= 0.0f || f32_ms <= 0.0f || small_ms <= 0.0f)
     return set_error(PONNI_ERR_DEVICE, std::string("peak measurement failed: ") + hipGetErrorString(err));
   double const mfmas = double(cus) * 8 * iters * 8;  // waves x rounds x MFMAs per round
   out->hbm_copy_gbps = 2.0 * double(bytes) / (copy_ms * 1e-3) / 1e9;
   out->hbm_read_gbps = double(bytes) / (read_ms * 1e-3) / 1e9;
   out->mfma_f16_tflops = mfmas * 16384.0 / (f16_ms * 1e-3) / 1e12;  // 16x16x32: 2*16*16*32 FLOP
   out->mfma_f32_tflops = mfmas * 2048.0 / (f32_ms * 1e-3) / 1e12;   // 16x16x4: 2*16*16*4 FLOP
+  out->copy_12mb_us = small_ms * 1e3;
+  out->hbm_copy_12mb_gbps = 12.0 * double(small_columns) / (small_ms * 1e-3) / 1e9;
   return PONNI_OK;
 }

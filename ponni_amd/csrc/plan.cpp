@@ -1467,6 +1467,30 @@ int ponni_forward_timed(ponni_plan plan, const void* x, int64_t ld_in, void* y, 
   return forward_impl(plan, x, ld_in, y, ld_out, batch, stream, start, stop, false);
 }
 
+int ponni_forward_steps(ponni_plan plan, const void* const* x, int64_t ld_in, void* const* y, int64_t ld_out,
+                        int64_t batch, int32_t sets, int32_t steps, hipStream_t stream, double* ms_per_step) {
+  if (x == nullptr || y == nullptr || ms_per_step == nullptr || sets <= 0 || steps <= 0)
+    return fail(PONNI_ERR_INVALID_ARGUMENT, "ponni_forward_steps: null arrays or no sets / steps");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  HIP_TRY(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return fail(PONNI_ERR_DEVICE, "hipEventCreate failed");
+  }
+  int st = PONNI_OK;
+  if (hipEventRecord(e0, stream) != hipSuccess) st = fail(PONNI_ERR_DEVICE, "hipEventRecord failed");
+  for (int32_t i = 0; st == PONNI_OK && i < steps; i++)
+    st = ponni_forward(plan, x[i % sets], ld_in, y[i % sets], ld_out, batch, stream);
+  float ms = 0.0f;
+  if (st == PONNI_OK && (hipEventRecord(e1, stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                         hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+    st = fail(PONNI_ERR_DEVICE, "timing the forward passes failed");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (st == PONNI_OK) *ms_per_step = double(ms) / steps;
+  return st;
+}
+
 int64_t ponni_plan_kernel_source(ponni_plan plan, char* buf, int64_t len) {
   if (plan == nullptr) {
     fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");

@@ -173,6 +173,7 @@ struct ponni_plan_s {
   // FUSED path (and generated NARROW): the plan's generated kernel (compiled on first forward).
   hipFunction_t fused_fn = nullptr;
   int fused_blocks_per_cu = 1;
+  int fused_cus = 0;              // compute units of the plan's device
   bool fused_persistent = false;  // grid sized to the resident workgroups
   int fused_columns_per_block = 128;
   int fused_waves = 4;  // waves per workgroup
