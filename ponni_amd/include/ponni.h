@@ -1568,6 +1568,13 @@ class BasicInference {
   // Dense layers (built-in or user) each start one fused block (ponni_Inference.h:66-85).
   static constexpr int get_num_fused_dense_blocks() { return (int(is_dense_layer_v<Layers>) + ...); }
   int get_num_saved_states() const { return info().num_saved_states; }
+  // get_saved_state_size<ISAVE>() (ponni_Inference.h:204-223): the widest
+  // state any Save_State<ISAVE> stores, 0 for an index no save uses.
+  template <int ISAVE>
+  int get_saved_state_size() const {
+    static_assert(ISAVE >= 0, "saved-state index must be nonnegative");
+    return ISAVE < get_num_saved_states() ? ponni_plan_saved_state_size(plan_.get(), ISAVE) : 0;
+  }
   template <int REQUESTED_BUFFER>
   int get_planned_temporary_size() const {
     return REQUESTED_BUFFER == 0 ? info().tmp1_features : info().tmp2_features;
@@ -1576,7 +1583,7 @@ class BasicInference {
   // Each layer's own validate() plus the chain check (ponni_Inference.h:719-737);
   // the plan already rejected an invalid chain, so this re-checks the layers.
   void validate() const {
-    int saved[8] = {};
+    std::vector<int> saved(max_slot_index() + 1, 0);
     std::apply(
         [&](auto const&... l) {
           auto one = [&](auto const& layer) {
@@ -1868,6 +1875,22 @@ class BasicInference {
   }
 
  private:
+  // Highest saved-state index any layer names (-1: none).
+  template <class L>
+  static constexpr int slot_index_of() {
+    if constexpr (has_save<L>()) {
+      if constexpr (L::save) return L::index;
+    }
+    if constexpr (has_binop<L>()) {
+      if constexpr (L::binop) return L::index;
+    }
+    return -1;
+  }
+  static constexpr int max_slot_index() {
+    int m = -1;
+    ((m = slot_index_of<Layers>() > m ? slot_index_of<Layers>() : m), ...);
+    return m;
+  }
   template <class L>
   static constexpr bool has_save() {
     return has_member_save<L>(0);

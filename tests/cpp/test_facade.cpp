@@ -109,6 +109,14 @@ void test_structure_and_planning() {
                                     Binop_Concatenate<0>(4, 6, true));
   CHECK(res.get_num_saved_states() == 2);
   res.validate();
+  // Slot indices past any fixed table: the reference takes any ISAVE and
+  // sizes every slot up to the highest (ponni_Inference.h:204-223).
+  auto far = create_inference_model(ex, S(), Save_State<11>(2), Relu<float>(2), Binop_Add<11>(2), Save_State<100>(2),
+                                    Binop_Concatenate<100>(2, 4, false));
+  CHECK(far.get_num_saved_states() == 101);
+  CHECK(far.template get_saved_state_size<11>() == 2 && far.template get_saved_state_size<100>() == 2);
+  CHECK(far.template get_saved_state_size<50>() == 0 && far.template get_saved_state_size<200>() == 0);
+  far.validate();
 }
 
 template <class S>
