@@ -353,6 +353,15 @@ __device__ inline void layer_norm(S<T, NT>& s, real const* __restrict__ gamma, r
 }
 
 // Softmax / LogSoftmax over N features, ponni_Softmax.h:45-56, ponni_LogSoftmax.h:45-57.
+// Softmax's exponentials (arguments <= 0 once the maximum is subtracted)
+// and its division on the hardware transcendentals in fp32 -- exp(v) as
+// 2^(v log2 e), the quotient as a product with 1 / sum (a sum >= 1) -- each
+// within a few ulps of the libm forms; fp64 keeps the libm forms.
+__device__ inline float softmax_exp(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
+__device__ inline double softmax_exp(double v) { return exp(v); }
+__device__ inline float softmax_recip(float v) { return __builtin_amdgcn_rcpf(v); }
+__device__ inline double softmax_recip(double v) { return 1.0 / v; }
+
 template <int N, bool LOG, int T, int NT>
 __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
 #pragma unroll
@@ -369,7 +378,7 @@ __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
     for (int m = 0; m < T; m++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        real const ex = d_exp(s.v[m][n][e] - mx);
+        real const ex = LOG ? d_exp(s.v[m][n][e] - mx) : softmax_exp(s.v[m][n][e] - mx);
         if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) sum += ex;
         if (!LOG) s.v[m][n][e] = ex;
       }
@@ -381,10 +390,11 @@ __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
 #pragma unroll
         for (int e = 0; e < 4; e++) s.v[m][n][e] -= lse;
     } else {
+      real const inv = softmax_recip(sum);
 #pragma unroll
       for (int m = 0; m < T; m++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) s.v[m][n][e] = s.v[m][n][e] / sum;
+        for (int e = 0; e < 4; e++) s.v[m][n][e] = s.v[m][n][e] * inv;
     }
   }
 }
