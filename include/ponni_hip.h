@@ -228,8 +228,12 @@ typedef enum ponni_path {
   PONNI_PATH_GENERIC = 1, /* one sample per lane, states in HBM scratch (any model) */
   PONNI_PATH_NARROW = 2,  /* one sample per lane, states in registers (width <= 16) */
   PONNI_PATH_MFMA = 3,    /* 16x16 MFMA tiles, states in registers (width <= 128)   */
-  PONNI_PATH_FUSED = 4    /* MFMA tiles in a kernel generated for this plan and
-                             compiled with hipRTC on first use (width <= 256)      */
+  PONNI_PATH_FUSED = 4,   /* MFMA tiles in a kernel generated for this plan and
+                             compiled with hipRTC on first use (16-bit width
+                             <= 1024, fp32 <= 512, fp64 <= 256)                     */
+  PONNI_PATH_LAYERED = 5  /* the GENERIC op list with every dense block run over the
+                             whole batch as an MFMA contraction (states in HBM
+                             scratch; any width)                                    */
 } ponni_path;
 
 typedef struct ponni_plan_s* ponni_plan;

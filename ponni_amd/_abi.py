@@ -17,9 +17,9 @@ PONNI_ERR_DEVICE = 5
 PONNI_ERR_IO = 6
 
 F32, F64, F16, BF16 = 1, 2, 3, 4
-PATH_AUTO, PATH_GENERIC, PATH_NARROW, PATH_MFMA, PATH_FUSED = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_GENERIC, PATH_NARROW, PATH_MFMA, PATH_FUSED, PATH_LAYERED = 0, 1, 2, 3, 4, 5
 PATH_NAMES = {PATH_AUTO: "auto", PATH_GENERIC: "generic", PATH_NARROW: "narrow", PATH_MFMA: "mfma",
-              PATH_FUSED: "fused"}
+              PATH_FUSED: "fused", PATH_LAYERED: "layered"}
 
 LAYER_MATVEC = 1
 LAYER_BIAS = 2

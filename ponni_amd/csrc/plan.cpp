@@ -326,6 +326,10 @@ Step make_step(ponni_layer_desc const& d) {
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
+// GENERIC and LAYERED plans share the op list, the reference parameter
+// layout and the HBM scratch.
+bool generic_layout(ponni_plan_s const& p) { return p.path == PONNI_PATH_GENERIC || p.path == PONNI_PATH_LAYERED; }
+
 // Rows of the saved-slot area (generic_ops.h Bufs): slot s after slots
 // 0 .. s-1, each get_saved_state_size<s>() rows high.
 void set_slot_rows(ponni_plan_s& p) {
@@ -434,7 +438,8 @@ int64_t packed_size(ponni_plan_s const& p, ponni_layer_desc const& d) {
 // Packed length of a per-feature vector of n features in the path's layout.
 int64_t vec_size(ponni_plan_s const& p, int n) {
   switch (p.path) {
-    case PONNI_PATH_GENERIC: return n;
+    case PONNI_PATH_GENERIC:
+    case PONNI_PATH_LAYERED: return n;
     case PONNI_PATH_NARROW: return p.width_class;
     default: return round_up(n, 16);
   }
@@ -685,7 +690,7 @@ void visit_param_slots(ponni_plan_s const& p, Emit&& emit) {
                 int const n = 16 * mo + (l & 15);
                 if (k < K && n < N) emit(hb + ((int64_t(mo) * TS + t) * 64 + l) * 8 + j, SLOT_HALF, i, idx(k, n));
               }
-      } else if (p.path == PONNI_PATH_GENERIC) {
+      } else if (generic_layout(p)) {
         for (int k = 0; k < K; k++)
           for (int n = 0; n < N; n++) emit(base + int64_t(k) * N + n, SLOT_VALUE, i, idx(k, n));
       } else if (p.path == PONNI_PATH_NARROW) {
@@ -1008,7 +1013,7 @@ int upload(ponni_plan_s& p) {
   // the fixed per-device scratch; its address is looked up here, where
   // loading the code object that holds it may allocate, so that
   // ponni_forward_no_alloc never does that lookup first.
-  if (p.path == PONNI_PATH_GENERIC) {
+  if (generic_layout(p)) {
     void* base = nullptr;
     HIP_TRY(static_scratch(dev, &base));
   }
@@ -1027,7 +1032,7 @@ int reallocate_scratch(ponni_plan_s& p, int64_t batch) {
   HIP_TRY(hipDeviceSynchronize());
   release_scratch(p);
   p.capacity = batch;
-  if (p.path != PONNI_PATH_GENERIC || batch == 0) return PONNI_OK;
+  if (!generic_layout(p) || batch == 0) return PONNI_OK;
   size_t const es = element_size(p.dtype);
   for (int b = 0; b < 2; b++) {
     if (p.tmp_features[b] > 0)
@@ -1072,7 +1077,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   *out_plan = nullptr;
   if (layers == nullptr || num_layers <= 0) return fail(PONNI_ERR_INVALID_ARGUMENT, "a model needs at least one layer");
   if (dtype < PONNI_F32 || dtype > PONNI_BF16) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown dtype");
-  if (path < PONNI_PATH_AUTO || path > PONNI_PATH_FUSED) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
+  if (path < PONNI_PATH_AUTO || path > PONNI_PATH_LAYERED) return fail(PONNI_ERR_INVALID_ARGUMENT, "unknown kernel path");
   int const st = validate_chain(layers, num_layers);
   if (st != PONNI_OK) return st;
 
@@ -1137,6 +1142,11 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
   }
   double const io_bytes = double(layers[0].n_in + layers[num_layers - 1].n_out) * (dtype == PONNI_F32 ? 4 : 2);
   bool const narrow_light = macs < 10.0 * io_bytes;
+  // A chain with a dense layer of at least 64 x 64 features is worth running
+  // its dense blocks on the matrix cores even with its states in HBM.
+  bool layered_pays = false;
+  for (int i = 0; i < num_layers; i++)
+    layered_pays = layered_pays || (is_dense(layers[i].kind) && layers[i].n_in >= 64 && layers[i].n_out >= 64);
   int chosen = path;
   if (chosen == PONNI_PATH_AUTO) {
     if (narrow_interp_ok && max_width <= 8) chosen = PONNI_PATH_NARROW;
@@ -1144,6 +1154,7 @@ int ponni_plan_create(const ponni_layer_desc* layers, int32_t num_layers, int32_
     else if (jit_enabled && fused_supports(*p)) chosen = PONNI_PATH_FUSED;
     else if (narrow_ok) chosen = PONNI_PATH_NARROW;
     else if (dtype != PONNI_F64 && mfma > 0 && p->num_slots <= kMfmaMaxSlots && mfma_supports(*p)) chosen = PONNI_PATH_MFMA;
+    else if (layered_pays) chosen = PONNI_PATH_LAYERED;
     else chosen = PONNI_PATH_GENERIC;
   } else if (chosen == PONNI_PATH_NARROW) {
     if (!narrow_ok) {
@@ -1348,6 +1359,53 @@ size_t carved_scratch_bytes(ponni_plan_s const& p, int64_t batch, int64_t (&offs
   return total;
 }
 
+// LAYERED: the GENERIC op list in runs, in order on one stream -- each dense
+// op one MFMA contraction over the batch (launch_layered_dense), each run of
+// other ops one generic_forward launch over that part of the list; the
+// timing events, if any, bracket the whole sequence.
+hipError_t layered_forward(ponni_plan_s const& p, LaunchArgs a, hipStream_t stream) {
+  hipEvent_t const ev_start = a.ev_start, ev_stop = a.ev_stop;
+  a.ev_start = a.ev_stop = nullptr;
+  if (ev_start != nullptr) {
+    hipError_t const e = hipEventRecord(ev_start, stream);
+    if (e != hipSuccess) return e;
+  }
+  int const n = static_cast<int>(p.ops.size());
+  for (int o = 0; o < n;) {
+    hipError_t e = hipSuccess;
+    Op const& op = p.ops[o];
+    if (op.code == OP_DENSE) {
+      if (op.src >= BUF_SAVED || op.dst >= BUF_SAVED) return hipErrorInvalidValue;  // (never lowered so)
+      DenseArgs d{};
+      d.x = a.buffers[op.src];
+      d.ldx = a.buffer_ld[op.src];
+      d.y = a.buffers[op.dst];
+      d.ldy = a.buffer_ld[op.dst];
+      d.batch = a.batch;
+      d.params = a.params;
+      d.woff = op.woff;
+      d.n_in = op.n_in;
+      d.n_out = op.n_out;
+      d.epi_begin = op.epi_begin;
+      d.epi_count = op.epi_count;
+      d.bias_first = (op.aux & DENSE_BIAS_FIRST) ? 1 : 0;
+      d.steps = a.steps;
+      e = launch_layered_dense(p.dtype, d, stream);
+      o++;
+    } else {
+      int end = o;
+      while (end < n && p.ops[end].code != OP_DENSE) end++;
+      LaunchArgs run = a;
+      run.ops = a.ops + o;
+      run.num_ops = end - o;
+      e = launch_generic(p.dtype, run, stream);
+      o = end;
+    }
+    if (e != hipSuccess) return e;
+  }
+  return ev_stop != nullptr ? hipEventRecord(ev_stop, stream) : hipSuccess;
+}
+
 int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t ld_out, int64_t batch,
                  hipStream_t stream, hipEvent_t ev_start, hipEvent_t ev_stop, bool no_alloc) {
   if (plan == nullptr) return fail(PONNI_ERR_INVALID_ARGUMENT, "plan is null");
@@ -1383,7 +1441,7 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
   void* scratch[3] = {};  // tmp1, tmp2, the saved-slot area
   int64_t scratch_ld = 0;
   if (no_alloc) {
-    if (plan->path == PONNI_PATH_GENERIC) {
+    if (generic_layout(*plan)) {
       int64_t offset[3];
       size_t const need = carved_scratch_bytes(*plan, batch, offset);
       if (need > kStaticScratchBytes)
@@ -1397,7 +1455,7 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
       scratch_ld = batch;
     }
   } else {
-    if (plan->path == PONNI_PATH_GENERIC && batch > plan->capacity) {
+    if (generic_layout(*plan) && batch > plan->capacity) {
       int const st = reallocate_scratch(*plan, batch);
       if (st != PONNI_OK) return st;
     } else if (batch > plan->capacity) {
@@ -1443,6 +1501,7 @@ int forward_impl(ponni_plan plan, const void* x, int64_t ld_in, void* y, int64_t
       break;
     case PONNI_PATH_MFMA: err = launch_mfma(plan->dtype, plan->width_class, plan->num_slots, a, stream); break;
     case PONNI_PATH_FUSED: err = fused_launch(*plan, a, stream); break;
+    case PONNI_PATH_LAYERED: err = layered_forward(*plan, a, stream); break;
     default: err = launch_generic(plan->dtype, a, stream); break;
   }
   if (err != hipSuccess) return fail(PONNI_ERR_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(err));

@@ -90,6 +90,25 @@ constexpr size_t kStaticScratchBytes = size_t(PONNI_NO_ALLOC_SCRATCH_BYTES);
 hipError_t static_scratch(int device, void** out);
 
 hipError_t launch_generic(int dtype, LaunchArgs const& args, hipStream_t stream);
+// One dense op of a LAYERED plan (kernels_generic.hip layered_dense): in and
+// out are the op's state buffers, params the plan's packed parameters in the
+// compute type (GENERIC packing: W [n_in][n_out] at woff).
+struct DenseArgs {
+  const void* x;
+  int64_t ldx;
+  void* y;
+  int64_t ldy;
+  int64_t batch;
+  const void* params;
+  int32_t woff;
+  int32_t n_in;
+  int32_t n_out;
+  int32_t epi_begin;
+  int32_t epi_count;
+  int32_t bias_first;  // the first step is a bias that seeds the sum
+  const Step* steps;
+};
+hipError_t launch_layered_dense(int dtype, DenseArgs const& a, hipStream_t stream);
 hipError_t launch_narrow(int dtype, int width_class, int num_slots, LaunchArgs const& args,
                          hipStream_t stream);
 hipError_t launch_mfma(int dtype, int width_class, int num_slots, LaunchArgs const& args,

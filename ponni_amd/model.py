@@ -20,7 +20,7 @@ from . import _abi as A
 
 _DTYPES = {"f32": A.F32, "f64": A.F64, "f16": A.F16, "bf16": A.BF16}
 _PATHS = {"auto": A.PATH_AUTO, "generic": A.PATH_GENERIC, "narrow": A.PATH_NARROW, "mfma": A.PATH_MFMA,
-          "fused": A.PATH_FUSED}
+          "fused": A.PATH_FUSED, "layered": A.PATH_LAYERED}
 
 
 @dataclass

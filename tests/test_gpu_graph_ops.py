@@ -77,7 +77,7 @@ def test_oracle_matches_numpy_graph(op):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-@pytest.mark.parametrize("path", ["generic", "narrow", "fused"])
+@pytest.mark.parametrize("path", ["generic", "narrow", "fused", "layered"])
 @pytest.mark.parametrize("op", OPS)
 def test_domain_ops_on_gpu(cuda, op, path, dtype):
     import torch
@@ -110,7 +110,7 @@ def test_domain_ops_on_gpu(cuda, op, path, dtype):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-@pytest.mark.parametrize("path", ["generic", "narrow", "fused"])
+@pytest.mark.parametrize("path", ["generic", "narrow", "fused", "layered"])
 @pytest.mark.parametrize("seed", range(6))
 def test_op_graphs_on_gpu(cuda, seed, path, dtype):
     """Random graphs over Where / comparisons / logic / Clip / PRelu /

@@ -19,7 +19,9 @@ pytestmark = pytest.mark.gpu
 
 # "narrow-aot" is the interpreted NARROW kernel (run-time compilation off);
 # "narrow" is the generated NARROW kernel.
-PATHS = ["generic", "narrow", "narrow-aot", "mfma", "fused"]
+# "layered" runs the GENERIC op list with each dense block as an MFMA
+# contraction over the batch.
+PATHS = ["generic", "narrow", "narrow-aot", "mfma", "fused", "layered"]
 TORCH_DT = {"f32": "float32", "f16": "float16", "bf16": "bfloat16", "f64": "float64"}
 ORACLE_MODE = {"f32": oracle.MODE_F32, "f64": oracle.MODE_F64, "f16": oracle.MODE_F16_OPERANDS,
                "bf16": oracle.MODE_BF16_OPERANDS}

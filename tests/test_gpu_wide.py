@@ -6,12 +6,13 @@ and one launch covers the chain (src/ponni_Inference.h:384-388).  Here FUSED
 keeps the states of 16-bit chains up to 1024 features and of fp32 chains up
 to 512 in registers (one 16-column tile per wave beyond 256 features; the
 contraction runs over 32-feature steps of any count); wider fp32 and fp64
-chains take GENERIC.
+chains take LAYERED (the GENERIC op list with every dense block run over
+the whole batch as an MFMA contraction, states in HBM).
 
 CPU: the path each width takes, and that every FUSED kernel compiles
 (hipRTC, no device).  GPU: chains of 320, 512 and 1024 features with a
-residual and a LayerNorm at full width, on the default path and on GENERIC,
-against the oracle at the fixed bars."""
+residual and a LayerNorm at full width, on the default path, on GENERIC
+and on LAYERED, against the oracle at the fixed bars."""
 import numpy as np
 import pytest
 
@@ -33,9 +34,9 @@ def wide_chain(width, n_in=40, n_out=24, seed=0):
             P.Matvec(W(width, n_out)), P.Bias(rng.uniform(-0.1, 0.1, n_out))]
 
 
-EXPECTED = {("f32", 320): "fused", ("f32", 512): "fused", ("f32", 1024): "generic",
+EXPECTED = {("f32", 320): "fused", ("f32", 512): "fused", ("f32", 1024): "layered",
             ("f16", 320): "fused", ("f16", 512): "fused", ("f16", 1024): "fused",
-            ("bf16", 512): "fused", ("f64", 320): "generic"}
+            ("bf16", 512): "fused", ("f64", 320): "layered"}
 
 
 @pytest.mark.parametrize("dtype,width", sorted(EXPECTED))
@@ -54,7 +55,7 @@ def test_wide_path_choice_and_compile(dtype, width, tmp_path, monkeypatch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("path", ["auto", "generic"])
+@pytest.mark.parametrize("path", ["auto", "generic", "layered"])
 @pytest.mark.parametrize("dtype,width", sorted(EXPECTED))
 def test_wide_chain_on_gpu(cuda, dtype, width, path):
     from tests.test_gpu_parity import ORACLE_MODE, check_f32, check_half, gpu_run

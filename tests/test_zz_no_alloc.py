@@ -28,7 +28,7 @@ def call(fn, m, x, y, B, stream):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("path,layers", [("generic", residual_chain()), ("fused", residual_chain(32)),
-                                         ("narrow", C.c1_layers())])
+                                         ("narrow", C.c1_layers()), ("layered", residual_chain(80))])
 def test_no_alloc_matches_forward(cuda, path, layers):
     import torch
 
