@@ -226,3 +226,40 @@ def test_random_cases(cuda, group):
         if r is not None and not r[1]:
             failed.append(f"seed {seed}: {r[0]}: {r[2]}")
     assert not failed, "\n".join(failed)
+
+
+def _wide_case(seed):
+    """A random chain wider than 256 features (fp32, fp16 or bf16) on a path
+    drawn from those that take it: AUTO, FUSED (16-bit up to 1024, fp32 up
+    to 512), LAYERED (any width) or GENERIC; fixed bars."""
+    rng = np.random.default_rng(seed)
+    B = int(rng.choice([1, 255, 1000, 4097]))
+    width = int(rng.choice([272, 320, 384, 512, 700, 1024]))
+    dtype = ["f32", "f16", "bf16"][int(rng.integers(3))]
+    layers = K.random_chain(rng, width, 2)
+    x = rng.standard_normal((width, B))
+    path = ["auto", "fused", "layered", "generic"][int(rng.integers(4))]
+    desc = f"wide chain {dtype} width={width} path={path} B={B}"
+    print(desc, flush=True)
+    r = _run_chain(layers, x, dtype, path, int(rng.integers(4)))
+    if r is None:
+        return None
+    got, xg = r
+    if dtype == "f32":
+        want = oracle.forward(layers, xg)
+        return desc, _fp32_ok(got, want), f"relL2={_rel(got, want):.2e}"
+    mode = oracle.MODE_F16_OPERANDS if dtype == "f16" else oracle.MODE_BF16_OPERANDS
+    rel = _rel(got, oracle.forward(layers, xg, mode))
+    return desc, bool(np.isfinite(got).all() and rel <= 2e-3), f"relL2={rel:.2e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", range(2))
+def test_random_wide_cases(cuda, group):
+    failed = []
+    for seed in range(9000 + group * 12, 9000 + (group + 1) * 12):
+        print(f"seed {seed}: ", end="", flush=True)
+        r = _wide_case(seed)
+        if r is not None and not r[1]:
+            failed.append(f"seed {seed}: {r[0]}: {r[2]}")
+    assert not failed, "\n".join(failed)
