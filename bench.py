@@ -230,6 +230,7 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
     A.check(A.lib().ponni_forward_steps(model._plan, xp, xs[0].stride(0), yp, ys[0].stride(0), B, len(xs), steps,
                                         stream, ctypes.byref(cabi)))
     work = cfg.flops_per_sample if cfg.bound == "mfma" else cfg.bytes_per_sample
+    registered = {**C.CONFIGS, **C.SUPPLEMENTARY}.get(cfg.name)
     unit = "TFLOP/s" if cfg.bound == "mfma" else "GB/s"
     scale = 1e12 if cfg.bound == "mfma" else 1e9
     achieved = work * B / (kernel_ms * 1e-3)
@@ -250,9 +251,8 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
             "frac": round(achieved / cfg.peak, 4),
             "frac_per_step": round(work * B / (ms_per_step * 1e-3) / cfg.peak, 4),
             # (PMC traffic is measured for the configurations' own precision and batch only)
-            "traffic": (pmc_traffic(cfg.name)
-                        if cfg.name in C.CONFIGS and cfg.dtype == C.CONFIGS[cfg.name].dtype
-                        and cfg.batch == C.CONFIGS[cfg.name].batch else None),
+            "traffic": (pmc_traffic(cfg.name) if registered is not None and cfg.dtype == registered.dtype
+                        and cfg.batch == registered.batch else None),
         },
         "path": model.path,
     }
