@@ -21,6 +21,9 @@
 #include <sstream>
 #include <string>
 #include <vector>
+#include <climits>
+#include <dlfcn.h>
+#include <link.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -421,6 +424,11 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
 
   if (dbl) o << "#define PONNI_REAL double\n";
   if (NT != 2) o << "#define PONNI_NT " << NT << "\n";
+  // One column tile per wave at two waves per SIMD: A fragments read two
+  // steps ahead (fused_f16.h kFragPipe; 64x512x512x64 3.28 against 3.38 ms,
+  // 320 / 384 features 5-7 % faster; at one wave per SIMD, and with two
+  // column tiles per wave (c4), reading ahead measured slower).
+  if (half && NT == 1 && cfg.waves_per_simd >= 2) o << "#define PONNI_PIPE 2\n";
   o << "#include \"" << (half ? "fused_f16.h" : "fused_f32.h") << "\"\n";
   o << "using namespace ponni_hip;\nusing namespace ponni_hip::fused;\n";
   if (half) o << "typedef " << E << " E;\n";
@@ -1027,15 +1035,49 @@ bool narrow_jit_supports(ponni_plan_s const& p) {
 
 namespace {
 
-// Source, options, embedded headers and the run-time compiler's version: a
-// compiler upgrade (whose code generation the kernels' numerics depend on)
-// never picks up an object an older one wrote.
+// The code generator behind hipRTC: the libamd_comgr the process has loaded,
+// else the one beside the loaded hipRTC library, which hipRTC loads at its
+// first compile.  hipRTC reports one version for different code generators:
+// torch ships its own hipRTC and comgr (older than the system ROCm's), which
+// a Python process that imported torch uses, while a C++ program uses the
+// system's, and their kernels differ in rounding (one fuses the last FMA
+// with the conversion to fp16, the other rounds twice).
+std::string compiler_identity() {
+  std::string path;
+  dl_iterate_phdr(
+      [](dl_phdr_info* info, size_t, void* out) -> int {
+        if (info->dlpi_name == nullptr || std::strstr(info->dlpi_name, "libamd_comgr") == nullptr) return 0;
+        *static_cast<std::string*>(out) = info->dlpi_name;
+        return 1;
+      },
+      &path);
+  char buf[PATH_MAX];
+  if (path.empty()) {
+    Dl_info di{};
+    if (dladdr(reinterpret_cast<void*>(&hiprtcCompileProgram), &di) != 0 && di.dli_fname != nullptr &&
+        realpath(di.dli_fname, buf) != nullptr) {
+      std::string dir(buf);
+      dir = dir.substr(0, dir.rfind('/'));
+      path = dir + "/libamd_comgr.so.3";
+    }
+  }
+  if (path.empty() || realpath(path.c_str(), buf) == nullptr) return "comgr unknown";
+  std::string id = std::string("comgr ") + buf;
+  struct stat sb;
+  if (stat(buf, &sb) == 0) id += " " + std::to_string(sb.st_size) + " " + std::to_string(sb.st_mtime);
+  return id;
+}
+
+// Source, options, embedded headers, the run-time compiler's version and
+// code generator: a compiler change (whose code generation the kernels'
+// numerics depend on) never picks up an object another one wrote.
 std::string cache_key(std::string const& src, bool contract) {
   std::string opts;
   for (auto const* o : jit_options(contract)) opts += std::string(o) + " ";
   int major = 0, minor = 0;
   if (hiprtcVersion(&major, &minor) == HIPRTC_SUCCESS)
     opts += "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + " ";
+  opts += compiler_identity() + " ";
   std::string hdrs;
   for (int i = 0; i < kJitHeaderCount; i++) hdrs += kJitHeaderTexts[i];
   char buf[32];
@@ -1090,10 +1132,17 @@ int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, st
       regs = (v < 0 ? 512 : v) + (a < 0 ? 0 : a);
       return static_cast<int>(PONNI_OK);
     };
+    // 16-bit plans with one column tile per wave keep two waves per SIMD
+    // with a few spilled registers (loop-invariant row addresses, reloaded
+    // once per tile): one wave per SIMD halves the columns each staged
+    // weight chunk serves, which costs more (64x512x512x64: 3.28 ms with 20
+    // registers spilled, 5.25 ms at one wave per SIMD).
+    bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
+    auto tolerated = [&](int w) { return half && fused_nt(p) == 1 && w == 2 ? 32 : 0; };
     int spills = 0, regs = 0;
     int st = spills_regs(wps, spills, regs);
     if (st != PONNI_OK) return st;
-    while (spills > 0 && wps > 1) {
+    while (spills > tolerated(wps) && wps > 1) {
       wps--;
       st = spills_regs(wps, spills, regs);
       if (st != PONNI_OK) return st;

@@ -281,6 +281,16 @@ __device__ inline void stage_begin(Stage<E>& st) {
 constexpr int kTileGroup = 2;
 constexpr bool kDeferEpilogue = true;
 constexpr bool kSetPrio = true;
+// A fragments read PONNI_PIPE contraction steps ahead of their MFMAs, with
+// a scheduling barrier after each step so that the compiler neither hoists
+// the reads further (their registers) nor sinks them: what plans with one
+// column tile per wave at two waves per SIMD use (320-512 features: 3-7 %
+// faster).  0 (the default, two column tiles per wave): each step's
+// fragments are read in the step, the compiler schedules freely.
+#ifndef PONNI_PIPE
+#define PONNI_PIPE 0
+#endif
+constexpr int kFragPipe = PONNI_PIPE;
 
 struct NoHook {
   __device__ void operator()() const {}
@@ -337,12 +347,20 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, Stage<E>& st, La
         // other wave fills the matrix pipe's shadow with its VALU epilogue
         // instead of both waves contending in the same phase.
         if (kSetPrio) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int t = 0; t < TS; t++) {
-          V8 a[GT];
+        // Fragment ring: step t's fragments sit in a[t % (D + 1)].
+        constexpr int D = kFragPipe;
+        V8 a[D + 1][GT];
+        auto read = [&](int t) {
 #pragma unroll
           for (int q = 0; q < GT; q++)
-            if (mo0 + q < TO) a[q] = sl[((tt + q) * TS + t) * 64];
+            if (mo0 + q < TO) a[t % (D + 1)][q] = sl[((tt + q) * TS + t) * 64];
+        };
+#pragma unroll
+        for (int t = 0; t < D && t < TS; t++) read(t);
+#pragma unroll
+        for (int t = 0; t < TS; t++) {
+          if (t + D < TS) read(t + D);
+          V8 const (&at)[GT] = a[t % (D + 1)];
 #pragma unroll
           for (int n = 0; n < NT; n++) {
             V4 const lo = in.v[2 * t][n];
@@ -351,8 +369,9 @@ __device__ inline H<TO, NT, E> dense_hs(H<TI, NT, E> const& in, Stage<E>& st, La
             V8 const b = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int q = 0; q < GT; q++)
-              if (mo0 + q < TO) acc[q][n] = TR ? Vec<E>::mfma(b, a[q], acc[q][n]) : Vec<E>::mfma(a[q], b, acc[q][n]);
+              if (mo0 + q < TO) acc[q][n] = TR ? Vec<E>::mfma(b, at[q], acc[q][n]) : Vec<E>::mfma(at[q], b, acc[q][n]);
           }
+          if (D > 0) __builtin_amdgcn_sched_barrier(0);
         }
         if (kSetPrio) __builtin_amdgcn_s_setprio(0);
         if (DEFER) {
