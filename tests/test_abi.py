@@ -272,6 +272,46 @@ def test_fused_kernels_compile_on_the_host(seed, tmp_path, monkeypatch):
     assert any(f.suffix == ".co" for f in tmp_path.iterdir())
 
 
+_COMPILE_C2 = """
+import sys
+if sys.argv[1] == "torch":
+    import torch  # brings its own hipRTC and comgr, which this process's compiles then use
+import ponni_amd as P
+m = P.create_inference_model(*P.configs.CONFIGS["c2"].layers(False), dtype="f32", path="fused")
+m.compile()
+print(min([l.split()[-1] for l in open("/proc/self/maps") if "libamd_comgr" in l] or ["none (cache hit)"]))
+"""
+
+
+def test_jit_cache_keyed_by_code_generator(tmp_path):
+    """The on-disk kernel cache is keyed by the code generator behind hipRTC,
+    not only by hipRTC's version: a process that imported torch compiles with
+    torch's comgr, one that did not with the system's (both report hipRTC
+    9.0), and their kernels differ in rounding, so each keeps its own object.
+    A second process of either kind hits the cache."""
+    import subprocess
+    import sys
+
+    env = dict(os.environ, PONNI_JIT_CACHE=str(tmp_path))
+
+    def run(kind):
+        r = subprocess.run([sys.executable, "-c", _COMPILE_C2, kind], env=env, cwd=ROOT, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+        return r.stdout.strip()
+
+    comgr_plain = run("plain")
+    objects = sorted(f.name for f in tmp_path.iterdir() if f.suffix == ".co")
+    assert len(objects) == 1
+    comgr_torch = run("torch")
+    after = sorted(f.name for f in tmp_path.iterdir() if f.suffix == ".co")
+    if os.path.realpath(comgr_torch) == os.path.realpath(comgr_plain):
+        assert after == objects  # one code generator: one object, found again
+    else:
+        assert len(after) == 2 and set(objects) < set(after)
+    assert run("plain") == "none (cache hit)"  # found on disk: the compiler was never loaded
+    assert sorted(f.name for f in tmp_path.iterdir() if f.suffix == ".co") == after
+
+
 def deep_half_chain(norms=8, seed=61):
     """16-bit chain whose per-feature vectors (17 KB) outgrow the LDS left
     next to the A-fragment staging and the input rows (96 + 48 KB): 96 -> 256

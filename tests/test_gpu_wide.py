@@ -9,8 +9,9 @@ contraction runs over 32-feature steps of any count); wider fp32 and fp64
 chains take LAYERED (the GENERIC op list with every dense block run over
 the whole batch as an MFMA contraction, states in HBM).
 
-CPU: the path each width takes, and that every FUSED kernel compiles
-(hipRTC, no device).  GPU: chains of 320, 512 and 1024 features with a
+CPU: the path each width takes, that every FUSED kernel compiles (hipRTC,
+no device), and the occupancy 16-bit plans settle on (two waves per SIMD up
+to 512 features, with fragments read two steps ahead; one at 1024).  GPU: chains of 320, 512 and 1024 features with a
 residual and a LayerNorm at full width, on the default path, on GENERIC
 and on LAYERED, against the oracle at the fixed bars."""
 import numpy as np
@@ -48,6 +49,13 @@ def test_wide_path_choice_and_compile(dtype, width, tmp_path, monkeypatch):
         m.compile()
         src = m.kernel_source()
         assert "#define PONNI_NT 1" in src
+        threads, _, _ = m.kernel_config()
+        if dtype in ("f16", "bf16") and width <= 512:
+            # two waves per SIMD (eight-wave workgroups), fragments read two steps ahead
+            assert threads == 512 and "#define PONNI_PIPE 2" in src
+        elif dtype in ("f16", "bf16"):
+            # 1024 features: both states fill the registers of one wave per SIMD
+            assert threads == 256 and "PONNI_PIPE" not in src
     else:
         with pytest.raises(P.PonniError) as e:
             P.create_inference_model(*wide_chain(width), dtype=dtype, path="fused")
