@@ -324,14 +324,9 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
   // dense_hs), or one when the widest layer's two states do not fit in
   // half the registers.
   int const NT = fused_nt(p);
-  int half_wps = 2;  // 16-bit plans: waves per SIMD (one workgroup per CU)
-  if (half) {
-    int widest = 0;  // 16-bit input and output tiles of the widest dense op
-    for (Op const& op : p.ops)
-      if (op.code == OP_DENSE) widest = std::max(widest, tiles(op.n_in) + tiles(op.n_out));
-    // 2 NT registers per 16-bit tile; accumulators, fragments, addresses.
-    if (widest * 2 * NT + 2 * 2 * NT * 4 + 2 * 4 + 48 > 256) half_wps = 1;
-  }
+  // 16-bit plans: two waves per SIMD (one eight-wave workgroup per CU), the
+  // compile permitting (fused_compile).
+  int const half_wps = 2;
   int64_t const param_bytes = (p.packed_elements * es + 31) / 32 * 32;
   cfg.lds_bytes = !half && param_bytes <= kFusedLdsParamBytes ? static_cast<int>(param_bytes) : 0;
   cfg.waves = 4;
@@ -1132,13 +1127,17 @@ int fused_compile(ponni_plan_s& p, std::string& key, std::vector<char>& code, st
       regs = (v < 0 ? 512 : v) + (a < 0 ? 0 : a);
       return static_cast<int>(PONNI_OK);
     };
-    // 16-bit plans with one column tile per wave keep two waves per SIMD
-    // with a few spilled registers (loop-invariant row addresses, reloaded
-    // once per tile): one wave per SIMD halves the columns each staged
-    // weight chunk serves, which costs more (64x512x512x64: 3.28 ms with 20
-    // registers spilled, 5.25 ms at one wave per SIMD).
+    // 16-bit plans keep two waves per SIMD with spilled registers: one wave
+    // per SIMD halves the columns each staged weight chunk serves.  With one
+    // column tile per wave (wider than 256 features) that costs more than any
+    // spilling measured (fp16 64x512x512x64, 20 registers spilled: 3.28
+    // against 5.25 ms; 40 -> 512 residual chain with a LayerNorm, 109: 3.60
+    // against 4.84 ms; the same at 1024 features, 691: 8.9 against 11.8 ms);
+    // with two, up to 64 (that chain at 192 / 256 features, 44 / 47
+    // spilled: 13-16 % faster; a 256-wide chain of three residual blocks,
+    // 328: 20 % slower).
     bool const half = p.dtype == PONNI_F16 || p.dtype == PONNI_BF16;
-    auto tolerated = [&](int w) { return half && fused_nt(p) == 1 && w == 2 ? 32 : 0; };
+    auto tolerated = [&](int w) { return half && w == 2 ? fused_nt(p) == 1 ? INT_MAX : 64 : 0; };
     int spills = 0, regs = 0;
     int st = spills_regs(wps, spills, regs);
     if (st != PONNI_OK) return st;
