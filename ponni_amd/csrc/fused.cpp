@@ -549,7 +549,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
     o << "  if (blockIdx.x < tiles && xvec && L.col0 + " << WCOLS << " <= batch) prefetch_rows_lds16<" << n_in0 << ", "
       << NT << ">(x, ldx, L, in_buf[wave_id()]);\n";
     // The LDS writes of these loads complete with vmcnt, which the compiler
-    // does not track for reads of in_buf: each tile's rows are waited for
+    // does not track (fused_f16.h dma16): each tile's rows are waited for
     // explicitly, here for the first tile and before the output stores for
     // the next one (requested during the tile, so long landed).
     o << "  wait_vmem();\n";

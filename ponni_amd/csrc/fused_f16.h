@@ -103,6 +103,26 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
 // loads are asynchronous: the caller waits (vmcnt) before reading buf.
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// One 16-byte global_load_lds_dwordx4 per lane: lane l's 16 bytes at g land
+// in LDS at lds + 16 l (lds uniform across the wave, passed in M0).  Issued
+// as inline asm so that the compiler's wait insertion does not see an LDS
+// write it cannot place: it cannot tell apart regions of one LDS array
+// addressed at run time (the staging slots), so after the builtin it waits
+// for every outstanding request (vmcnt(0)) before the next read of the
+// array -- the first fragment read of every chunk waited for the requests
+// just made for two chunks ahead.  Every read of data requested here is
+// ordered by the kernel's own explicit waits (a vmcnt that leaves only
+// later requests outstanding, then a barrier where other waves' requests
+// are read); the compiler's own vmcnt values stay correct, because vector
+// memory loads complete in issue order and untracked requests only make
+// them wait longer.  The s_nop is the wait state the hardware needs
+// between the write of M0 and an LDS DMA, which the compiler inserts for
+// its own instructions but not in front of inline asm.
+__device__ inline void dma16(void const* g, void* lds) {
+  unsigned const m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uint64_t>((lds_ptr)lds)));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
+
 template <int N, int NT, class E>
 __device__ inline void prefetch_rows_lds16(E const* __restrict__ x, int64_t ld, Lane const& L,
                                            unsigned short* __restrict__ buf) {
@@ -114,8 +134,7 @@ __device__ inline void prefetch_rows_lds16(E const* __restrict__ x, int64_t ld, 
     int const piece = 64 * i + L.lane;
     int const r = piece / PR, k = piece % PR;
     if (N % 16 == 0 || r < N)
-      __builtin_amdgcn_global_load_lds(static_cast<void const*>(x + int64_t(r) * ld + L.col0 + 8 * k),
-                                       (lds_ptr)(buf + 64 * 8 * i), 16, 0, 0);
+      dma16(x + int64_t(r) * ld + L.col0 + 8 * k, buf + 64 * 8 * i);
   }
 }
 
@@ -252,8 +271,7 @@ __device__ inline void request_chunk(Stage<E> const& st, int kk, int wave, int l
   for (int r = 0; r < chunk_requests<WAVES>(); r++) {
     int const f = wave + WAVES * r;
     int const fs = f < nf ? f : nf - 1;  // (a repeat lands in an unused fragment of the slot)
-    __builtin_amdgcn_global_load_lds(static_cast<void const*>(src + fs * 512 + lane * 8),
-                                     (lds_ptr)(st.slots + (slot * kSlotFrags + f) * 64), 16, 0, 0);
+    dma16(src + fs * 512 + lane * 8, st.slots + (slot * kSlotFrags + f) * 64);
   }
 }
 
