@@ -312,6 +312,45 @@ def test_jit_cache_keyed_by_code_generator(tmp_path):
     assert sorted(f.name for f in tmp_path.iterdir() if f.suffix == ".co") == after
 
 
+def _chunk_start_vmem_waits(code_object):
+    """For each s_barrier of a compiled kernel followed by MFMAs before the
+    next barrier: whether a vmcnt(0) wait sits between the two.  Returns
+    (regions checked, regions with such a wait)."""
+    import shutil
+    import subprocess
+
+    objdump = shutil.which("llvm-objdump") or "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not found")
+    out = subprocess.run([objdump, "-d", "--mcpu=gfx950", str(code_object)], capture_output=True, text=True,
+                         check=True).stdout
+    ins = [l.split("//")[0].strip() for l in out.splitlines()]
+    ins = [l for l in ins if l and not l.endswith(":") and not l.startswith("Disassembly")]
+    checked = waiting = 0
+    for b in (i for i, l in enumerate(ins) if l.startswith("s_barrier")):
+        j = b + 1
+        while j < len(ins) and not ins[j].startswith(("v_mfma", "s_barrier", "s_endpgm")):
+            j += 1
+        if j < len(ins) and ins[j].startswith("v_mfma"):
+            checked += 1
+            waiting += any(re.match(r"s_waitcnt.*vmcnt\(0\)", l) for l in ins[b + 1:j])
+    return checked, waiting
+
+
+def test_half_fused_chunks_do_not_wait_for_their_own_requests(tmp_path, monkeypatch):
+    """The 16-bit FUSED kernel requests weight chunk k + 2 at the start of
+    chunk k, out of the compiler's wait tracking: in c4's compiled kernel no
+    chunk starts (barrier, then its MFMAs) with a wait for every outstanding
+    request -- only the kernel's first tile, which waits for its input rows,
+    does.  (Issued through the compiler's builtin, every chunk did.)"""
+    monkeypatch.setenv("PONNI_JIT_CACHE", str(tmp_path))
+    m = create(P.configs.CONFIGS["c4"].layers(False), dtype="f16", path="fused")
+    m.compile()
+    (co,) = [f for f in tmp_path.iterdir() if f.suffix == ".co"]
+    checked, waiting = _chunk_start_vmem_waits(co)
+    assert checked >= 10 and waiting <= 1, (checked, waiting)
+
+
 def deep_half_chain(norms=8, seed=61):
     """16-bit chain whose per-feature vectors (17 KB) outgrow the LDS left
     next to the A-fragment staging and the input rows (96 + 48 KB): 96 -> 256
