@@ -61,18 +61,30 @@ struct Lane {
   int64_t col0, batch;
 };
 
+// Cross-lane-group reductions: op(v, lane ^ 16) then op(v, lane ^ 32).  In
+// fp32 each step is one v_permlane{16,32}_swap of v with a copy of itself,
+// which leaves v's and its partner's values in the two results of every
+// lane, combined by op (commutative); fp64 uses the LDS crossbar.
+template <class Op>
+__device__ inline float xreduce(float v, Op op) {
+  auto const a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto const b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+template <class Op>
+__device__ inline double xreduce(double v, Op op) {
+  v = op(v, __shfl_xor(v, 16));
+  return op(v, __shfl_xor(v, 32));
+}
 __device__ inline real xsum(real v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return xreduce(v, [](real a, real b) { return a + b; });
 }
 __device__ inline real xmax(real v) {
-  v = d_max(v, __shfl_xor(v, 16));
-  return d_max(v, __shfl_xor(v, 32));
+  return xreduce(v, [](real a, real b) { return d_max(a, b); });
 }
 __device__ inline real xmin(real v) {
-  v = d_min(v, __shfl_xor(v, 16));
-  return d_min(v, __shfl_xor(v, 32));
+  return xreduce(v, [](real a, real b) { return d_min(a, b); });
 }
 
 __device__ inline realx4 ld4(real const* p) { return *reinterpret_cast<realx4 const*>(p); }
