@@ -204,12 +204,14 @@ def time_config(cfg, steps, warmup, torch, P, C, ev):
     starts = [ev.create() for _ in range(steps)]
     stops = [ev.create() for _ in range(steps)]
     t0, t1 = ev.create(), ev.create()
+    # The rotation continues past the warm-up's buffer sets, so no timed
+    # launch finds its input still in the MALL from a recent launch; the
+    # launches' arguments are formed before the timed region.
+    launches = [(*args(warmup + i), starts[i], stops[i]) for i in range(steps)]
     try:
         ev.record(t0, stream)
-        # The rotation continues past the warm-up's buffer sets, so no timed
-        # launch finds its input still in the MALL from a recent launch.
-        for i in range(steps):
-            model.forward_raw_timed(*args(warmup + i), starts[i], stops[i])
+        for a in launches:
+            model.forward_raw_timed(*a)
         ev.record(t1, stream)
         torch.cuda.synchronize()
         total_ms = ev.elapsed_ms(t0, t1)
