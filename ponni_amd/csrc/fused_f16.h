@@ -96,8 +96,12 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_h(E const* __restrict__ x, i
 // ---- input rows prefetched into LDS one tile ahead ----------------------
 // A wave's input tile (rows 0..16T-1, columns col0 .. col0 + 16 NT - 1) is
 // requested with global_load_lds_dwordx4: piece p = 64 i + l of instruction
-// i is row p / (2 NT), columns 8 (p % (2 NT)) .. +7, and lands at buf + 8 p,
-// so buf holds the tile row-major ([row][16 NT columns]).  Only whole tiles
+// i fills row slot s = p / (2 NT), columns 8 (p % (2 NT)) .. +7, landing at
+// buf + 8 p, so buf holds 16 NT columns per slot.  Within each block of 16
+// slots, slot 4a + b holds row 4b + a (a 4 x 4 transpose): the tile's
+// reader takes rows 4g + e in lane group g, which then sit in slots 4e + g,
+// 16 NT elements apart instead of 4 x that, in four different LDS banks
+// (row-major, all four groups read one bank).  Only whole tiles
 // of a 16-byte aligned x with a row stride of a multiple of 8 elements are
 // requested this way (the caller checks); rows >= N issue nothing.  The
 // loads are asynchronous: the caller waits (vmcnt) before reading buf.
@@ -132,13 +136,15 @@ __device__ inline void prefetch_rows_lds16(E const* __restrict__ x, int64_t ld, 
 #pragma unroll
   for (int i = 0; i < T * 16 * PR / 64; i++) {
     int const piece = 64 * i + L.lane;
-    int const r = piece / PR, k = piece % PR;
+    int const slot = piece / PR, k = piece % PR;
+    int const r = (slot & ~15) | ((slot & 3) << 2) | ((slot >> 2) & 3);
     if (N % 16 == 0 || r < N)
       dma16(x + int64_t(r) * ld + L.col0 + 8 * k, buf + 64 * 8 * i);
   }
 }
 
-// The lane's tile elements from a prefetched buf; rows >= N read 0.
+// The lane's tile elements from a prefetched buf (row f = 16m + 4g + e in
+// slot 16m + 4e + g); rows >= N read 0.
 template <int N, int NT, class E>
 __device__ inline H<(N + 15) / 16, NT, E> load_rows_lds16(unsigned short const* __restrict__ buf, Lane const& L) {
   constexpr int T = (N + 15) / 16;
@@ -150,7 +156,7 @@ __device__ inline H<(N + 15) / 16, NT, E> load_rows_lds16(unsigned short const* 
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         int const f = 16 * m + 4 * L.g + e;
-        unsigned short const bits = buf[f * (16 * NT) + 16 * n + L.c];
+        unsigned short const bits = buf[(16 * m + 4 * e + L.g) * (16 * NT) + 16 * n + L.c];
         s.v[m][n][e] = (N % 16 == 0 || f < N) ? __builtin_bit_cast(E, bits) : E(0.0f);
       }
   return s;
