@@ -132,7 +132,7 @@ def _generated_case(tmp_path, model):
         if dt == np.float64:
             assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * max(1.0, np.abs(want).max()))
         else:
-            check_f32(got, want, scale_tol=False)
+            check_f32(got, want)
 
     mode = oracle.MODE_F64 if dt == np.float64 else oracle.MODE_F32
     return make_graph, weights, ref, x, B, dt, out, oracle_layers, mode, check

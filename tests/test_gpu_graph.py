@@ -59,7 +59,7 @@ def test_c5_generated_model(cuda, path):
     gm = G.GeneratedModel(C.c5_graph(True), path=path)
     x = C.normal(24 * 5000, 4, C.INPUT_TAG, 0.0, 1.0).reshape(24, 5000)
     got, xg = run_model(gm, x)
-    check_f32(got, oracle.forward(lowered_with_params(gm.graph), xg), scale_tol=False)
+    check_f32(got, oracle.forward(lowered_with_params(gm.graph), xg))
     assert np.allclose(got.sum(axis=0), 1.0, atol=1e-5)  # softmax rows
 
 
@@ -82,7 +82,7 @@ def test_weights_reload_changes_outputs(cuda, tmp_path):
     after, xg = run_model(dst, x)
     want, _ = run_model(src, x)
     assert not np.allclose(before, after)
-    check_f32(after, want, scale_tol=False)
+    check_f32(after, want)
 
 
 @pytest.mark.parametrize("seed", range(4))

@@ -65,7 +65,7 @@ def test_configs_on_host(name):
     layers = cfg.layers(True)
     x = np.random.default_rng(3).standard_normal((cfg.n_in, 777)).astype(np.float32).astype(np.float64)
     got = P.create_inference_model(*layers).forward_host(x).astype(np.float64)
-    check_f32(got, oracle.forward(layers, x), scale_tol=False)
+    check_f32(got, oracle.forward(layers, x))
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2, 5, 7])
