@@ -411,6 +411,19 @@ __device__ inline void softmax(S<T, NT>& s, Lane const& L) {
   }
 }
 
+// The reference's running minimum / maximum (MinMaxNorm, ReduceMax,
+// ReduceMin, ReduceLogSumExp) starts from feature 0 and replaces it only on
+// a strict comparison, so a NaN in feature 0 makes the result NaN and a NaN
+// in any other feature is passed over.  The tile reductions use fmin / fmax,
+// which pass over every NaN; this supplies feature 0's part: true in every
+// lane of column tile n whose feature 0 (lane group 0, element 0 of tile 0)
+// is NaN.
+template <int T, int NT>
+__device__ inline bool first_feature_nan(S<T, NT> const& s, int n, Lane const& L) {
+  real const x0 = s.v[0][n][0];
+  return xmax(L.g == 0 && x0 != x0 ? real(1) : real(0)) != real(0);
+}
+
 // MinMaxNorm over N features, ponni_MinMaxNorm.h:67-84.
 template <int N, int T, int NT>
 __device__ inline void min_max(S<T, NT>& s, real out_min, real out_max, real eps, Lane const& L) {
@@ -427,6 +440,7 @@ __device__ inline void min_max(S<T, NT>& s, real out_min, real out_max, real eps
         }
     lo = xmin(lo);
     hi = xmax(hi);
+    if (first_feature_nan(s, n, L)) lo = hi = real(__builtin_nanf(""));
     real const scale = (out_max - out_min) / ((hi - lo) + eps);
 #pragma unroll
     for (int m = 0; m < T; m++)
@@ -627,6 +641,7 @@ __device__ inline S<1, NT> reduce(S<T, NT> const& s, Lane const& L) {
         for (int e = 0; e < 4; e++)
           if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = OP == 3 ? d_min(mx, s.v[m][n][e]) : d_max(mx, s.v[m][n][e]);
       mx = OP == 3 ? xmin(mx) : xmax(mx);
+      if (first_feature_nan(s, n, L)) mx = real(__builtin_nanf(""));
       r = mx;
       if constexpr (OP == 8) {
         real sum = 0.0f;

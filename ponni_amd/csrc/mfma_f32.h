@@ -255,6 +255,11 @@ __global__ __launch_bounds__(256) void mfma_forward_f32(LaunchArgs a) {
               }
           lo = xor_min(lo);
           hi = xor_max(hi);
+          // The reference's running minimum / maximum starts from feature 0
+          // and replaces it only on a strict comparison: a NaN there makes
+          // both NaN, a NaN elsewhere is passed over (as fminf / fmaxf do).
+          float const x0 = st[0][n][0];  // feature 0: lane group 0, element 0
+          if (xor_max(g == 0 && x0 != x0 ? 1.0f : 0.0f) != 0.0f) lo = hi = __builtin_nanf("");
           float const scale = (float(op.f1) - float(op.f0)) / ((hi - lo) + float(op.f2));
 #pragma unroll
           for (int m = 0; m < MT; m++)

@@ -10,7 +10,7 @@ their real domain.  The oracle's restatement of each operation is pinned
 first against the float64 numpy evaluation of the graph itself
 (tests/numpy_graph.py), on the CPU.
 
-fp32 bar: relative L2 <= 1e-5 and max-abs <= 1e-4 x max(1, max|ref|);
+fp32 bar: relative L2 <= 1e-5 and max-abs <= 1e-4 (unscaled);
 fp16 bar: relative L2 <= 2e-3 against the oracle's fp16-operand /
 fp32-accumulate mode on the same fp16-rounded inputs.
 """
@@ -150,3 +150,45 @@ def test_op_graphs_on_gpu(cuda, seed, path, dtype):
         check_f32(got, oracle.forward(layers, x))
     else:
         check_half(got, oracle.forward(layers, x, oracle.MODE_F16_OPERANDS))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("path", ["generic", "narrow", "fused", "layered"])
+@pytest.mark.parametrize("n", [12, 16])
+def test_reductions_of_non_finite_inputs(cuda, n, path, dtype):
+    """ReduceMax / ReduceMin / ReduceLogSumExp (kokkos_nn/emitter.py:502-526)
+    straight on inputs holding NaN, infinities, values that overflow fp16
+    and signed zeros: the running maximum or minimum starts from feature 0,
+    so a NaN there makes it NaN and a NaN elsewhere is passed over, on every
+    kernel family as in the oracle."""
+    import torch
+
+    from tests.test_gpu_parity import check_non_finite, non_finite_input
+
+    g = G.GraphBuilder(n)
+    x = g.input
+    gr = g.finish(g.concat(g.reduce("ReduceMax", x), g.reduce("ReduceMin", x), g.reduce("ReduceLogSumExp", x)))
+    gm = G.GeneratedModel(gr, path=path)
+    try:
+        plan = gm.plan(dtype)
+    except P.PonniError as e:
+        if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+            pytest.skip(e.message)
+        raise
+    assert plan.path == path
+    B = 4099
+    xin = non_finite_input(n, B, np.random.default_rng(90 + n))
+    print(f"non-finite reductions: n={n} path={path} dtype={dtype} B={B}", flush=True)
+    xt = torch.from_numpy(xin.astype(np.float32)).cuda()
+    y = torch.full((gm.num_outputs, B), 7.0, dtype=torch.float32, device="cuda:0")
+    (gm.infer_batch_half2 if dtype == "f16" else gm.infer_batch)(xt, y)
+    torch.cuda.synchronize()
+    xg = xt.double().cpu().numpy()
+    if dtype == "f16":
+        with np.errstate(over="ignore"):  # 1e30 rounds to inf in fp16, as on the GPU
+            xh = xg.astype(np.float16).astype(np.float64)
+        want = oracle.forward(lowered_with_params(gr), xh, oracle.MODE_F16_OPERANDS)
+    else:
+        want = oracle.forward(lowered_with_params(gr), xg)
+    check_non_finite(y.double().cpu().numpy(), want, dtype)

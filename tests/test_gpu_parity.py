@@ -560,6 +560,77 @@ def test_column_subviews_at_any_offset(cuda, chain, path, dtype):
             check_half(got, want)
 
 
+NONFINITE_CHAINS = {
+    "MinMaxNorm16": (lambda: [P.MinMaxNorm(16, -1.0, 2.0)], True),
+    "MinMaxNorm12": (lambda: [P.MinMaxNorm(12)], True),
+    "Softmax12": (lambda: [P.Softmax(12)], True),
+    "LogSoftmax16": (lambda: [P.LogSoftmax(16)], True),
+    "LayerNorm12": (lambda: [P.LayerNorm(12)], True),
+    "Tanh12": (lambda: [P.Tanh(12)], False),
+    "Sigmoid12": (lambda: [P.Sigmoid(12)], False),
+    "Silu12": (lambda: [P.Silu(12)], False),
+    "GeluTanh12": (lambda: [P.Gelu(12, True)], False),
+    "Relu12": (lambda: [P.Relu(12)], False),
+}
+
+
+def non_finite_input(n, B, rng):
+    """Normal samples with NaN, +-inf, +-1e30 and signed zeros planted:
+    feature 0 of columns 0-63, a later feature of columns 64-127, two
+    features of columns 128-191 and one feature of every tenth column after."""
+    special = np.array([np.nan, np.inf, -np.inf, 1e30, -1e30, 0.0, -0.0])
+    x = rng.standard_normal((n, B))
+    for j in range(64):
+        x[0, j] = special[j % 7]
+        x[1 + j % (n - 1), 64 + j] = special[(j + 3) % 7]
+        x[rng.choice(n, 2, replace=False), 128 + j] = special[rng.integers(7, size=2)]
+    for j in range(192, B, 10):
+        x[rng.integers(n), j] = special[rng.integers(7)]
+    return x
+
+
+def check_non_finite(got, want, dtype):
+    """NaN where the oracle has NaN, the same infinities, and the finite
+    outputs within the dtype's bar (fp32 per element: 1e-4 + 1e-5 |ref|)."""
+    bad = np.isnan(got) != np.isnan(want)
+    assert not bad.any(), f"NaN mismatch at (feature, column) {np.argwhere(bad)[:5].tolist()}"
+    inf = np.isinf(want)
+    assert np.array_equal(np.isinf(got), inf) and np.array_equal(got[inf], want[inf]), "infinities differ"
+    fin = np.isfinite(want)
+    g, w = got[fin], want[fin]
+    if dtype == "f32":
+        err = np.abs(g - w) - (1e-4 + 1e-5 * np.abs(w))
+        assert err.max() <= 0, f"finite outputs off by {np.abs(g - w)[err.argmax()]:.3e}"
+    elif dtype == "f64":
+        assert np.all(np.abs(g - w) <= 1e-10 * np.maximum(1.0, np.abs(w)))
+    else:
+        check_half(g, w)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16", "f64"])
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("chain", sorted(NONFINITE_CHAINS))
+def test_non_finite_inputs(cuda, chain, path, dtype):
+    """NaN, infinities, values that overflow fp16 and signed zeros fed
+    straight into each barrier layer and into the activations the generated
+    kernels evaluate on the hardware transcendentals: every path gives the
+    oracle's NaNs and infinities (the reference's loops: a NaN in feature 0
+    of a MinMaxNorm makes the whole column NaN, elsewhere only its own
+    output; tanh(+-inf) = +-1) and its finite values."""
+    import torch
+
+    make, barrier = NONFINITE_CHAINS[chain]
+    if not barrier and dtype in ("bf16", "f64"):
+        pytest.skip("pointwise layers: fp32 and fp16 cover the generated forms")
+    layers = make()
+    rng = np.random.default_rng(int.from_bytes(chain.encode()[:4], "little"))
+    x = non_finite_input(layers[0].n_in, 4099, rng)
+    print(f"non-finite: chain={chain} path={path} dtype={dtype}", flush=True)
+    got, xg, _ = gpu_run(layers, x, dtype=dtype, path=path, pad=5)
+    want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
+    check_non_finite(got, want, dtype)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch

@@ -362,3 +362,54 @@ def test_mid_chain_concatenation_before_records_the_reference_defect():
     assert got.tolist() == [[-1.0, 4.0], [2.0, -3.0], [0.0, 4.0], [2.0, 0.0]]
     ref = [reference_mid_chain_concat_before([max(v, 0.0) for v in x[:, b]], list(x[:, b])) for b in range(2)]
     assert np.array(ref).T.tolist() == [[-1.0, 4.0], [2.0, -3.0], [-1.0, 4.0], [2.0, -3.0]]
+
+
+def test_non_finite_inputs_follow_the_reference_loops():
+    """NaN and infinity through the oracle, against answers read off the
+    reference's loops.  The running minimum / maximum of MinMaxNorm
+    (ponni_MinMaxNorm.h:74-78), Softmax / LogSoftmax (ponni_Softmax.h:49-52,
+    ponni_LogSoftmax.h:49-52) and the generated ReduceMax / ReduceMin /
+    ReduceLogSumExp (kokkos_nn/emitter.py:502-526) starts from feature 0 and
+    is replaced only on a strict comparison: a NaN in feature 0 makes it NaN,
+    a NaN elsewhere is passed over.  Relu is `x > 0 ? x : 0` (NaN -> 0),
+    LeakyRelu `x > 0 ? x : a x` (NaN stays NaN)."""
+    from ponni_amd import graph as G
+    from tests.test_graph import lowered_with_params
+
+    nan, inf = math.nan, math.inf
+
+    def run(layers, x, mode=oracle.MODE_F64):
+        return oracle.forward(layers, np.array(x, dtype=np.float64)[:, None], mode)[:, 0]
+
+    for mode in (oracle.MODE_F64, oracle.MODE_F32):
+        mm = [P.MinMaxNorm(3, -1.0, 1.0, 0.0)]
+        assert np.isnan(run(mm, [nan, 1.0, 3.0], mode)).all()
+        y = run(mm, [1.0, nan, 3.0], mode)
+        assert y[0] == -1.0 and np.isnan(y[1]) and y[2] == 1.0
+        y = run(mm, [1.0, 3.0, nan], mode)
+        assert y[0] == -1.0 and y[1] == 1.0 and np.isnan(y[2])
+        y = run(mm, [1.0, inf, 3.0], mode)  # scale 2 / inf = 0: finite inputs -> out_min
+        assert y[0] == -1.0 and np.isnan(y[1]) and y[2] == -1.0
+        for x in ([nan, 1.0, 2.0], [1.0, nan, 2.0], [1.0, 2.0, inf], [inf, 0.0, 0.0]):
+            assert np.isnan(run([P.Softmax(3)], x, mode)).all(), x
+            assert np.isnan(run([P.LogSoftmax(3)], x, mode)).all(), x
+        y = run([P.Softmax(3)], [0.0, -inf, 0.0], mode)
+        assert y.tolist() == [0.5, 0.0, 0.5]
+        assert run([P.Relu(2)], [nan, -inf], mode).tolist() == [0.0, 0.0]
+        y = run([P.LeakyRelu(2, 0.5)], [nan, -inf], mode)
+        assert np.isnan(y[0]) and y[1] == -inf
+        assert run([P.Tanh(3)], [inf, -inf, 0.0], mode).tolist() == [1.0, -1.0, 0.0]
+        assert np.isnan(run([P.Tanh(1)], [nan], mode)).all()
+
+    g = G.GraphBuilder(3)
+    x = g.input
+    gr = g.finish(g.concat(g.reduce("ReduceMax", x), g.reduce("ReduceMin", x), g.reduce("ReduceLogSumExp", x)))
+    layers = lowered_with_params(gr)
+    assert np.isnan(run(layers, [nan, 1.0, 3.0])).all()
+    y = run(layers, [1.0, nan, 3.0])  # max 3, min 1; the sum meets exp(NaN - 3)
+    assert y[0] == 3.0 and y[1] == 1.0 and np.isnan(y[2])
+    y = run(layers, [inf, nan, 1.0])  # max inf (log-sum-exp returns it), min 1
+    assert y.tolist() == [inf, 1.0, inf]
+    assert np.isnan(run(layers, [nan, inf, 1.0])).all()
+    y = run(layers, [1.0, -inf, 2.0])
+    assert y[0] == 2.0 and y[1] == -inf and abs(y[2] - math.log(math.e + math.e ** 2)) < 1e-14
