@@ -461,10 +461,20 @@ void barrier(Ctx<T> const& c, int i, Buf<T> in, Buf<T> saved, Buf<T> out, int64_
       int const op = static_cast<int>(d.attr[0]);
       T r;
       if (op == PONNI_REDUCE_MAX || op == PONNI_REDUCE_MIN || op == PONNI_REDUCE_LOG_SUM_EXP) {
+        // The float path keeps the running value unless the next one compares
+        // past it (emitter.py:506-511); the half2 path (16-bit modes) keeps it
+        // only if it compares past the next one, TwoHalf::maximum(reduction,
+        // value) (emitter.py:578-592, ponni_TwoHalf.h:243-251).  They differ
+        // only for NaN: the float order keeps a NaN in feature 0 and passes
+        // over later ones, the half2 order hands every NaN on to the next
+        // feature.
+        bool const h2 = c.mode == 2 || c.mode == 3 || c.mode == 6 || c.mode == 7;
+        bool const mn = op == PONNI_REDUCE_MIN;
         r = in(0, b);
         for (int f = 1; f < n; f++) {
           T const v = in(f, b);
-          r = op == PONNI_REDUCE_MIN ? (v < r ? v : r) : (v > r ? v : r);
+          if (h2) r = mn ? (r < v ? r : v) : (r > v ? r : v);
+          else r = mn ? (v < r ? v : r) : (v > r ? v : r);
         }
         if (op == PONNI_REDUCE_LOG_SUM_EXP) {
           T sum = T(0);

@@ -813,7 +813,8 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
       }
       case OP_REDUCE: {
         std::string const nv = fresh();
-        std::string call = "reduce<" + std::to_string(op.aux) + ", " + std::to_string(cur_n) + ">(" +
+        std::string call = "reduce<" + std::to_string(op.aux) + ", " + std::to_string(cur_n) + ", " +
+                           (half ? "true" : "false") + ">(" +
                            (half ? "to_f32(" + cur + ")" : cur) + ", L)";
         if (half) call = "to_h<E>(" + call + ")";
         o << "    auto " << nv << " = " << call << ";\n";
@@ -936,7 +937,8 @@ std::string narrow_source(ponni_plan_s const& p, FusedConfig& cfg) {
         break;
       }
       case OP_REDUCE:
-        o << "    reduce<" << V << ", " << cur_n << ", " << W << ", " << op.aux << ">(s);\n";
+        o << "    reduce<" << V << ", " << cur_n << ", " << W << ", " << op.aux << ", "
+          << (p.dtype == PONNI_F16 || p.dtype == PONNI_BF16 ? "true" : "false") << ">(s);\n";
         o << finish(1) << "(s, s);\n";
         break;
       case OP_POINTWISE:

@@ -627,21 +627,39 @@ __device__ inline real xprod(real v) {
 
 // Feature reduction to one feature, emitter.py:475-547; OP is a
 // ponni_reduce_op value.  The result is feature 0; padding rows are 0.
-template <int OP, int N, int T, int NT>
+// H2 (16-bit plans) follows the generated half2 path's running maximum /
+// minimum, TwoHalf::maximum(reduction, value) = reduction > value ?
+// reduction : value (emitter.py:578-592, ponni_TwoHalf.h:243-251): every NaN
+// is handed on to the next feature, so the result is NaN when the last
+// feature is, and otherwise the maximum of the features after the last NaN.
+template <int OP, int N, bool H2, int T, int NT>
 __device__ inline S<1, NT> reduce(S<T, NT> const& s, Lane const& L) {
   S<1, NT> out;
 #pragma unroll
   for (int n = 0; n < NT; n++) {
     real r;
     if constexpr (OP == 2 || OP == 3 || OP == 8) {  // MAX, MIN, LOG_SUM_EXP
+      real last = real(-1);  // H2: the last NaN feature (features ascend with m, e)
+      if constexpr (H2) {
+#pragma unroll
+        for (int m = 0; m < T; m++)
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if ((N % 16 == 0 || 16 * m + 4 * L.g + e < N) && s.v[m][n][e] != s.v[m][n][e])
+              last = real(16 * m + 4 * L.g + e);
+        last = xmax(last);
+      }
       real mx = OP == 3 ? real(__builtin_huge_val()) : -real(__builtin_huge_val());
 #pragma unroll
       for (int m = 0; m < T; m++)
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (N % 16 == 0 || 16 * m + 4 * L.g + e < N) mx = OP == 3 ? d_min(mx, s.v[m][n][e]) : d_max(mx, s.v[m][n][e]);
+        for (int e = 0; e < 4; e++) {
+          int const f = 16 * m + 4 * L.g + e;
+          if ((N % 16 == 0 || f < N) && (!H2 || real(f) > last))
+            mx = OP == 3 ? d_min(mx, s.v[m][n][e]) : d_max(mx, s.v[m][n][e]);
+        }
       mx = OP == 3 ? xmin(mx) : xmax(mx);
-      if (first_feature_nan(s, n, L)) mx = real(__builtin_nanf(""));
+      if (H2 ? last == real(N - 1) : first_feature_nan(s, n, L)) mx = real(__builtin_nanf(""));
       r = mx;
       if constexpr (OP == 8) {
         real sum = 0.0f;

@@ -251,10 +251,16 @@ __host__ __device__ __attribute__((always_inline)) inline void run_op(
         C r;
         if (op.aux == PONNI_REDUCE_MAX || op.aux == PONNI_REDUCE_MIN || op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
           bool const mn = op.aux == PONNI_REDUCE_MIN;
+          // 16-bit plans follow the generated half2 path, which keeps the
+          // running value only if it compares past the next one
+          // (TwoHalf::maximum(reduction, value), emitter.py:578-592): the
+          // two orders differ only in where a NaN ends up.
+          constexpr bool h2 = sizeof(S) == 2;
           r = load_as<S>(at<S>(in, 0, b));
           for (int f = 1; f < n; f++) {
             C const v = load_as<S>(at<S>(in, f, b));
-            r = mn ? (v < r ? v : r) : (v > r ? v : r);
+            if (h2) r = mn ? (r < v ? r : v) : (r > v ? r : v);
+            else r = mn ? (v < r ? v : r) : (v > r ? v : r);
           }
           if (op.aux == PONNI_REDUCE_LOG_SUM_EXP) {
             C sum = C(0);

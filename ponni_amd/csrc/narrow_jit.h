@@ -307,8 +307,12 @@ __device__ inline void select3(C (&s)[W][V], C const (&sv1)[W][V], C const (&sv2
 
 // Reduction over the N features into feature 0 (emitter.py:475-547); OP is
 // a ponni_reduce_op value: 0 sum, 1 mean, 2 max, 3 min, 4 L1, 5 L2,
-// 6 sum of squares, 7 log-sum, 8 log-sum-exp, 9 product.
-template <int V, int N, int W, int OP, class C>
+// 6 sum of squares, 7 log-sum, 8 log-sum-exp, 9 product.  H2 (16-bit plans)
+// keeps the running maximum / minimum only if it compares past the next
+// value, the generated half2 path's TwoHalf::maximum(reduction, value)
+// (emitter.py:578-592); the float path replaces it when the next value
+// compares past it.  The two differ only in where a NaN ends up.
+template <int V, int N, int W, int OP, bool H2, class C>
 __device__ inline void reduce(C (&s)[W][V]) {
 #pragma unroll
   for (int v = 0; v < V; v++) {
@@ -316,7 +320,11 @@ __device__ inline void reduce(C (&s)[W][V]) {
     if (OP == 2 || OP == 3 || OP == 8) {
       r = s[0][v];
 #pragma unroll
-      for (int f = 1; f < N; f++) r = OP == 3 ? (s[f][v] < r ? s[f][v] : r) : (s[f][v] > r ? s[f][v] : r);
+      for (int f = 1; f < N; f++) {
+        C const x = s[f][v];
+        if (H2) r = OP == 3 ? (r < x ? r : x) : (r > x ? r : x);
+        else r = OP == 3 ? (x < r ? x : r) : (x > r ? x : r);
+      }
       if (OP == 8) {
         C sum = C(0);
 #pragma unroll

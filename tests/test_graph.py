@@ -368,7 +368,7 @@ def test_c5_plan_is_fused_and_compiles():
     assert src.count("dense_ep_il<16, ") == 5 and src.count("dense_ep<") == 0
     assert "bias_rows<6>(P + 12480, L)" in src and "add_rows<" not in src
     assert src.count("tile_add_state(t, ") == 1 and "    add(" not in src
-    assert "reduce<1, 96>" in src and "binary<96, false, true>" in src
+    assert "reduce<1, 96, false>" in src and "binary<96, false, true>" in src
     assert "concat<3, 3>" in src and "softmax<10, false>" in src
     plan.compile()
     half = gm.plan("f16")

@@ -413,3 +413,18 @@ def test_non_finite_inputs_follow_the_reference_loops():
     assert np.isnan(run(layers, [nan, inf, 1.0])).all()
     y = run(layers, [1.0, -inf, 2.0])
     assert y[0] == 2.0 and y[1] == -inf and abs(y[2] - math.log(math.e + math.e ** 2)) < 1e-14
+
+    # The generated half2 path (16-bit modes) compares the other way round,
+    # reduction = TwoHalf::maximum(reduction, value) = reduction > value ?
+    # reduction : value (emitter.py:578-592, ponni_TwoHalf.h:243-251): a NaN
+    # is handed on to the next feature, which then replaces it.
+    for mode in (oracle.MODE_F16_OPERANDS, oracle.MODE_BF16_OPERANDS):
+        assert run(layers, [nan, 1.0, 3.0], mode)[:2].tolist() == [3.0, 1.0]
+        assert run(layers, [1.0, nan, 3.0], mode)[:2].tolist() == [3.0, 3.0]
+        assert np.isnan(run(layers, [1.0, 3.0, nan], mode)).all()
+        y = run(layers, [inf, nan, 1.0], mode)  # maximum 1: the log-sum-exp meets exp(NaN - 1)
+        assert y[0] == 1.0 and y[1] == 1.0 and np.isnan(y[2])
+        g4 = G.GraphBuilder(4)
+        four = lowered_with_params(g4.finish(g4.reduce("ReduceMax", g4.input)))
+        assert run(four, [1.0, 5.0, nan, 2.0], mode).tolist() == [2.0]
+        assert run(four, [1.0, 5.0, nan, 2.0], oracle.MODE_F32).tolist() == [5.0]
