@@ -652,7 +652,12 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
             if (!zero_at_zero(st.act)) pad = true;
           }
         }
-        // (a transposed tile's padding rows are never read nor stored)
+        // Padding rows of the output: zero weights times an infinite or NaN
+        // input make them NaN, and a later contraction would read them
+        // (zero weights times NaN), so they are zeroed unless nothing reads
+        // them -- the plan's last op, whose store stops at row n, or a
+        // transposed tile, whose padding rows are never read nor stored.
+        if (n % 16 && pad_ok && &op != &p.ops.back()) pad = true;
         if (pad && n % 16 && pad_ok) o << "      if (mo == " << tiles(n) - 1 << ") tile_zero_pad<" << n << ">(t, mo, L);\n";
         if (half) o << "      tile_round<E>(t, o);\n";
         o << (dense_hook.empty() ? "    });\n" : dense_hook);
@@ -740,7 +745,7 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
         // proj = b + W^T saved (bias first, ponni_Binop_Projection_Add.h:91-92); out = in + proj.
         auto const& sv = saved[op.slot];
         if (half) {
-          o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ">(" << cur << ", " << sv.first
+          o << "    proj_add_h<" << tiles(sv.second) << ", " << tiles(cur_n) << ", " << cur_n << ">(" << cur << ", " << sv.first
             << ", reinterpret_cast<E const*>(P + " << op.woff << "), " << vec(op.boff, cur_n) << ", L);\n";
         } else {
           // The bias seeds the accumulators; each finished tile adds the
@@ -750,7 +755,11 @@ std::string fused_source_once(ponni_plan_s const& p, FusedConfig& cfg, bool allo
             << (epi_interleave > 0 ? "dense_ep_il<" + std::to_string(epi_interleave) + ", " : std::string("dense_ep<"))
             << tiles(sv.second) << ", " << tiles(cur_n) << k_steps(op.woff, sv.second) << ">(" << sv.first
             << ", P + " << op.woff << ", bias_rows<" << tiles(cur_n) << ">(" << vec(op.boff, cur_n)
-            << ", L), L, [&](int mo, " << F4 << " (&t)[" << NT << "]) { tile_add_state(t, " << cur << ", mo); });\n";
+            << ", L), L, [&](int mo, " << F4 << " (&t)[" << NT << "]) { tile_add_state(t, " << cur << ", mo);"
+            << (cur_n % 16 ? " if (mo == " + std::to_string(tiles(cur_n) - 1) + ") tile_zero_pad<" +
+                                 std::to_string(cur_n) + ">(t, mo, L);"
+                           : std::string())
+            << " });\n";
           cur = nv;
         }
         break;

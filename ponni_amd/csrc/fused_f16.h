@@ -462,7 +462,9 @@ __device__ inline void stage_bytes(void* __restrict__ lds, void const* __restric
 }
 
 // Projection add: out = in + round(b + W^T saved) computed in fp32, rounded once.
-template <int TK, int TO, int NT, class E>
+// Rows >= N (padding) are set to zero: their zero weights times an infinite
+// or NaN saved feature are NaN, which a later contraction would read.
+template <int TK, int TO, int N, int NT, class E>
 __device__ inline void proj_add_h(H<TO, NT, E>& cur, H<TK, NT, E> const& sv, E const* __restrict__ w,
                                   float const* __restrict__ bias, Lane const& L) {
   using V8 = typename Vec<E>::x8;
@@ -485,7 +487,14 @@ __device__ inline void proj_add_h(H<TO, NT, E>& cur, H<TK, NT, E> const& sv, E c
       }
     }
 #pragma unroll
-    for (int n = 0; n < NT; n++) cur.v[mo][n] = round4<E>(widen4<E>(cur.v[mo][n]) + acc[n]);
+    for (int n = 0; n < NT; n++) {
+      cur.v[mo][n] = round4<E>(widen4<E>(cur.v[mo][n]) + acc[n]);
+      if constexpr (N % 16 != 0)
+        if (mo == TO - 1)
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (16 * mo + 4 * L.g + e >= N) cur.v[mo][n][e] = E(0.0f);
+    }
   }
 }
 

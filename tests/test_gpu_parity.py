@@ -631,6 +631,42 @@ def test_non_finite_inputs(cuda, chain, path, dtype):
     check_non_finite(got, want, dtype)
 
 
+PADDED_DENSE_CHAINS = {
+    # infinities out of the first dense layer, finite again after the
+    # activation; the next dense layer must not see the padding rows
+    "narrow": lambda r: [P.Matvec(r.uniform(-1, 1, (5, 7))), P.Bias(r.uniform(-0.1, 0.1, 7)), P.Tanh(7),
+                         P.Matvec(r.uniform(-1, 1, (7, 3))), P.Bias(r.uniform(-0.1, 0.1, 3))],
+    "tiles": lambda r: [P.Matvec(r.uniform(-1, 1, (20, 23))), P.Bias(r.uniform(-0.1, 0.1, 23)), P.Sigmoid(23),
+                        P.Matvec(r.uniform(-1, 1, (23, 9))), P.Bias(r.uniform(-0.1, 0.1, 9)), P.Selu(9),
+                        P.Matvec(r.uniform(-1, 1, (9, 18)))],
+    # the projection of a saved state holding the infinity
+    "projection": lambda r: [P.Save_State(0, 5), P.Matvec(r.uniform(-1, 1, (5, 7))), P.Tanh(7),
+                             P.Binop_Projection_Add(0, r.uniform(-1, 1, (5, 7)), r.uniform(-0.1, 0.1, 7)),
+                             P.Tanh(7), P.Matvec(r.uniform(-1, 1, (7, 3)))],
+}
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16", "f64"])
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("chain", sorted(PADDED_DENSE_CHAINS))
+def test_infinities_through_padded_dense_layers(cuda, chain, path, dtype):
+    """An infinite input makes every output of the next dense layer infinite
+    and a Tanh / Sigmoid / Selu after it finite again.  Kernels that pad a
+    layer to whole tiles must keep the padding rows at zero: a zero weight
+    times an infinity is NaN, and a NaN padding row read by the next
+    contraction would turn the finite outputs into NaN."""
+    rng = np.random.default_rng(606)
+    layers = PADDED_DENSE_CHAINS[chain](rng)
+    n_in, B = layers[0].n_in, 4099
+    x = rng.standard_normal((n_in, B))
+    x[rng.integers(n_in, size=300), np.arange(0, 600, 2)] = np.where(np.arange(300) % 2, np.inf, -np.inf)
+    print(f"padded dense: chain={chain} path={path} dtype={dtype}", flush=True)
+    got, xg, _ = gpu_run(layers, x, dtype=dtype, path=path, pad=3)
+    want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
+    assert np.isfinite(want[:, 0:600:2]).mean() > 0.5  # the case this test is about
+    check_non_finite(got, want, dtype)
+
+
 def test_strided_views_and_stream(cuda):
     """ld > batch (a column subview of a wider LayoutRight array) on a side stream."""
     import torch
