@@ -262,3 +262,99 @@ def test_random_wide_cases(cuda, group):
         if r is not None and not r[1]:
             failed.append(f"seed {seed}: {r[0]}: {r[2]}")
     assert not failed, "\n".join(failed)
+
+
+_SPECIAL = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0])
+
+
+def _non_finite_chain(rng, w):
+    """Save, then 1-4 of: an activation, LayerNorm, MinMaxNorm, Softmax /
+    LogSoftmax, a residual Tanh, a concatenation, a dense block."""
+    acts = [P.Relu, P.Elu, P.Selu, P.Silu, P.Sigmoid, P.Tanh, P.HardSwish, P.Mish, lambda n: P.Gelu(n, True)]
+    n, layers = w, [P.Save_State(0, w)]
+    for _ in range(int(rng.integers(1, 5))):
+        c = int(rng.integers(8))
+        if c <= 1:
+            layers.append(acts[int(rng.integers(len(acts)))](n))
+        elif c == 2:
+            layers.append(P.LayerNorm(rng.uniform(0.5, 1.5, n), rng.uniform(-0.2, 0.2, n), 1e-5))
+        elif c == 3:
+            layers.append(P.MinMaxNorm(n, -1.0, 2.0))
+        elif c == 4:
+            layers.append([P.Softmax, P.LogSoftmax][int(rng.integers(2))](n))
+        elif c == 5:
+            layers += [P.Save_State(1, n), P.Tanh(n), P.Binop_Add(1, n)]
+        elif c == 6 and n + w <= 48:
+            layers.append(P.Binop_Concatenate(0, n, n + w, bool(rng.integers(2))))
+            n += w
+        else:
+            m = int(rng.integers(max(2, n // 2), n + 1))
+            layers += [P.Matvec(rng.standard_normal((n, m)) / np.sqrt(n)), P.Bias(rng.uniform(-0.2, 0.2, m))]
+            n = m
+    return layers
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", range(2))
+def test_random_non_finite_cases(cuda, group):
+    """Random chains (above) and generated graphs on inputs holding NaN, +-inf
+    and signed zeros, on a path and dtype drawn per case: the oracle's NaNs
+    and infinities exactly, its finite values within the dtype's bar."""
+    import torch
+
+    from tests.test_gpu_parity import ORACLE_MODE, PATHS, TORCH_DT, check_non_finite, make_model
+
+    failed = []
+    for seed in range(11000 + 30 * group, 11000 + 30 * (group + 1)):
+        rng = np.random.default_rng(seed)
+        graph = seed % 3 == 0
+        if graph:
+            gr = random_graph(seed, aligned=bool(rng.integers(2)))
+            n = gr.size(gr.inputs[0])
+        else:
+            n = int(rng.choice([2, 5, 12, 16, 24]))
+            layers = _non_finite_chain(rng, n)
+        B = int(rng.choice([17, 1000, 4099]))
+        x = rng.standard_normal((n, B))
+        for j in range(min(B, 256)):
+            k = int(rng.integers(1, 3))
+            x[rng.choice(n, k, replace=False), j] = _SPECIAL[rng.integers(5, size=k)]
+        if graph:
+            path = ["auto", "fused", "generic", "layered"][int(rng.integers(4))]
+            dtype = ["f32", "f16"][int(rng.integers(2))]
+            print(f"seed {seed}: graph path={path} dtype={dtype} B={B}", flush=True)
+            gm = G.GeneratedModel(gr, path=path)
+            try:
+                gm.plan(dtype)
+            except P.PonniError as e:
+                if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+                    continue
+                raise
+            xt = torch.from_numpy(x.astype(np.float32)).cuda()
+            y = torch.full((gm.num_outputs, B), 7.0, dtype=torch.float32, device="cuda:0")
+            (gm.infer_batch_half2 if dtype == "f16" else gm.infer_batch)(xt, y)
+            torch.cuda.synchronize()
+            got, xg, layers = y.double().cpu().numpy(), xt.double().cpu().numpy(), lowered_with_params(gr)
+            if dtype == "f16":
+                with np.errstate(over="ignore"):
+                    xg = xg.astype(np.float16).astype(np.float64)
+        else:
+            path = PATHS[int(rng.integers(len(PATHS)))]
+            dtype = ["f32", "f16", "bf16", "f64"][int(rng.integers(4))]
+            print(f"seed {seed}: chain width={n} path={path} dtype={dtype} B={B}", flush=True)
+            try:
+                m = make_model(layers, dtype, path)
+            except P.PonniError as e:
+                if e.status == P._abi.PONNI_ERR_UNSUPPORTED:
+                    continue
+                raise
+            xs = torch.from_numpy(x).to(getattr(torch, TORCH_DT[dtype])).cuda()
+            y = m.forward_batch_parallel(xs)
+            torch.cuda.synchronize()
+            got, xg = y.double().cpu().numpy(), xs.double().cpu().numpy()
+        want = oracle.forward(layers, xg, ORACLE_MODE[dtype])
+        try:
+            check_non_finite(got, want, dtype)
+        except AssertionError as e:
+            failed.append(f"seed {seed} ({path}, {dtype}): {e}")
+    assert not failed, "\n".join(failed)
